@@ -1,0 +1,208 @@
+/*
+ * shared_amd_sampler.h - C ABI of the MI355X logit-processing and sampling
+ * library (libshared_amd_sampler.so).
+ *
+ * One call turns a batch of fp32 logit rows that already sit in HBM into
+ * one token id per row: history penalties, the packed grammar bitmask,
+ * temperature, top-k, top-p and the categorical draw with a host-supplied
+ * uniform (or greedy argmax).  A second call runs speculative verification
+ * (accept/resample of draft tokens).  Everything is stream-ordered on the
+ * caller's HIP stream; no call blocks unless its name says so.
+ *
+ * Reference interfaces replaced (paths relative to the reference repo):
+ *   sas_sample        <- sample()            lib/webgpu-llm/tokenizer.js:151-178
+ *                        topk WGSL kernel    lib/webgpu-llm/kernels.js:1389-1449
+ *                        sampler WGSL kernel lib/webgpu-llm/kernels.js:65-201
+ *   sas_verify        <- acceptSpec kernel   lib/webgpu-llm/kernels.js:211-369
+ *                        argmaxMerge kernel  lib/webgpu-llm/kernels.js:373-401
+ *   sas_mask_from_ids <- TokenMask + isListed()
+ *                        lib/webgpu-llm/tool-constraint.ts:39-42,
+ *                        lib/webgpu-llm/kernels.js:1401-1412,
+ *                        lib/webgpu-llm/token-mask-state.js:8-31
+ *   sas_clamp_params  <- #packSamplerParams  lib/webgpu-llm/model.js:401-426,
+ *                        lib/webgpu-llm/gemma-model.js:900-919
+ *   sas_pcg_uniform   <- pcg() + draw        lib/webgpu-llm/kernels.js:91-95, 181, 320
+ *
+ * Token ids are uint32 (the reference's Uint32Array).  All floating-point
+ * parameters are IEEE doubles, as JS numbers are.
+ */
+#ifndef SHARED_AMD_SAMPLER_H
+#define SHARED_AMD_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAS_ABI_VERSION 1
+
+/* Largest top_k honoured; the request API accepts 1..128
+ * (lib/completions.ts:271).  The reference GPU path caps at 20
+ * (lib/webgpu-llm/config.js:48); this library does not. */
+#define SAS_MAX_TOP_K 128
+/* Largest vocabulary a row may have (ids must fit in 24 bits). */
+#define SAS_MAX_VOCAB (1 << 22)
+/* Largest history (penalty window) per row. */
+#define SAS_MAX_HISTORY 65535
+/* Largest number of draft tokens per sequence for sas_verify. */
+#define SAS_MAX_DRAFT 16
+
+/* Written to out_ids for a row in which no token is allowed. */
+#define SAS_NO_TOKEN 0xFFFFFFFFu
+
+/* Return codes. */
+#define SAS_OK 0
+#define SAS_ERR_INVALID 1     /* bad argument; see sas_last_error() */
+#define SAS_ERR_HIP 2         /* a HIP runtime call failed */
+#define SAS_ERR_NOMEM 3       /* device allocation failed */
+
+/* Per-row flags (out_flags). */
+#define SAS_FLAG_EMPTY_ROW 1u      /* no allowed, non-NaN token in the row */
+#define SAS_FLAG_TOPP_EDGE 2u      /* a running top-p mass was within 1e-6 of top_p */
+#define SAS_FLAG_DRAW_EDGE 4u      /* the draw residual was within 1e-12*mass of 0 */
+#define SAS_FLAG_SLOW_SELECT 8u    /* exact tie-safe fallback selection ran */
+
+/* TokenMask kinds (lib/webgpu-llm/tool-constraint.ts:39-42). */
+#define SAS_MASK_ALL 0
+#define SAS_MASK_ALLOW 1
+#define SAS_MASK_DENY 2
+
+/*
+ * Sampling parameters of one row.  Semantics follow sample()
+ * (lib/webgpu-llm/tokenizer.js:151-178) on the full vocabulary:
+ *   v = logit                                   (fp32 value, promoted to double)
+ *   v = softcap > 0 ? softcap*tanh(v/softcap) : v   (fp32, kernels.js:1393-1395)
+ *   if the id occurs c > 0 times in the row history:
+ *       v = v > 0 ? v / repetition_penalty : v * repetition_penalty
+ *       v = v - frequency_penalty * c - presence_penalty
+ *   candidates = allowed, non-NaN ids ordered by (v desc, id asc)
+ *   temperature <= 0 (or NaN): the first candidate (greedy)
+ *   otherwise softmax over the first top_k, top-p cut, draw with U.
+ * Presence alone with the 512-token window reproduces tokenizer.js:157.
+ */
+typedef struct sas_params {
+  double temperature;
+  double top_p;
+  double repetition_penalty; /* 1 = off */
+  double presence_penalty;   /* 0 = off */
+  double frequency_penalty;  /* 0 = off */
+  float softcap;             /* 0 = off; Gemma uses 30 (gemma-config.js:47) */
+  int32_t top_k;             /* clamped to [1, SAS_MAX_TOP_K] */
+} sas_params;
+
+/*
+ * One batch of rows for sas_sample.  Pointers marked "device" are HBM
+ * addresses; the call only reads inputs and writes the outputs.
+ */
+typedef struct sas_rows {
+  const float *logits;         /* device [rows][logits_stride] fp32 */
+  int64_t logits_stride;       /* elements between rows, >= vocab */
+  int32_t vocab;               /* 1..SAS_MAX_VOCAB */
+  int32_t rows;                /* >= 0 */
+  const uint32_t *mask;        /* device [rows][mask_stride] or NULL (all allowed);
+                                  bit (id & 31) of word id >> 5 set = id allowed */
+  int64_t mask_stride;         /* words between rows, >= ceil(vocab / 32) */
+  const uint32_t *hist_ids;    /* device, all rows' histories back to back, or NULL */
+  const int32_t *hist_offsets; /* device [rows + 1]: row r owns
+                                  hist_ids[hist_offsets[r] .. hist_offsets[r+1]) */
+  const double *uniforms;      /* device [rows], U in [0, 1); may be NULL when every
+                                  row is greedy */
+  sas_params params;           /* used for every row unless row_params is set */
+  const sas_params *row_params;/* device [rows] or NULL */
+  uint32_t *out_ids;           /* device [rows] (required) */
+  double *out_probs;           /* device [rows][SAS_MAX_TOP_K] or NULL: softmax
+                                  probability of each top-k candidate */
+  uint32_t *out_cand_ids;      /* device [rows][SAS_MAX_TOP_K] or NULL: the ranked
+                                  top-k candidate ids */
+  int32_t *out_counts;         /* device [rows][2] or NULL: {k, cut} (0,0 greedy) */
+  uint32_t *out_flags;         /* device [rows] or NULL: SAS_FLAG_* bits */
+} sas_rows;
+
+/*
+ * Speculative verification (rejection sampling, Leviathan et al. 2023 /
+ * Chen et al. 2023).  Sequence s has draft_len draft tokens d_j sampled
+ * from q_j = softmax(draft logits row j / T) over allowed ids, and
+ * draft_len + 1 target rows p_j = softmax(target logits row j / T).
+ * Position j accepts d_j iff U1 * q_j(d_j) <= p_j(d_j); the first
+ * rejected position draws from normalize(max(0, p_j - q_j)) with U2; if
+ * all drafts are accepted, the bonus token is drawn from p_{draft_len}
+ * with its U2.  Draws are inverse-CDF over ids in ascending order.
+ */
+typedef struct sas_verify_rows {
+  const float *target_logits;  /* device [seqs * (draft_len + 1)][logits_stride] */
+  const float *draft_logits;   /* device [seqs * draft_len][logits_stride] */
+  int64_t logits_stride;
+  int32_t vocab;
+  int32_t seqs;
+  int32_t draft_len;           /* 1..SAS_MAX_DRAFT */
+  const uint32_t *draft_ids;   /* device [seqs][draft_len] */
+  const uint32_t *mask;        /* device [seqs * (draft_len + 1)][mask_stride] or NULL;
+                                  row j of a sequence applies to target row j and
+                                  draft row j */
+  int64_t mask_stride;
+  const double *uniforms;      /* device [seqs][draft_len + 1][2] = {U1, U2} */
+  double temperature;          /* > 0 */
+  uint32_t *out_tokens;        /* device [seqs][draft_len + 1]: accepted drafts then
+                                  the correction or bonus token; unused tail slots
+                                  are SAS_NO_TOKEN */
+  int32_t *out_accepted;       /* device [seqs]: number of accepted drafts */
+} sas_verify_rows;
+
+typedef struct sas_sampler sas_sampler;
+
+/* Library version string ("shared_amd_sampler <abi> gfx950"). */
+const char *sas_version(void);
+
+/* Create a sampler bound to HIP device `device`.  Owns device scratch. */
+int sas_create(int device, sas_sampler **out);
+void sas_destroy(sas_sampler *s);
+
+/* Message of the last failed call on `s` (or of the last failed
+ * sas_create / handle-free call on this thread when s is NULL). */
+const char *sas_last_error(const sas_sampler *s);
+
+/* Pre-size scratch so later calls of at most this shape allocate nothing. */
+int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab);
+
+/* Sample one token per row.  stream = hipStream_t or NULL (the handle's own
+ * stream).  A handle must not run two calls concurrently. */
+int sas_sample(sas_sampler *s, const sas_rows *rows, void *stream);
+
+/* Speculative accept/resample, stream-ordered like sas_sample. */
+int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
+
+/* Host: clamp parameters with the reference packer's rules
+ * (model.js:418-423): non-finite or negative temperature -> 0 (greedy),
+ * top_p -> [0, 1] (non-finite -> 1), presence -> [0, 10] (non-finite -> 0),
+ * top_k -> [1, SAS_MAX_TOP_K] (non-finite handled by the caller), softcap
+ * non-finite or negative -> 0, repetition non-finite or <= 0 -> 1,
+ * frequency non-finite -> 0. */
+int sas_clamp_params(const sas_params *in, sas_params *out);
+
+/* Host: build the packed bitmask for a TokenMask.  kind = SAS_MASK_*;
+ * ids need not be sorted; ids >= vocab are ignored.  nwords >= ceil(vocab/32);
+ * bits at ids >= vocab are left clear.  Returns the number of allowed ids
+ * (>= 0) or -SAS_ERR_INVALID. */
+int64_t sas_mask_from_ids(int32_t kind, const uint32_t *ids, size_t count,
+                          int32_t vocab, uint32_t *words, int64_t nwords);
+
+/* Host: the reference GPU sampler's uniform,
+ * (pcg(seed ^ it*0x9E3779B9 ^ row*0x85EBCA6B) & 0xFFFFFF) / 2^24. */
+double sas_pcg_uniform(uint32_t seed, uint32_t it, uint32_t row);
+
+/* Device memory plumbing for hosts that have no HIP binding (N-API, ctypes). */
+int sas_alloc(sas_sampler *s, size_t bytes, void **out);
+int sas_free(sas_sampler *s, void *p);
+/* kind: 0 host->device, 1 device->host, 2 device->device.  Asynchronous on
+ * `stream` for device->device; host copies complete before returning. */
+int sas_memcpy(sas_sampler *s, void *dst, const void *src, size_t bytes,
+               int kind, void *stream);
+int sas_synchronize(sas_sampler *s, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHARED_AMD_SAMPLER_H */

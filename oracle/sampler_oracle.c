@@ -1,0 +1,455 @@
+/*
+ * sampler_oracle.c - CPU restatement of the reference sampling path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see sampler_oracle.h).  Compiled with
+ * -ffp-contract=off so every double operation rounds exactly as a JS
+ * engine's does.
+ *
+ * Function -> reference it follows -> how it is pinned:
+ *   orc_exp            V8 Math.exp, used by sample() (tokenizer.js:165); the
+ *                      algorithm is fdlibm e_exp.c (Sun Microsystems 1993),
+ *                      which V8's base::ieee754::exp implements.  Pinned by
+ *                      tests/golden/v8_math_exp.json (outputs of Node's own
+ *                      Math.exp) and closed forms (exp(0)=1, exp(-inf)=0).
+ *   orc_sample_row     tokenizer.js:151-178 (penalty, stable sort, greedy,
+ *                      softmax over top-k, top-p cut, draw), with the
+ *                      per-element mask test of kernels.js:1422-1426 and the
+ *                      tie order of kernels.js:1433,1439 (lowest id first).
+ *                      Pinned by hand-derived known answers, brute-force
+ *                      ordering (select_mode 1), exact-distribution tests and
+ *                      bit-equality with the Node restatement sample_js.js
+ *                      run on V8.
+ *   orc_penalize       presence: tokenizer.js:157.  Repetition / frequency do
+ *                      not exist in the reference ("parity unpinned" against
+ *                      it); they follow the CTRL / OpenAI definitions and are
+ *                      pinned by invariants (identity at r=1,f=0,p=0; ids
+ *                      outside the history untouched; sign rule; monotone).
+ *   orc_softcap        kernels.js:1393-1395 (cap*tanh(x/cap) in fp32).  tanhf
+ *                      of the host libm and of the GPU may differ by an ulp:
+ *                      parity unpinned at that ulp (tolerance-checked).
+ *   orc_pcg            kernels.js:91-95, uniform kernels.js:181, 320.
+ *                      Pinned by a closed-form recomputation of the hash.
+ *   orc_mask_from_ids  TokenMask (tool-constraint.ts:39-42) + isListed
+ *                      (kernels.js:1401-1412); pinned by the reference test
+ *                      tests/token-mask-state.test.ts:49-55 semantics and
+ *                      brute force.
+ *   orc_verify         no reference (acceptSpec is an exact-match cascade,
+ *                      kernels.js:328-339): textbook rejection sampling;
+ *                      pinned by distribution tests (empirical marginal = p,
+ *                      q = p accepts always, one-hot q accepts w.p. p(d)).
+ */
+#include "sampler_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ exp -- */
+
+static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
+static inline double u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
+
+/* fdlibm exp: x = k*ln2 + r, |r| <= ln2/2, exp(r) from a degree-5 Remez
+ * rational form, scaled by 2^k.  Constants are fdlibm's published ones. */
+double orc_exp(double x) {
+  static const double ln2_hi[2] = {6.93147180369123816490e-01, -6.93147180369123816490e-01};
+  static const double ln2_lo[2] = {1.90821492927058770002e-10, -1.90821492927058770002e-10};
+  static const double half[2] = {0.5, -0.5};
+  const double inv_ln2 = 1.44269504088896338700e+00;
+  const double P1 = 1.66666666666666019037e-01, P2 = -2.77777777770155933842e-03,
+               P3 = 6.61375632143793436117e-05, P4 = -1.65339022054652515390e-06,
+               P5 = 4.13813679705723846039e-08;
+  const double over = 7.09782712893383973096e+02, under = -7.45133219101941108420e+02;
+  const double two_m1000 = 9.33263618503218878990e-302, big = 1.0e300;
+  uint64_t bits = d2u(x);
+  uint32_t hx = (uint32_t)(bits >> 32);
+  int neg = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  double hi = 0.0, lo = 0.0;
+  int k = 0;
+  if (hx >= 0x40862E42u) {                 /* |x| >= 709.78 */
+    if (hx >= 0x7ff00000u) {
+      if (((hx & 0xfffffu) | (uint32_t)bits) != 0) return x + x; /* NaN */
+      return neg ? 0.0 : x;                /* exp(+-inf) */
+    }
+    if (x > over) return big * big;
+    if (x < under) return two_m1000 * two_m1000;
+  }
+  if (hx > 0x3fd62e42u) {                  /* |x| > ln2/2 */
+    if (hx < 0x3FF0A2B2u) {                /* |x| < 1.5 ln2 */
+      if (x == 1.0) return 2.718281828459045;
+      hi = x - ln2_hi[neg];
+      lo = ln2_lo[neg];
+      k = 1 - neg - neg;
+    } else {
+      k = (int)(inv_ln2 * x + half[neg]);
+      double t = (double)k;
+      hi = x - t * ln2_hi[0];
+      lo = t * ln2_lo[0];
+    }
+    x = hi - lo;
+  } else if (hx < 0x3e300000u) {           /* |x| < 2^-28 */
+    if (big + x > 1.0) return 1.0 + x;
+  } else {
+    k = 0;
+  }
+  double t = x * x;
+  double c = x - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+  if (k == 0) return 1.0 - ((x * c) / (c - 2.0) - x);
+  double y = 1.0 - ((lo - (x * c) / (2.0 - c)) - hi);
+  if (k >= -1021) {
+    if (k == 1024) return y * 2.0 * 8.988465674311579539e307;
+    return y * u2d((uint64_t)(0x3ff00000 + (k << 20)) << 32);
+  }
+  return y * u2d((uint64_t)(0x3ff00000 + ((k + 1000) << 20)) << 32) * two_m1000;
+}
+
+/* ------------------------------------------------------------ pcg draw -- */
+
+uint32_t orc_pcg(uint32_t x) {
+  uint32_t h = x * 747796405u + 2891336453u;
+  h = ((h >> ((h >> 28u) + 4u)) ^ h) * 277803737u;
+  return (h >> 22u) ^ h;
+}
+
+double orc_pcg_uniform(uint32_t seed, uint32_t it, uint32_t row) {
+  uint32_t h = orc_pcg(seed ^ (it * 0x9E3779B9u) ^ (row * 0x85EBCA6Bu));
+  /* kernels.js:181 computes this in f32; 24-bit integer / 2^24 is exact. */
+  return (double)(h & 0xFFFFFFu) / 16777216.0;
+}
+
+/* ------------------------------------------------------ value pipeline -- */
+
+float orc_softcap(float x, float cap) {
+  float q = x / cap;
+  float t = tanhf(q);
+  return cap * t;
+}
+
+double orc_penalize(double v, uint32_t count, const orc_params *p) {
+  if (count == 0) return v;
+  double r = p->repetition_penalty;
+  v = v > 0.0 ? v / r : v * r;
+  v = v - p->frequency_penalty * (double)count;
+  v = v - p->presence_penalty;
+  return v;
+}
+
+typedef struct cand { double v; uint32_t id; } cand;
+
+/* (v desc, id asc): the order a stable descending sort of the reference's
+ * id-ascending candidate list produces (tokenizer.js:160). */
+static inline int better(const cand *a, const cand *b) {
+  return a->v > b->v || (a->v == b->v && a->id < b->id);
+}
+
+static int cmp_cand(const void *pa, const void *pb) {
+  const cand *a = (const cand *)pa, *b = (const cand *)pb;
+  if (better(a, b)) return -1;
+  if (better(b, a)) return 1;
+  return 0;
+}
+
+/* min-heap on "worst first" of at most cap entries */
+static void heap_push(cand *h, int *n, int cap, cand c) {
+  if (*n < cap) {
+    int i = (*n)++;
+    h[i] = c;
+    while (i > 0) {
+      int par = (i - 1) >> 1;
+      if (!better(&h[par], &h[i])) break;
+      cand t = h[par]; h[par] = h[i]; h[i] = t;
+      i = par;
+    }
+    return;
+  }
+  if (!better(&c, &h[0])) return;
+  h[0] = c;
+  int i = 0;
+  for (;;) {
+    int l = 2 * i + 1, r = l + 1, w = i;
+    if (l < *n && better(&h[w], &h[l])) w = l;
+    if (r < *n && better(&h[w], &h[r])) w = r;
+    if (w == i) break;
+    cand t = h[w]; h[w] = h[i]; h[i] = t;
+    i = w;
+  }
+}
+
+static int clamp_top_k(int32_t k) {
+  if (k < 1) return 1;
+  if (k > ORC_MAX_TOP_K) return ORC_MAX_TOP_K;
+  return k;
+}
+
+void orc_sample_row(const float *logits, int32_t vocab, const uint32_t *mask,
+                    const uint32_t *hist, int32_t hist_len,
+                    const orc_params *p, double uniform, int select_mode,
+                    orc_result *out) {
+  memset(out, 0, sizeof(*out));
+  out->id = ORC_NO_TOKEN;
+  /* history counts */
+  uint32_t *counts = NULL;
+  if (hist && hist_len > 0) {
+    counts = (uint32_t *)calloc((size_t)vocab, sizeof(uint32_t));
+    for (int32_t i = 0; i < hist_len; i++)
+      if (hist[i] < (uint32_t)vocab) counts[hist[i]]++;
+  }
+  int greedy = !(p->temperature > 0.0);
+  int kreq = greedy ? 1 : clamp_top_k(p->top_k);
+  cand *sel;
+  int nsel = 0;
+  int64_t nvalid = 0;
+  cand *all = NULL;
+  if (select_mode == 1) all = (cand *)malloc(sizeof(cand) * (size_t)vocab);
+  cand heap[ORC_MAX_TOP_K];
+  for (int32_t i = 0; i < vocab; i++) {
+    if (mask && !((mask[i >> 5] >> (i & 31)) & 1u)) continue;
+    float x = logits[i];
+    if (p->softcap > 0.0f) x = orc_softcap(x, p->softcap);
+    if (x != x) continue; /* NaN never becomes a candidate */
+    double v = (double)x;
+    if (counts) v = orc_penalize(v, counts[i], p);
+    if (v != v) continue;
+    cand c = {v, (uint32_t)i};
+    nvalid++;
+    if (select_mode == 1) all[nsel++] = c;
+    else heap_push(heap, &nsel, kreq, c);
+  }
+  free(counts);
+  if (nvalid == 0) {
+    out->flags |= ORC_FLAG_EMPTY_ROW;
+    free(all);
+    return;
+  }
+  if (select_mode == 1) {
+    qsort(all, (size_t)nsel, sizeof(cand), cmp_cand);
+    sel = all;
+    if (nsel > kreq) nsel = kreq;
+  } else {
+    qsort(heap, (size_t)nsel, sizeof(cand), cmp_cand);
+    sel = heap;
+  }
+  /* tokenizer.js:161-162 */
+  int k = nsel < kreq ? nsel : kreq;
+  if (greedy) {
+    out->id = sel[0].id;
+    free(all);
+    return;
+  }
+  /* tokenizer.js:163-168: p_i = exp((v_i - v_0) / T), sum in order */
+  double probs[ORC_MAX_TOP_K], prefix[ORC_MAX_TOP_K];
+  double mx = sel[0].v, sum = 0.0;
+  for (int i = 0; i < k; i++) {
+    probs[i] = orc_exp((sel[i].v - mx) / p->temperature);
+    sum += probs[i];
+    prefix[i] = sum;
+  }
+  /* tokenizer.js:169-174: top-p cut */
+  double cum = 0.0;
+  int cut = k;
+  for (int i = 0; i < k; i++) {
+    cum += probs[i] / sum;
+    if (fabs(cum - p->top_p) < 1e-6) out->flags |= ORC_FLAG_TOPP_EDGE;
+    if (cum >= p->top_p) { cut = i + 1; break; }
+  }
+  /* tokenizer.js:175-177: r = U * sum(probs[0..cut)) with reduce from 0,
+   * which equals the running sum prefix[cut-1] bit for bit. */
+  double sub = prefix[cut - 1];
+  double r = uniform * sub;
+  uint32_t id = sel[cut - 1].id;
+  for (int i = 0; i < cut; i++) {
+    r -= probs[i];
+    if (fabs(r) <= 1e-12 * sub) out->flags |= ORC_FLAG_DRAW_EDGE;
+    if (r <= 0.0) { id = sel[i].id; break; }
+  }
+  out->id = id;
+  out->k = k;
+  out->cut = cut;
+  for (int i = 0; i < k; i++) {
+    out->cand_ids[i] = sel[i].id;
+    out->probs[i] = probs[i] / sum;
+  }
+  free(all);
+}
+
+/* ----------------------------------------------------------------- batch -- */
+
+typedef struct batch_job {
+  const float *logits; int64_t logits_stride; int32_t vocab; int32_t rows;
+  const uint32_t *mask; int64_t mask_stride;
+  const uint32_t *hist_ids; const int32_t *hist_offsets;
+  const double *uniforms; const orc_params *params; const orc_params *row_params;
+  uint32_t *out_ids; double *out_probs; uint32_t *out_cand_ids;
+  int32_t *out_counts; uint32_t *out_flags;
+  int32_t r0, r1;
+} batch_job;
+
+static void *batch_worker(void *arg) {
+  batch_job *j = (batch_job *)arg;
+  orc_result res;
+  for (int32_t r = j->r0; r < j->r1; r++) {
+    const orc_params *p = j->row_params ? &j->row_params[r] : j->params;
+    const uint32_t *h = NULL;
+    int32_t hl = 0;
+    if (j->hist_ids && j->hist_offsets) {
+      h = j->hist_ids + j->hist_offsets[r];
+      hl = j->hist_offsets[r + 1] - j->hist_offsets[r];
+    }
+    double u = j->uniforms ? j->uniforms[r] : 0.0;
+    orc_sample_row(j->logits + (int64_t)r * j->logits_stride, j->vocab,
+                   j->mask ? j->mask + (int64_t)r * j->mask_stride : NULL, h, hl,
+                   p, u, 0, &res);
+    j->out_ids[r] = res.id;
+    if (j->out_counts) { j->out_counts[2 * r] = res.k; j->out_counts[2 * r + 1] = res.cut; }
+    if (j->out_flags) j->out_flags[r] = res.flags;
+    if (j->out_probs)
+      for (int i = 0; i < ORC_MAX_TOP_K; i++)
+        j->out_probs[(int64_t)r * ORC_MAX_TOP_K + i] = i < res.k ? res.probs[i] : 0.0;
+    if (j->out_cand_ids)
+      for (int i = 0; i < ORC_MAX_TOP_K; i++)
+        j->out_cand_ids[(int64_t)r * ORC_MAX_TOP_K + i] = i < res.k ? res.cand_ids[i] : ORC_NO_TOKEN;
+  }
+  return NULL;
+}
+
+void orc_sample_rows(const float *logits, int64_t logits_stride, int32_t vocab,
+                     int32_t rows, const uint32_t *mask, int64_t mask_stride,
+                     const uint32_t *hist_ids, const int32_t *hist_offsets,
+                     const double *uniforms, const orc_params *params,
+                     const orc_params *row_params, uint32_t *out_ids,
+                     double *out_probs, uint32_t *out_cand_ids,
+                     int32_t *out_counts, uint32_t *out_flags, int threads) {
+  if (threads < 1) threads = 1;
+  if (threads > rows) threads = rows > 0 ? rows : 1;
+  batch_job base = {logits, logits_stride, vocab, rows, mask, mask_stride,
+                    hist_ids, hist_offsets, uniforms, params, row_params,
+                    out_ids, out_probs, out_cand_ids, out_counts, out_flags, 0, rows};
+  if (threads == 1) { batch_worker(&base); return; }
+  pthread_t tid[64];
+  batch_job jobs[64];
+  if (threads > 64) threads = 64;
+  for (int t = 0; t < threads; t++) {
+    jobs[t] = base;
+    jobs[t].r0 = (int32_t)((int64_t)rows * t / threads);
+    jobs[t].r1 = (int32_t)((int64_t)rows * (t + 1) / threads);
+    pthread_create(&tid[t], NULL, batch_worker, &jobs[t]);
+  }
+  for (int t = 0; t < threads; t++) pthread_join(tid[t], NULL);
+}
+
+/* ------------------------------------------------------------------ mask -- */
+
+int64_t orc_mask_from_ids(int32_t kind, const uint32_t *ids, size_t count,
+                          int32_t vocab, uint32_t *words, int64_t nwords) {
+  int64_t need = ((int64_t)vocab + 31) / 32;
+  if (nwords < need || kind < 0 || kind > 2) return -1;
+  memset(words, 0, sizeof(uint32_t) * (size_t)nwords);
+  if (kind == 1) {
+    for (size_t i = 0; i < count; i++)
+      if (ids[i] < (uint32_t)vocab) words[ids[i] >> 5] |= 1u << (ids[i] & 31);
+  } else {
+    for (int32_t i = 0; i < vocab; i++) words[i >> 5] |= 1u << (i & 31);
+    if (kind == 2)
+      for (size_t i = 0; i < count; i++)
+        if (ids[i] < (uint32_t)vocab) words[ids[i] >> 5] &= ~(1u << (ids[i] & 31));
+  }
+  int64_t n = 0;
+  for (int64_t w = 0; w < need; w++) n += __builtin_popcount(words[w]);
+  return n;
+}
+
+/* ---------------------------------------------------------------- verify -- */
+
+/* Masked softmax weights of one row: w_i = exp((x_i - M) / T) for allowed
+ * non-NaN ids (0 otherwise); returns Z = sum in ascending id order. */
+static double soft_weights(const float *x, int32_t vocab, const uint32_t *mask,
+                           double T, double *w) {
+  double m = -INFINITY;
+  for (int32_t i = 0; i < vocab; i++) {
+    if (mask && !((mask[i >> 5] >> (i & 31)) & 1u)) continue;
+    if (x[i] != x[i]) continue;
+    if ((double)x[i] > m) m = (double)x[i];
+  }
+  double z = 0.0;
+  for (int32_t i = 0; i < vocab; i++) {
+    w[i] = 0.0;
+    if (mask && !((mask[i >> 5] >> (i & 31)) & 1u)) continue;
+    if (x[i] != x[i]) continue;
+    w[i] = orc_exp(((double)x[i] - m) / T);
+    z += w[i];
+  }
+  return z;
+}
+
+/* smallest id with w > 0 whose running sum exceeds u * total */
+static uint32_t draw_cdf(const double *w, int32_t vocab, double total, double u) {
+  double target = u * total, cum = 0.0;
+  uint32_t last = ORC_NO_TOKEN;
+  for (int32_t i = 0; i < vocab; i++) {
+    if (w[i] <= 0.0) continue;
+    cum += w[i];
+    last = (uint32_t)i;
+    if (cum > target) return (uint32_t)i;
+  }
+  return last;
+}
+
+void orc_verify(const float *target, const float *draft, int64_t stride,
+                int32_t vocab, int32_t seqs, int32_t draft_len,
+                const uint32_t *draft_ids, const uint32_t *mask,
+                int64_t mask_stride, const double *uniforms,
+                double temperature, uint32_t *out_tokens,
+                int32_t *out_accepted, double *out_ratio) {
+  double *wp = (double *)malloc(sizeof(double) * (size_t)vocab);
+  double *wq = (double *)malloc(sizeof(double) * (size_t)vocab);
+  int32_t L = draft_len;
+  for (int32_t s = 0; s < seqs; s++) {
+    uint32_t *out = out_tokens + (int64_t)s * (L + 1);
+    for (int32_t j = 0; j <= L; j++) out[j] = ORC_NO_TOKEN;
+    int32_t acc = 0;
+    int done = 0;
+    for (int32_t j = 0; j < L && !done; j++) {
+      const uint32_t *m = mask ? mask + ((int64_t)s * (L + 1) + j) * mask_stride : NULL;
+      const float *tx = target + ((int64_t)s * (L + 1) + j) * stride;
+      const float *dx = draft + ((int64_t)s * L + j) * stride;
+      double zp = soft_weights(tx, vocab, m, temperature, wp);
+      double zq = soft_weights(dx, vocab, m, temperature, wq);
+      uint32_t d = draft_ids[(int64_t)s * L + j];
+      double pd = d < (uint32_t)vocab ? wp[d] / zp : 0.0;
+      double qd = d < (uint32_t)vocab ? wq[d] / zq : 0.0;
+      const double *u = uniforms + ((int64_t)s * (L + 1) + j) * 2;
+      if (out_ratio) out_ratio[(int64_t)s * (L + 1) + j] = qd > 0.0 ? pd / qd : INFINITY;
+      if (d < (uint32_t)vocab && pd > 0.0 && u[0] * qd <= pd) {
+        out[j] = d;
+        acc++;
+        continue;
+      }
+      /* residual max(0, p - q), drawn in ascending id order */
+      double tot = 0.0;
+      for (int32_t i = 0; i < vocab; i++) {
+        double r = wp[i] / zp - wq[i] / zq;
+        wp[i] = r > 0.0 ? r : 0.0;
+        tot += wp[i];
+      }
+      if (tot > 0.0) {
+        out[j] = draw_cdf(wp, vocab, tot, u[1]);
+      } else {
+        soft_weights(tx, vocab, m, temperature, wp);
+        out[j] = draw_cdf(wp, vocab, zp, u[1]);
+      }
+      done = 1;
+    }
+    if (!done) {
+      const uint32_t *m = mask ? mask + ((int64_t)s * (L + 1) + L) * mask_stride : NULL;
+      const float *tx = target + ((int64_t)s * (L + 1) + L) * stride;
+      double zp = soft_weights(tx, vocab, m, temperature, wp);
+      const double *u = uniforms + ((int64_t)s * (L + 1) + L) * 2;
+      out[L] = draw_cdf(wp, vocab, zp, u[1]);
+    }
+    out_accepted[s] = acc;
+  }
+  free(wp);
+  free(wq);
+}

@@ -1,0 +1,84 @@
+/*
+ * sampler_oracle.h - CPU oracle for the logit-processing / sampling path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this code, and only as the checker.
+ * The product library (shared_amd/) never links or calls it.
+ *
+ * The oracle restates, in plain C with IEEE doubles and no FMA contraction,
+ * the reference's sampling semantics (lib/webgpu-llm/tokenizer.js:151-178)
+ * applied to the full vocabulary, plus the extensions the reference lacks
+ * (repetition / frequency penalties, packed bitmask, rejection-sampling
+ * verify).  Parity status of each function is listed in sampler_oracle.c.
+ */
+#ifndef SAMPLER_ORACLE_H
+#define SAMPLER_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define ORC_MAX_TOP_K 128
+#define ORC_NO_TOKEN 0xFFFFFFFFu
+
+#define ORC_FLAG_EMPTY_ROW 1u
+#define ORC_FLAG_TOPP_EDGE 2u
+#define ORC_FLAG_DRAW_EDGE 4u
+
+/* Same layout as sas_params (include/shared_amd_sampler.h). */
+typedef struct orc_params {
+  double temperature;
+  double top_p;
+  double repetition_penalty;
+  double presence_penalty;
+  double frequency_penalty;
+  float softcap;
+  int32_t top_k;
+} orc_params;
+
+typedef struct orc_result {
+  uint32_t id;
+  int32_t k;       /* candidates in the softmax (0 when greedy) */
+  int32_t cut;     /* top-p cut (0 when greedy) */
+  uint32_t flags;
+  uint32_t cand_ids[ORC_MAX_TOP_K];
+  double probs[ORC_MAX_TOP_K];
+} orc_result;
+
+double orc_exp(double x);
+uint32_t orc_pcg(uint32_t x);
+double orc_pcg_uniform(uint32_t seed, uint32_t it, uint32_t row);
+float orc_softcap(float x, float cap);
+double orc_penalize(double v, uint32_t count, const orc_params *p);
+
+/* One row.  mask: ceil(V/32) words or NULL; hist: H ids or NULL.
+ * select_mode 0 = bounded heap, 1 = full qsort (slow, obviously ordered). */
+void orc_sample_row(const float *logits, int32_t vocab, const uint32_t *mask,
+                    const uint32_t *hist, int32_t hist_len,
+                    const orc_params *p, double uniform, int select_mode,
+                    orc_result *out);
+
+/* Batch form mirroring sas_sample: strides in elements / words, CSR history,
+ * params per row (row_params) or shared (params).  Outputs may be NULL except
+ * out_ids.  Rows are processed on `threads` pthreads (<= 0: one). */
+void orc_sample_rows(const float *logits, int64_t logits_stride, int32_t vocab,
+                     int32_t rows, const uint32_t *mask, int64_t mask_stride,
+                     const uint32_t *hist_ids, const int32_t *hist_offsets,
+                     const double *uniforms, const orc_params *params,
+                     const orc_params *row_params, uint32_t *out_ids,
+                     double *out_probs, uint32_t *out_cand_ids,
+                     int32_t *out_counts, uint32_t *out_flags, int threads);
+
+/* TokenMask -> packed words (kind 0 all, 1 allow, 2 deny).  Returns the
+ * number of allowed ids. */
+int64_t orc_mask_from_ids(int32_t kind, const uint32_t *ids, size_t count,
+                          int32_t vocab, uint32_t *words, int64_t nwords);
+
+/* Rejection-sampling verify for `seqs` sequences (layout as sas_verify_rows). */
+void orc_verify(const float *target, const float *draft, int64_t stride,
+                int32_t vocab, int32_t seqs, int32_t draft_len,
+                const uint32_t *draft_ids, const uint32_t *mask,
+                int64_t mask_stride, const double *uniforms,
+                double temperature, uint32_t *out_tokens,
+                int32_t *out_accepted, double *out_ratio);
+
+#endif

@@ -1,0 +1,293 @@
+// capi.hip - the extern "C" boundary of libshared_amd_sampler.so.
+//
+// Validation, scratch ownership and launches.  No compute happens on the
+// host; a missing device is an error, never a fallback.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "sas_device.h"
+#include "sas_launch.h"
+#include "shared_amd_sampler.h"
+
+struct sas_sampler {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  void *recs = nullptr;
+  size_t recs_cap = 0;
+  void *hdrs = nullptr;
+  size_t hdrs_cap = 0;
+  uint32_t *counters = nullptr;
+  int32_t counters_cap = 0;
+  void *vscratch = nullptr;   // sas_verify partials
+  size_t vscratch_cap = 0;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(sas_sampler *s, int code, const std::string &msg) {
+  if (s) s->err = msg;
+  else g_err = msg;
+  return code;
+}
+
+int hip_fail(sas_sampler *s, hipError_t e, const char *what) {
+  return fail(s, SAS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+hipStream_t pick_stream(sas_sampler *s, void *stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : s->stream;
+}
+
+// Grow a scratch buffer; waits for queued work before freeing the old one.
+int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
+  if (need <= *cap) return SAS_OK;
+  hipError_t e;
+  if (*buf) {
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(s, e, "hipDeviceSynchronize");
+    if ((e = hipFree(*buf)) != hipSuccess) return hip_fail(s, e, "hipFree");
+    *buf = nullptr;
+    *cap = 0;
+  }
+  size_t bytes = (need + 255) & ~size_t(255);
+  if ((e = hipMalloc(buf, bytes)) != hipSuccess) {
+    *buf = nullptr;
+    return fail(s, SAS_ERR_NOMEM, std::string("hipMalloc scratch: ") + hipGetErrorString(e));
+  }
+  if (zero && (e = hipMemset(*buf, 0, bytes)) != hipSuccess) return hip_fail(s, e, "hipMemset");
+  *cap = bytes;
+  return SAS_OK;
+}
+
+int ensure_sample_scratch(sas_sampler *s, int rows, int splits) {
+  int rc = grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, splits), false);
+  if (rc) return rc;
+  rc = grow(s, &s->hdrs, &s->hdrs_cap, sas::sample_hdr_bytes(rows, splits), false);
+  if (rc) return rc;
+  if (rows > s->counters_cap) {
+    size_t cap = (size_t)s->counters_cap * 4;
+    void *p = s->counters;
+    rc = grow(s, &p, &cap, (size_t)rows * 4, true);
+    s->counters = reinterpret_cast<uint32_t *>(p);
+    if (rc) return rc;
+    s->counters_cap = (int32_t)(cap / 4);
+  }
+  return SAS_OK;
+}
+
+int splits_for(int f4, int vocab) { return (vocab + f4 * 1024 - 1) / (f4 * 1024); }
+
+int set_device(sas_sampler *s) {
+  hipError_t e = hipSetDevice(s->device);
+  return e == hipSuccess ? SAS_OK : hip_fail(s, e, "hipSetDevice");
+}
+
+}  // namespace
+
+namespace sas {
+size_t sample_rec_bytes(int rows, int splits) { return (size_t)rows * splits * kCapBlock * sizeof(Rec); }
+size_t sample_hdr_bytes(int rows, int splits) { return (size_t)rows * splits * sizeof(BlockHdr); }
+}  // namespace sas
+
+extern "C" {
+
+const char *sas_version(void) { return "shared_amd_sampler 1 gfx950"; }
+
+int sas_create(int device, sas_sampler **out) {
+  if (!out) return fail(nullptr, SAS_ERR_INVALID, "sas_create: out is NULL");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0)
+    return fail(nullptr, SAS_ERR_HIP, "sas_create: no HIP device is available");
+  if (device < 0 || device >= count)
+    return fail(nullptr, SAS_ERR_INVALID, "sas_create: device index out of range");
+  if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+  sas_sampler *s = new sas_sampler();
+  s->device = device;
+  if ((e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking)) != hipSuccess) {
+    delete s;
+    return hip_fail(nullptr, e, "hipStreamCreate");
+  }
+  *out = s;
+  return SAS_OK;
+}
+
+void sas_destroy(sas_sampler *s) {
+  if (!s) return;
+  (void)hipSetDevice(s->device);
+  (void)hipDeviceSynchronize();
+  if (s->recs) (void)hipFree(s->recs);
+  if (s->hdrs) (void)hipFree(s->hdrs);
+  if (s->counters) (void)hipFree(s->counters);
+  if (s->vscratch) (void)hipFree(s->vscratch);
+  if (s->stream) (void)hipStreamDestroy(s->stream);
+  delete s;
+}
+
+const char *sas_last_error(const sas_sampler *s) { return s ? s->err.c_str() : g_err.c_str(); }
+
+int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_reserve: handle is NULL");
+  if (rows < 0 || vocab < 1 || vocab > SAS_MAX_VOCAB)
+    return fail(s, SAS_ERR_INVALID, "sas_reserve: rows must be >= 0 and vocab in [1, SAS_MAX_VOCAB]");
+  if (int rc = set_device(s)) return rc;
+  // the smallest chunk any batch of <= rows rows may pick
+  int splits = splits_for(2, vocab);
+  if (splits > sas::kMaxSplits) splits = splits_for(sas::choose_f4(1, vocab), vocab);
+  return ensure_sample_scratch(s, rows, splits);
+}
+
+int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_sample: handle is NULL");
+  if (!r) return fail(s, SAS_ERR_INVALID, "sas_sample: rows descriptor is NULL");
+  if (r->rows < 0) return fail(s, SAS_ERR_INVALID, "sas_sample: rows must be >= 0");
+  if (r->vocab < 1 || r->vocab > SAS_MAX_VOCAB)
+    return fail(s, SAS_ERR_INVALID, "sas_sample: vocab must be in [1, SAS_MAX_VOCAB]");
+  if (r->rows == 0) return SAS_OK;
+  if (!r->logits || !r->out_ids) return fail(s, SAS_ERR_INVALID, "sas_sample: logits and out_ids are required");
+  if (r->logits_stride < r->vocab) return fail(s, SAS_ERR_INVALID, "sas_sample: logits_stride < vocab");
+  if (r->mask && r->mask_stride < ((int64_t)r->vocab + 31) / 32)
+    return fail(s, SAS_ERR_INVALID, "sas_sample: mask_stride < ceil(vocab / 32)");
+  if (r->hist_ids && !r->hist_offsets)
+    return fail(s, SAS_ERR_INVALID, "sas_sample: hist_ids requires hist_offsets");
+  const bool all_greedy = !r->row_params && !(r->params.temperature > 0.0);
+  if (!r->uniforms && !all_greedy)
+    return fail(s, SAS_ERR_INVALID, "sas_sample: uniforms are required unless every row is greedy");
+  if (int rc = set_device(s)) return rc;
+  const int f4 = sas::choose_f4(r->rows, r->vocab);
+  const int splits = splits_for(f4, r->vocab);
+  if (int rc = ensure_sample_scratch(s, r->rows, splits)) return rc;
+
+  sas::SampleArgs a;
+  a.logits = r->logits;
+  a.logits_stride = r->logits_stride;
+  a.mask = r->mask;
+  a.mask_stride = r->mask_stride;
+  a.hist_ids = r->hist_ids;
+  a.hist_offsets = r->hist_ids ? r->hist_offsets : nullptr;
+  a.uniforms = r->uniforms;
+  a.row_params = r->row_params;
+  a.params = r->params;
+  a.out_ids = r->out_ids;
+  a.out_probs = r->out_probs;
+  a.out_cand_ids = r->out_cand_ids;
+  a.out_counts = r->out_counts;
+  a.out_flags = r->out_flags;
+  a.recs = reinterpret_cast<sas::Rec *>(s->recs);
+  a.hdrs = reinterpret_cast<sas::BlockHdr *>(s->hdrs);
+  a.counters = s->counters;
+  a.vocab = r->vocab;
+  a.rows = r->rows;
+  a.splits = splits;
+  const bool aligned = (reinterpret_cast<uintptr_t>(r->logits) & 15u) == 0 && (r->logits_stride & 3) == 0;
+  hipError_t e = sas::launch_sample(a, f4, aligned, pick_stream(s, stream));
+  if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
+  return SAS_OK;
+}
+
+int sas_clamp_params(const sas_params *in, sas_params *out) {
+  if (!in || !out) return fail(nullptr, SAS_ERR_INVALID, "sas_clamp_params: NULL argument");
+  sas_params p = *in;
+  p.temperature = std::isfinite(in->temperature) && in->temperature > 0.0 ? in->temperature : 0.0;
+  p.top_p = std::isfinite(in->top_p) ? std::fmin(1.0, std::fmax(0.0, in->top_p)) : 1.0;
+  p.presence_penalty =
+      std::isfinite(in->presence_penalty) ? std::fmin(10.0, std::fmax(0.0, in->presence_penalty)) : 0.0;
+  p.repetition_penalty =
+      std::isfinite(in->repetition_penalty) && in->repetition_penalty > 0.0 ? in->repetition_penalty : 1.0;
+  p.frequency_penalty = std::isfinite(in->frequency_penalty) ? in->frequency_penalty : 0.0;
+  p.softcap = std::isfinite(in->softcap) && in->softcap > 0.0f ? in->softcap : 0.0f;
+  p.top_k = in->top_k < 1 ? 1 : (in->top_k > SAS_MAX_TOP_K ? SAS_MAX_TOP_K : in->top_k);
+  *out = p;
+  return SAS_OK;
+}
+
+int64_t sas_mask_from_ids(int32_t kind, const uint32_t *ids, size_t count, int32_t vocab, uint32_t *words,
+                          int64_t nwords) {
+  if (vocab < 1 || vocab > SAS_MAX_VOCAB || !words || nwords < ((int64_t)vocab + 31) / 32 ||
+      (kind != SAS_MASK_ALL && kind != SAS_MASK_ALLOW && kind != SAS_MASK_DENY) || (count && !ids)) {
+    fail(nullptr, SAS_ERR_INVALID, "sas_mask_from_ids: invalid argument");
+    return -SAS_ERR_INVALID;
+  }
+  const int64_t used = ((int64_t)vocab + 31) / 32;
+  const uint32_t fill = kind == SAS_MASK_ALLOW ? 0u : ~0u;
+  for (int64_t w = 0; w < nwords; ++w) words[w] = w < used ? fill : 0u;
+  if (kind != SAS_MASK_ALLOW && (vocab & 31)) words[used - 1] = (1u << (vocab & 31)) - 1u;
+  for (size_t i = 0; i < count; ++i) {
+    const uint32_t id = ids[i];
+    if (id >= (uint32_t)vocab) continue;
+    if (kind == SAS_MASK_ALLOW) words[id >> 5] |= 1u << (id & 31);
+    else if (kind == SAS_MASK_DENY) words[id >> 5] &= ~(1u << (id & 31));
+  }
+  int64_t allowed = 0;
+  for (int64_t w = 0; w < used; ++w) allowed += __builtin_popcount(words[w]);
+  return allowed;
+}
+
+double sas_pcg_uniform(uint32_t seed, uint32_t it, uint32_t row) {
+  uint32_t h = (seed ^ (it * 0x9E3779B9u) ^ (row * 0x85EBCA6Bu)) * 747796405u + 2891336453u;
+  h = ((h >> ((h >> 28u) + 4u)) ^ h) * 277803737u;
+  h = (h >> 22u) ^ h;
+  return (double)(h & 0xFFFFFFu) / 16777216.0;
+}
+
+int sas_alloc(sas_sampler *s, size_t bytes, void **out) {
+  if (!s || !out) return fail(s, SAS_ERR_INVALID, "sas_alloc: NULL argument");
+  if (int rc = set_device(s)) return rc;
+  hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    *out = nullptr;
+    return fail(s, SAS_ERR_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+  }
+  return SAS_OK;
+}
+
+int sas_free(sas_sampler *s, void *p) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_free: handle is NULL");
+  if (!p) return SAS_OK;
+  if (int rc = set_device(s)) return rc;
+  hipError_t e = hipFree(p);
+  return e == hipSuccess ? SAS_OK : hip_fail(s, e, "hipFree");
+}
+
+int sas_memcpy(sas_sampler *s, void *dst, const void *src, size_t bytes, int kind, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_memcpy: handle is NULL");
+  if (bytes == 0) return SAS_OK;
+  if (!dst || !src) return fail(s, SAS_ERR_INVALID, "sas_memcpy: NULL pointer");
+  if (int rc = set_device(s)) return rc;
+  hipStream_t st = pick_stream(s, stream);
+  hipError_t e;
+  switch (kind) {
+    case 0:
+      e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
+      if (e == hipSuccess) e = hipStreamSynchronize(st);
+      break;
+    case 1:
+      e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st);
+      if (e == hipSuccess) e = hipStreamSynchronize(st);
+      break;
+    case 2:
+      e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st);
+      break;
+    default:
+      return fail(s, SAS_ERR_INVALID, "sas_memcpy: kind must be 0, 1 or 2");
+  }
+  return e == hipSuccess ? SAS_OK : hip_fail(s, e, "hipMemcpyAsync");
+}
+
+int sas_synchronize(sas_sampler *s, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_synchronize: handle is NULL");
+  if (int rc = set_device(s)) return rc;
+  hipError_t e = hipStreamSynchronize(pick_stream(s, stream));
+  return e == hipSuccess ? SAS_OK : hip_fail(s, e, "hipStreamSynchronize");
+}
+
+int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+// sas_device.h - device-side helpers shared by the sampling kernels (gfx950).
+//
+// Every translation unit that includes this is compiled with
+// -ffp-contract=off: the double-precision tail must round each operation
+// separately, exactly as a JS engine does in sample()
+// (lib/webgpu-llm/tokenizer.js:163-177).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "shared_amd_sampler.h"
+
+namespace sas {
+
+constexpr int kThreads = 256;           // 4 wave64s per block
+constexpr int kWaves = kThreads / 64;
+constexpr int kCapBlock = 256;          // records one block may emit
+constexpr int kCapMerge = 512;          // candidates ranked in LDS by the merge
+constexpr int kMaxSplits = 512;         // SAS_MAX_VOCAB / 8192
+constexpr uint32_t kPenFlag = 0x80000000u;
+
+// Candidate record written by a split block for its row's merge.
+struct Rec {
+  double val;    // exact ranking value (penalized ids: the double result)
+  uint32_t id;
+  float key;     // val rounded toward -inf to fp32 (monotone selection key)
+};
+static_assert(sizeof(Rec) == 16, "Rec layout");
+
+struct BlockHdr {
+  uint32_t n;    // records emitted
+  float thr;     // at least top_k of the block's values are >= thr
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float qnan() { return __builtin_nanf(""); }
+
+// fp64 -> fp32 rounding toward -inf.  Monotone, and val >= t implies
+// rd(val) >= t for every fp32 t, so fp32 keys can filter double values.
+__device__ __forceinline__ float rd_f32(double d) {
+  float f = (float)d;
+  if ((double)f > d) {
+    uint32_t b = __float_as_uint(f);
+    if (f > 0.0f) b -= 1u;
+    else if (f == 0.0f) b = 0x80000001u;
+    else b += 1u;
+    f = __uint_as_float(b);
+  }
+  return f;
+}
+
+// History penalty of a token seen `count` > 0 times: CTRL repetition
+// (sign-wise), then OpenAI frequency and presence.  Presence alone is the
+// reference's rule (tokenizer.js:157).
+__device__ __forceinline__ double penalize(double v, uint32_t count, const sas_params &p) {
+  double r = p.repetition_penalty;
+  v = v > 0.0 ? v / r : v * r;
+  v = v - p.frequency_penalty * (double)count;
+  v = v - p.presence_penalty;
+  return v;
+}
+
+// Gemma's final-logit softcap in fp32 (kernels.js:1393-1395).
+__device__ __forceinline__ float softcap_f32(float x, float cap) {
+  float q = x / cap;
+  return cap * tanhf(q);
+}
+
+// exp(x) by fdlibm's e_exp.c algorithm (Sun Microsystems, 1993): reduce
+// x = k*ln2 + r with ln2 split in a 32-bit-exact high part and a low part,
+// approximate exp(r) with the degree-5 Remez rational form, scale by 2^k.
+// V8's Math.exp is this algorithm, so probabilities come out bit-identical
+// to the reference's JS sample().
+__device__ __forceinline__ double fd_exp(double x) {
+  const double inv_ln2 = 1.44269504088896338700e+00;
+  const double ln2_hi = 6.93147180369123816490e-01, ln2_lo = 1.90821492927058770002e-10;
+  const double P1 = 1.66666666666666019037e-01, P2 = -2.77777777770155933842e-03,
+               P3 = 6.61375632143793436117e-05, P4 = -1.65339022054652515390e-06,
+               P5 = 4.13813679705723846039e-08;
+  const double over = 7.09782712893383973096e+02, under = -7.45133219101941108420e+02;
+  const double two_m1000 = 9.33263618503218878990e-302;
+  uint64_t bits = (uint64_t)__double_as_longlong(x);
+  uint32_t hx = (uint32_t)(bits >> 32);
+  const int neg = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  double hi = 0.0, lo = 0.0;
+  int k = 0;
+  if (hx >= 0x40862E42u) {
+    if (hx >= 0x7ff00000u) {
+      if (((hx & 0xfffffu) | (uint32_t)bits) != 0u) return x + x;
+      return neg ? 0.0 : x;
+    }
+    if (x > over) return __longlong_as_double(0x7ff0000000000000ll);
+    if (x < under) return 0.0;
+  }
+  if (hx > 0x3fd62e42u) {
+    if (hx < 0x3FF0A2B2u) {
+      if (x == 1.0) return 2.718281828459045;
+      hi = neg ? x + ln2_hi : x - ln2_hi;
+      lo = neg ? -ln2_lo : ln2_lo;
+      k = neg ? -1 : 1;
+    } else {
+      k = (int)(inv_ln2 * x + (neg ? -0.5 : 0.5));
+      double t = (double)k;
+      hi = x - t * ln2_hi;
+      lo = t * ln2_lo;
+    }
+    x = hi - lo;
+  } else if (hx < 0x3e300000u) {
+    return 1.0 + x;
+  }
+  double t = x * x;
+  double c = x - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+  if (k == 0) return 1.0 - ((x * c) / (c - 2.0) - x);
+  double y = 1.0 - ((lo - (x * c) / (2.0 - c)) - hi);
+  if (k >= -1021) {
+    if (k == 1024) return y * 2.0 * 8.988465674311579539e307;
+    return y * __longlong_as_double((long long)(uint64_t)(0x3ff00000u + ((uint32_t)k << 20)) << 32);
+  }
+  return y * __longlong_as_double((long long)(uint64_t)(0x3ff00000u + ((uint32_t)(k + 1000) << 20)) << 32) *
+         two_m1000;
+}
+
+// (v desc, id asc): the order of the reference's stable descending sort
+// over an id-ascending candidate list (tokenizer.js:160).
+__device__ __forceinline__ bool ranks_before(double va, uint32_t ia, double vb, uint32_t ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// j-th largest (1-based) of the 64 lane values of a wave.  Bitonic network
+// over lanes, descending; inputs must not be NaN.
+__device__ __forceinline__ float wave_jth_largest(float x, int j) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      float y = __shfl_xor(x, stride, 64);
+      bool lower = (lane & stride) == 0;
+      bool up = (lane & size) == 0;
+      float mx = fmaxf(x, y), mn = fminf(x, y);
+      x = (lower == up) ? mx : mn;
+    }
+  }
+  return __shfl(x, j - 1, 64);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) x = fmaxf(x, __shfl_xor(x, s, 64));
+  return x;
+}
+
+// Best (value, id) over the wave under ranks_before; lanes without a
+// candidate pass have = false.
+__device__ __forceinline__ void wave_best(bool &have, double &v, uint32_t &id) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    int oh = __shfl_xor((int)have, s, 64);
+    double ov = __shfl_xor(v, s, 64);
+    uint32_t oi = (uint32_t)__shfl_xor((int)id, s, 64);
+    if (oh && (!have || ranks_before(ov, oi & ~kPenFlag, v, id & ~kPenFlag))) {
+      have = true;
+      v = ov;
+      id = oi;
+    }
+  }
+}
+
+// Inclusive prefix sum over the wave.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+    uint32_t y = (uint32_t)__shfl_up((int)x, s, 64);
+    if (lane >= s) x += y;
+  }
+  return x;
+}
+
+}  // namespace sas

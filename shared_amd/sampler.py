@@ -1,0 +1,194 @@
+"""Python handle over the C ABI, for tests and benchmarks.
+
+Device buffers are torch CUDA tensors (plumbing only): every computation
+runs in the HIP kernels of libshared_amd_sampler.so, on torch's current
+stream unless another is given.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _capi
+from ._capi import SasParams, SasRows, SasVerifyRows, check, load
+
+
+@dataclass
+class Params:
+    """One row's sampling parameters (sas_params)."""
+
+    temperature: float = 0.0
+    top_k: int = 1
+    top_p: float = 1.0
+    repetition_penalty: float = 1.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+    softcap: float = 0.0
+
+    def to_c(self) -> SasParams:
+        return SasParams(float(self.temperature), float(self.top_p), float(self.repetition_penalty),
+                         float(self.presence_penalty), float(self.frequency_penalty), float(self.softcap),
+                         int(self.top_k))
+
+    def as_dict(self) -> dict:
+        return {"temperature": self.temperature, "top_k": self.top_k, "top_p": self.top_p,
+                "repetition_penalty": self.repetition_penalty, "presence_penalty": self.presence_penalty,
+                "frequency_penalty": self.frequency_penalty, "softcap": self.softcap}
+
+
+PARAMS_DTYPE = np.dtype([("temperature", "<f8"), ("top_p", "<f8"), ("repetition_penalty", "<f8"),
+                         ("presence_penalty", "<f8"), ("frequency_penalty", "<f8"), ("softcap", "<f4"),
+                         ("top_k", "<i4")])
+assert PARAMS_DTYPE.itemsize == ctypes.sizeof(SasParams)
+
+
+def pack_params(rows: Sequence[Params]) -> np.ndarray:
+    """Array of sas_params (for row_params)."""
+    out = np.zeros(len(rows), dtype=PARAMS_DTYPE)
+    for i, p in enumerate(rows):
+        out[i] = (p.temperature, p.top_p, p.repetition_penalty, p.presence_penalty, p.frequency_penalty,
+                  p.softcap, p.top_k)
+    return out
+
+
+def clamp_params(p: Params) -> Params:
+    """The reference packer's clamps (sas_clamp_params)."""
+    out = SasParams()
+    check(load().sas_clamp_params(ctypes.byref(p.to_c()), ctypes.byref(out)))
+    return Params(out.temperature, out.top_k, out.top_p, out.repetition_penalty, out.presence_penalty,
+                  out.frequency_penalty, out.softcap)
+
+
+def mask_from_ids(kind: int, ids, vocab: int) -> np.ndarray:
+    """Packed uint32 bitmask of a TokenMask (sas_mask_from_ids)."""
+    ids = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32))
+    words = np.zeros((vocab + 31) // 32, dtype=np.uint32)
+    n = load().sas_mask_from_ids(int(kind), ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), ids.size,
+                                 int(vocab), words.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), words.size)
+    if n < 0:
+        check(-n)
+    return words
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("device tensors are required")
+    if not t.is_contiguous() and t.dim() == 1:
+        raise ValueError("1-D inputs must be contiguous")
+    return t.data_ptr()
+
+
+class Sampler:
+    """A sas_sampler handle bound to one device."""
+
+    def __init__(self, device: int = 0):
+        self._lib = load()
+        h = ctypes.c_void_p()
+        rc = self._lib.sas_create(int(device), ctypes.byref(h))
+        check(rc, None)
+        self._h = h
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.sas_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def reserve(self, rows: int, vocab: int) -> None:
+        check(self._lib.sas_reserve(self._h, int(rows), int(vocab)), self._h)
+
+    def _stream(self, stream):
+        import torch
+        if stream is None:
+            stream = torch.cuda.current_stream()
+        return ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+    def sample_into(self, logits, out_ids, *, vocab: Optional[int] = None, mask=None, hist_ids=None,
+                    hist_offsets=None, uniforms=None, params: Optional[Params] = None, row_params=None,
+                    out_probs=None, out_cand_ids=None, out_counts=None, out_flags=None, stream=None) -> None:
+        """Launch sas_sample on caller-provided device buffers (no allocation)."""
+        rows = logits.shape[0]
+        vocab = int(vocab if vocab is not None else logits.shape[1])
+        if logits.dtype.itemsize != 4 or logits.stride(1) != 1:
+            raise ValueError("logits must be fp32 with unit element stride")
+        d = SasRows()
+        d.logits = logits.data_ptr()
+        d.logits_stride = logits.stride(0)
+        d.vocab = vocab
+        d.rows = rows
+        if mask is not None:
+            d.mask = _ptr(mask)
+            d.mask_stride = mask.stride(0)
+        d.hist_ids = _ptr(hist_ids)
+        d.hist_offsets = _ptr(hist_offsets)
+        d.uniforms = _ptr(uniforms)
+        d.params = (params or Params()).to_c()
+        d.row_params = _ptr(row_params)
+        d.out_ids = _ptr(out_ids)
+        d.out_probs = _ptr(out_probs)
+        d.out_cand_ids = _ptr(out_cand_ids)
+        d.out_counts = _ptr(out_counts)
+        d.out_flags = _ptr(out_flags)
+        check(self._lib.sas_sample(self._h, ctypes.byref(d), self._stream(stream)), self._h)
+
+    def sample(self, logits, *, full: bool = False, **kw):
+        """Allocate outputs and sample; returns ids (and the extras if full)."""
+        import torch
+        rows = logits.shape[0]
+        dev = logits.device
+        out = {"ids": torch.empty(rows, dtype=torch.int32, device=dev)}
+        if full:
+            out["probs"] = torch.empty((rows, _capi.MAX_TOP_K), dtype=torch.float64, device=dev)
+            out["cand_ids"] = torch.empty((rows, _capi.MAX_TOP_K), dtype=torch.int32, device=dev)
+            out["counts"] = torch.empty((rows, 2), dtype=torch.int32, device=dev)
+            out["flags"] = torch.empty(rows, dtype=torch.int32, device=dev)
+        self.sample_into(logits, out["ids"], out_probs=out.get("probs"), out_cand_ids=out.get("cand_ids"),
+                         out_counts=out.get("counts"), out_flags=out.get("flags"), **kw)
+        return out if full else out["ids"]
+
+    def verify_into(self, target, draft, draft_ids, uniforms, out_tokens, out_accepted, *, temperature=1.0,
+                    mask=None, vocab: Optional[int] = None, stream=None) -> None:
+        seqs, L = draft_ids.shape
+        d = SasVerifyRows()
+        d.target_logits = target.data_ptr()
+        d.draft_logits = draft.data_ptr()
+        d.logits_stride = target.stride(0)
+        if draft.stride(0) != target.stride(0):
+            raise ValueError("target and draft rows must share a stride")
+        d.vocab = int(vocab if vocab is not None else target.shape[1])
+        d.seqs = seqs
+        d.draft_len = L
+        d.draft_ids = _ptr(draft_ids)
+        if mask is not None:
+            d.mask = _ptr(mask)
+            d.mask_stride = mask.stride(0)
+        d.uniforms = _ptr(uniforms)
+        d.temperature = float(temperature)
+        d.out_tokens = _ptr(out_tokens)
+        d.out_accepted = _ptr(out_accepted)
+        check(self._lib.sas_verify(self._h, ctypes.byref(d), self._stream(stream)), self._h)
+
+    def verify(self, target, draft, draft_ids, uniforms, **kw):
+        import torch
+        seqs, L = draft_ids.shape
+        toks = torch.empty((seqs, L + 1), dtype=torch.int32, device=target.device)
+        acc = torch.empty(seqs, dtype=torch.int32, device=target.device)
+        self.verify_into(target, draft, draft_ids, uniforms, toks, acc, **kw)
+        return toks, acc

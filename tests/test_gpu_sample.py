@@ -1,0 +1,161 @@
+"""GPU parity of sas_sample against the C oracle (bit-exact ids, ranked
+candidates and double probabilities), through the C ABI."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import assert_parity, run_gpu, to_dev
+from shared_amd import Params
+from shared_amd import workloads as W
+from shared_amd._capi import FLAG_EMPTY_ROW, FLAG_SLOW_SELECT, NO_TOKEN
+
+pytestmark = pytest.mark.gpu
+
+
+def check(s, b, row_params=None, label=""):
+    g = run_gpu(s, b, row_params=row_params)
+    o = O.sample_rows(b, row_params=row_params)
+    assert_parity(g, o, label or b.name)
+    return g, o
+
+
+# ---------------------------------------------------------------- configs --
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C3P", "C4"])
+def test_config_full_size(sampler, name):
+    b = W.CONFIGS[name]()
+    print(f"[gpu] config {name} rows={b.rows} vocab={b.vocab}", flush=True)
+    check(sampler, b)
+
+
+# ------------------------------------------------------- random small cases --
+
+def _small_batch(seed, rows, vocab, params, mask_density=None, hist=0, sigma=3.0):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, vocab)) * sigma).astype(np.float32)
+    mask = None
+    if mask_density is not None:
+        mask = W.random_mask(rng, rows, vocab, mask_density, mask_density)
+    hi = ho = None
+    if hist:
+        hi, ho = W._csr([rng.integers(0, vocab, hist) for _ in range(rows)])
+    return W.Batch("small", x, params, mask=mask, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("vocab", [1000, 4099, 33333, 151936])
+def test_random_params(sampler, seed, vocab):
+    rng = np.random.default_rng(100 + seed)
+    p = Params(temperature=float(rng.choice([0.0, 0.3, 0.7, 1.0, 1.5])), top_k=int(rng.integers(1, 129)),
+               top_p=float(rng.choice([0.0, 0.5, 0.9, 0.95, 1.0])),
+               repetition_penalty=float(rng.choice([1.0, 1.1, 1.3])),
+               presence_penalty=float(rng.choice([0.0, 0.5, 1.5])),
+               frequency_penalty=float(rng.choice([0.0, 0.3])))
+    b = _small_batch(seed, rows=int(rng.integers(1, 40)), vocab=vocab, params=p,
+                     mask_density=rng.choice([None, 0.01, 0.3]), hist=int(rng.choice([0, 7, 300])))
+    print(f"[gpu] random seed={seed} vocab={vocab} rows={b.rows} {p}", flush=True)
+    check(sampler, b)
+
+
+def test_row_params_mixed(sampler):
+    rng = np.random.default_rng(7)
+    rows = 24
+    plist = [Params(temperature=float(t), top_k=int(k), top_p=float(pp), presence_penalty=float(pr))
+             for t, k, pp, pr in zip(rng.choice([0.0, 0.6, 1.0], rows), rng.integers(1, 129, rows),
+                                     rng.choice([0.3, 0.95, 1.0], rows), rng.choice([0.0, 1.5], rows))]
+    b = _small_batch(11, rows, 20000, Params(temperature=1.0), mask_density=0.2, hist=64)
+    check(sampler, b, row_params=plist, label="row_params")
+
+
+# ------------------------------------------------------------------ edges --
+
+def test_empty_and_single_allowed_rows(sampler):
+    vocab, rows = 5000, 4
+    b = _small_batch(1, rows, vocab, Params(temperature=1.0, top_k=50, top_p=0.9))
+    bits = np.zeros((rows, vocab), bool)
+    bits[1, 4321] = True                # exactly one allowed id
+    bits[2, [7, 4999]] = True           # two, far apart
+    bits[3, :] = True
+    b.mask = W.pack_bits(bits)          # row 0: nothing allowed
+    g, _ = check(sampler, b, label="empty")
+    assert g["ids"][0] == NO_TOKEN and g["flags"][0] & FLAG_EMPTY_ROW
+    assert g["ids"][1] == 4321
+
+
+def test_ties_take_lowest_id(sampler):
+    # every logit equal: greedy takes id 0, top-k takes the k lowest ids
+    vocab, rows = 70000, 3
+    x = np.full((rows, vocab), 1.25, np.float32)
+    b = W.Batch("ties", x, Params(temperature=1.0, top_k=64, top_p=1.0), uniforms=np.array([0.0, 0.5, 0.999]))
+    g, _ = check(sampler, b, label="ties")
+    assert np.array_equal(g["cand_ids"][0, :64], np.arange(64))
+    assert g["flags"][0] & FLAG_SLOW_SELECT
+    b.params = Params(temperature=0.0)
+    g, _ = check(sampler, b, label="ties-greedy")
+    assert (g["ids"] == 0).all()
+
+
+def test_many_ties_at_threshold(sampler):
+    # a few distinct levels, each shared by thousands of ids
+    rng = np.random.default_rng(3)
+    vocab, rows = 100000, 6
+    x = rng.integers(0, 5, (rows, vocab)).astype(np.float32)
+    b = W.Batch("levels", x, Params(temperature=0.8, top_k=100, top_p=0.99), uniforms=rng.random(rows))
+    check(sampler, b, label="levels")
+
+
+def test_nan_inf_logits(sampler):
+    rng = np.random.default_rng(4)
+    vocab, rows = 9000, 5
+    x = rng.standard_normal((rows, vocab)).astype(np.float32)
+    x[0, ::3] = np.nan
+    x[1, 17] = np.inf
+    x[2, :] = -np.inf
+    x[2, 100] = 0.5
+    x[3, :] = np.nan
+    x[4, 5] = -np.inf
+    b = W.Batch("naninf", x, Params(temperature=1.0, top_k=20, top_p=0.9), uniforms=rng.random(rows))
+    check(sampler, b, label="naninf")
+
+
+def test_stride_and_unaligned(sampler):
+    import torch
+    rng = np.random.default_rng(5)
+    vocab, rows, stride = 30001, 7, 30017
+    full = rng.standard_normal((rows, stride + 1)).astype(np.float32)
+    b = W.Batch("stride", np.ascontiguousarray(full[:, 1:1 + vocab]), Params(temperature=0.9, top_k=30, top_p=0.8),
+                uniforms=rng.random(rows))
+    dev = torch.from_numpy(full).cuda()
+    view = dev[:, 1:1 + vocab]          # misaligned rows, stride != vocab
+    g = run_gpu(sampler, b, logits_dev=view)
+    assert_parity(g, O.sample_rows(b), "unaligned")
+
+
+def test_history_edge_ids(sampler):
+    rng = np.random.default_rng(6)
+    vocab, rows = 12345, 3
+    x = rng.standard_normal((rows, vocab)).astype(np.float32) * 2
+    top = np.argsort(-x, axis=1)[:, :5]
+    hist = [np.concatenate([top[0], top[0], [vocab + 10, 0xFFFFFFF0]]),  # duplicates + out-of-range ids
+            np.zeros(0, np.int64), np.repeat(top[2, :1], 3000)]          # empty; one id many times
+    hi, ho = W._csr(hist)
+    b = W.Batch("hist", x, Params(temperature=1.0, top_k=10, top_p=1.0, repetition_penalty=1.3,
+                                  presence_penalty=0.7, frequency_penalty=0.01),
+                hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+    check(sampler, b, label="hist")
+
+
+def test_repeated_launches_reset_state(sampler):
+    b = W.c3p(rows=32, vocab=50000)
+    first = run_gpu(sampler, b)
+    for _ in range(3):
+        again = run_gpu(sampler, b)
+        assert np.array_equal(first["ids"], again["ids"])
+        assert np.array_equal(first["probs"].view(np.uint64), again["probs"].view(np.uint64))
+
+
+def test_pcg_uniform_matches_reference_hash():
+    from shared_amd import _capi
+    lib = _capi.load()
+    for seed, it, row in [(1, 0, 0), (0xDEADBEEF, 7, 2), (12345, 99, 1)]:
+        assert lib.sas_pcg_uniform(seed, it, row) == O.lib().orc_pcg_uniform(seed, it, row)
