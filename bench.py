@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Headline benchmark: one MI355X sampling step over a batch of logit rows.
+
+A step is one sas_sample launch over one batch of synthetic inputs that are
+already resident in HBM: 262,144-vocab fp32 logits, the packed grammar
+bitmask, repetition / presence / frequency penalties from a 512-id history,
+then temperature 1.0 / top-k 50 / top-p 0.9 and the seeded draw, batch 128
+(workload C3P).  Inputs rotate over several independent sets totalling more
+than 512 MB so the 256 MB Infinity Cache cannot serve them.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C3P]
+
+Prints ONE JSON line (rank 0): rows/s, the roofline of the sampling kernel
+(algorithmic bytes / average launch time, HIP events on the launch stream)
+and the CPU baseline: the Node restatement of the reference's JS sampling
+path timed on this host's cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import tempfile
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "rows/s + % HBM peak: 262k-vocab penalties+mask+top-k/top-p, B=128"
+HBM_PEAK_GBPS = 8000.0
+KERNEL = "sample_rows_kernel"
+WORKLOAD_DOC = {
+    "C2": "T0.7 top-k40 top-p0.95, vocab 151936, batch 64, Zipf-biased N(0,3) logits",
+    "C3": "bitmask 0.5-20% + top-k50 top-p0.9 T1.0, vocab 262144, batch 128, N(0,4) logits",
+    "C3P": "C3 + repetition 1.1 / presence 0.5 / frequency 0.3 over 512 history ids, vocab 262144, batch 128",
+    "C4": "repetition 1.15 / presence 0.5 / frequency 0.3 over 4096 Zipf history ids, greedy, vocab 262144, "
+          "batch 256",
+}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="C3P", choices=sorted(WORKLOAD_DOC))
+    ap.add_argument("--min-set-mb", type=float, default=512.0,
+                    help="rotate over input sets totalling at least this many MB")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU work of the baseline sample (0 disables it)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), if a summary for this workload is
+    committed under profiles/."""
+    path = os.path.join(ROOT, "profiles", f"{KERNEL}_{workload}_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)", line)
+                if m:
+                    return float(m.group(1))
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(batch, target_s: float) -> dict:
+    """Time the Node restatement of the reference JS path (oracle/sample_js.js)
+    on a bounded sample of the same workload: the first set's rows, repeated
+    until about target_s seconds of single-thread work.  Falls back to the C
+    restatement when Node is absent."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import oracle as O
+
+    if O.node_binary() is not None:
+        with tempfile.TemporaryDirectory(prefix="sas_cpu_") as tmp:
+            _, probe = O.run_node(batch, threads=1, repeat=1, workdir=tmp)
+            repeat = max(1, min(50, int(round(target_s / max(probe["median_s"], 1e-3)))))
+            out, t = O.run_node(batch, threads=1, repeat=repeat, workdir=tmp)
+        return {"value": batch.rows / t["median_s"], "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"{batch.rows} rows of the first input set, {repeat} timed passes (median), "
+                          f"Node {t['node']} single thread on {t['cpu_model']} ({t['host_cpus']} host cpus)",
+                "ids": out["ids"]}
+    import time
+    t0 = time.perf_counter()
+    o = O.sample_rows(batch, threads=1)
+    dt = time.perf_counter() - t0
+    return {"value": batch.rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"{batch.rows} rows of the first input set, C restatement single thread (Node absent)",
+            "ids": np.asarray(o["ids"])}
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "rows shard across GPUs with no exchange, so run one process per GPU.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    from shared_amd import workloads as W
+
+    gen = W.CONFIGS[args.workload]
+    first = gen()
+    set_bytes = first.algorithmic_bytes()
+    nsets = max(2, int(np.ceil(args.min_set_mb * 1e6 / set_bytes)))
+    batches = [first] + [gen(seed=1000 + i) for i in range(1, nsets)]
+
+    # CPU baseline before the GPU is touched (its Node child never sees HIP).
+    base = None
+    if not args.no_cpu_baseline and args.cpu_seconds > 0:
+        base = cpu_baseline(first, args.cpu_seconds)
+
+    import torch
+
+    from shared_amd import Sampler
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device is visible", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+
+    def dev(a, view=None):
+        if a is None:
+            return None
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        return (t.view(view) if view is not None else t).cuda()
+
+    sets = []
+    for b in batches:
+        sets.append(dict(logits=dev(b.logits), vocab=b.vocab, mask=dev(b.mask, torch.int32),
+                         hist_ids=dev(b.hist_ids, torch.int32), hist_offsets=dev(b.hist_offsets),
+                         uniforms=dev(b.uniforms), params=b.params))
+    rows, vocab = first.rows, first.vocab
+    out_ids = [torch.empty(rows, dtype=torch.int32, device="cuda") for _ in sets]
+    stream = torch.cuda.current_stream()
+
+    with Sampler(0) as s:
+        s.reserve(rows, vocab)
+        for i in range(args.warmup):
+            j = i % nsets
+            s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(args.steps):
+            j = i % nsets
+            s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms_total = start.elapsed_time(end)
+        gpu_ids0 = out_ids[0].cpu().numpy().view(np.uint32)
+
+    ms_step = ms_total / args.steps
+    value = rows * args.steps / (ms_total / 1e3)
+    achieved = set_bytes / (ms_step * 1e-3) / 1e9
+    traffic = traffic_from_profiles(args.workload)
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {WORKLOAD_DOC[args.workload]}", "rows": rows, "vocab": vocab,
+                   "top_k": first.params.top_k, "top_p": first.params.top_p,
+                   "temperature": first.params.temperature, "input_sets": nsets,
+                   "rotating_set_mb": round(nsets * set_bytes / 1e6, 1)},
+        "gbps": achieved,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "kernel": KERNEL, "algorithmic_bytes_per_launch": set_bytes},
+        "cpu_baseline": None,
+    }
+    if base is not None:
+        ids = base.pop("ids")
+        base["ids_match_gpu"] = f"{int((ids == gpu_ids0).sum())}/{rows}"
+        line["cpu_baseline"] = base
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -166,8 +166,9 @@ const char *sas_last_error(const sas_sampler *s);
 /* Pre-size scratch so later calls of at most this shape allocate nothing. */
 int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab);
 
-/* Sample one token per row.  stream = hipStream_t or NULL (the handle's own
- * stream).  A handle must not run two calls concurrently. */
+/* Sample one token per row, stream-ordered on `stream` (a hipStream_t; NULL
+ * is HIP's null stream, as everywhere in HIP).  A handle must not run two
+ * calls concurrently. */
 int sas_sample(sas_sampler *s, const sas_rows *rows, void *stream);
 
 /* Speculative accept/resample, stream-ordered like sas_sample. */
@@ -200,6 +201,9 @@ int sas_free(sas_sampler *s, void *p);
 int sas_memcpy(sas_sampler *s, void *dst, const void *src, size_t bytes,
                int kind, void *stream);
 int sas_synchronize(sas_sampler *s, void *stream);
+/* The handle's own non-blocking hipStream_t, for hosts that have no HIP
+ * binding of their own (the N-API addon passes it to every call). */
+void *sas_stream(sas_sampler *s);
 
 #ifdef __cplusplus
 }

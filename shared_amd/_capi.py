@@ -103,6 +103,7 @@ SIGNATURES = {
     "sas_free": (c_int, [c_void_p, c_void_p]),
     "sas_memcpy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_void_p]),
     "sas_synchronize": (c_int, [c_void_p, c_void_p]),
+    "sas_stream": (c_void_p, [c_void_p]),
 }
 
 _lib = None

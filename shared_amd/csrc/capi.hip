@@ -17,10 +17,8 @@ struct sas_sampler {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
-  void *recs = nullptr;
+  void *recs = nullptr;        // candidate records
   size_t recs_cap = 0;
-  void *hdrs = nullptr;
-  size_t hdrs_cap = 0;
   uint32_t *counters = nullptr;
   int32_t counters_cap = 0;
   void *vscratch = nullptr;   // sas_verify partials
@@ -41,9 +39,7 @@ int hip_fail(sas_sampler *s, hipError_t e, const char *what) {
   return fail(s, SAS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-hipStream_t pick_stream(sas_sampler *s, void *stream) {
-  return stream ? reinterpret_cast<hipStream_t>(stream) : s->stream;
-}
+hipStream_t pick_stream(sas_sampler *, void *stream) { return reinterpret_cast<hipStream_t>(stream); }
 
 // Grow a scratch buffer; waits for queued work before freeing the old one.
 int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
@@ -68,8 +64,6 @@ int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
 int ensure_sample_scratch(sas_sampler *s, int rows, int splits) {
   int rc = grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, splits), false);
   if (rc) return rc;
-  rc = grow(s, &s->hdrs, &s->hdrs_cap, sas::sample_hdr_bytes(rows, splits), false);
-  if (rc) return rc;
   if (rows > s->counters_cap) {
     size_t cap = (size_t)s->counters_cap * 4;
     void *p = s->counters;
@@ -89,11 +83,6 @@ int set_device(sas_sampler *s) {
 }
 
 }  // namespace
-
-namespace sas {
-size_t sample_rec_bytes(int rows, int splits) { return (size_t)rows * splits * kCapBlock * sizeof(Rec); }
-size_t sample_hdr_bytes(int rows, int splits) { return (size_t)rows * splits * sizeof(BlockHdr); }
-}  // namespace sas
 
 extern "C" {
 
@@ -124,7 +113,6 @@ void sas_destroy(sas_sampler *s) {
   (void)hipSetDevice(s->device);
   (void)hipDeviceSynchronize();
   if (s->recs) (void)hipFree(s->recs);
-  if (s->hdrs) (void)hipFree(s->hdrs);
   if (s->counters) (void)hipFree(s->counters);
   if (s->vscratch) (void)hipFree(s->vscratch);
   if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -181,7 +169,7 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.out_counts = r->out_counts;
   a.out_flags = r->out_flags;
   a.recs = reinterpret_cast<sas::Rec *>(s->recs);
-  a.hdrs = reinterpret_cast<sas::BlockHdr *>(s->hdrs);
+  a.rec_cap = sas::sample_rec_cap(splits);
   a.counters = s->counters;
   a.vocab = r->vocab;
   a.rows = r->rows;
@@ -288,6 +276,6 @@ int sas_synchronize(sas_sampler *s, void *stream) {
   return e == hipSuccess ? SAS_OK : hip_fail(s, e, "hipStreamSynchronize");
 }
 
-int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
+void *sas_stream(sas_sampler *s) { return s ? reinterpret_cast<void *>(s->stream) : nullptr; }
 
 }  // extern "C"

@@ -16,22 +16,17 @@ namespace sas {
 constexpr int kThreads = 256;           // 4 wave64s per block
 constexpr int kWaves = kThreads / 64;
 constexpr int kCapBlock = 256;          // records one block may emit
-constexpr int kCapMerge = 512;          // candidates ranked in LDS by the merge
+constexpr int kCapMerge = 512;          // survivors ranked exactly in LDS by the merge
 constexpr int kMaxSplits = 512;         // SAS_MAX_VOCAB / 8192
 constexpr uint32_t kPenFlag = 0x80000000u;
 
 // Candidate record written by a split block for its row's merge.
 struct Rec {
-  double val;    // exact ranking value (penalized ids: the double result)
+  double val;  // exact ranking value (double result for penalized ids)
   uint32_t id;
-  float key;     // val rounded toward -inf to fp32 (monotone selection key)
+  float key;   // val rounded toward -inf to fp32 (monotone selection key)
 };
 static_assert(sizeof(Rec) == 16, "Rec layout");
-
-struct BlockHdr {
-  uint32_t n;    // records emitted
-  float thr;     // at least top_k of the block's values are >= thr
-};
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -134,22 +129,30 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-// j-th largest (1-based) of the 64 lane values of a wave.  Bitonic network
-// over lanes, descending; inputs must not be NaN.
-__device__ __forceinline__ float wave_jth_largest(float x, int j) {
-  const int lane = threadIdx.x & 63;
+// Order-preserving map of an fp32 key to uint32 (larger float, larger
+// uint); NaN maps to 0, which marks "no key".
+__device__ __forceinline__ uint32_t okey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if (f != f) return 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inverse of okey for nonzero images.
+__device__ __forceinline__ float fkey(uint32_t x) {
+  return __uint_as_float((x & 0x80000000u) ? (x & 0x7FFFFFFFu) : ~x);
+}
+
+// j-th largest (1-based) of the 64 lane keys of a wave (okey images, 0 =
+// none); 0 when fewer than j lanes hold a key.  Bit-by-bit search from the
+// top: each step is one compare and a ballot count, no cross-lane moves.
+__device__ __forceinline__ uint32_t wave_jth_largest_key(uint32_t u, int j) {
+  uint32_t res = 0u;
 #pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      float y = __shfl_xor(x, stride, 64);
-      bool lower = (lane & stride) == 0;
-      bool up = (lane & size) == 0;
-      float mx = fmaxf(x, y), mn = fminf(x, y);
-      x = (lower == up) ? mx : mn;
-    }
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = res | (1u << b);
+    if (__popcll(__ballot(u >= cand)) >= j) res = cand;
   }
-  return __shfl(x, j - 1, 64);
+  return res;
 }
 
 __device__ __forceinline__ float wave_max(float x) {

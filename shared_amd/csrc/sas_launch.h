@@ -9,9 +9,8 @@
 namespace sas {
 
 struct Rec;
-struct BlockHdr;
 
-// Kernel arguments of sample_rows_kernel (validated by sas_sample).
+// Kernel arguments of the split and merge kernels (validated by sas_sample).
 struct SampleArgs {
   const float *logits;
   int64_t logits_stride;
@@ -27,9 +26,12 @@ struct SampleArgs {
   uint32_t *out_cand_ids;
   int32_t *out_counts;
   uint32_t *out_flags;
-  Rec *recs;          // [rows][splits][kCapBlock]
-  BlockHdr *hdrs;     // [rows][splits]
+  // Candidate records, rec_cap slots per row.  Split blocks append at
+  // counters[row] (relaxed atomic reservation); the merge kernel, next in
+  // stream order, reads them and resets the counter to zero.
+  Rec *recs;          // [rows][rec_cap]
   uint32_t *counters; // [rows], zero between launches
+  int64_t rec_cap;
   int32_t vocab;
   int32_t rows;
   int32_t splits;
@@ -37,10 +39,12 @@ struct SampleArgs {
 
 // float4 loads per thread (chunk = f4 * 1024 ids) for a batch shape.
 int choose_f4(int rows, int vocab);
+// Launches the split kernel then the merge kernel on `stream`.
 hipError_t launch_sample(const SampleArgs &a, int f4, bool aligned, hipStream_t stream);
 
-// Scratch bytes sas_sample needs for a shape.
+// Record slots per row for a split count.
+int64_t sample_rec_cap(int splits);
+// Scratch bytes of the record arrays for `rows` rows.
 size_t sample_rec_bytes(int rows, int splits);
-size_t sample_hdr_bytes(int rows, int splits);
 
 }  // namespace sas
