@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.orc_pcg_uniform.argtypes = [c_uint32, c_uint32, c_uint32]
         L.orc_softcap.restype = c_float
         L.orc_softcap.argtypes = [c_float, c_float]
+        L.orc_tanhf.restype = c_float
+        L.orc_tanhf.argtypes = [c_float]
         L.orc_penalize.restype = c_double
         L.orc_penalize.argtypes = [c_double, c_uint32, POINTER(OrcParams)]
         L.orc_sample_row.restype = None

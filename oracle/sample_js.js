@@ -26,9 +26,26 @@ function clampTopK(k) {
   return k > MAX_TOP_K ? MAX_TOP_K : Math.floor(k);
 }
 
+/* tanh rounded once to fp32 from a double evaluation (the same expression
+ * the C oracle and the GPU use); Math.exp is fdlibm's exp in V8. */
+function tanhF32(x) {
+  var ax = Math.abs(x), r;
+  if (ax !== ax) return x;
+  if (ax >= 9.5) r = 1;
+  else if (ax < 0.001953125) {
+    var x2 = ax * ax;
+    r = ax * (1 - x2 * (1 / 3 - x2 * (2 / 15 - x2 * (17 / 315))));
+  } else {
+    var t = Math.exp(2 * ax);
+    r = (t - 1) / (t + 1);
+  }
+  r = Math.fround(r);
+  return (x < 0 || (x === 0 && 1 / x < 0)) ? -r : r;
+}
+
 function softcap(x, cap) {
   var q = Math.fround(x / cap);
-  return Math.fround(cap * Math.fround(Math.tanh(q)));
+  return Math.fround(cap * tanhF32(q));
 }
 
 function penalize(v, count, p) {
@@ -50,7 +67,7 @@ function blockCandidates(logits, off, vocab, mask, moff, counts, p, K) {
     for (var g = base; g < end; g++) {
       if (mask && !((mask[moff + (g >>> 5)] >>> (g & 31)) & 1)) continue;
       var x = logits[off + g];
-      if (p.softcap > 0) x = softcap(x, p.softcap);
+      if (p.softcap > 0) x = softcap(x, Math.fround(p.softcap));
       if (x !== x) continue;
       var v = counts ? penalize(x, counts[g], p) : x;
       if (v !== v) continue;
@@ -159,8 +176,10 @@ function makeOut(rows, shared) {
     var b = shared ? new SharedArrayBuffer(n * Ctor.BYTES_PER_ELEMENT) : new ArrayBuffer(n * Ctor.BYTES_PER_ELEMENT);
     return new Ctor(b);
   }
-  return { ids: mk(Uint32Array, rows), counts: mk(Int32Array, 2 * rows),
-           probs: mk(Float64Array, rows * MAX_TOP_K), cand: mk(Uint32Array, rows * MAX_TOP_K) };
+  var out = { ids: mk(Uint32Array, rows), counts: mk(Int32Array, 2 * rows),
+              probs: mk(Float64Array, rows * MAX_TOP_K), cand: mk(Uint32Array, rows * MAX_TOP_K) };
+  out.cand.fill(0xFFFFFFFF);  // unused candidate slots hold the no-token id
+  return out;
 }
 
 function writeOut(dir, out) {

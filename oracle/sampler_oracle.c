@@ -24,9 +24,12 @@
  *                      it); they follow the CTRL / OpenAI definitions and are
  *                      pinned by invariants (identity at r=1,f=0,p=0; ids
  *                      outside the history untouched; sign rule; monotone).
- *   orc_softcap        kernels.js:1393-1395 (cap*tanh(x/cap) in fp32).  tanhf
- *                      of the host libm and of the GPU may differ by an ulp:
- *                      parity unpinned at that ulp (tolerance-checked).
+ *   orc_softcap        kernels.js:1393-1395 (cap*tanh(x/cap) in fp32), with
+ *                      tanh defined by orc_tanhf so host and GPU agree bit for
+ *                      bit.  Pinned against the correctly rounded tanh (from
+ *                      double) and cap*tanh's closed form.  Against the
+ *                      reference's WGSL tanh on Dawn the last ulp is parity
+ *                      unpinned (no reference vectors exist).
  *   orc_pcg            kernels.js:91-95, uniform kernels.js:181, 320.
  *                      Pinned by a closed-form recomputation of the hash.
  *   orc_mask_from_ids  TokenMask (tool-constraint.ts:39-42) + isListed
@@ -121,9 +124,30 @@ double orc_pcg_uniform(uint32_t seed, uint32_t it, uint32_t row) {
 
 /* ------------------------------------------------------ value pipeline -- */
 
+/* tanh of an fp32 value rounded once from a double evaluation: odd Taylor
+ * polynomial below 2^-9, (e^2x - 1)/(e^2x + 1) with the fdlibm exp above,
+ * 1 from 9.5 on.  The GPU evaluates the same expression, so both sides
+ * produce the same bits; the result is the correctly rounded tanhf except
+ * where the double result falls within its own error of a rounding
+ * boundary. */
+float orc_tanhf(float x) {
+  double ax = fabs((double)x), r;
+  if (ax != ax) return x;
+  if (ax >= 9.5) {
+    r = 1.0;
+  } else if (ax < 0.001953125) {
+    double x2 = ax * ax;
+    r = ax * (1.0 - x2 * (1.0 / 3.0 - x2 * (2.0 / 15.0 - x2 * (17.0 / 315.0))));
+  } else {
+    double t = orc_exp(2.0 * ax);
+    r = (t - 1.0) / (t + 1.0);
+  }
+  return copysignf((float)r, x);
+}
+
 float orc_softcap(float x, float cap) {
   float q = x / cap;
-  float t = tanhf(q);
+  float t = orc_tanhf(q);
   return cap * t;
 }
 

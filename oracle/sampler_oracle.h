@@ -47,6 +47,7 @@ typedef struct orc_result {
 double orc_exp(double x);
 uint32_t orc_pcg(uint32_t x);
 double orc_pcg_uniform(uint32_t seed, uint32_t it, uint32_t row);
+float orc_tanhf(float x);
 float orc_softcap(float x, float cap);
 double orc_penalize(double v, uint32_t count, const orc_params *p);
 

@@ -57,12 +57,6 @@ __device__ __forceinline__ double penalize(double v, uint32_t count, const sas_p
   return v;
 }
 
-// Gemma's final-logit softcap in fp32 (kernels.js:1393-1395).
-__device__ __forceinline__ float softcap_f32(float x, float cap) {
-  float q = x / cap;
-  return cap * tanhf(q);
-}
-
 // exp(x) by fdlibm's e_exp.c algorithm (Sun Microsystems, 1993): reduce
 // x = k*ln2 + r with ln2 split in a 32-bit-exact high part and a low part,
 // approximate exp(r) with the degree-5 Remez rational form, scale by 2^k.
@@ -116,6 +110,33 @@ __device__ __forceinline__ double fd_exp(double x) {
   }
   return y * __longlong_as_double((long long)(uint64_t)(0x3ff00000u + ((uint32_t)(k + 1000) << 20)) << 32) *
          two_m1000;
+}
+
+// tanh of an fp32 value, rounded once to fp32 from a double-precision
+// evaluation: an odd Taylor polynomial below 2^-9, (e^2x - 1)/(e^2x + 1)
+// with the fdlibm exp above, 1 from 9.5 on.  Only correctly rounded double
+// operations and fd_exp are used, so the host oracle computes the same bits.
+__device__ __forceinline__ float tanh_f32(float x) {
+  const double ax = fabs((double)x);
+  double r;
+  if (!(ax == ax)) return x;
+  if (ax >= 9.5) {
+    r = 1.0;
+  } else if (ax < 0.001953125) {
+    const double x2 = ax * ax;
+    r = ax * (1.0 - x2 * (1.0 / 3.0 - x2 * (2.0 / 15.0 - x2 * (17.0 / 315.0))));
+  } else {
+    const double t = fd_exp(2.0 * ax);
+    r = (t - 1.0) / (t + 1.0);
+  }
+  return copysignf((float)r, x);
+}
+
+// Gemma's final-logit softcap cap*tanh(x/cap) in fp32 (kernels.js:1393-1395;
+// cap 30, gemma-config.js:47).
+__device__ __forceinline__ float softcap_f32(float x, float cap) {
+  const float q = x / cap;
+  return cap * tanh_f32(q);
 }
 
 // (v desc, id asc): the order of the reference's stable descending sort

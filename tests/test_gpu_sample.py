@@ -159,3 +159,52 @@ def test_pcg_uniform_matches_reference_hash():
     lib = _capi.load()
     for seed, it, row in [(1, 0, 0), (0xDEADBEEF, 7, 2), (12345, 99, 1)]:
         assert lib.sas_pcg_uniform(seed, it, row) == O.lib().orc_pcg_uniform(seed, it, row)
+
+
+# -------------------------------------------------- softcap, reuse, errors --
+
+@pytest.mark.parametrize("params", [Params(temperature=1.0, top_k=64, top_p=0.95, softcap=30.0),
+                                    Params(temperature=0.0, softcap=30.0, presence_penalty=1.5)])
+def test_gemma_softcap_rows(sampler, params):
+    rng = np.random.default_rng(21)
+    rows, vocab = 16, W.GEMMA_VOCAB
+    x = (rng.standard_normal((rows, vocab)) * 12).astype(np.float32)      # beyond the cap's linear range
+    hi, ho = W._csr([rng.integers(0, vocab, 512) for _ in range(rows)])
+    b = W.Batch("softcap", x, params, mask=W.random_mask(rng, rows, vocab, 0.02, 0.5), hist_ids=hi,
+                hist_offsets=ho, uniforms=rng.random(rows))
+    check(sampler, b, label="softcap")
+
+
+def test_back_to_back_launches_with_different_inputs(sampler):
+    # the record area and its counters are reused by every launch: a stale
+    # record would change ids or probabilities of the next batch
+    import torch
+    batches = [W.c3p(rows=24, vocab=70000, seed=s) for s in (40, 41, 42)]
+    batches.append(W.c4(rows=24, vocab=70000, seed=43, hist=1000))
+    outs = []
+    for b in batches:
+        dev = {k: to_dev(getattr(b, k), torch.int32 if k in ("mask", "hist_ids") else None)
+               for k in ("mask", "hist_ids", "hist_offsets", "uniforms")}
+        outs.append(sampler.sample(to_dev(b.logits), vocab=b.vocab, params=b.params, full=True, **dev))
+    torch.cuda.synchronize()
+    for b, o in zip(batches, outs):
+        g = {"ids": o["ids"].cpu().numpy().view(np.uint32), "probs": o["probs"].cpu().numpy(),
+             "cand_ids": o["cand_ids"].cpu().numpy().view(np.uint32), "counts": o["counts"].cpu().numpy(),
+             "flags": o["flags"].cpu().numpy().view(np.uint32)}
+        assert_parity(g, O.sample_rows(b), b.name)
+
+
+def test_argument_errors_are_reported(sampler):
+    import torch
+    from shared_amd import SasError
+    x = torch.zeros((2, 100), dtype=torch.float32, device="cuda")
+    ids = torch.empty(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(SasError, match="uniforms are required"):
+        sampler.sample_into(x, ids, params=Params(temperature=1.0))
+    with pytest.raises(SasError, match="vocab"):
+        sampler.sample_into(x, ids, vocab=0, params=Params())
+    with pytest.raises(SasError, match="logits_stride"):
+        sampler.sample_into(x, ids, vocab=101, params=Params())
+    with pytest.raises(SasError, match="mask_stride"):
+        sampler.sample_into(x, ids, mask=torch.zeros((2, 2), dtype=torch.int32, device="cuda"), params=Params())
+    sampler.sample_into(x[:0], ids, params=Params())          # zero rows is a no-op

@@ -1,0 +1,341 @@
+"""CPU tests that pin the oracle (oracle/sampler_oracle.c) before it is
+trusted as the GPU path's checker.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped
+term, a wrong sign or index, a transposed comparison, a different rounding
+order) fails it:
+
+* exp against V8's own Math.exp outputs (tests/golden/v8_math_exp.json,
+  written by tests/golden/make_v8_exp.js) - the engine the reference's
+  sample() (lib/webgpu-llm/tokenizer.js:165) runs on;
+* sample() semantics (tokenizer.js:151-178) against answers derived by hand
+  from the closed forms (logistic weights, the top-p cut, the draw bound);
+* the bounded-heap selection against a full sort (brute force);
+* the draw against its exact distribution over a fine grid of uniforms;
+* the whole row pipeline against the independent Node restatement
+  (oracle/sample_js.js, a different two-stage structure) run on V8;
+* rejection-sampling verify against the properties that fix it.
+"""
+import json
+import math
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+from shared_amd import Params
+from shared_amd import workloads as W
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _bits(x: float) -> bytes:
+    return struct.pack(">d", x)
+
+
+# -------------------------------------------------------------------- exp --
+
+def test_exp_matches_v8_math_exp_bit_for_bit():
+    with open(os.path.join(HERE, "golden", "v8_math_exp.json")) as f:
+        cases = json.load(f)["cases"]
+    assert len(cases) > 5000
+    exp = O.lib().orc_exp
+    bad = []
+    for xin, yout in cases:
+        x = struct.unpack(">d", bytes.fromhex(xin))[0]
+        y = struct.unpack(">d", bytes.fromhex(yout))[0]
+        z = exp(x)
+        if math.isnan(y):
+            ok = math.isnan(z)
+        else:
+            ok = _bits(z) == _bits(y)
+        if not ok:
+            bad.append((x, y, z))
+    assert not bad, f"{len(bad)} mismatches, first {bad[:3]}"
+
+
+def test_exp_against_libm_within_one_ulp():
+    rng = np.random.default_rng(0)
+    exp = O.lib().orc_exp
+    for x in np.concatenate([rng.uniform(-700, 700, 2000), -rng.exponential(3.0, 2000)]):
+        y, z = math.exp(x), exp(float(x))
+        assert abs(z - y) <= math.ulp(y), (x, y, z)
+    assert exp(0.0) == 1.0 and exp(-math.inf) == 0.0 and exp(math.inf) == math.inf
+    assert math.isnan(exp(math.nan))
+
+
+# ------------------------------------------------------- sample() by hand --
+
+def _row(logits, p, *, mask_ids=None, hist=None, u=0.0, mode=0):
+    x = np.asarray(logits, np.float32)
+    mask = None
+    if mask_ids is not None:
+        bits = np.zeros((1, x.size), bool)
+        bits[0, list(mask_ids)] = True
+        mask = W.pack_bits(bits)[0]
+    h = None if hist is None else np.asarray(hist, np.uint32)
+    return O.sample_row(x, p, mask=mask, hist=h, uniform=u, select_mode=mode)
+
+
+LOG4 = [1.0, 3.0, 2.0, -1.0]          # ranked: id1 (3), id2 (2), id0 (1), id3 (-1)
+
+
+def test_softmax_weights_and_topp_cut_closed_form():
+    r = _row(LOG4, Params(temperature=1.0, top_k=3, top_p=0.9), u=0.5)
+    w = [1.0, math.exp(-1.0), math.exp(-2.0)]
+    s = sum(w)
+    assert (r.k, r.cut) == (3, 2)          # 0.665 < 0.9 <= 0.665 + 0.245
+    assert list(r.cand_ids[:3]) == [1, 2, 0]
+    for i in range(3):
+        assert abs(r.probs[i] - w[i] / s) <= 2e-16
+    # temperature divides the logit gaps
+    r = _row(LOG4, Params(temperature=0.5, top_k=4, top_p=1.0))
+    w = [1.0, math.exp(-2.0), math.exp(-4.0), math.exp(-8.0)]
+    for i in range(4):
+        assert abs(r.probs[i] - w[i] / sum(w)) <= 2e-16
+
+
+def test_draw_boundary_is_the_logistic_of_the_gap():
+    # with cut = 2 the draw picks id1 iff U * (1 + e^-1) - 1 <= 0, i.e.
+    # U <= 1 / (1 + e^-1) = 0.7310585...
+    p = Params(temperature=1.0, top_k=3, top_p=0.9)
+    edge = 1.0 / (1.0 + math.exp(-1.0))
+    assert _row(LOG4, p, u=0.0).id == 1
+    assert _row(LOG4, p, u=edge - 1e-9).id == 1
+    assert _row(LOG4, p, u=edge + 1e-9).id == 2
+    assert _row(LOG4, p, u=0.999999).id == 2
+
+
+def test_greedy_topk1_and_topp0_take_the_best():
+    for p in [Params(temperature=0.0), Params(temperature=-1.0), Params(temperature=1.0, top_k=1),
+              Params(temperature=1.0, top_k=4, top_p=0.0)]:
+        for u in (0.0, 0.5, 0.99):
+            assert _row(LOG4, p, u=u).id == 1
+
+
+def test_ties_take_the_lowest_id():
+    assert _row([2.0, 2.0, 1.0], Params(temperature=0.0)).id == 0
+    r = _row([5.0, 7.0, 7.0, 7.0, 1.0], Params(temperature=1.0, top_k=2, top_p=1.0))
+    assert list(r.cand_ids[:2]) == [1, 2]
+    assert r.probs[0] == r.probs[1] == 0.5
+
+
+def test_mask_excludes_ids_and_empty_row_has_no_token():
+    assert _row(LOG4, Params(temperature=0.0), mask_ids=[0, 3]).id == 0
+    assert _row(LOG4, Params(temperature=0.0), mask_ids=[3]).id == 3
+    r = _row(LOG4, Params(temperature=1.0, top_k=5), mask_ids=[])
+    assert r.id == O.NO_TOKEN and r.flags & 1
+    # fewer allowed ids than top_k: k shrinks to the allowed count
+    r = _row(LOG4, Params(temperature=1.0, top_k=20), mask_ids=[0, 2])
+    assert r.k == 2 and list(r.cand_ids[:2]) == [2, 0]
+
+
+def test_presence_penalty_as_tokenizer_js_157():
+    # v -= pp for ids in the recent set: 3 - 2.5 = 0.5 drops below id2 and id0
+    assert _row(LOG4, Params(temperature=0.0, presence_penalty=2.5), hist=[1]).id == 2
+    # a repeated id is penalised once by presence
+    assert _row(LOG4, Params(temperature=0.0, presence_penalty=0.9), hist=[1, 1, 1]).id == 1
+
+
+def test_repetition_and_frequency_penalties():
+    # CTRL repetition: positive logits divide, negative multiply
+    assert _row(LOG4, Params(temperature=0.0, repetition_penalty=2.0), hist=[1]).id == 2   # 1.5 < 2
+    assert _row(LOG4, Params(temperature=0.0, repetition_penalty=1.4), hist=[1]).id == 1   # 2.14 > 2
+    r = _row([-1.0, -2.0], Params(temperature=1.0, top_k=2, repetition_penalty=3.0), hist=[0])
+    assert list(r.cand_ids[:2]) == [1, 0]                    # -3 < -2
+    # frequency: count 3 * 0.4 = 1.2 -> 1.8 < 2
+    assert _row(LOG4, Params(temperature=0.0, frequency_penalty=0.4), hist=[1, 1, 1]).id == 2
+    assert _row(LOG4, Params(temperature=0.0, frequency_penalty=0.4), hist=[1, 1]).id == 1
+
+
+def test_penalty_invariants():
+    pen = O.lib().orc_penalize
+    rng = np.random.default_rng(1)
+    ident = O.params(Params())
+    for v in rng.standard_normal(200) * 5:
+        for c in (1, 2, 7):
+            assert pen(float(v), c, ident) == float(v)     # r=1, f=0, p=0 is the identity
+    p = O.params(Params(repetition_penalty=1.3, frequency_penalty=0.2, presence_penalty=0.5))
+    for v in rng.standard_normal(200) * 5:
+        assert pen(float(v), 0, p) == float(v)            # ids outside the history are untouched
+        a, b = pen(float(v), 1, p), pen(float(v), 2, p)
+        assert b < a < float(v) + 1e-12                    # more occurrences, lower value
+    lo = O.params(Params(repetition_penalty=1.1))
+    hi = O.params(Params(repetition_penalty=1.5))
+    for v in rng.standard_normal(200) * 5:
+        assert pen(float(v), 1, hi) <= pen(float(v), 1, lo)  # monotone in r
+
+
+def test_tanh_is_correctly_rounded_fp32():
+    # the double evaluation rounded once to fp32 equals the correctly rounded
+    # tanh (math.tanh in double, rounded to fp32) except within double
+    # rounding error of an fp32 rounding boundary
+    rng = np.random.default_rng(2)
+    xs = np.concatenate([rng.standard_normal(20000) * 2, rng.standard_normal(2000) * 1e-3,
+                         [0.0, -0.0, 1e-30, -1e-30, 9.4, 9.6, 20.0, -20.0, np.inf, -np.inf]]).astype(np.float32)
+    tanhf = O.lib().orc_tanhf
+    off = 0
+    for x in xs:
+        want = np.float32(math.tanh(float(x)))
+        got = np.float32(tanhf(float(x)))
+        d = abs(int(got.view(np.int32)) - int(want.view(np.int32)))
+        assert d <= 1, (x, got, want)
+        off += d
+    assert off <= 2
+    assert math.copysign(1.0, tanhf(-0.0)) == -1.0 and math.isnan(tanhf(math.nan))
+
+
+def test_softcap_is_cap_tanh_of_the_fp32_quotient():
+    cap = np.float32(30.0)
+    xs = np.random.default_rng(3).standard_normal(3000).astype(np.float32) * np.float32(40)
+    for x in xs:
+        q = np.float32(x / cap)
+        want = np.float32(cap * np.float32(O.lib().orc_tanhf(float(q))))
+        assert np.float32(O.lib().orc_softcap(float(x), 30.0)) == want
+        assert abs(float(want) - 30.0 * math.tanh(float(x) / 30.0)) <= 4e-6 * 30.0
+
+
+# --------------------------------------------------- selection and draws --
+
+def test_heap_selection_equals_full_sort_with_ties():
+    rng = np.random.default_rng(3)
+    for trial in range(60):
+        vocab = int(rng.integers(1, 3000))
+        x = rng.integers(-3, 4, vocab).astype(np.float32) * np.float32(0.5)   # heavy ties
+        x[rng.random(vocab) < 0.05] = np.nan
+        p = Params(temperature=float(rng.choice([0.0, 0.7, 1.3])), top_k=int(rng.integers(1, 129)),
+                   top_p=float(rng.choice([0.5, 0.9, 1.0])), presence_penalty=float(rng.choice([0.0, 0.5])),
+                   repetition_penalty=float(rng.choice([1.0, 1.2])))
+        mask = None
+        if trial % 2:
+            mask = W.pack_bits((rng.random((1, vocab)) < 0.3))[0]
+        hist = rng.integers(0, vocab, int(rng.integers(0, 40))).astype(np.uint32)
+        u = float(rng.random())
+        a = O.sample_row(x, p, mask=mask, hist=hist, uniform=u, select_mode=0)
+        b = O.sample_row(x, p, mask=mask, hist=hist, uniform=u, select_mode=1)
+        assert (a.id, a.k, a.cut, a.flags) == (b.id, b.k, b.cut, b.flags)
+        assert list(a.cand_ids[:a.k]) == list(b.cand_ids[:b.k])
+        assert list(a.probs[:a.k]) == list(b.probs[:b.k])
+
+
+def test_draw_frequencies_match_the_cut_distribution():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(64) * 2).astype(np.float32)
+    p = Params(temperature=0.8, top_k=10, top_p=0.8)
+    n = 20000
+    counts = {}
+    for i in range(n):
+        r = O.sample_row(x, p, uniform=(i + 0.5) / n)
+        counts[r.id] = counts.get(r.id, 0) + 1
+    ref = O.sample_row(x, p, uniform=0.5)
+    q = np.array(ref.probs[:ref.cut]) / sum(ref.probs[:ref.cut])
+    ids = list(ref.cand_ids[:ref.cut])
+    assert set(counts) <= set(ids)
+    for i, t in zip(ids, q):
+        assert abs(counts.get(i, 0) / n - t) <= 2.0 / n
+
+
+# ------------------------------------------------ Node restatement on V8 --
+
+@pytest.mark.skipif(O.node_binary() is None, reason="node is not installed")
+@pytest.mark.parametrize("case", range(4))
+def test_node_restatement_agrees_bit_for_bit(case):
+    rng = np.random.default_rng(10 + case)
+    rows, vocab = 6, int(rng.choice([1000, 2049, 5000, 7777]))
+    x = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    x[:, rng.integers(0, vocab, 5)] += np.float32(8)
+    params = [Params(temperature=0.7, top_k=40, top_p=0.95),
+              Params(temperature=1.0, top_k=50, top_p=0.9, repetition_penalty=1.1, presence_penalty=0.5,
+                     frequency_penalty=0.3),
+              Params(temperature=0.0, repetition_penalty=1.15),
+              Params(temperature=1.3, top_k=128, top_p=1.0, softcap=30.0)][case]
+    mask = W.random_mask(rng, rows, vocab, 0.05, 0.6) if case in (1, 3) else None
+    hi, ho = W._csr([rng.integers(0, vocab, 300) for _ in range(rows)]) if case in (1, 2) else (None, None)
+    b = W.Batch("node", x, params, mask=mask, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+    js, _ = O.run_node(b)
+    c = O.sample_rows(b)
+    assert np.array_equal(js["ids"], c["ids"])
+    assert np.array_equal(js["counts"], c["counts"])
+    assert np.array_equal(js["cand_ids"], c["cand_ids"])
+    assert np.array_equal(js["probs"].view(np.uint64), c["probs"].view(np.uint64))
+
+
+# ------------------------------------------------------------------- mask --
+
+def test_mask_from_ids_brute_force():
+    rng = np.random.default_rng(5)
+    for vocab in (1, 31, 32, 33, 1000, 4099):
+        ids = rng.integers(0, vocab + 40, 50).astype(np.uint32)   # includes ids >= vocab
+        for kind in (0, 1, 2):
+            w = O.mask_from_ids(kind, ids, vocab)
+            bits = np.unpackbits(w.view(np.uint8), bitorder="little")
+            want = np.zeros(w.size * 32, np.uint8)
+            listed = ids[ids < vocab]
+            if kind == 0:
+                want[:vocab] = 1
+            elif kind == 1:
+                want[listed] = 1
+            else:
+                want[:vocab] = 1
+                want[listed] = 0
+            assert np.array_equal(bits, want), (vocab, kind)
+
+
+# ----------------------------------------------------------------- verify --
+
+def _verify_inp(target, draft, draft_ids, u, mask=None, T=1.0):
+    t = np.asarray(target, np.float32)
+    L = len(draft_ids)
+    return {"target": t.reshape(L + 1, -1), "draft": np.asarray(draft, np.float32).reshape(L, -1),
+            "mask": mask, "draft_ids": np.asarray([draft_ids], np.uint32),
+            "uniforms": np.asarray(u, np.float64).reshape(1, L + 1, 2), "temperature": T,
+            "vocab": t.size // (L + 1), "seqs": 1, "drafts": L}
+
+
+def test_verify_accepts_always_when_draft_equals_target():
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((3, 50)) * 2).astype(np.float32)
+    for trial in range(50):
+        d = [int(i) for i in rng.integers(0, 50, 2)]
+        u = rng.random((3, 2))
+        out = O.verify(_verify_inp(x, x[:2], d, u))
+        assert out["accepted"][0] == 2 and list(out["tokens"][0, :2]) == d
+
+
+def test_verify_one_hot_draft_accepts_with_target_probability():
+    rng = np.random.default_rng(7)
+    V = 16
+    t = (rng.standard_normal((2, V))).astype(np.float32)
+    d = 5
+    q = np.full((1, V), -1000.0, np.float32)
+    q[0, d] = 10.0                                   # q(d) = 1 in double
+    w = np.exp(t[0].astype(np.float64) - t[0].max())
+    pd = w[d] / w.sum()
+    n = 4000
+    acc = sum(O.verify(_verify_inp(t, q, [d], [[(i + 0.5) / n, 0.5], [0.5, 0.5]]))["accepted"][0]
+              for i in range(n))
+    assert abs(acc / n - pd) <= 1.5 / n
+
+
+def test_verify_output_marginal_equals_target():
+    # P(token at position 0) = sum_d q(d) [a_d 1{d} + (1 - a_d) residual_d] = p,
+    # with the acceptance a_d and the residual draw measured on uniform grids
+    rng = np.random.default_rng(8)
+    V = 6
+    t = (rng.standard_normal((2, V)) * 1.5).astype(np.float32)
+    dl = (rng.standard_normal((1, V)) * 1.5).astype(np.float32)
+    p = np.exp(t[0].astype(np.float64) - t[0].max()); p /= p.sum()
+    q = np.exp(dl[0].astype(np.float64) - dl[0].max()); q /= q.sum()
+    g = 400
+    grid = (np.arange(g) + 0.5) / g
+    marg = np.zeros(V)
+    for d in range(V):
+        acc = np.mean([O.verify(_verify_inp(t, dl, [d], [[u, 0.5], [0.5, 0.5]]))["accepted"][0] for u in grid])
+        marg[d] += q[d] * acc
+        if acc < 1.0:
+            for u2 in grid:
+                tok = O.verify(_verify_inp(t, dl, [d], [[1.0 - 1e-12, u2], [0.5, 0.5]]))["tokens"][0, 0]
+                marg[tok] += q[d] * (1.0 - acc) / g
+    assert np.abs(marg - p).max() < 4.0 / g
