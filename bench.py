@@ -30,7 +30,7 @@ if ROOT not in sys.path:
 
 METRIC = "rows/s + % HBM peak: 262k-vocab penalties+mask+top-k/top-p, B=128"
 HBM_PEAK_GBPS = 8000.0
-KERNEL = "sample_rows_kernel"
+KERNEL = "sample_kernel"
 WORKLOAD_DOC = {
     "C2": "T0.7 top-k40 top-p0.95, vocab 151936, batch 64, Zipf-biased N(0,3) logits",
     "C3": "bitmask 0.5-20% + top-k50 top-p0.9 T1.0, vocab 262144, batch 128, N(0,4) logits",

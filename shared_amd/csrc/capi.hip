@@ -17,10 +17,10 @@ struct sas_sampler {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
-  void *recs = nullptr;        // candidate records
+  void *recs = nullptr;        // candidate record slots, then their counts
   size_t recs_cap = 0;
-  uint32_t *counters = nullptr;
-  int32_t counters_cap = 0;
+  uint32_t *ctl = nullptr;     // per-row arrival counters and thresholds, zero between launches
+  int32_t ctl_rows = 0;
   void *vscratch = nullptr;   // sas_verify partials
   size_t vscratch_cap = 0;
 };
@@ -62,15 +62,16 @@ int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
 }
 
 int ensure_sample_scratch(sas_sampler *s, int rows, int splits) {
-  int rc = grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, splits), false);
+  int rc = grow(s, &s->recs, &s->recs_cap,
+                sas::sample_rec_bytes(rows, splits) + sas::sample_count_bytes(rows, splits), false);
   if (rc) return rc;
-  if (rows > s->counters_cap) {
-    size_t cap = (size_t)s->counters_cap * 4;
-    void *p = s->counters;
-    rc = grow(s, &p, &cap, (size_t)rows * 4, true);
-    s->counters = reinterpret_cast<uint32_t *>(p);
+  if (rows > s->ctl_rows) {
+    size_t cap = (size_t)s->ctl_rows * sas::kCtlStride * 4;
+    void *p = s->ctl;
+    rc = grow(s, &p, &cap, (size_t)rows * sas::kCtlStride * 4, true);
+    s->ctl = reinterpret_cast<uint32_t *>(p);
     if (rc) return rc;
-    s->counters_cap = (int32_t)(cap / 4);
+    s->ctl_rows = (int32_t)(cap / (sas::kCtlStride * 4));
   }
   return SAS_OK;
 }
@@ -113,7 +114,7 @@ void sas_destroy(sas_sampler *s) {
   (void)hipSetDevice(s->device);
   (void)hipDeviceSynchronize();
   if (s->recs) (void)hipFree(s->recs);
-  if (s->counters) (void)hipFree(s->counters);
+  if (s->ctl) (void)hipFree(s->ctl);
   if (s->vscratch) (void)hipFree(s->vscratch);
   if (s->stream) (void)hipStreamDestroy(s->stream);
   delete s;
@@ -168,14 +169,19 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.out_cand_ids = r->out_cand_ids;
   a.out_counts = r->out_counts;
   a.out_flags = r->out_flags;
-  a.recs = reinterpret_cast<sas::Rec *>(s->recs);
-  a.rec_cap = sas::sample_rec_cap(splits);
-  a.counters = s->counters;
+  // record arrays carved from one allocation: values (8-byte) first
+  const size_t slots = (size_t)r->rows * splits * sas::kCapBlock;
+  a.rval = reinterpret_cast<double *>(s->recs);
+  a.rkey = reinterpret_cast<float *>(a.rval + slots);
+  a.rid = reinterpret_cast<uint32_t *>(a.rkey + slots);
+  a.counts = a.rid + slots;
+  a.ctl = s->ctl;
   a.vocab = r->vocab;
   a.rows = r->rows;
   a.splits = splits;
-  const bool aligned = (reinterpret_cast<uintptr_t>(r->logits) & 15u) == 0 && (r->logits_stride & 3) == 0;
-  hipError_t e = sas::launch_sample(a, f4, aligned, pick_stream(s, stream));
+  a.aligned = (reinterpret_cast<uintptr_t>(r->logits) & 15u) == 0 && (r->logits_stride & 3) == 0;
+  const bool softcap = r->row_params != nullptr || r->params.softcap > 0.0f;
+  hipError_t e = sas::launch_sample(a, f4, softcap, pick_stream(s, stream));
   if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
   return SAS_OK;
 }

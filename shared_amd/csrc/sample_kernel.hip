@@ -1,34 +1,40 @@
 // sample_kernel.hip - fused logit processing + top-k/top-p sampling for gfx950.
 //
-// Two launches per decode step, stream-ordered:
+// One launch per decode step.  Grid = rows x splits blocks; block (row, s)
+// owns vocabulary chunk [s*CHUNK, (s+1)*CHUNK) of one row:
 //
-// split_kernel   grid = rows x splits blocks; block (row, s) owns vocabulary
-//                chunk [s*CHUNK, (s+1)*CHUNK) of one row:
-//   1. the row's history ids, then the chunk's fp32 logits (128-bit loads
-//      straight into registers, CHUNK/256 values per thread) and the mask
-//      words (one 32-bit load per float4: the 8 threads of a word share it);
-//      history ids falling in the chunk are counted into a packed u16 LDS
-//      table while the logits are in flight;
+//   1. the chunk's fp32 logits (128-bit loads straight into registers,
+//      CHUNK/256 values per thread), its mask words (one 32-bit load per
+//      float4; the 8 threads of a word share it), the row's published
+//      threshold and its history ids, counted into a packed u16 LDS table;
 //   2. per value: softcap, mask (masked -> NaN, never selected), history
 //      penalties for the few ids with a count (double precision, kept as a
 //      round-down fp32 key; the exact double is recomputed when emitted);
 //   3. block threshold: the j-th largest lane max of each wave by a ballot
-//      bit search over order-preserving keys, combined so that >= top_k
-//      values are >= it;
-//   4. values >= threshold (typically a little over top_k of them) are
-//      appended to an LDS list with wave-aggregated atomics; if more than
-//      kCapBlock pass, a radix search over the chunk's keys finds a tighter
-//      bound; then a relaxed atomic reserves space in the row's record area
-//      and 16-byte records are written.  No fence: nothing in this launch
-//      reads them.
-//
-// merge_kernel   one block per row, after the split kernel has completed:
-//   5. the row's records are loaded into registers in one round and a radix
-//      search (8-bit digits from the top, LDS histograms) finds a key bound
-//      that keeps at least top_k and at most top_k + kMergeSlack records;
-//   6. exact rank of the survivors by (value desc, id asc) in double;
+//      search over order-preserving keys, combined so that >= top_k values
+//      are >= it.  It is published to the row (atomic max, not waited on):
+//      a chunk of the row that starts later drops everything below the
+//      largest threshold published so far, since the row's top_k cannot
+//      lie there;
+//   4. values >= the threshold (typically a little over top_k of them) are
+//      appended to an LDS list (one LDS atomic per wave) and written into
+//      the block's own record slots with their count;
+//   5. the block counts itself in on the row (one atomic on a counter with
+//      a cache line to itself); the row's last block merges:
+//   6. a radix search over the row's record keys (8-bit digits starting at
+//      the highest bit in which they differ) finds a bound keeping at least
+//      top_k and at most top_k + kMergeSlack records; the survivors are
+//      ranked exactly by (value desc, id asc) in double;
 //   7. the reference's sample() tail in double precision: exp weights and
-//      divisions in parallel, the running sums sequentially in JS order.
+//      divisions across lanes, the running sums sequentially in JS order.
+//
+// Cross-block data (records, counts, row counters and thresholds) is only
+// accessed with agent-scope atomic loads and stores, which are coherent
+// across the XCDs' L2 caches without cache maintenance; each block waits
+// for its record stores to complete before it counts itself in, so the
+// last block, which observes every other block's count, reads complete
+// records.  The merging block resets the row's counter and threshold for
+// the next launch.
 //
 // Logits cross HBM once.  Replaces the topk + sampler WGSL pair
 // (lib/webgpu-llm/kernels.js:1389-1449, 65-201) and the CPU sample()
@@ -45,8 +51,9 @@ struct SplitLds {
 };
 
 constexpr int kHistRegs = 4;     // history ids per thread held in registers
-constexpr int kMergeRecs = 16;   // records per merge thread held in registers
-constexpr int kMergeSlack = 32;  // survivors beyond top_k the merge may rank
+constexpr int kSurvCap = 256;    // survivors the merge ranks in LDS
+constexpr int kMergeSlack = 32;  // survivors beyond top_k the merge aims for
+constexpr int kMergeRegs = 32;   // blocks per row whose record keys the merge holds in registers
 
 // LDS used by block-wide reductions.
 struct Red {
@@ -55,24 +62,44 @@ struct Red {
   uint32_t id[kWaves];
 };
 
-// Block-wide search, 8-bit digits from the most significant, for a bound L
-// on the keys key(0..N-1) of all threads (0 = no key): at least `need` keys
-// are >= L, and at most `cap` are unless more than that tie at the need-th
-// largest key (then L is that key exactly).  `need` must not exceed the
-// number of keys.  LDS: hist[256], sel[3].
-// U bounds the unrolling of the key loop (and with it the keys in flight).
-template <int N, int U = N, typename KeyFn>
-__device__ uint32_t radix_bound(KeyFn key, uint32_t need, uint32_t cap, uint32_t *hist, uint32_t *sel) {
+// Agent-scope relaxed accesses: coherent across the XCDs without fences.
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every vector memory operation this wave issued (stores and
+// atomics included) has completed: s_waitcnt vmcnt(0).
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Block-wide search for a bound L on keys (0 = no key): at least `need`
+// keys are >= L, and at most `cap` are unless more than that tie at the
+// need-th largest key (then L is that key exactly).  Digits of 8 bits run
+// from bit `hb` (the highest bit in which the keys may differ; `hprefix`
+// holds the bits above it) down to bit 0.  `need` must not exceed the
+// number of keys.  for_keys(f) calls f(key) for each of this thread's keys.
+// LDS: hist[256], sel[3].
+template <typename ForKeys>
+__device__ uint32_t radix_bound(ForKeys for_keys, int hb, uint32_t hprefix, uint32_t need, uint32_t cap,
+                                uint32_t *hist, uint32_t *sel) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t prefix = 0u, kr = need, taken = 0u;
-  for (int shift = 24;; shift -= 8) {
+  uint32_t prefix = hprefix, kr = need, taken = 0u;
+  int top = hb + 1;  // bits >= top are fixed by prefix
+  for (;;) {
+    const int width = top < 8 ? top : 8;
+    const int shift = top - width;
     for (int i = tid; i < 256; i += kThreads) hist[i] = 0u;
     __syncthreads();
-#pragma unroll U
-    for (int j = 0; j < N; ++j) {
-      const uint32_t x = key(j);
-      if (x != 0u && (shift == 24 || (x >> (shift + 8)) == prefix)) atomicAdd(&hist[(x >> shift) & 255u], 1u);
-    }
+    for_keys([&](uint32_t x) {
+      if (x != 0u && (top == 32 || (x >> top) == prefix)) atomicAdd(&hist[(x >> shift) & ((1u << width) - 1u)], 1u);
+    });
     __syncthreads();
     if (wave == 0) {
       // lane l holds bins 255-4l .. 252-4l (largest digits first)
@@ -102,19 +129,19 @@ __device__ uint32_t radix_bound(KeyFn key, uint32_t need, uint32_t cap, uint32_t
     __syncthreads();
     const uint32_t bin = sel[0], above = sel[1], cnt = sel[2];
     __syncthreads();  // hist and sel are reused
-    prefix = (prefix << 8) | bin;
+    prefix = (prefix << width) | bin;
     if (taken + above + cnt <= cap || shift == 0) return prefix << shift;
+    top = shift;
     taken += above;
     kr -= above;
   }
 }
 
 // Appends the ids whose predicate holds to the LDS candidate list with one
-// LDS atomic per wave per element slot.  pred(i) / key(i) for slot i; U
-// bounds the unrolling.
-template <int E, int U = E, typename Pred, typename Key>
-__device__ __forceinline__ void emit_candidates(int lo, uint32_t penbits, Pred pred_of, Key key_of,
-                                                uint32_t *s_n, uint32_t *s_rec_id, float *s_rec_key) {
+// LDS atomic per wave per element slot (the rare paths).
+template <int E, int U, typename Pred, typename Key>
+__device__ __forceinline__ void emit_each(int lo, uint32_t penbits, Pred pred_of, Key key_of, uint32_t *s_n,
+                                         uint32_t *s_rec_id, float *s_rec_key) {
   const int tid = threadIdx.x, lane = tid & 63;
 #pragma unroll U
   for (int i = 0; i < E; ++i) {
@@ -136,6 +163,23 @@ __device__ __forceinline__ void emit_candidates(int lo, uint32_t penbits, Pred p
       }
     }
   }
+}
+
+// Reserves popcount(bits) consecutive LDS list slots for this lane (wave
+// prefix of the counts by ballots, one atomic per wave) and returns the
+// first.  bits holds at most 32 set bits.
+__device__ __forceinline__ uint32_t wave_reserve(uint32_t bits, uint32_t *s_n) {
+  const uint32_t cnt = __popc(bits);
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int b = 0; b < 6; ++b) {
+    const uint64_t bb = __ballot((cnt >> b) & 1u);
+    pre += lanes_below(bb) << b;
+    tot += (uint32_t)__popcll(bb) << b;
+  }
+  uint32_t base = 0u;
+  if (tot && (threadIdx.x & 63) == 0) base = atomicAdd(s_n, tot);
+  return __builtin_amdgcn_readlane(base, 0) + pre;
 }
 
 // Recomputes one chunk element from global memory and the LDS count table;
@@ -249,31 +293,415 @@ __device__ __forceinline__ int block_topk_slow(const ElemCtx &c, int E, int k, u
   return got;
 }
 
-template <int F4, bool kAligned>
-__global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
+// More than kCapBlock values passed the wave thresholds (few valid lanes or
+// heavy ties): bound the block's keys exactly (at least k, at or above
+// `floor_key`) and emit again; with more than kCapBlock exact ties, fall
+// back to repeated block argmax.  The keys are recomputed from memory, so
+// nothing of the hot path's registers is live here.  Returns the count.
+template <int E>
+__device__ uint32_t overflow_select(const ElemCtx &ec, int k, uint32_t floor_key, uint32_t *s_rec_id,
+                                                 float *s_rec_key, uint32_t *s_hist, uint32_t *s_sel,
+                                                 uint32_t *s_n, Red *red) {
+  auto key = [&](int i) {
+    double val;
+    uint32_t id;
+    return ec.value(i, val, id) ? okey(rd_f32(val)) : 0u;
+  };
+  auto for_keys = [&](auto f) {
+#pragma unroll 4
+    for (int i = 0; i < E; ++i) f(key(i));
+  };
+  uint32_t bound = radix_bound(for_keys, 31, 0u, (uint32_t)k, (uint32_t)kCapBlock, s_hist, s_sel);
+  bound = max(bound, floor_key);
+  if (threadIdx.x == 0) *s_n = 0u;
+  __syncthreads();
+  // every record of this path recomputes its exact value when written
+  emit_each<E, 4>(
+      ec.lo, ~0u,
+      [&](int i) {
+        const uint32_t x = key(i);
+        return x != 0u && x >= bound;
+      },
+      [&](int i) { return fkey(key(i)); }, s_n, s_rec_id, s_rec_key);
+  __syncthreads();
+  uint32_t n = *s_n;
+  if (n > (uint32_t)kCapBlock) n = (uint32_t)block_topk_slow(ec, E, k, s_rec_id, s_rec_key, red);
+  return n;
+}
+
+// ------------------------------------------------------------------ merge --
+
+// Block-wide max and min; every thread returns them.  LDS: red[2 * kWaves].
+__device__ __forceinline__ void block_minmax(uint32_t &mx, uint32_t &mn, uint32_t *red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, s, 64));
+    mn = min(mn, (uint32_t)__shfl_xor((int)mn, s, 64));
+  }
+  if (lane == 0) {
+    red[wave] = mx;
+    red[kWaves + wave] = mn;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    mx = max(mx, red[w]);
+    mn = min(mn, red[kWaves + w]);
+  }
+}
+
+// A row's candidate records: block b's j-th at slot b*kCapBlock + j, read
+// with agent-scope loads.
+struct RowRecs {
+  const uint32_t *key;  // fp32 bits
+  const uint32_t *id;
+  const uint64_t *val;  // fp64 bits
+  __device__ uint32_t okey_at(int64_t g) const { return okey(__uint_as_float(ld_agent(key + g))); }
+  __device__ double val_at(int64_t g) const { return __longlong_as_double((long long)ld_agent(val + g)); }
+  __device__ uint32_t id_at(int64_t g) const { return ld_agent(id + g); }
+};
+
+// LDS of the merge; overlays the split phase's count table.
+struct MergeLds {
+  uint32_t cntb[kMaxSplits];
+  uint32_t pre[kMaxSplits + 1];
+  uint32_t hist[256];
+  uint32_t sel[4];
+  uint32_t red32[2 * kWaves];
+  uint32_t m_slot[kSurvCap];     // survivors' record slots
+  double m_val[kSurvCap];
+  uint32_t m_id[kSurvCap];
+  double t_val[SAS_MAX_TOP_K];   // ranked top-k values
+  uint32_t t_id[SAS_MAX_TOP_K];
+  double t_p[SAS_MAX_TOP_K];     // exp weights
+  double t_pre[SAS_MAX_TOP_K];   // their running sums
+  double t_q[SAS_MAX_TOP_K];     // weights / sum
+  uint32_t n, lower;
+  Red red;
+};
+
+// Exact top-k over the records whose key maps to >= lower when more than
+// kSurvCap of them survive (degenerate ties); repeated block argmax.
+__device__ __forceinline__ int merge_topk_slow(const RowRecs &rr, const uint32_t *cnt, int S, uint32_t lower,
+                                               int k, double *t_val, uint32_t *t_id, Red *red) {
+  double pv = 0.0;
+  uint32_t pid = 0;
+  int got = 0;
+  for (int r = 0; r < k; ++r) {
+    bool have = false;
+    double bv = 0.0;
+    uint32_t bi = 0;
+    for (int b = 0; b < S; ++b) {
+      for (uint32_t j = threadIdx.x; j < cnt[b]; j += kThreads) {
+        const int64_t g = (int64_t)b * kCapBlock + j;
+        const uint32_t x = rr.okey_at(g);
+        if (x == 0u || x < lower) continue;
+        const double val = rr.val_at(g);
+        const uint32_t id = rr.id_at(g);
+        if (r > 0 && !ranks_before(pv, pid, val, id)) continue;
+        if (!have || ranks_before(val, id, bv, bi)) {
+          have = true;
+          bv = val;
+          bi = id;
+        }
+      }
+    }
+    double wv;
+    uint32_t wi;
+    if (!block_best(have, bv, bi, red, wv, wi)) break;
+    if (threadIdx.x == 0) {
+      t_val[r] = wv;
+      t_id[r] = wi;
+    }
+    pv = wv;
+    pid = wi;
+    ++got;
+  }
+  return got;
+}
+
+// The merge of one row by its last block: bound, rank, sample() tail, outputs.
+__device__ void merge_row(const SampleArgs &a, int row, const sas_params &p, MergeLds &ml) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int S = a.splits;
+  const int64_t r0 = (int64_t)row * S * kCapBlock;
+  const RowRecs rr{reinterpret_cast<const uint32_t *>(a.rkey) + r0, a.rid + r0,
+                   reinterpret_cast<const uint64_t *>(a.rval) + r0};
+  const bool in_regs = S <= kMergeRegs;
+  const bool greedy = !(p.temperature > 0.0);
+  const double u_row = greedy ? 0.0 : a.uniforms[row];
+
+  // Thread t holds slot t of every block in registers: the loads are
+  // in-bounds whatever the counts, all in flight at once (issued before the
+  // counts are known), and a slot at or beyond its block's count is dropped.
+  uint32_t key[kMergeRegs];
+  if (in_regs) {
+#pragma unroll
+    for (int b = 0; b < kMergeRegs; ++b) key[b] = b < S ? ld_agent(rr.key + (int64_t)b * kCapBlock + tid) : 0u;
+  }
+
+  // ---- counts per block, offsets -----------------------------------------
+  for (int b = tid; b < S; b += kThreads) ml.cntb[b] = ld_agent(a.counts + (int64_t)row * S + b);
+  if (tid == 0) ml.n = 0u;
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t carry = 0;
+    for (int b0 = 0; b0 < S; b0 += 64) {
+      const int b = b0 + lane;
+      const uint32_t nb = b < S ? ml.cntb[b] : 0u;
+      const uint32_t inc = wave_incl_scan(nb);
+      if (b < S) ml.pre[b] = carry + inc - nb;
+      carry += __shfl(inc, 63, 64);
+    }
+    if (lane == 0) ml.pre[S] = carry;
+  }
+  __syncthreads();
+  const uint32_t total = ml.pre[S];
+  const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
+  const uint32_t need = min((uint32_t)k, total);
+  const uint32_t cap = min((uint32_t)kSurvCap, (uint32_t)k + (uint32_t)kMergeSlack);
+
+  // ---- 6. bound, survivors -----------------------------------------------
+  if (in_regs) {
+    uint32_t valid = 0u;
+#pragma unroll
+    for (int b = 0; b < kMergeRegs; ++b)
+      if (b < S && (uint32_t)tid < ml.cntb[b]) valid |= 1u << b;
+    uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int b = 0; b < kMergeRegs; ++b) {
+      key[b] = ((valid >> b) & 1u) ? okey(__uint_as_float(key[b])) : 0u;
+      if (key[b]) {
+        kmax = max(kmax, key[b]);
+        kmin = min(kmin, key[b]);
+      }
+    }
+    block_minmax(kmax, kmin, ml.red32);
+    uint32_t lower = 1u;
+    if (total > cap && kmax != kmin) {
+      const int hb = 31 - __clz(kmax ^ kmin);
+      auto for_keys = [&](auto f) {
+#pragma unroll
+        for (int b = 0; b < kMergeRegs; ++b) f(key[b]);
+      };
+      lower = radix_bound(for_keys, hb, hb == 31 ? 0u : kmax >> (hb + 1), need, cap, ml.hist, ml.sel);
+    } else if (total > cap) {
+      lower = kmax;  // every key is equal
+    }
+    uint32_t bits = 0u;
+#pragma unroll
+    for (int b = 0; b < kMergeRegs; ++b) bits |= (key[b] != 0u && key[b] >= lower ? 1u : 0u) << b;
+    uint32_t slot = wave_reserve(bits, &ml.n);
+#pragma unroll
+    for (int b = 0; b < kMergeRegs; ++b)
+      if ((bits >> b) & 1u) {
+        if (slot < (uint32_t)kSurvCap) ml.m_slot[slot] = (uint32_t)b * kCapBlock + tid;
+        ++slot;
+      }
+    ml.lower = lower;
+  } else {
+    // many blocks: the keys are read from memory on every pass
+    uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
+    for (int b = 0; b < S; ++b)
+      if ((uint32_t)tid < ml.cntb[b]) {
+        const uint32_t ok = rr.okey_at((int64_t)b * kCapBlock + tid);
+        kmax = max(kmax, ok);
+        kmin = min(kmin, ok);
+      }
+    block_minmax(kmax, kmin, ml.red32);
+    uint32_t lower = 1u;
+    if (total > cap && kmax != kmin) {
+      const int hb = 31 - __clz(kmax ^ kmin);
+      auto for_keys = [&](auto f) {
+        for (int b = 0; b < S; ++b)
+          if ((uint32_t)tid < ml.cntb[b]) f(rr.okey_at((int64_t)b * kCapBlock + tid));
+      };
+      lower = radix_bound(for_keys, hb, hb == 31 ? 0u : kmax >> (hb + 1), need, cap, ml.hist, ml.sel);
+    } else if (total > cap) {
+      lower = kmax;
+    }
+    for (int b = 0; b < S; ++b)
+      if ((uint32_t)tid < ml.cntb[b]) {
+        const uint32_t g = (uint32_t)b * kCapBlock + tid;
+        const uint32_t x = rr.okey_at(g);
+        if (x != 0u && x >= lower) {
+          const uint32_t slot = atomicAdd(&ml.n, 1u);
+          if (slot < (uint32_t)kSurvCap) ml.m_slot[slot] = g;
+        }
+      }
+    ml.lower = lower;
+  }
+  __syncthreads();
+  const uint32_t m = ml.n;
+  const uint32_t lower = ml.lower;
+  // the survivors' values and ids, one round of loads
+  if ((uint32_t)tid < min(m, (uint32_t)kSurvCap)) {
+    const uint32_t g = ml.m_slot[tid];
+    ml.m_val[tid] = rr.val_at(g);
+    ml.m_id[tid] = rr.id_at(g);
+  }
+
+  // ---- exact rank --------------------------------------------------------
+  int kk = 0;  // candidates ranked into t_val/t_id
+  uint32_t flags = 0;
+  if (m <= (uint32_t)kSurvCap) {
+    // pad to a multiple of 4 with entries that never rank before another
+    const uint32_t mp = (m + 3u) & ~3u;
+    if ((uint32_t)tid >= m && (uint32_t)tid < mp) {
+      ml.m_val[tid] = -__builtin_inf();
+      ml.m_id[tid] = 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    if ((uint32_t)tid < m) {
+      const double vc = ml.m_val[tid];
+      const uint32_t ic = ml.m_id[tid];
+      uint32_t rank = 0;
+      for (uint32_t j = 0; j < mp; j += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const double vj = ml.m_val[j + u];
+          const uint32_t ij = ml.m_id[j + u];
+          rank += (uint32_t)((vj > vc) | ((vj == vc) & (ij < ic)));
+        }
+      }
+      if (rank < (uint32_t)k) {
+        ml.t_val[rank] = vc;
+        ml.t_id[rank] = ic;
+      }
+    }
+    kk = (int)min(m, (uint32_t)k);
+  } else {
+    flags |= SAS_FLAG_SLOW_SELECT;
+    kk = merge_topk_slow(rr, ml.cntb, S, lower, k, ml.t_val, ml.t_id, &ml.red);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // ---- 7. sample() tail (tokenizer.js:161-177), double precision -----------
+  // exp and division are correctly rounded in any lane, so the weights and
+  // their normalised values are computed across lanes; the running sums
+  // follow the reference's left-to-right order in lane 0, which reads its
+  // operands from LDS eight at a time.
+  const bool draw = !greedy && kk > 0;
+  uint32_t out_id = SAS_NO_TOKEN;
+  int cut = 0;
+  if (kk == 0) {
+    flags |= SAS_FLAG_EMPTY_ROW;
+  } else if (greedy) {
+    out_id = ml.t_id[0];
+  } else {
+    const double T = p.temperature;
+    const double v0 = ml.t_val[0];
+    for (int i = lane; i < kk; i += 64) ml.t_p[i] = fd_exp((ml.t_val[i] - v0) / T);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+      double run = 0.0;
+      for (int i = 0; i < kk; i += 8) {
+        double x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = ml.t_p[min(i + u, kk - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i + u < kk) {
+            run += x[u];
+            ml.t_pre[i + u] = run;
+          }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    const double sum = ml.t_pre[kk - 1];
+    for (int i = lane; i < kk; i += 64) ml.t_q[i] = ml.t_p[i] / sum;
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+      // top-p cut: the first i with p_0/sum + ... + p_i/sum >= top_p
+      double cum = 0.0;
+      cut = kk;
+      for (int i = 0; i < kk && cut == kk; i += 8) {
+        double x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = ml.t_q[min(i + u, kk - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i + u < kk && cut == kk) {
+            cum += x[u];
+            if (fabs(cum - p.top_p) < 1e-6) flags |= SAS_FLAG_TOPP_EDGE;
+            if (cum >= p.top_p) cut = i + u + 1;
+          }
+      }
+      // r = U * (p_0 + ... + p_{cut-1}), the sum taken left to right; the
+      // first i at which r - p_0 - ... - p_i <= 0 is drawn
+      const double sub = ml.t_pre[cut - 1];
+      double r = u_row * sub;
+      int pick = cut - 1;
+      bool found = false;
+      for (int i = 0; i < cut && !found; i += 8) {
+        double x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = ml.t_p[min(i + u, cut - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i + u < cut && !found) {
+            r -= x[u];
+            if (fabs(r) <= 1e-12 * sub) flags |= SAS_FLAG_DRAW_EDGE;
+            if (r <= 0.0) {
+              pick = i + u;
+              found = true;
+            }
+          }
+      }
+      out_id = ml.t_id[pick];
+    }
+  }
+  if (lane == 0) {
+    a.out_ids[row] = out_id;
+    if (a.out_counts) {
+      a.out_counts[2 * row] = draw ? kk : 0;
+      a.out_counts[2 * row + 1] = draw ? cut : 0;
+    }
+    if (a.out_flags) a.out_flags[row] = flags;
+  }
+  const int np = draw ? kk : 0;
+  if (a.out_probs) {
+    double *op = a.out_probs + (int64_t)row * SAS_MAX_TOP_K;
+    for (int i = lane; i < SAS_MAX_TOP_K; i += 64) op[i] = i < np ? ml.t_q[i] : 0.0;
+  }
+  if (a.out_cand_ids) {
+    uint32_t *oc = a.out_cand_ids + (int64_t)row * SAS_MAX_TOP_K;
+    for (int i = lane; i < SAS_MAX_TOP_K; i += 64) oc[i] = i < np ? ml.t_id[i] : SAS_NO_TOKEN;
+  }
+}
+
+template <int F4, bool kMask, bool kHist, bool kSoftcap>
+__global__ __launch_bounds__(kThreads) void sample_kernel(const SampleArgs a) {
   using L = SplitLds<F4>;
   constexpr int kChunk = L::kChunk;
   constexpr int E = F4 * 4;
+  static_assert(E <= 32, "candidate bit masks are 32-bit");
 
-  __shared__ __align__(16) uint32_t s_cnt[L::kCountWords];
+  constexpr size_t kCntBytes = kHist ? L::kCountWords * 4 : 16;
+  constexpr size_t kRawBytes = kCntBytes > sizeof(MergeLds) ? kCntBytes : sizeof(MergeLds);
+  __shared__ __align__(16) unsigned char s_raw[kRawBytes];  // count table, then the merge's LDS
+  uint32_t *s_cnt = reinterpret_cast<uint32_t *>(s_raw);
   __shared__ uint32_t s_rec_id[kCapBlock];
   __shared__ float s_rec_key[kCapBlock];
   __shared__ uint32_t s_hist[256];
   __shared__ uint32_t s_sel[3];
   __shared__ uint32_t s_wkey[2 * kWaves];
   __shared__ uint32_t s_n;
-  __shared__ uint32_t s_base;
+  __shared__ int s_last;
   __shared__ Red s_red;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nblocks = a.rows * a.splits;
+  const int rows = a.rows, S = a.splits;
   int lb = blockIdx.x;
   // XCD-aware order: consecutive dispatches rotate over the 8 XCDs, so give
   // each XCD a contiguous run of rows; a row's splits then share one L2 for
-  // the history reads.
+  // the history and mask reads.
+  const int nblocks = rows * S;
   if ((nblocks & 7) == 0) lb = (lb & 7) * (nblocks >> 3) + (lb >> 3);
-  const int row = lb / a.splits;
-  const int split = lb - row * a.splits;
+  const int row = lb / S;
+  const int split = lb - row * S;
   const int lo = split * kChunk;
   const int vocab = a.vocab;
 
@@ -281,29 +709,26 @@ __global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
   const float *lrow = a.logits + (int64_t)row * a.logits_stride;
-  const uint32_t *mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
+  const uint32_t *mrow = kMask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
 
-  // ---- 1. loads: history first, so its atomics overlap the logits' flight --
-  int h0 = 0, h1 = 0;
-  if (a.hist_ids) {
-    h0 = a.hist_offsets[row];
-    h1 = a.hist_offsets[row + 1];
-  }
-  const bool has_hist = h1 > h0;
-  uint32_t hreg[kHistRegs];
-#pragma unroll
-  for (int j = 0; j < kHistRegs; ++j) {
-    const int i = h0 + j * kThreads + tid;
-    hreg[j] = i < h1 ? a.hist_ids[i] : 0xFFFFFFFFu;
-  }
+  uint32_t *ctl = a.ctl + (int64_t)row * kCtlStride;  // [0] arrivals, [kCtlThr] threshold key
+
+  // ---- 1. loads --------------------------------------------------------
+  // the row's threshold as published by the chunks that finished earlier
+  const uint32_t row_key0 = ld_agent(ctl + kCtlThr);
   float4 v[F4];
+  if (a.aligned && lo + kChunk <= vocab) {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(lrow + lo) + tid;
 #pragma unroll
-  for (int f = 0; f < F4; ++f) {
-    const int e = lo + 4 * (f * kThreads + tid);
-    if (kAligned && e + 3 < vocab) {
-      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(lrow + e));
+    for (int f = 0; f < F4; ++f) {
+      const f32x4 t = __builtin_nontemporal_load(src + f * kThreads);
       v[f] = make_float4(t.x, t.y, t.z, t.w);
-    } else {
+    }
+  } else {
+    // a partial chunk or an unaligned row
+#pragma unroll
+    for (int f = 0; f < F4; ++f) {
+      const int e = lo + 4 * (f * kThreads + tid);
       v[f].x = e + 0 < vocab ? lrow[e + 0] : qnan();
       v[f].y = e + 1 < vocab ? lrow[e + 1] : qnan();
       v[f].z = e + 2 < vocab ? lrow[e + 2] : qnan();
@@ -311,8 +736,8 @@ __global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
     }
   }
   // mask word of float4 f: word (lo + 4q) / 32 with q = f*256 + tid
-  uint32_t mw[F4];
-  if (mrow) {
+  uint32_t mw[kMask ? F4 : 1];
+  if (kMask) {
     const int nw = (vocab + 31) >> 5;
 #pragma unroll
     for (int f = 0; f < F4; ++f) {
@@ -320,13 +745,23 @@ __global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
       mw[f] = w < nw ? mrow[w] : 0u;
     }
   }
+  int h0 = 0, h1 = 0;
+  if (kHist) {
+    h0 = a.hist_offsets[row];
+    h1 = a.hist_offsets[row + 1];
+  }
+  const bool has_hist = kHist && h1 > h0;
   if (has_hist) {
+    uint32_t hreg[kHistRegs];
+#pragma unroll
+    for (int j = 0; j < kHistRegs; ++j) {
+      const int i = h0 + j * kThreads + tid;
+      hreg[j] = i < h1 ? a.hist_ids[i] : 0xFFFFFFFFu;
+    }
     uint4 *c4 = reinterpret_cast<uint4 *>(s_cnt);
     for (int w = tid; w < L::kCountWords / 4; w += kThreads) c4[w] = make_uint4(0u, 0u, 0u, 0u);
-  }
-  if (tid == 0) s_n = 0u;
-  __syncthreads();
-  if (has_hist) {
+    if (tid == 0) s_n = 0u;
+    __syncthreads();
     auto count = [&](uint32_t id) {
       const uint32_t off = id - (uint32_t)lo;
       if (off < (uint32_t)kChunk && id < (uint32_t)vocab) atomicAdd(&s_cnt[off >> 1], 1u << ((off & 1u) * 16u));
@@ -335,30 +770,31 @@ __global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
     for (int j = 0; j < kHistRegs; ++j) count(hreg[j]);
     for (int i = h0 + kHistRegs * kThreads + tid; i < h1; i += kThreads) count(a.hist_ids[i]);
     __syncthreads();
+  } else if (tid == 0) {
+    s_n = 0u;  // published by the threshold barrier below
   }
   const ElemCtx ec{lrow, mrow, has_hist ? s_cnt : nullptr, lo, vocab, p};
 
   // ---- 2. values (in place in v) -----------------------------------------
   uint32_t penbits = 0;
   float tmax = qnan();  // stays NaN in a lane without a valid value
-  const int nshift = 4 * (tid & 7);
 #pragma unroll
   for (int f = 0; f < F4; ++f) {
-    const int q = f * kThreads + tid;
-    if (p.softcap > 0.0f) {
+    if (kSoftcap && p.softcap > 0.0f) {
       v[f].x = softcap_f32(v[f].x, p.softcap);
       v[f].y = softcap_f32(v[f].y, p.softcap);
       v[f].z = softcap_f32(v[f].z, p.softcap);
       v[f].w = softcap_f32(v[f].w, p.softcap);
     }
-    if (mrow) {
-      const uint32_t nib = mw[f] >> nshift;
+    if (kMask) {
+      const uint32_t nib = mw[f] >> (4 * (tid & 7));
       v[f].x = (nib & 1u) ? v[f].x : qnan();
       v[f].y = (nib & 2u) ? v[f].y : qnan();
       v[f].z = (nib & 4u) ? v[f].z : qnan();
       v[f].w = (nib & 8u) ? v[f].w : qnan();
     }
     if (has_hist) {
+      const int q = f * kThreads + tid;
       const uint2 c = *reinterpret_cast<const uint2 *>(&s_cnt[2 * q]);
       if ((c.x | c.y) != 0u) {
         float x[4] = {v[f].x, v[f].y, v[f].z, v[f].w};
@@ -385,11 +821,12 @@ __global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
   // the mth largest of the wave thresholds then has >= mth*jth >= k values
   // at or above it.  If some wave cannot (too few valid lanes: a sparse
   // mask, a partial chunk), a wave that alone has k valid lanes can; with
-  // neither, every valid value passes.
+  // neither, every valid value passes.  Keys are searched to 16 bits: the
+  // bound only gets lower, the guarantee holds.
   const int jth = (k + kWaves - 1) / kWaves;
   const int mth = (k + jth - 1) / jth;
   const uint32_t lkey = okey(tmax);
-  const uint32_t tw = wave_jth_largest_key(lkey, jth);
+  const uint32_t tw = wave_jth_largest_key16(lkey, jth);
   if (lane == 0) s_wkey[wave] = tw;
   __syncthreads();
   uint32_t t4[kWaves];
@@ -410,311 +847,73 @@ __global__ __launch_bounds__(kThreads) void split_kernel(const SampleArgs a) {
     if (w == mth - 1) tkey = t4[w];
   if (tkey == 0u && k <= 64) {
     // block-uniform: the combination failed; try one wave alone
-    const uint32_t tk = wave_jth_largest_key(lkey, k);
+    const uint32_t tk = wave_jth_largest_key16(lkey, k);
     if (lane == 0) s_wkey[kWaves + wave] = tk;
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) tkey = max(tkey, s_wkey[kWaves + w]);
   }
-  const float thr = tkey ? fkey(tkey) : -__builtin_inff();
+  // publish; nothing waits for the result
+  if (tid == 0 && tkey > row_key0)
+    __hip_atomic_fetch_max(ctl + kCtlThr, tkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // keys below okey(-inf) + 1 (0 or truncated) admit every valid value
+  const uint32_t ekey = max(tkey, row_key0);
+  const float thr = ekey > 0x007FFFFFu ? fkey(ekey) : -__builtin_inff();
 
   // ---- 4. emission -----------------------------------------------------
-  emit_candidates<E>(lo, penbits, [&](int i) { return elem(i) >= thr; }, elem, &s_n, s_rec_id, s_rec_key);
+  // per-lane bit mask of passing slots, wave prefix of the counts by
+  // ballots, one LDS atomic per wave
+  uint32_t bits = 0u;
+#pragma unroll
+  for (int i = 0; i < E; ++i) bits |= (elem(i) >= thr ? 1u : 0u) << i;
+  if (__ballot(bits != 0u)) {
+    uint32_t slot = wave_reserve(bits, &s_n);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if ((bits >> i) & 1u) {
+        if (slot < (uint32_t)kCapBlock) {
+          const int f = i >> 2, j = i & 3;
+          s_rec_id[slot] = (uint32_t)(lo + 4 * (f * kThreads + tid) + j) | (((penbits >> i) & 1u) ? kPenFlag : 0u);
+          s_rec_key[slot] = elem(i);
+        }
+        ++slot;
+      }
+    }
+  }
   __syncthreads();
   uint32_t n = s_n;
-  if (n > (uint32_t)kCapBlock) {
-    // The wave thresholds were too weak (few valid lanes or heavy ties):
-    // bound the keys exactly and emit again.  The keys are recomputed from
-    // memory so the register-resident values are dead here and this rare
-    // path costs the hot one no registers.
-    auto key = [&](int i) {
-      double val;
-      uint32_t id;
-      return ec.value(i, val, id) ? okey(rd_f32(val)) : 0u;
-    };
-    const uint32_t bound = radix_bound<E, 8>(key, (uint32_t)k, (uint32_t)kCapBlock, s_hist, s_sel);
-    if (tid == 0) s_n = 0u;
-    __syncthreads();
-    // every record of this path recomputes its exact value when written
-    emit_candidates<E, 8>(
-        lo, ~0u,
-        [&](int i) {
-          const uint32_t x = key(i);
-          return x != 0u && x >= bound;
-        },
-        [&](int i) { return fkey(key(i)); }, &s_n, s_rec_id, s_rec_key);
-    __syncthreads();
-    n = s_n;
-    if (n > (uint32_t)kCapBlock) n = (uint32_t)block_topk_slow(ec, E, k, s_rec_id, s_rec_key, &s_red);
-  }
+  if (n > (uint32_t)kCapBlock) n = overflow_select<E>(ec, k, ekey, s_rec_id, s_rec_key, s_hist, s_sel, &s_n, &s_red);
 
-  // ---- records out -----------------------------------------------------
-  // Reservation only: the merge kernel reads the records after this launch
-  // has completed, so no ordering beyond the atomic itself is needed.
-  if (tid == 0) s_base = n ? atomicAdd(&a.counters[row], n) : 0u;
-  __syncthreads();
-  Rec *out = a.recs + (int64_t)row * a.rec_cap + s_base;
+  // ---- records out: the block's own slots ---------------------------------
+  const int64_t slot0 = (int64_t)row * S + split;
+  const int64_t r0 = slot0 * kCapBlock;
   for (int i = tid; i < (int)n; i += kThreads) {
     const uint32_t idf = s_rec_id[i];
     const float kk = s_rec_key[i];
-    Rec r;
-    r.val = ec.exact(idf, kk);
-    r.id = idf & ~kPenFlag;
-    r.key = kk;
-    out[i] = r;
+    st_agent(reinterpret_cast<uint32_t *>(a.rkey) + r0 + i, __float_as_uint(kk));
+    st_agent(a.rid + r0 + i, idf & ~kPenFlag);
+    st_agent(reinterpret_cast<uint64_t *>(a.rval) + r0 + i, (uint64_t)__double_as_longlong(ec.exact(idf, kk)));
   }
-}
+  if (tid == 0) st_agent(a.counts + slot0, n);
 
-// ------------------------------------------------------------------ merge --
-
-// Radix bound over record keys read from global memory on every pass; used
-// when a row has more records than the merge holds in registers.
-__device__ uint32_t radix_bound_global(const Rec *recs, uint32_t total, uint32_t need, uint32_t cap,
-                                       uint32_t *hist, uint32_t *sel) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t prefix = 0u, kr = need, taken = 0u;
-  for (int shift = 24;; shift -= 8) {
-    for (int i = tid; i < 256; i += kThreads) hist[i] = 0u;
-    __syncthreads();
-    for (uint32_t g = tid; g < total; g += kThreads) {
-      const uint32_t x = okey(recs[g].key);
-      if (x != 0u && (shift == 24 || (x >> (shift + 8)) == prefix)) atomicAdd(&hist[(x >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    if (wave == 0) {
-      uint32_t c[4], sum = 0u;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = hist[255 - 4 * lane - j];
-        sum += c[j];
-      }
-      const uint32_t incl = wave_incl_scan(sum);
-      const uint64_t hit = __ballot(incl >= kr);
-      const int first = __ffsll((unsigned long long)hit) - 1;
-      if (lane == first) {
-        uint32_t acc = incl - sum;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (acc + c[j] >= kr) {
-            sel[0] = (uint32_t)(255 - 4 * lane - j);
-            sel[1] = acc;
-            sel[2] = c[j];
-            break;
-          }
-          acc += c[j];
-        }
-      }
-    }
-    __syncthreads();
-    const uint32_t bin = sel[0], above = sel[1], cnt = sel[2];
-    __syncthreads();
-    prefix = (prefix << 8) | bin;
-    if (taken + above + cnt <= cap || shift == 0) return prefix << shift;
-    taken += above;
-    kr -= above;
-  }
-}
-
-// Exact top-k over the records whose key maps to >= lower when more than
-// kCapMerge of them survive (degenerate ties); repeated block argmax.
-__device__ __forceinline__ int merge_topk_slow(const Rec *recs, uint32_t total, uint32_t lower, int k,
-                                               double *t_val, uint32_t *t_id, Red *red) {
-  double pv = 0.0;
-  uint32_t pid = 0;
-  int got = 0;
-  for (int r = 0; r < k; ++r) {
-    bool have = false;
-    double bv = 0.0;
-    uint32_t bi = 0;
-    for (uint32_t g = threadIdx.x; g < total; g += kThreads) {
-      const Rec rc = recs[g];
-      const uint32_t x = okey(rc.key);
-      if (x == 0u || x < lower) continue;
-      if (r > 0 && !ranks_before(pv, pid, rc.val, rc.id)) continue;
-      if (!have || ranks_before(rc.val, rc.id, bv, bi)) {
-        have = true;
-        bv = rc.val;
-        bi = rc.id;
-      }
-    }
-    double wv;
-    uint32_t wi;
-    if (!block_best(have, bv, bi, red, wv, wi)) break;
-    if (threadIdx.x == 0) {
-      t_val[r] = wv;
-      t_id[r] = wi;
-    }
-    pv = wv;
-    pid = wi;
-    ++got;
-  }
-  return got;
-}
-
-__global__ __launch_bounds__(kThreads) void merge_kernel(const SampleArgs a) {
-  __shared__ uint32_t s_hist[256];
-  __shared__ uint32_t s_sel[3];
-  __shared__ double m_val[kCapMerge];
-  __shared__ uint32_t m_id[kCapMerge];
-  __shared__ double t_val[SAS_MAX_TOP_K];  // ranked top-k values
-  __shared__ double t_p[SAS_MAX_TOP_K];    // exp weights
-  __shared__ double t_q[SAS_MAX_TOP_K];    // weights / sum
-  __shared__ double t_pre[SAS_MAX_TOP_K];  // running sums
-  __shared__ uint32_t t_id[SAS_MAX_TOP_K];
-  __shared__ uint32_t s_n;
-  __shared__ Red s_red;
-
-  const int tid = threadIdx.x;
-  const int row = blockIdx.x;
-  const sas_params p = a.row_params ? a.row_params[row] : a.params;
-  const bool greedy = !(p.temperature > 0.0);
-  const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
-  const Rec *recs = a.recs + (int64_t)row * a.rec_cap;
-
-  const uint32_t total = a.counters[row];
-  if (tid == 0) s_n = 0u;
+  // ---- 5. count in; the row's last block merges ----------------------------
+  wait_vm();  // this wave's records, count and threshold are complete
   __syncthreads();
-  if (tid == 0) a.counters[row] = 0u;  // every wave has read it; ready for the next launch
-  const uint32_t need = min((uint32_t)k, total);
-  const uint32_t cap = min((uint32_t)kCapMerge, (uint32_t)k + (uint32_t)kMergeSlack);
-
-  // ---- 5/6. bound the keys, gather the survivors -------------------------
-  uint32_t lower = 1u;
-  if (total <= (uint32_t)(kThreads * kMergeRecs)) {
-    Rec r[kMergeRecs];
-#pragma unroll
-    for (int j = 0; j < kMergeRecs; ++j) {
-      const uint32_t g = (uint32_t)(tid + j * kThreads);
-      if (g < total) {
-        r[j] = recs[g];
-      } else {
-        r[j].key = qnan();
-        r[j].id = 0u;
-        r[j].val = 0.0;
-      }
-    }
-    if (total > cap)
-      lower = radix_bound<kMergeRecs>([&](int j) { return okey(r[j].key); }, need, cap, s_hist, s_sel);
-#pragma unroll
-    for (int j = 0; j < kMergeRecs; ++j) {
-      const uint32_t x = okey(r[j].key);
-      if (x != 0u && x >= lower) {
-        const uint32_t slot = atomicAdd(&s_n, 1u);
-        if (slot < (uint32_t)kCapMerge) {
-          m_val[slot] = r[j].val;
-          m_id[slot] = r[j].id;
-        }
-      }
-    }
-  } else {
-    lower = radix_bound_global(recs, total, need, cap, s_hist, s_sel);
-    for (uint32_t g = tid; g < total; g += kThreads) {
-      const Rec rc = recs[g];
-      const uint32_t x = okey(rc.key);
-      if (x != 0u && x >= lower) {
-        const uint32_t slot = atomicAdd(&s_n, 1u);
-        if (slot < (uint32_t)kCapMerge) {
-          m_val[slot] = rc.val;
-          m_id[slot] = rc.id;
-        }
-      }
-    }
-  }
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
   __syncthreads();
-  const uint32_t m = s_n;
-  int kk = 0;  // candidates ranked into t_val/t_id
-  uint32_t flags = 0;
-  if (m <= (uint32_t)kCapMerge) {
-    for (uint32_t c = tid; c < m; c += kThreads) {
-      const double vc0 = m_val[c];
-      const uint32_t ic = m_id[c];
-      uint32_t rank = 0;
-#pragma unroll 8
-      for (uint32_t j = 0; j < m; ++j) rank += ranks_before(m_val[j], m_id[j], vc0, ic) ? 1u : 0u;
-      if (rank < (uint32_t)k) {
-        t_val[rank] = vc0;
-        t_id[rank] = ic;
-      }
-    }
-    kk = (int)min(m, (uint32_t)k);
-  } else {
-    flags |= SAS_FLAG_SLOW_SELECT;
-    kk = merge_topk_slow(recs, total, lower, k, t_val, t_id, &s_red);
-  }
-  __syncthreads();
-
-  // ---- 7. sample() tail (tokenizer.js:161-177), double precision -----------
-  // exp and division are correctly rounded wherever they run; only the
-  // running sums must follow the reference's left-to-right order.
-  const double T = p.temperature;
-  const bool draw = !greedy && kk > 0;
-  if (draw) {
-    const double v0 = t_val[0];
-    for (int i = tid; i < kk; i += kThreads) t_p[i] = fd_exp((t_val[i] - v0) / T);
-  }
-  __syncthreads();
-  if (draw && tid == 0) {
-    double sum = 0.0;
-#pragma unroll 8
-    for (int i = 0; i < kk; ++i) {
-      sum += t_p[i];
-      t_pre[i] = sum;
-    }
-  }
-  __syncthreads();
-  if (draw) {
-    const double sum = t_pre[kk - 1];
-    for (int i = tid; i < kk; i += kThreads) t_q[i] = t_p[i] / sum;
-  }
-  __syncthreads();
+  if (!s_last) return;
   if (tid == 0) {
-    uint32_t out_id = SAS_NO_TOKEN;
-    int cut = 0;
-    if (kk == 0) {
-      flags |= SAS_FLAG_EMPTY_ROW;
-    } else if (greedy) {
-      out_id = t_id[0];
-    } else {
-      double cum = 0.0;
-      cut = kk;
-      for (int i = 0; i < kk; ++i) {
-        cum += t_q[i];
-        if (fabs(cum - p.top_p) < 1e-6) flags |= SAS_FLAG_TOPP_EDGE;
-        if (cum >= p.top_p) {
-          cut = i + 1;
-          break;
-        }
-      }
-      const double sub = t_pre[cut - 1];
-      double r = a.uniforms[row] * sub;
-      out_id = t_id[cut - 1];
-      for (int i = 0; i < cut; ++i) {
-        r -= t_p[i];
-        if (fabs(r) <= 1e-12 * sub) flags |= SAS_FLAG_DRAW_EDGE;
-        if (r <= 0.0) {
-          out_id = t_id[i];
-          break;
-        }
-      }
-    }
-    a.out_ids[row] = out_id;
-    if (a.out_counts) {
-      a.out_counts[2 * row] = greedy ? 0 : kk;
-      a.out_counts[2 * row + 1] = greedy ? 0 : cut;
-    }
-    if (a.out_flags) a.out_flags[row] = flags;
+    // every block of the row has counted in and published: reset for the next launch
+    ctl[0] = 0u;
+    ctl[kCtlThr] = 0u;
   }
-  if (a.out_probs || a.out_cand_ids) {
-    const int np = draw ? kk : 0;
-    for (int i = tid; i < SAS_MAX_TOP_K; i += kThreads) {
-      if (a.out_probs) a.out_probs[(int64_t)row * SAS_MAX_TOP_K + i] = i < np ? t_q[i] : 0.0;
-      if (a.out_cand_ids) a.out_cand_ids[(int64_t)row * SAS_MAX_TOP_K + i] = i < np ? t_id[i] : SAS_NO_TOKEN;
-    }
-  }
+  merge_row(a, row, p, *reinterpret_cast<MergeLds *>(s_raw));
 }
 
-// Splits per row: the largest chunk that still gives every CU several
-// blocks, bounded so that a row never has more than kMaxSplits splits.
+// Chunk size (float4 loads per thread): the largest that still gives every
+// CU several blocks; then grown while a row would have more splits than the
+// merge holds in registers.
 int choose_f4(int rows, int vocab) {
   const int f4s[3] = {8, 4, 2};
   int pick = 2;
@@ -726,31 +925,42 @@ int choose_f4(int rows, int vocab) {
       break;
     }
   }
-  while (pick < 8 && (vocab + pick * 1024 - 1) / (pick * 1024) > kMaxSplits) pick *= 2;
+  while (pick < 8 && (vocab + pick * 1024 - 1) / (pick * 1024) > kMergeRegs) pick *= 2;
   return pick;
 }
 
-int64_t sample_rec_cap(int splits) { return (int64_t)splits * kCapBlock; }
+size_t sample_rec_bytes(int rows, int splits) {
+  return (size_t)rows * splits * kCapBlock * (sizeof(float) + sizeof(uint32_t) + sizeof(double));
+}
+size_t sample_count_bytes(int rows, int splits) { return (size_t)rows * splits * sizeof(uint32_t); }
 
-size_t sample_rec_bytes(int rows, int splits) { return (size_t)rows * (size_t)sample_rec_cap(splits) * sizeof(Rec); }
-
-template <int F4>
-static hipError_t launch_split(const SampleArgs &a, bool aligned, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.rows * a.splits)), block(kThreads);
-  if (aligned) hipLaunchKernelGGL((split_kernel<F4, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((split_kernel<F4, false>), grid, block, 0, stream, a);
-  return hipGetLastError();
+template <int F4, bool kMask, bool kHist, bool kSoftcap>
+static void launch_one(const SampleArgs &a, hipStream_t stream) {
+  hipLaunchKernelGGL((sample_kernel<F4, kMask, kHist, kSoftcap>), dim3((unsigned)(a.rows * a.splits)),
+                     dim3(kThreads), 0, stream, a);
 }
 
-hipError_t launch_sample(const SampleArgs &a, int f4, bool aligned, hipStream_t stream) {
-  hipError_t e;
-  switch (f4) {
-    case 8: e = launch_split<8>(a, aligned, stream); break;
-    case 4: e = launch_split<4>(a, aligned, stream); break;
-    default: e = launch_split<2>(a, aligned, stream); break;
+template <int F4>
+static void launch_f4(const SampleArgs &a, bool softcap, hipStream_t stream) {
+  const int v = (a.mask ? 4 : 0) | (a.hist_ids ? 2 : 0) | (softcap ? 1 : 0);
+  switch (v) {
+    case 0: launch_one<F4, false, false, false>(a, stream); break;
+    case 1: launch_one<F4, false, false, true>(a, stream); break;
+    case 2: launch_one<F4, false, true, false>(a, stream); break;
+    case 3: launch_one<F4, false, true, true>(a, stream); break;
+    case 4: launch_one<F4, true, false, false>(a, stream); break;
+    case 5: launch_one<F4, true, false, true>(a, stream); break;
+    case 6: launch_one<F4, true, true, false>(a, stream); break;
+    default: launch_one<F4, true, true, true>(a, stream); break;
   }
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+}
+
+hipError_t launch_sample(const SampleArgs &a, int f4, bool softcap, hipStream_t stream) {
+  switch (f4) {
+    case 8: launch_f4<8>(a, softcap, stream); break;
+    case 4: launch_f4<4>(a, softcap, stream); break;
+    default: launch_f4<2>(a, softcap, stream); break;
+  }
   return hipGetLastError();
 }
 

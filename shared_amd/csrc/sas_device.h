@@ -20,13 +20,6 @@ constexpr int kCapMerge = 512;          // survivors ranked exactly in LDS by th
 constexpr int kMaxSplits = 512;         // SAS_MAX_VOCAB / 8192
 constexpr uint32_t kPenFlag = 0x80000000u;
 
-// Candidate record written by a split block for its row's merge.
-struct Rec {
-  double val;  // exact ranking value (double result for penalized ids)
-  uint32_t id;
-  float key;   // val rounded toward -inf to fp32 (monotone selection key)
-};
-static_assert(sizeof(Rec) == 16, "Rec layout");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -170,6 +163,19 @@ __device__ __forceinline__ uint32_t wave_jth_largest_key(uint32_t u, int j) {
   uint32_t res = 0u;
 #pragma unroll
   for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = res | (1u << b);
+    if (__popcll(__ballot(u >= cand)) >= j) res = cand;
+  }
+  return res;
+}
+
+// As wave_jth_largest_key searched to the top 16 bits only: the largest
+// key with zero low half that at least j lane keys reach.  A lower bound of
+// the exact j-th largest, at half the steps.
+__device__ __forceinline__ uint32_t wave_jth_largest_key16(uint32_t u, int j) {
+  uint32_t res = 0u;
+#pragma unroll
+  for (int b = 31; b >= 16; --b) {
     const uint32_t cand = res | (1u << b);
     if (__popcll(__ballot(u >= cand)) >= j) res = cand;
   }
