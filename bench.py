@@ -51,7 +51,27 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work of the baseline sample (0 disables it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mb", type=float, default=0.0,
+                    help="instead of the benchmark, run device-to-device copies of this many MB (the "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
+
+
+def calibrate_copy(mb: float, steps: int) -> int:
+    """Copies of a known size: under rocprofv3 --pmc, FETCH_SIZE and WRITE_SIZE
+    of this copy kernel against its true byte count give the factor that turns
+    the counters into bytes."""
+    import torch
+
+    n = int(mb * 1e6) // 16 * 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read_per_launch": src.numel() * 4,
+                      "bytes_written_per_launch": dst.numel() * 4, "launches": steps}), flush=True)
+    return 0
 
 
 def traffic_from_profiles(workload: str):
@@ -105,6 +125,8 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
               "rows shard across GPUs with no exchange, so run one process per GPU.", file=sys.stderr)
         return 2
+    if args.calibrate_copy_mb > 0:
+        return calibrate_copy(args.calibrate_copy_mb, min(args.steps, 50))
 
     import numpy as np
 
