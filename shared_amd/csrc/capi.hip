@@ -186,6 +186,57 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   return SAS_OK;
 }
 
+int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_verify: handle is NULL");
+  if (!v) return fail(s, SAS_ERR_INVALID, "sas_verify: descriptor is NULL");
+  if (v->seqs < 0) return fail(s, SAS_ERR_INVALID, "sas_verify: seqs must be >= 0");
+  if (v->vocab < 1 || v->vocab > SAS_MAX_VOCAB)
+    return fail(s, SAS_ERR_INVALID, "sas_verify: vocab must be in [1, SAS_MAX_VOCAB]");
+  if (v->draft_len < 1 || v->draft_len > SAS_MAX_DRAFT)
+    return fail(s, SAS_ERR_INVALID, "sas_verify: draft_len must be in [1, SAS_MAX_DRAFT]");
+  if (!(v->temperature > 0.0) || !std::isfinite(v->temperature))
+    return fail(s, SAS_ERR_INVALID, "sas_verify: temperature must be finite and > 0");
+  if (v->seqs == 0) return SAS_OK;
+  if (!v->target_logits || !v->draft_logits || !v->draft_ids || !v->uniforms || !v->out_tokens ||
+      !v->out_accepted)
+    return fail(s, SAS_ERR_INVALID,
+                "sas_verify: target_logits, draft_logits, draft_ids, uniforms, out_tokens and out_accepted "
+                "are required");
+  if (v->logits_stride < v->vocab) return fail(s, SAS_ERR_INVALID, "sas_verify: logits_stride < vocab");
+  if (v->mask && v->mask_stride < ((int64_t)v->vocab + 31) / 32)
+    return fail(s, SAS_ERR_INVALID, "sas_verify: mask_stride < ceil(vocab / 32)");
+  if ((int64_t)v->seqs * (v->draft_len + 1) > 65535)
+    return fail(s, SAS_ERR_INVALID, "sas_verify: seqs * (draft_len + 1) must be <= 65535");
+  if (int rc = set_device(s)) return rc;
+  if (int rc = grow(s, &s->vscratch, &s->vscratch_cap, sas::verify_scratch_bytes(v->seqs, v->draft_len, v->vocab),
+                    false))
+    return rc;
+  sas::VerifyArgs a;
+  a.target = v->target_logits;
+  a.draft = v->draft_logits;
+  a.stride = v->logits_stride;
+  a.mask = v->mask;
+  a.mask_stride = v->mask_stride;
+  a.draft_ids = v->draft_ids;
+  a.uniforms = v->uniforms;
+  a.temperature = v->temperature;
+  a.out_tokens = v->out_tokens;
+  a.out_accepted = v->out_accepted;
+  a.vocab = v->vocab;
+  a.seqs = v->seqs;
+  a.L = v->draft_len;
+  a.chunks = (v->vocab + sas::kVChunk - 1) / sas::kVChunk;
+  const size_t positions = (size_t)v->seqs * (v->draft_len + 1);
+  a.stats = reinterpret_cast<double *>(s->vscratch);
+  a.part = a.stats + positions * a.chunks * 4;
+  a.seqrec = a.part + (size_t)v->seqs * a.chunks * 2;
+  a.aligned = (reinterpret_cast<uintptr_t>(v->target_logits) & 15u) == 0 &&
+              (reinterpret_cast<uintptr_t>(v->draft_logits) & 15u) == 0 && (v->logits_stride & 3) == 0;
+  hipError_t e = sas::launch_verify(a, pick_stream(s, stream));
+  if (e != hipSuccess) return hip_fail(s, e, "sas_verify launch");
+  return SAS_OK;
+}
+
 int sas_clamp_params(const sas_params *in, sas_params *out) {
   if (!in || !out) return fail(nullptr, SAS_ERR_INVALID, "sas_clamp_params: NULL argument");
   sas_params p = *in;

@@ -55,4 +55,36 @@ hipError_t launch_sample(const SampleArgs &a, int f4, bool softcap, hipStream_t 
 size_t sample_rec_bytes(int rows, int splits);
 size_t sample_count_bytes(int rows, int splits);
 
+// ---------------------------------------------------------------- verify --
+// Positions are the rows of target_logits: position p = seq * (L + 1) + j,
+// j = 0..L; draft row seq * L + j pairs with target row p for j < L.  The
+// vocabulary is cut into chunks of kVChunk ids.
+constexpr int kVChunk = 4096;
+
+struct VerifyArgs {
+  const float *target;
+  const float *draft;
+  int64_t stride;
+  const uint32_t *mask;      // [positions][mask_stride] or null
+  int64_t mask_stride;
+  const uint32_t *draft_ids; // [seqs][L]
+  const double *uniforms;    // [seqs][L + 1][2]
+  double temperature;
+  uint32_t *out_tokens;      // [seqs][L + 1]
+  int32_t *out_accepted;     // [seqs]
+  // Scratch, each written before it is read within one call:
+  double *stats;   // [positions][chunks][4]: target max, target sum, draft max, draft sum
+  double *part;    // [seqs][chunks][2]: residual mass, target mass of the decided position
+  double *seqrec;  // [seqs][8]: decided position, its target max / sum, draft max / sum
+  int32_t vocab;
+  int32_t seqs;
+  int32_t L;
+  int32_t chunks;
+  bool aligned;    // both logits arrays start 16-byte aligned and stride % 4 == 0
+};
+
+size_t verify_scratch_bytes(int seqs, int L, int vocab);
+// The three verify launches, in stream order on `stream`.
+hipError_t launch_verify(const VerifyArgs &a, hipStream_t stream);
+
 }  // namespace sas

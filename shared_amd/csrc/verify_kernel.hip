@@ -1,12 +1,512 @@
-// verify_kernel.hip - speculative accept/resample (placeholder until the
-// rejection-sampling kernels land; fails loudly).
+// verify_kernel.hip - speculative verification by rejection sampling
+// (Leviathan et al. 2023, "Fast Inference from Transformers via Speculative
+// Decoding"; Chen et al. 2023, "Accelerating Large Language Model Decoding
+// with Speculative Sampling").
+//
+// The reference verifies drafts by an exact-match cascade
+// (lib/webgpu-llm/kernels.js:328-339, acceptSpec); this path implements the
+// distribution-preserving rule the sampling API needs at temperature > 0:
+//
+//   p_j = softmax(target row j / T), q_j = softmax(draft row j / T), both over
+//   allowed, non-NaN ids.  Position j accepts draft d_j iff
+//   d_j < vocab and p_j(d_j) > 0 and U1 * q_j(d_j) <= p_j(d_j).  The first
+//   rejected position a draws from max(0, p_a - q_a) (from p_a when that is
+//   all zero) with U2; when every draft is accepted the bonus position L
+//   draws from p_L with its U2.  A draw returns the smallest id whose
+//   running weight (ascending ids) exceeds U2 * total.
+//
+// Three launches, each reading what the previous one wrote:
+//   1. verify_stats_kernel, one block per (position, 4096-id chunk): reads
+//      the target chunk, the draft chunk and the mask words once, and writes
+//      the chunk's max and sum of exp((x - max) / T) for both rows.  This is
+//      the pass that streams the whole input.
+//   2. verify_decide_kernel, one block per (sequence, chunk): combines the
+//      chunk statistics of the sequence's positions (every block the same
+//      way, in the same order, so they agree bit for bit), decides the
+//      accepted prefix, and for the one position that draws, writes its
+//      chunk's residual mass and target mass.  Only that position's rows are
+//      read again.
+//   3. verify_draw_kernel, one block per sequence: finds the chunk in which
+//      U2 * total falls, scans that chunk's ids in ascending order, and
+//      writes the tokens.
+//
+// Weights are fdlibm exp (fd_exp) of double differences, as the host oracle
+// computes them; only the order of the sums differs from a sequential loop.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+
+#include "sas_device.h"
+#include "sas_launch.h"
 #include "shared_amd_sampler.h"
 
-extern "C" int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
-  (void)s;
-  (void)v;
-  (void)stream;
-  return SAS_ERR_INVALID;
+namespace sas {
+namespace {
+
+constexpr int kPerThread = kVChunk / kThreads;  // 16 ids per thread
+static_assert(kPerThread == 16, "a thread owns four float4 of a chunk");
+
+__device__ __forceinline__ double dneg_inf() { return -__longlong_as_double(0x7ff0000000000000ll); }
+
+__device__ __forceinline__ double wave_max_d(double x) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) x = fmax(x, __shfl_xor(x, s, 64));
+  return x;
 }
+
+// Butterfly sum: lane i adds x_i + x_(i^s) and lane i^s adds the same two
+// numbers, so every lane ends with the identical sum.
+__device__ __forceinline__ double wave_sum_d(double x) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) x += __shfl_xor(x, s, 64);
+  return x;
+}
+
+__device__ __forceinline__ double wave_incl_scan_d(double x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+    double y = __shfl_up(x, s, 64);
+    if (lane >= s) x += y;
+  }
+  return x;
+}
+
+// Strided chunk layout (passes 1 and 2): thread t owns ids
+// base + (f * 256 + t) * 4 + k, f, k in 0..3, loaded as four coalesced float4.
+__device__ __forceinline__ void load_strided(const float *row, int64_t base, int vocab, bool aligned,
+                                             float x[kPerThread]) {
+  const int tid = threadIdx.x;
+  if (aligned && base + kVChunk <= vocab) {
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(row + base);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      f32x4 v = __builtin_nontemporal_load(p + f * kThreads + tid);
+      x[f * 4 + 0] = v.x;
+      x[f * 4 + 1] = v.y;
+      x[f * 4 + 2] = v.z;
+      x[f * 4 + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t id = base + (f * kThreads + tid) * 4 + k;
+        x[f * 4 + k] = id < vocab ? row[id] : 0.0f;
+      }
+  }
+}
+
+// Bit f*4+k set: id base + (f*256+t)*4 + k is below vocab and its mask bit is set.
+template <bool kMask>
+__device__ __forceinline__ uint32_t allow_strided(const uint32_t *mrow, int64_t base, int vocab) {
+  const int tid = threadIdx.x;
+  uint32_t bits = 0;
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int64_t id0 = base + (f * kThreads + tid) * 4;
+    uint32_t nib = 0;
+    if (id0 < vocab) {
+      nib = kMask ? (mrow[id0 >> 5] >> (id0 & 31)) & 0xFu : 0xFu;
+      const int64_t left = vocab - id0;
+      if (left < 4) nib &= (1u << left) - 1u;
+    }
+    bits |= nib << (f * 4);
+  }
+  return bits;
+}
+
+struct StatsLds {
+  float m[kWaves][2];
+  double z[kWaves][2];
+};
+
+// Masked max and sum of exp((x - max) / T) of one chunk; thread 0's results
+// are the block's.
+__device__ __forceinline__ void chunk_stats(const float x[kPerThread], uint32_t ok, double T, int side,
+                                            StatsLds &l, double &m_out, double &z_out) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if ((ok >> i) & 1u) m = fmaxf(m, x[i]);
+  m = wave_max(m);
+  if (lane == 0) l.m[wave][side] = m;
+  __syncthreads();
+  float bm = l.m[0][side];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) bm = fmaxf(bm, l.m[w][side]);
+  const double M = (double)bm;
+  double z = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if ((ok >> i) & 1u) z += fd_exp(((double)x[i] - M) / T);
+  z = wave_sum_d(z);
+  if (lane == 0) l.z[wave][side] = z;
+  __syncthreads();
+  if (tid == 0) {
+    double t = l.z[0][side];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) t += l.z[w][side];
+    m_out = M;
+    z_out = t;
+  }
+}
+
+__device__ __forceinline__ uint32_t nan_free(const float x[kPerThread], uint32_t ok) {
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if (x[i] != x[i]) ok &= ~(1u << i);
+  return ok;
+}
+
+template <bool kMask>
+__global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
+  __shared__ StatsLds l;
+  const int c = blockIdx.x, pos = blockIdx.y;
+  const int P1 = a.L + 1;
+  const int s = pos / P1, j = pos - s * P1;
+  const int64_t base = (int64_t)c * kVChunk;
+  const bool has_draft = j < a.L;
+  float xt[kPerThread], xq[kPerThread];
+  load_strided(a.target + (int64_t)pos * a.stride, base, a.vocab, a.aligned, xt);
+  if (has_draft) load_strided(a.draft + ((int64_t)s * a.L + j) * a.stride, base, a.vocab, a.aligned, xq);
+  const uint32_t ok = allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr, base, a.vocab);
+  double mt = 0.0, zt = 0.0, mq = dneg_inf(), zq = 0.0;
+  chunk_stats(xt, nan_free(xt, ok), a.temperature, 0, l, mt, zt);
+  if (has_draft) chunk_stats(xq, nan_free(xq, ok), a.temperature, 1, l, mq, zq);
+  if (threadIdx.x == 0) {
+    double *o = a.stats + ((int64_t)pos * a.chunks + c) * 4;
+    o[0] = mt;
+    o[1] = zt;
+    o[2] = mq;
+    o[3] = zq;
+  }
+}
+
+struct Decided {
+  int a;         // accepted drafts; the position that draws
+  double mt, zt, mq, zq;
+};
+
+struct DecideLds {
+  double m[SAS_MAX_DRAFT + 1][2];
+  double z[SAS_MAX_DRAFT + 1][2];
+  int acc[SAS_MAX_DRAFT];
+  double red[kWaves][2];
+};
+
+// Softmax statistics of every position of sequence s from the chunk
+// statistics, then the accepted prefix.  Identical in every block.
+__device__ Decided decide(const VerifyArgs &a, int s, DecideLds &l) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int L = a.L, P1 = L + 1;
+  const double T = a.temperature;
+  for (int j = wave; j < P1; j += kWaves) {
+    const double *st = a.stats + (int64_t)(s * P1 + j) * a.chunks * 4;
+    for (int side = 0; side < (j < L ? 2 : 1); ++side) {
+      double m = dneg_inf();
+      for (int c = lane; c < a.chunks; c += 64) m = fmax(m, st[c * 4 + side * 2]);
+      m = wave_max_d(m);
+      double z = 0.0;
+      for (int c = lane; c < a.chunks; c += 64) {
+        const double zc = st[c * 4 + side * 2 + 1];
+        if (zc > 0.0) z += zc * fd_exp((st[c * 4 + side * 2] - m) / T);
+      }
+      z = wave_sum_d(z);
+      if (lane == 0) {
+        l.m[j][side] = m;
+        l.z[j][side] = z;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < L) {
+    const int j = tid;
+    const int pos = s * P1 + j;
+    const uint32_t d = a.draft_ids[(int64_t)s * L + j];
+    double pd = 0.0, qd = 0.0;
+    const bool in_vocab = d < (uint32_t)a.vocab;
+    if (in_vocab) {
+      const bool allowed = !a.mask || ((a.mask[(int64_t)pos * a.mask_stride + (d >> 5)] >> (d & 31)) & 1u);
+      const float xt = a.target[(int64_t)pos * a.stride + d];
+      const float xq = a.draft[((int64_t)s * L + j) * a.stride + d];
+      const double wt = allowed && xt == xt ? fd_exp(((double)xt - l.m[j][0]) / T) : 0.0;
+      const double wq = allowed && xq == xq ? fd_exp(((double)xq - l.m[j][1]) / T) : 0.0;
+      pd = wt / l.z[j][0];
+      qd = wq / l.z[j][1];
+    }
+    const double u1 = a.uniforms[(int64_t)pos * 2];
+    l.acc[j] = in_vocab && pd > 0.0 && u1 * qd <= pd;
+  }
+  __syncthreads();
+  Decided r;
+  r.a = L;
+  for (int j = 0; j < L; ++j)
+    if (!l.acc[j]) {
+      r.a = j;
+      break;
+    }
+  r.mt = l.m[r.a][0];
+  r.zt = l.z[r.a][0];
+  r.mq = r.a < L ? l.m[r.a][1] : 0.0;
+  r.zq = r.a < L ? l.z[r.a][1] : 0.0;
+  return r;
+}
+
+// Residual weight max(0, p - q) and target weight exp((x - M) / T) of one
+// id whose target value is allowed and not NaN.
+struct Weights {
+  double mt, zt, mq, zq, T;
+  bool resid;
+  __device__ __forceinline__ void at(float xt, float xq, bool q_ok, double &wt, double &r) const {
+    wt = fd_exp(((double)xt - mt) / T);
+    r = 0.0;
+    if (resid) {
+      const double wq = q_ok ? fd_exp(((double)xq - mq) / T) : 0.0;
+      const double d = wt / zt - wq / zq;
+      r = d > 0.0 ? d : 0.0;
+    }
+  }
+};
+
+template <bool kMask>
+__global__ __launch_bounds__(kThreads) void verify_decide_kernel(VerifyArgs a) {
+  __shared__ DecideLds l;
+  const int c = blockIdx.x, s = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const Decided d = decide(a, s, l);
+  const int P1 = a.L + 1;
+  const int pos = s * P1 + d.a;
+  const bool resid = d.a < a.L;
+  const int64_t base = (int64_t)c * kVChunk;
+  float xt[kPerThread], xq[kPerThread];
+  load_strided(a.target + (int64_t)pos * a.stride, base, a.vocab, a.aligned, xt);
+  if (resid) load_strided(a.draft + ((int64_t)s * a.L + d.a) * a.stride, base, a.vocab, a.aligned, xq);
+  const uint32_t ok = nan_free(xt, allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr,
+                                                         base, a.vocab));
+  const Weights w{d.mt, d.zt, d.mq, d.zq, a.temperature, resid};
+  double pm = 0.0, rs = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if ((ok >> i) & 1u) {
+      double wt, r;
+      w.at(xt[i], resid ? xq[i] : 0.0f, resid && xq[i] == xq[i], wt, r);
+      pm += wt;
+      rs += r;
+    }
+  pm = wave_sum_d(pm);
+  rs = wave_sum_d(rs);
+  if (lane == 0) {
+    l.red[wave][0] = rs;
+    l.red[wave][1] = pm;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double r = l.red[0][0], p = l.red[0][1];
+#pragma unroll
+    for (int v = 1; v < kWaves; ++v) {
+      r += l.red[v][0];
+      p += l.red[v][1];
+    }
+    double *o = a.part + ((int64_t)s * a.chunks + c) * 2;
+    o[0] = r;
+    o[1] = p;
+    if (c == 0) {
+      double *q = a.seqrec + (int64_t)s * 8;
+      q[0] = (double)d.a;
+      q[1] = d.mt;
+      q[2] = d.zt;
+      q[3] = d.mq;
+      q[4] = d.zq;
+    }
+  }
+}
+
+struct DrawLds {
+  double wsum[kWaves];
+  int chunk;
+  int resid;
+  int last_mode;
+  double before;
+  double target;
+  uint32_t found;
+  uint32_t last;
+};
+
+template <bool kMask>
+__global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
+  __shared__ DrawLds l;
+  const int s = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int L = a.L, P1 = L + 1;
+  const double *q = a.seqrec + (int64_t)s * 8;
+  const int acc = (int)q[0];
+  const int pos = s * P1 + acc;
+  if (tid == 0) {
+    l.found = SAS_NO_TOKEN;
+    l.last = 0;
+    l.chunk = -1;
+    l.last_mode = 1;
+  }
+  if (tid <= L && tid != acc)
+    a.out_tokens[(int64_t)s * P1 + tid] = tid < acc ? a.draft_ids[(int64_t)s * L + tid] : SAS_NO_TOKEN;
+  if (tid == 0) a.out_accepted[s] = acc;
+  const double u2 = a.uniforms[(int64_t)pos * 2 + 1];
+
+  // Which weights draw: the residual unless it is all zero, else the target.
+  if (wave == 0) {
+    const int C = a.chunks, R = (C + 63) / 64;
+    const int c0 = lane * R, c1 = min(C, c0 + R);
+    const double *part = a.part + (int64_t)s * C * 2;
+    bool resid = acc < L;
+    if (resid) {
+      double v = 0.0;
+      for (int c = c0; c < c1; ++c) v += part[c * 2];
+      v = wave_incl_scan_d(v);
+      resid = __shfl(v, 63, 64) > 0.0;
+    }
+    const int col = resid ? 0 : 1;
+    double v = 0.0;
+    for (int c = c0; c < c1; ++c) v += part[c * 2 + col];
+    const double incl = wave_incl_scan_d(v);
+    double excl = __shfl_up(incl, 1, 64);
+    if (lane == 0) excl = 0.0;
+    const double tot = __shfl(incl, 63, 64);
+    const double target = u2 * tot;
+    // first chunk whose running total passes the target
+    int hit = -1;
+    double cum = excl, hit_before = 0.0;
+    int lastc = -1;
+    double last_before = 0.0;
+    for (int c = c0; c < c1; ++c) {
+      const double wc = part[c * 2 + col];
+      if (!(wc > 0.0)) continue;
+      lastc = c;
+      last_before = cum;
+      const double nxt = cum + wc;
+      if (hit < 0 && nxt > target) {
+        hit = c;
+        hit_before = cum;
+      }
+      cum = nxt;
+    }
+    const uint64_t hits = __ballot(hit >= 0);
+    const uint64_t lasts = __ballot(lastc >= 0);
+    if (tot > 0.0) {
+      if (hits) {
+        const int src = __ffsll((long long)hits) - 1;
+        const int hc = __shfl(hit, src, 64);
+        const double hb = __shfl(hit_before, src, 64);
+        if (lane == 0) {
+          l.chunk = hc;
+          l.before = hb;
+          l.last_mode = 0;
+        }
+      } else if (lasts) {
+        const int src = 63 - __clzll((long long)lasts);
+        const int lc = __shfl(lastc, src, 64);
+        const double lb = __shfl(last_before, src, 64);
+        if (lane == 0) {
+          l.chunk = lc;
+          l.before = lb;
+          l.last_mode = 1;
+        }
+      }
+    }
+    if (lane == 0) {
+      l.target = target;
+      l.resid = resid;
+    }
+  }
+  __syncthreads();
+  const int chunk = l.chunk;
+  if (chunk < 0) {
+    if (tid == 0) a.out_tokens[(int64_t)s * P1 + acc] = SAS_NO_TOKEN;
+    return;
+  }
+  const bool resid = l.resid != 0;
+  const double target = l.target, before = l.before;
+  const bool last_mode = l.last_mode != 0;
+
+  // Contiguous layout: thread t owns ids chunk*4096 + 16t .. +15.
+  const int64_t id0 = (int64_t)chunk * kVChunk + (int64_t)tid * kPerThread;
+  const float *trow = a.target + (int64_t)pos * a.stride;
+  const float *drow = resid ? a.draft + ((int64_t)s * L + acc) * a.stride : nullptr;
+  uint32_t bits = 0;
+  if (id0 < a.vocab) {
+    bits = a.mask ? (a.mask[(int64_t)pos * a.mask_stride + (id0 >> 5)] >> (id0 & 31)) & 0xFFFFu : 0xFFFFu;
+    const int64_t left = a.vocab - id0;
+    if (left < kPerThread) bits &= (1u << left) - 1u;
+  }
+  const Weights w{q[1], q[2], q[3], q[4], a.temperature, resid};
+  double wv[kPerThread];
+  double mine = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    wv[i] = 0.0;
+    if ((bits >> i) & 1u) {
+      const float xt = trow[id0 + i];
+      if (xt != xt) continue;
+      const float xq = resid ? drow[id0 + i] : 0.0f;
+      double wt, r;
+      w.at(xt, xq, resid && xq == xq, wt, r);
+      wv[i] = resid ? r : wt;
+      mine += wv[i];
+    }
+  }
+  // exclusive prefix of the per-thread sums in thread order
+  const double incl = wave_incl_scan_d(mine);
+  if (lane == 63) l.wsum[wave] = incl;
+  __syncthreads();
+  double start = before;
+  for (int v = 0; v < wave; ++v) start += l.wsum[v];
+  double ex = __shfl_up(incl, 1, 64);
+  if (lane == 0) ex = 0.0;
+  start += ex;
+  uint32_t found = SAS_NO_TOKEN, last = 0;
+  bool any = false;
+  double cum = start;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if (wv[i] > 0.0) {
+      any = true;
+      last = (uint32_t)(id0 + i);
+      cum += wv[i];
+      if (found == SAS_NO_TOKEN && cum > target) found = (uint32_t)(id0 + i);
+    }
+  if (!last_mode && found != SAS_NO_TOKEN) atomicMin(&l.found, found);
+  if (any) atomicMax(&l.last, last + 1u);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t tok = l.found;
+    if (last_mode || tok == SAS_NO_TOKEN) tok = l.last ? l.last - 1u : SAS_NO_TOKEN;
+    a.out_tokens[(int64_t)s * P1 + acc] = tok;
+  }
+}
+
+}  // namespace
+
+size_t verify_scratch_bytes(int seqs, int L, int vocab) {
+  const size_t chunks = ((size_t)vocab + kVChunk - 1) / kVChunk;
+  const size_t positions = (size_t)seqs * (L + 1);
+  return (positions * chunks * 4 + (size_t)seqs * chunks * 2 + (size_t)seqs * 8) * sizeof(double);
+}
+
+hipError_t launch_verify(const VerifyArgs &a, hipStream_t stream) {
+  const dim3 block(kThreads);
+  const dim3 g1(a.chunks, a.seqs * (a.L + 1)), g2(a.chunks, a.seqs), g3(a.seqs);
+  if (a.mask) {
+    hipLaunchKernelGGL(verify_stats_kernel<true>, g1, block, 0, stream, a);
+    hipLaunchKernelGGL(verify_decide_kernel<true>, g2, block, 0, stream, a);
+    hipLaunchKernelGGL(verify_draw_kernel<true>, g3, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(verify_stats_kernel<false>, g1, block, 0, stream, a);
+    hipLaunchKernelGGL(verify_decide_kernel<false>, g2, block, 0, stream, a);
+    hipLaunchKernelGGL(verify_draw_kernel<false>, g3, block, 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sas

@@ -1,0 +1,214 @@
+"""GPU parity of sas_verify (rejection-sampling speculative verification)
+against the C oracle, through the C ABI.
+
+The accept test and the draws are float64 sums over the vocabulary; the GPU
+adds the same fdlibm-exp weights in another order, so a token may differ from
+the oracle's only where the oracle's own decision sits within a relative 1e-9
+of its threshold (u1 against p/q, or u2 * total against a running sum).  Such
+rows are counted and must stay rare; every other token must be identical."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import to_dev
+from shared_amd import workloads as W
+from shared_amd._capi import NO_TOKEN
+
+pytestmark = pytest.mark.gpu
+
+EDGE = 1e-9
+
+
+def run_verify(s, inp, stride_pad=0):
+    import torch
+    L, seqs, vocab = inp["drafts"], inp["seqs"], inp["vocab"]
+
+    def padded(x):
+        if not stride_pad:
+            return to_dev(x)
+        y = np.zeros((x.shape[0], x.shape[1] + stride_pad), np.float32)
+        y[:, :x.shape[1]] = x
+        return to_dev(y)
+
+    t, d = padded(inp["target"]), padded(inp["draft"])
+    m = None if inp.get("mask") is None else to_dev(inp["mask"].view(np.int32))
+    ids = to_dev(np.ascontiguousarray(inp["draft_ids"], np.uint32).view(np.int32))
+    u = to_dev(np.ascontiguousarray(inp["uniforms"], np.float64))
+    toks, acc = s.verify(t, d, ids, u, temperature=inp["temperature"], mask=m, vocab=vocab)
+    torch.cuda.synchronize()
+    return {"tokens": toks.cpu().numpy().view(np.uint32), "accepted": acc.cpu().numpy()}
+
+
+def _weights(inp, row_t, row_q, mrow):
+    """float64 weights of one position (numpy exp: only used to measure margins)."""
+    T, vocab = inp["temperature"], inp["vocab"]
+    ok = np.ones(vocab, bool) if mrow is None else \
+        np.unpackbits(mrow.view(np.uint8), bitorder="little")[:vocab].astype(bool)
+
+    def soft(x):
+        if x is None:
+            return None
+        x = x.astype(np.float64)
+        a = ok & ~np.isnan(x)
+        if not a.any():
+            return np.zeros(vocab)
+        w = np.where(a, np.exp((np.where(a, x, 0) - x[a].max()) / T), 0.0)
+        return w
+    return soft(row_t), soft(row_q)
+
+
+def edge_rows(inp, gpu, orc):
+    """Sequences whose outputs differ; each must be explained by a margin < EDGE."""
+    L, seqs = inp["drafts"], inp["seqs"]
+    m = inp.get("mask")
+    bad, edges = [], []
+    for s in range(seqs):
+        if np.array_equal(gpu["tokens"][s], orc["tokens"][s]) and gpu["accepted"][s] == orc["accepted"][s]:
+            continue
+        ga, oa = int(gpu["accepted"][s]), int(orc["accepted"][s])
+        if ga != oa:
+            j = min(ga, oa)
+            u1 = inp["uniforms"][s, j, 0]
+            r = orc["ratio"][s, j]
+            (edges if abs(u1 - r) <= EDGE * max(1.0, abs(r)) else bad).append(s)
+            continue
+        a = oa
+        pos = s * (L + 1) + a
+        wt, wq = _weights(inp, inp["target"][pos], inp["draft"][s * L + a] if a < L else None,
+                          None if m is None else m[pos])
+        w = wt
+        if a < L:
+            r = np.maximum(0.0, wt / wt.sum() - wq / wq.sum())
+            if r.sum() > 0:
+                w = r
+        cum = np.cumsum(w)
+        target = inp["uniforms"][s, a, 1] * cum[-1]
+        g, o = int(gpu["tokens"][s, a]), int(orc["tokens"][s, a])
+        lo = min(g, o)
+        (edges if lo < len(cum) and abs(cum[lo] - target) <= EDGE * cum[-1] else bad).append(s)
+    return bad, edges
+
+
+def check(s, inp, label, stride_pad=0, max_edges=1):
+    g = run_verify(s, inp, stride_pad)
+    o = O.verify(inp)
+    bad, edges = edge_rows(inp, g, o)
+    print(f"[gpu] verify {label}: seqs={inp['seqs']} L={inp['drafts']} vocab={inp['vocab']} "
+          f"accepted={g['accepted'].tolist()} edge_rows={len(edges)}", flush=True)
+    assert not bad, f"{label}: sequences {bad} differ from the oracle away from any threshold"
+    assert len(edges) <= max_edges, f"{label}: {len(edges)} threshold rows"
+    return g, o
+
+
+def test_c5_full_size(sampler):
+    inp = W.c5()
+    g, o = check(sampler, inp, "C5")
+    # 0.8-correlated drafts are accepted often but not always
+    assert 0 < g["accepted"].sum() < inp["seqs"] * inp["drafts"]
+
+
+def _random_inp(seed, seqs, L, vocab, density=None, rho=0.8, T=1.0):
+    rng = np.random.default_rng(seed)
+    t = (rng.standard_normal((seqs * (L + 1), vocab)) * 3).astype(np.float32)
+    tv = t.reshape(seqs, L + 1, vocab)
+    d = (rho * tv[:, :L] + np.sqrt(1 - rho * rho) * 3 * rng.standard_normal((seqs, L, vocab)))
+    d = np.ascontiguousarray(d.reshape(seqs * L, vocab), np.float32)
+    mask = None if density is None else W.random_mask(rng, seqs * (L + 1), vocab, density, density)
+    ids = rng.integers(0, vocab, (seqs, L)).astype(np.uint32)
+    # half of the drafts are the draft row's argmax, so some are accepted
+    for s in range(seqs):
+        for j in range(L):
+            if rng.random() < 0.5:
+                ids[s, j] = int(np.argmax(d[s * L + j]))
+    u = rng.random((seqs, L + 1, 2))
+    return {"target": t, "draft": d, "mask": mask, "draft_ids": ids, "uniforms": u, "temperature": T,
+            "vocab": vocab, "seqs": seqs, "drafts": L}
+
+
+@pytest.mark.parametrize("seed,seqs,L,vocab,density,T", [
+    (1, 8, 1, 1000, None, 1.0),
+    (2, 5, 3, 4096, 0.3, 0.7),
+    (3, 7, 4, 4097, None, 1.5),
+    (4, 3, 16, 33333, 0.05, 1.0),
+    (5, 16, 2, 151936, 0.02, 0.6),
+    (6, 4, 5, 262144, None, 1.0),
+    (7, 2, 2, 7, 0.5, 1.0),
+])
+def test_random_cases(sampler, seed, seqs, L, vocab, density, T):
+    check(sampler, _random_inp(seed, seqs, L, vocab, density, T=T), f"random{seed}")
+
+
+def test_unaligned_row_stride(sampler):
+    check(sampler, _random_inp(11, 6, 3, 10006, 0.1), "stride 10007", stride_pad=1)
+
+
+def test_draft_equal_to_target_accepts_every_draft(sampler):
+    inp = _random_inp(12, 8, 4, 5000, 0.2)
+    t = inp["target"].reshape(8, 5, 5000)
+    inp["draft"] = np.ascontiguousarray(t[:, :4].reshape(32, 5000))
+    rng = np.random.default_rng(0)
+    for s in range(8):
+        for j in range(4):       # any allowed id: p(d) = q(d) > 0
+            bits = np.unpackbits(inp["mask"][s * 5 + j].view(np.uint8), bitorder="little")[:5000]
+            inp["draft_ids"][s, j] = rng.choice(np.flatnonzero(bits))
+    g, _ = check(sampler, inp, "q=p")
+    assert (g["accepted"] == 4).all()
+
+
+def test_out_of_vocab_drafts_are_rejected(sampler):
+    inp = _random_inp(13, 4, 3, 2048)
+    inp["draft_ids"][:, 0] = 2048 + np.arange(4)
+    g, _ = check(sampler, inp, "oov")
+    assert (g["accepted"] == 0).all()
+    assert (g["tokens"][:, 0] < 2048).all()
+    assert (g["tokens"][:, 1:] == NO_TOKEN).all()
+
+
+def test_masked_out_rows_and_nans(sampler):
+    inp = _random_inp(14, 4, 2, 3000, 0.2)
+    inp["mask"][0] = 0                         # seq 0, position 0: nothing allowed
+    inp["target"][3 * 1 + 1, ::7] = np.nan     # seq 1, position 1: NaNs in the target
+    inp["draft"][2 * 2 + 0, ::5] = np.nan      # seq 2, position 0: NaNs in the draft
+    g, o = check(sampler, inp, "masked+nan")
+    assert g["tokens"][0, 0] == NO_TOKEN and g["accepted"][0] == 0
+    for s in range(4):
+        a = g["accepted"][s]
+        for j in range(a + 1):
+            tok = g["tokens"][s, j]
+            if tok == NO_TOKEN:
+                continue
+            w = inp["mask"][s * 3 + j, tok >> 5]
+            assert (w >> (tok & 31)) & 1, (s, j, tok)
+
+
+def test_tokens_respect_the_mask_at_c5(sampler):
+    inp = W.c5(seqs=8)
+    g = run_verify(sampler, inp)
+    L = inp["drafts"]
+    for s in range(8):
+        for j in range(int(g["accepted"][s]) + 1):
+            tok = int(g["tokens"][s, j])
+            assert tok != NO_TOKEN
+            assert (inp["mask"][s * (L + 1) + j, tok >> 5] >> (tok & 31)) & 1
+
+
+def test_back_to_back_calls(sampler):
+    a, b = _random_inp(15, 6, 4, 20000, 0.1), _random_inp(16, 3, 2, 5000)
+    g1 = run_verify(sampler, a)
+    g2 = run_verify(sampler, b)
+    g3 = run_verify(sampler, a)
+    assert np.array_equal(g1["tokens"], g3["tokens"]) and np.array_equal(g1["accepted"], g3["accepted"])
+    check(sampler, b, "second shape")
+
+
+def test_argument_errors(sampler):
+    import torch
+    from shared_amd._capi import SasError
+    inp = _random_inp(17, 2, 2, 100)
+    t, d = to_dev(inp["target"]), to_dev(inp["draft"])
+    ids = to_dev(inp["draft_ids"].view(np.int32))
+    u = to_dev(inp["uniforms"])
+    with pytest.raises(SasError, match="temperature"):
+        sampler.verify(t, d, ids, u, temperature=0.0)
+    with pytest.raises(SasError, match="draft_len"):
+        sampler.verify(t, d, torch.zeros((2, 17), dtype=torch.int32, device="cuda"), u)
