@@ -103,7 +103,8 @@ typedef struct sas_rows {
   int32_t rows;                /* >= 0 */
   const uint32_t *mask;        /* device [rows][mask_stride] or NULL (all allowed);
                                   bit (id & 31) of word id >> 5 set = id allowed */
-  int64_t mask_stride;         /* words between rows, >= ceil(vocab / 32) */
+  int64_t mask_stride;         /* words between rows, >= ceil(vocab / 32); 0 = every
+                                  row uses the same words (one grammar state) */
   const uint32_t *hist_ids;    /* device, all rows' histories back to back, or NULL */
   const int32_t *hist_offsets; /* device [rows + 1]: row r owns
                                   hist_ids[hist_offsets[r] .. hist_offsets[r+1]) */
@@ -141,7 +142,7 @@ typedef struct sas_verify_rows {
   const uint32_t *mask;        /* device [seqs * (draft_len + 1)][mask_stride] or NULL;
                                   row j of a sequence applies to target row j and
                                   draft row j */
-  int64_t mask_stride;
+  int64_t mask_stride;         /* as in sas_rows (0 = one mask for every position) */
   const double *uniforms;      /* device [seqs][draft_len + 1][2] = {U1, U2} */
   double temperature;          /* > 0 */
   uint32_t *out_tokens;        /* device [seqs][draft_len + 1]: accepted drafts then

@@ -142,8 +142,8 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   if (r->rows == 0) return SAS_OK;
   if (!r->logits || !r->out_ids) return fail(s, SAS_ERR_INVALID, "sas_sample: logits and out_ids are required");
   if (r->logits_stride < r->vocab) return fail(s, SAS_ERR_INVALID, "sas_sample: logits_stride < vocab");
-  if (r->mask && r->mask_stride < ((int64_t)r->vocab + 31) / 32)
-    return fail(s, SAS_ERR_INVALID, "sas_sample: mask_stride < ceil(vocab / 32)");
+  if (r->mask && r->mask_stride != 0 && r->mask_stride < ((int64_t)r->vocab + 31) / 32)
+    return fail(s, SAS_ERR_INVALID, "sas_sample: mask_stride must be 0 or >= ceil(vocab / 32)");
   if (r->hist_ids && !r->hist_offsets)
     return fail(s, SAS_ERR_INVALID, "sas_sample: hist_ids requires hist_offsets");
   const bool all_greedy = !r->row_params && !(r->params.temperature > 0.0);
@@ -203,8 +203,8 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
                 "sas_verify: target_logits, draft_logits, draft_ids, uniforms, out_tokens and out_accepted "
                 "are required");
   if (v->logits_stride < v->vocab) return fail(s, SAS_ERR_INVALID, "sas_verify: logits_stride < vocab");
-  if (v->mask && v->mask_stride < ((int64_t)v->vocab + 31) / 32)
-    return fail(s, SAS_ERR_INVALID, "sas_verify: mask_stride < ceil(vocab / 32)");
+  if (v->mask && v->mask_stride != 0 && v->mask_stride < ((int64_t)v->vocab + 31) / 32)
+    return fail(s, SAS_ERR_INVALID, "sas_verify: mask_stride must be 0 or >= ceil(vocab / 32)");
   if ((int64_t)v->seqs * (v->draft_len + 1) > 65535)
     return fail(s, SAS_ERR_INVALID, "sas_verify: seqs * (draft_len + 1) must be <= 65535");
   if (int rc = set_device(s)) return rc;

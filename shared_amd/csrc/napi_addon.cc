@@ -1,0 +1,540 @@
+// napi_addon.cc - Node-API binding of libshared_amd_sampler.so (sas_napi.node).
+//
+// A thin, synchronous-by-default mirror of the C ABI for a Node host: device
+// pointers cross as BigInt, descriptors as plain objects whose keys are the
+// C fields in camelCase.  Every call runs on the handle's own HIP stream
+// (sas_stream).  sampleAsync / verifyAsync run the launch and the stream
+// synchronisation on a libuv worker and resolve a Promise, so the JS thread
+// is free while the GPU works (the reference awaits mapAsync the same way,
+// lib/webgpu-llm/model.js:724).  Errors throw a JS Error carrying
+// sas_last_error().  Host code only: no HIP header is needed here.
+#define NAPI_VERSION 8
+#include <node_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "shared_amd_sampler.h"
+
+namespace {
+
+#define NAPI_OK(call)                                    \
+  do {                                                   \
+    if ((call) != napi_ok) return throw_napi(env, #call); \
+  } while (0)
+
+napi_value throw_napi(napi_env env, const char *what) {
+  const napi_extended_error_info *info = nullptr;
+  napi_get_last_error_info(env, &info);
+  bool pending = false;
+  napi_is_exception_pending(env, &pending);
+  if (!pending) {
+    std::string msg = std::string("sas_napi: ") + what;
+    if (info && info->error_message) msg += std::string(": ") + info->error_message;
+    napi_throw_error(env, nullptr, msg.c_str());
+  }
+  return nullptr;
+}
+
+napi_value throw_sas(napi_env env, const sas_sampler *s, int rc) {
+  const char *m = sas_last_error(s);
+  std::string msg = (m && *m) ? m : "shared_amd_sampler call failed";
+  napi_value err, code, text;
+  napi_create_string_utf8(env, msg.c_str(), NAPI_AUTO_LENGTH, &text);
+  napi_create_error(env, nullptr, text, &err);
+  napi_create_int32(env, rc, &code);
+  napi_set_named_property(env, err, "code", code);
+  napi_throw(env, err);
+  return nullptr;
+}
+
+napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+// ---------------------------------------------------------------- values --
+
+bool has(napi_env env, napi_value obj, const char *key, napi_value *out) {
+  bool present = false;
+  if (napi_has_named_property(env, obj, key, &present) != napi_ok || !present) return false;
+  if (napi_get_named_property(env, obj, key, out) != napi_ok) return false;
+  napi_valuetype t;
+  napi_typeof(env, *out, &t);
+  return t != napi_undefined && t != napi_null;
+}
+
+bool get_f64(napi_env env, napi_value obj, const char *key, double *v) {
+  napi_value x;
+  if (!has(env, obj, key, &x)) return true;
+  return napi_get_value_double(env, x, v) == napi_ok;
+}
+
+bool get_i64(napi_env env, napi_value obj, const char *key, int64_t *v) {
+  napi_value x;
+  if (!has(env, obj, key, &x)) return true;
+  napi_valuetype t;
+  napi_typeof(env, x, &t);
+  if (t == napi_bigint) {
+    bool lossless;
+    return napi_get_value_bigint_int64(env, x, v, &lossless) == napi_ok;
+  }
+  double d;
+  if (napi_get_value_double(env, x, &d) != napi_ok || !std::isfinite(d) || d != std::floor(d)) return false;
+  *v = (int64_t)d;
+  return true;
+}
+
+// A device address: BigInt, or null / undefined for "none".
+bool get_ptr(napi_env env, napi_value obj, const char *key, void **p) {
+  napi_value x;
+  *p = nullptr;
+  if (!has(env, obj, key, &x)) return true;
+  uint64_t u;
+  bool lossless;
+  if (napi_get_value_bigint_uint64(env, x, &u, &lossless) != napi_ok || !lossless) return false;
+  *p = reinterpret_cast<void *>((uintptr_t)u);
+  return true;
+}
+
+napi_value make_ptr(napi_env env, const void *p) {
+  napi_value v;
+  napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)p, &v);
+  return v;
+}
+
+sas_sampler *get_handle(napi_env env, napi_value v) {
+  void *p = nullptr;
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) return nullptr;
+  napi_get_value_external(env, v, &p);
+  return reinterpret_cast<sas_sampler *>(p);
+}
+
+bool read_params(napi_env env, napi_value obj, sas_params *p) {
+  std::memset(p, 0, sizeof *p);
+  p->top_p = 1.0;
+  p->repetition_penalty = 1.0;
+  p->top_k = 1;
+  double softcap = 0.0;
+  int64_t top_k = 1;
+  bool ok = get_f64(env, obj, "temperature", &p->temperature) && get_f64(env, obj, "topP", &p->top_p) &&
+            get_f64(env, obj, "repetitionPenalty", &p->repetition_penalty) &&
+            get_f64(env, obj, "presencePenalty", &p->presence_penalty) &&
+            get_f64(env, obj, "frequencyPenalty", &p->frequency_penalty) && get_f64(env, obj, "softcap", &softcap) &&
+            get_i64(env, obj, "topK", &top_k);
+  p->softcap = (float)softcap;
+  p->top_k = top_k > INT32_MAX ? INT32_MAX : (top_k < INT32_MIN ? INT32_MIN : (int32_t)top_k);
+  return ok;
+}
+
+napi_value params_object(napi_env env, const sas_params &p) {
+  napi_value o, v;
+  napi_create_object(env, &o);
+  napi_create_double(env, p.temperature, &v);
+  napi_set_named_property(env, o, "temperature", v);
+  napi_create_double(env, p.top_p, &v);
+  napi_set_named_property(env, o, "topP", v);
+  napi_create_int32(env, p.top_k, &v);
+  napi_set_named_property(env, o, "topK", v);
+  napi_create_double(env, p.repetition_penalty, &v);
+  napi_set_named_property(env, o, "repetitionPenalty", v);
+  napi_create_double(env, p.presence_penalty, &v);
+  napi_set_named_property(env, o, "presencePenalty", v);
+  napi_create_double(env, p.frequency_penalty, &v);
+  napi_set_named_property(env, o, "frequencyPenalty", v);
+  napi_create_double(env, (double)p.softcap, &v);
+  napi_set_named_property(env, o, "softcap", v);
+  return o;
+}
+
+bool read_rows(napi_env env, napi_value d, sas_rows *r) {
+  std::memset(r, 0, sizeof *r);
+  int64_t vocab = 0, rows = 0;
+  napi_value pv;
+  bool ok = get_ptr(env, d, "logits", (void **)&r->logits) && get_i64(env, d, "logitsStride", &r->logits_stride) &&
+            get_i64(env, d, "vocab", &vocab) && get_i64(env, d, "rows", &rows) &&
+            get_ptr(env, d, "mask", (void **)&r->mask) && get_i64(env, d, "maskStride", &r->mask_stride) &&
+            get_ptr(env, d, "histIds", (void **)&r->hist_ids) &&
+            get_ptr(env, d, "histOffsets", (void **)&r->hist_offsets) &&
+            get_ptr(env, d, "uniforms", (void **)&r->uniforms) &&
+            get_ptr(env, d, "rowParams", (void **)&r->row_params) && get_ptr(env, d, "outIds", (void **)&r->out_ids) &&
+            get_ptr(env, d, "outProbs", (void **)&r->out_probs) &&
+            get_ptr(env, d, "outCandIds", (void **)&r->out_cand_ids) &&
+            get_ptr(env, d, "outCounts", (void **)&r->out_counts) &&
+            get_ptr(env, d, "outFlags", (void **)&r->out_flags);
+  if (!ok || vocab < INT32_MIN || vocab > INT32_MAX || rows < INT32_MIN || rows > INT32_MAX) return false;
+  r->vocab = (int32_t)vocab;
+  r->rows = (int32_t)rows;
+  if (has(env, d, "params", &pv) && !read_params(env, pv, &r->params)) return false;
+  return true;
+}
+
+bool read_verify(napi_env env, napi_value d, sas_verify_rows *v) {
+  std::memset(v, 0, sizeof *v);
+  int64_t vocab = 0, seqs = 0, L = 0;
+  bool ok = get_ptr(env, d, "targetLogits", (void **)&v->target_logits) &&
+            get_ptr(env, d, "draftLogits", (void **)&v->draft_logits) &&
+            get_i64(env, d, "logitsStride", &v->logits_stride) && get_i64(env, d, "vocab", &vocab) &&
+            get_i64(env, d, "seqs", &seqs) && get_i64(env, d, "draftLen", &L) &&
+            get_ptr(env, d, "draftIds", (void **)&v->draft_ids) && get_ptr(env, d, "mask", (void **)&v->mask) &&
+            get_i64(env, d, "maskStride", &v->mask_stride) && get_ptr(env, d, "uniforms", (void **)&v->uniforms) &&
+            get_f64(env, d, "temperature", &v->temperature) &&
+            get_ptr(env, d, "outTokens", (void **)&v->out_tokens) &&
+            get_ptr(env, d, "outAccepted", (void **)&v->out_accepted);
+  if (!ok || vocab < INT32_MIN || vocab > INT32_MAX || seqs < INT32_MIN || seqs > INT32_MAX || L < INT32_MIN ||
+      L > INT32_MAX)
+    return false;
+  v->vocab = (int32_t)vocab;
+  v->seqs = (int32_t)seqs;
+  v->draft_len = (int32_t)L;
+  return true;
+}
+
+bool args(napi_env env, napi_callback_info info, size_t want, napi_value *argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr) != napi_ok) return false;
+  for (size_t i = argc; i < want; ++i) napi_get_undefined(env, &argv[i]);
+  return true;
+}
+
+// ----------------------------------------------------------- functions --
+
+napi_value Version(napi_env env, napi_callback_info) {
+  napi_value v;
+  napi_create_string_utf8(env, sas_version(), NAPI_AUTO_LENGTH, &v);
+  return v;
+}
+
+napi_value Create(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args(env, info, 1, argv)) return throw_napi(env, "arguments");
+  int32_t device = 0;
+  napi_valuetype t;
+  napi_typeof(env, argv[0], &t);
+  if (t == napi_number) napi_get_value_int32(env, argv[0], &device);
+  sas_sampler *s = nullptr;
+  int rc = sas_create(device, &s);
+  if (rc != SAS_OK) return throw_sas(env, nullptr, rc);
+  napi_value ext;
+  NAPI_OK(napi_create_external(env, s, nullptr, nullptr, &ext));
+  return ext;
+}
+
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args(env, info, 1, argv)) return throw_napi(env, "arguments");
+  sas_destroy(get_handle(env, argv[0]));
+  return undefined(env);
+}
+
+#define HANDLE_OR_THROW(v, s)                                        \
+  sas_sampler *s = get_handle(env, v);                               \
+  if (!s) {                                                          \
+    napi_throw_type_error(env, nullptr, "sas_napi: expected a sampler handle"); \
+    return nullptr;                                                  \
+  }
+
+napi_value Reserve(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  int32_t rows = 0, vocab = 0;
+  NAPI_OK(napi_get_value_int32(env, argv[1], &rows));
+  NAPI_OK(napi_get_value_int32(env, argv[2], &vocab));
+  int rc = sas_reserve(s, rows, vocab);
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
+napi_value Alloc(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  double bytes = 0;
+  NAPI_OK(napi_get_value_double(env, argv[1], &bytes));
+  if (!(bytes >= 0) || bytes > 9.0e15) {
+    napi_throw_range_error(env, nullptr, "sas_napi: alloc size out of range");
+    return nullptr;
+  }
+  void *p = nullptr;
+  int rc = sas_alloc(s, (size_t)bytes, &p);
+  return rc == SAS_OK ? make_ptr(env, p) : throw_sas(env, s, rc);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  uint64_t u = 0;
+  bool lossless;
+  NAPI_OK(napi_get_value_bigint_uint64(env, argv[1], &u, &lossless));
+  int rc = sas_free(s, reinterpret_cast<void *>((uintptr_t)u));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
+// copy(handle, devicePtr: BigInt, typedArray, direction 0 = to device, 1 = to host)
+napi_value Copy(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!args(env, info, 4, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  uint64_t u = 0;
+  bool lossless;
+  NAPI_OK(napi_get_value_bigint_uint64(env, argv[1], &u, &lossless));
+  bool is_ta = false;
+  NAPI_OK(napi_is_typedarray(env, argv[2], &is_ta));
+  if (!is_ta) {
+    napi_throw_type_error(env, nullptr, "sas_napi: copy needs a TypedArray");
+    return nullptr;
+  }
+  napi_typedarray_type type;
+  size_t length = 0, offset = 0;
+  void *data = nullptr;
+  napi_value ab;
+  NAPI_OK(napi_get_typedarray_info(env, argv[2], &type, &length, &data, &ab, &offset));
+  size_t elem = 1;
+  switch (type) {
+    case napi_int16_array:
+    case napi_uint16_array: elem = 2; break;
+    case napi_int32_array:
+    case napi_uint32_array:
+    case napi_float32_array: elem = 4; break;
+    case napi_float64_array:
+    case napi_bigint64_array:
+    case napi_biguint64_array: elem = 8; break;
+    default: elem = 1;
+  }
+  int32_t dir = 0;
+  NAPI_OK(napi_get_value_int32(env, argv[3], &dir));
+  void *dev = reinterpret_cast<void *>((uintptr_t)u);
+  int rc = dir == 0 ? sas_memcpy(s, dev, data, length * elem, 0, sas_stream(s))
+                    : sas_memcpy(s, data, dev, length * elem, 1, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
+napi_value Synchronize(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args(env, info, 1, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  int rc = sas_synchronize(s, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
+napi_value Sample(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_rows r;
+  if (!read_rows(env, argv[1], &r)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad sample descriptor");
+    return nullptr;
+  }
+  int rc = sas_sample(s, &r, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
+napi_value Verify(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_verify_rows v;
+  if (!read_verify(env, argv[1], &v)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad verify descriptor");
+    return nullptr;
+  }
+  int rc = sas_verify(s, &v, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
+// --------------------------------------------------------------- async --
+
+struct AsyncCall {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  sas_sampler *s = nullptr;
+  bool verify = false;
+  sas_rows rows;
+  sas_verify_rows vrows;
+  int rc = SAS_OK;
+  std::string err;
+};
+
+void async_execute(napi_env, void *data) {
+  AsyncCall *c = static_cast<AsyncCall *>(data);
+  c->rc = c->verify ? sas_verify(c->s, &c->vrows, sas_stream(c->s)) : sas_sample(c->s, &c->rows, sas_stream(c->s));
+  if (c->rc == SAS_OK) c->rc = sas_synchronize(c->s, sas_stream(c->s));
+  if (c->rc != SAS_OK) c->err = sas_last_error(c->s);
+}
+
+void async_complete(napi_env env, napi_status, void *data) {
+  AsyncCall *c = static_cast<AsyncCall *>(data);
+  if (c->rc == SAS_OK) {
+    napi_resolve_deferred(env, c->deferred, undefined(env));
+  } else {
+    napi_value err, text, code;
+    napi_create_string_utf8(env, c->err.c_str(), NAPI_AUTO_LENGTH, &text);
+    napi_create_error(env, nullptr, text, &err);
+    napi_create_int32(env, c->rc, &code);
+    napi_set_named_property(env, err, "code", code);
+    napi_reject_deferred(env, c->deferred, err);
+  }
+  napi_delete_async_work(env, c->work);
+  delete c;
+}
+
+napi_value start_async(napi_env env, AsyncCall *c, const char *name) {
+  napi_value promise, rname;
+  if (napi_create_promise(env, &c->deferred, &promise) != napi_ok) {
+    delete c;
+    return throw_napi(env, "napi_create_promise");
+  }
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &rname);
+  if (napi_create_async_work(env, nullptr, rname, async_execute, async_complete, c, &c->work) != napi_ok ||
+      napi_queue_async_work(env, c->work) != napi_ok) {
+    delete c;
+    return throw_napi(env, "napi_queue_async_work");
+  }
+  return promise;
+}
+
+napi_value SampleAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  AsyncCall *c = new AsyncCall();
+  c->s = s;
+  if (!read_rows(env, argv[1], &c->rows)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad sample descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, "sas_sample");
+}
+
+napi_value VerifyAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  AsyncCall *c = new AsyncCall();
+  c->s = s;
+  c->verify = true;
+  if (!read_verify(env, argv[1], &c->vrows)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad verify descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, "sas_verify");
+}
+
+// --------------------------------------------------------- host helpers --
+
+napi_value ClampParams(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args(env, info, 1, argv)) return throw_napi(env, "arguments");
+  sas_params in, out;
+  if (!read_params(env, argv[0], &in)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad params object");
+    return nullptr;
+  }
+  int rc = sas_clamp_params(&in, &out);
+  if (rc != SAS_OK) return throw_sas(env, nullptr, rc);
+  return params_object(env, out);
+}
+
+// maskFromIds(kind, Uint32Array ids, vocab) -> {words: Uint32Array, allowed: number}
+napi_value MaskFromIds(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  int32_t kind = 0, vocab = 0;
+  NAPI_OK(napi_get_value_int32(env, argv[0], &kind));
+  NAPI_OK(napi_get_value_int32(env, argv[2], &vocab));
+  const uint32_t *ids = nullptr;
+  size_t count = 0;
+  napi_valuetype t;
+  napi_typeof(env, argv[1], &t);
+  if (t != napi_undefined && t != napi_null) {
+    bool is_ta = false;
+    napi_is_typedarray(env, argv[1], &is_ta);
+    napi_typedarray_type type = napi_int8_array;
+    void *data = nullptr;
+    napi_value ab;
+    size_t off;
+    if (is_ta) napi_get_typedarray_info(env, argv[1], &type, &count, &data, &ab, &off);
+    if (!is_ta || type != napi_uint32_array) {
+      napi_throw_type_error(env, nullptr, "sas_napi: ids must be a Uint32Array");
+      return nullptr;
+    }
+    ids = static_cast<const uint32_t *>(data);
+  }
+  if (vocab < 1 || vocab > SAS_MAX_VOCAB) {
+    napi_throw_range_error(env, nullptr, "sas_napi: vocab must be in [1, SAS_MAX_VOCAB]");
+    return nullptr;
+  }
+  const size_t nwords = ((size_t)vocab + 31) / 32;
+  napi_value ab, words, result, allowed_v;
+  void *wdata = nullptr;
+  NAPI_OK(napi_create_arraybuffer(env, nwords * 4, &wdata, &ab));
+  NAPI_OK(napi_create_typedarray(env, napi_uint32_array, nwords, ab, 0, &words));
+  int64_t allowed = sas_mask_from_ids(kind, ids, count, vocab, static_cast<uint32_t *>(wdata), (int64_t)nwords);
+  if (allowed < 0) return throw_sas(env, nullptr, (int)-allowed);
+  napi_create_object(env, &result);
+  napi_set_named_property(env, result, "words", words);
+  napi_create_double(env, (double)allowed, &allowed_v);
+  napi_set_named_property(env, result, "allowed", allowed_v);
+  return result;
+}
+
+napi_value PcgUniform(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  uint32_t seed = 0, it = 0, row = 0;
+  NAPI_OK(napi_get_value_uint32(env, argv[0], &seed));
+  NAPI_OK(napi_get_value_uint32(env, argv[1], &it));
+  NAPI_OK(napi_get_value_uint32(env, argv[2], &row));
+  napi_value v;
+  napi_create_double(env, sas_pcg_uniform(seed, it, row), &v);
+  return v;
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  const napi_property_descriptor fns[] = {
+      {"version", nullptr, Version, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"create", nullptr, Create, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"destroy", nullptr, Destroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"reserve", nullptr, Reserve, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"alloc", nullptr, Alloc, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"free", nullptr, Free, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"copy", nullptr, Copy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"synchronize", nullptr, Synchronize, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sampleAsync", nullptr, SampleAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"verify", nullptr, Verify, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"verifyAsync", nullptr, VerifyAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"clampParams", nullptr, ClampParams, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"maskFromIds", nullptr, MaskFromIds, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"pcgUniform", nullptr, PcgUniform, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+  };
+  napi_define_properties(env, exports, sizeof fns / sizeof fns[0], fns);
+  napi_value c;
+  const struct {
+    const char *name;
+    double value;
+  } consts[] = {{"MAX_TOP_K", SAS_MAX_TOP_K},       {"MAX_VOCAB", SAS_MAX_VOCAB},
+                {"MAX_HISTORY", SAS_MAX_HISTORY},   {"MAX_DRAFT", SAS_MAX_DRAFT},
+                {"NO_TOKEN", (double)SAS_NO_TOKEN}, {"MASK_ALL", SAS_MASK_ALL},
+                {"MASK_ALLOW", SAS_MASK_ALLOW},     {"MASK_DENY", SAS_MASK_DENY},
+                {"FLAG_EMPTY_ROW", SAS_FLAG_EMPTY_ROW}, {"FLAG_TOPP_EDGE", SAS_FLAG_TOPP_EDGE},
+                {"FLAG_DRAW_EDGE", SAS_FLAG_DRAW_EDGE}, {"FLAG_SLOW_SELECT", SAS_FLAG_SLOW_SELECT},
+                {"PARAMS_BYTES", (double)sizeof(sas_params)}};
+  for (const auto &k : consts) {
+    napi_create_double(env, k.value, &c);
+    napi_set_named_property(env, exports, k.name, c);
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(sas_napi, Init)

@@ -1,0 +1,429 @@
+'use strict';
+// Node host side of the MI355X sampling path: the sampler / token-mask API of
+// lib/webgpu-llm kept as a drop-in, over the C ABI through the N-API addon.
+//
+//   TokenMask + updateTokenMaskState  <- lib/webgpu-llm/tool-constraint.ts:39-42,
+//                                        lib/webgpu-llm/token-mask-state.js:8-31
+//   packSamplerParams                 <- lib/webgpu-llm/model.js:401-426,
+//                                        lib/webgpu-llm/gemma-model.js:900-919
+//   Sampler#sample(cands, opts)       <- sample(), lib/webgpu-llm/tokenizer.js:151-178
+//   Sampler#sampleRows                <- the topk + sampler WGSL pair,
+//                                        lib/webgpu-llm/kernels.js:65-201, 1389-1449
+//   Sampler#verify                    <- acceptSpec, lib/webgpu-llm/kernels.js:211-369
+//
+// Grammar state stays on the host: a TokenMask becomes the packed u32
+// bitmask (bit id & 31 of word id >> 5 = allowed) once per distinct
+// immutable mask, and only those words cross to the GPU.  Written for
+// Node >= 12 (no optional chaining, no class fields).
+
+const addon = require('./sas_napi.node');
+
+const MAX_STOP_IDS = 4;
+const STOP_PAD = 0xFFFFFFFF;
+const PARAMS_BYTES = addon.PARAMS_BYTES;
+const KIND_CODE = { all: addon.MASK_ALL, allow: addon.MASK_ALLOW, deny: addon.MASK_DENY };
+
+function orDefault(v, d) { return v === undefined || v === null ? d : v; }
+
+/**
+ * Apply an immutable TokenMask to a mask state, as the reference does: the
+ * same checks and messages (token-mask-state.js:9-20), and nothing is
+ * re-uploaded for the same kind and the same Uint32Array object (:21).
+ * A changed mask is packed into bitmask words on the host and handed to
+ * state.upload(words).  Kind 'all' needs no words: rows sample unmasked.
+ */
+function updateTokenMaskState(state, mask) {
+  const kind = orDefault(mask ? mask.kind : undefined, 'all');
+  if (kind !== 'all' && kind !== 'allow' && kind !== 'deny') {
+    throw new Error('Unknown token mask kind: ' + kind);
+  }
+  const ids = kind === 'all' ? null : (mask ? mask.tokenIds : undefined);
+  if (kind !== 'all' && !(ids instanceof Uint32Array)) {
+    throw new Error('A ' + kind + ' token mask requires Uint32Array tokenIds.');
+  }
+  const count = ids ? ids.length : 0;
+  if (count > state.cfg.text.vocab) {
+    throw new Error('Tool constraint has too many token IDs.');
+  }
+  if (kind === state.tokenMaskKind && ids === state.tokenMaskIds) return;
+  if (kind !== 'all') {
+    const packed = addon.maskFromIds(KIND_CODE[kind], ids, state.cfg.text.vocab);
+    state.upload(packed.words);
+    state.allowedTokens = packed.allowed;
+  } else {
+    state.allowedTokens = state.cfg.text.vocab;
+  }
+  state.allowedCount = count;
+  state.tokenMaskKind = kind;
+  state.tokenMaskIds = ids;
+}
+
+/**
+ * The reference packer's validation and clamps (model.js:401-426): stop ids
+ * are checked and padded, and every numeric field is clamped by
+ * sas_clamp_params.  top_k may go to 128 here (the request API's range,
+ * completions.ts:271) where the reference GPU path stopped at 20.
+ * Defaults follow model.js (temperature 0 / greedy, topP 1, topK 20); pass
+ * defaults = {temperature: 0.6, topP: 0.95} for the Gemma packer.
+ */
+function packSamplerParams(sp, defaults) {
+  sp = sp || {};
+  defaults = defaults || {};
+  const rawStopIds = sp.stopIds !== undefined ? sp.stopIds
+    : (sp.eosId !== undefined ? [sp.eosId] : []);
+  if (!Array.isArray(rawStopIds)) throw new Error('stopIds must be an array');
+  if (rawStopIds.length > MAX_STOP_IDS) throw new Error('stopIds supports at most ' + MAX_STOP_IDS + ' ids');
+  const stopIds = rawStopIds.map(function (id) {
+    if (!Number.isInteger(id)) throw new Error('invalid stop token id: ' + id);
+    return id >>> 0;
+  });
+  const pick = function (name, d) { return Number.isFinite(sp[name]) ? sp[name] : orDefault(defaults[name], d); };
+  const params = addon.clampParams({
+    temperature: pick('temperature', 0),
+    topP: pick('topP', 1),
+    topK: Number.isFinite(sp.topK) ? Math.floor(sp.topK) : orDefault(defaults.topK, 20),
+    presencePenalty: pick('presencePenalty', 0),
+    repetitionPenalty: pick('repetitionPenalty', 1),
+    frequencyPenalty: pick('frequencyPenalty', 0),
+    softcap: pick('softcap', 0),
+  });
+  const seed = sp.seed !== undefined && sp.seed !== null ? sp.seed >>> 0 : orDefault(defaults.seed, 1) >>> 0;
+  const padded = [];
+  for (let i = 0; i < MAX_STOP_IDS; i++) padded.push(i < stopIds.length ? stopIds[i] : STOP_PAD);
+  return { params: params, seed: seed, stopIds: stopIds, paddedStopIds: padded, stopSet: new Set(stopIds) };
+}
+
+/** sas_params layout: five doubles, a float softcap, an int32 top_k (48 bytes). */
+function writeParams(view, offset, p) {
+  view.setFloat64(offset + 0, p.temperature, true);
+  view.setFloat64(offset + 8, p.topP, true);
+  view.setFloat64(offset + 16, p.repetitionPenalty, true);
+  view.setFloat64(offset + 24, p.presencePenalty, true);
+  view.setFloat64(offset + 32, p.frequencyPenalty, true);
+  view.setFloat32(offset + 40, p.softcap, true);
+  view.setInt32(offset + 44, p.topK, true);
+}
+
+function toU32(list) {
+  if (list instanceof Uint32Array) return list;
+  if (list instanceof Set) return Uint32Array.from(list);
+  return Uint32Array.from(list || []);
+}
+
+class DeviceBuffer {
+  constructor(sampler, bytes) {
+    this.sampler = sampler;
+    this.bytes = bytes;
+    this.ptr = addon.alloc(sampler._handle(), bytes);
+  }
+  upload(typed) {
+    if (typed.byteLength > this.bytes) throw new RangeError('upload larger than the device buffer');
+    addon.copy(this.sampler._handle(), this.ptr, typed, 0);
+    return this;
+  }
+  download(typed) {
+    if (typed.byteLength > this.bytes) throw new RangeError('download larger than the device buffer');
+    addon.copy(this.sampler._handle(), this.ptr, typed, 1);
+    return typed;
+  }
+  free() {
+    if (this.ptr !== null && this.sampler._h !== null) addon.free(this.sampler._h, this.ptr);
+    this.ptr = null;
+  }
+}
+
+class Sampler {
+  /** A sampler bound to HIP device `device`; throws when no device exists. */
+  constructor(device) {
+    this._h = addon.create(device || 0);
+    this._scratch = {};
+    this._queue = Promise.resolve();
+  }
+
+  _handle() {
+    if (this._h === null) throw new Error('sampler is closed');
+    return this._h;
+  }
+
+  close() {
+    if (this._h === null) return;
+    const names = Object.keys(this._scratch);
+    for (let i = 0; i < names.length; i++) this._scratch[names[i]].free();
+    this._scratch = {};
+    addon.destroy(this._h);
+    this._h = null;
+  }
+
+  reserve(rows, vocab) { addon.reserve(this._handle(), rows, vocab); }
+
+  /** Device memory owned by the caller (e.g. the LM head's logits). */
+  alloc(bytes) { return new DeviceBuffer(this, bytes); }
+
+  synchronize() { addon.synchronize(this._handle()); }
+
+  // Grow-only per-name scratch, so steady-state calls allocate nothing.
+  _buf(name, bytes) {
+    const have = this._scratch[name];
+    if (have && have.bytes >= bytes) return have;
+    if (have) have.free();
+    const b = new DeviceBuffer(this, Math.max(256, bytes));
+    this._scratch[name] = b;
+    return b;
+  }
+
+  /**
+   * Mask state that mirrors the reference's (cfg.text.vocab, tokenMaskKind,
+   * tokenMaskIds, allowedCount) plus the device words it uploads to.
+   */
+  createTokenMaskState(vocab) {
+    const self = this;
+    const words = this.alloc(Math.ceil(vocab / 32) * 4);
+    return {
+      cfg: { text: { vocab: vocab } },
+      allowedCount: 0,
+      allowedTokens: vocab,
+      tokenMaskKind: 'all',
+      tokenMaskIds: null,
+      words: words,
+      uploads: 0,
+      upload: function (w) { words.upload(w); this.uploads++; },
+      sampler: self,
+    };
+  }
+
+  _describe(opts) {
+    const rows = opts.rows;
+    const vocab = opts.vocab;
+    const stride = orDefault(opts.stride, vocab);
+    const d = { rows: rows, vocab: vocab, logitsStride: stride };
+    // logits: device buffer (resident), or a host Float32Array staged up
+    if (opts.logits instanceof DeviceBuffer) {
+      d.logits = opts.logits.ptr;
+    } else if (opts.logits instanceof Float32Array) {
+      d.logits = this._buf('logits', opts.logits.byteLength).upload(opts.logits).ptr;
+    } else {
+      throw new TypeError('logits must be a DeviceBuffer or a Float32Array');
+    }
+    // mask: a token-mask state (one grammar state for every row), a
+    // TokenMask, host words [rows][ceil(vocab/32)], or a DeviceBuffer of them
+    const nwords = Math.ceil(vocab / 32);
+    const m = opts.mask;
+    if (m && m.cfg && m.words) {
+      if (m.tokenMaskKind !== 'all') { d.mask = m.words.ptr; d.maskStride = 0; }
+    } else if (m && m.kind !== undefined) {
+      if (m.kind !== 'all') {
+        const st = this._maskState || (this._maskState = this.createTokenMaskState(vocab));
+        if (st.cfg.text.vocab !== vocab) {
+          st.words.free();
+          this._maskState = this.createTokenMaskState(vocab);
+        }
+        updateTokenMaskState(this._maskState, m);
+        d.mask = this._maskState.words.ptr;
+        d.maskStride = 0;
+      }
+    } else if (m instanceof Uint32Array) {
+      d.mask = this._buf('mask', m.byteLength).upload(m).ptr;
+      d.maskStride = m.length === nwords ? 0 : nwords;
+    } else if (m instanceof DeviceBuffer) {
+      d.mask = m.ptr;
+      d.maskStride = orDefault(opts.maskStride, nwords);
+    }
+    // params: one SampleParams for every row, or one per row
+    const ps = Array.isArray(opts.params) ? opts.params : null;
+    const packed = ps ? ps.map(function (p) { return packSamplerParams(p, opts.defaults); })
+      : [packSamplerParams(opts.params, opts.defaults)];
+    if (ps) {
+      if (ps.length !== rows) throw new RangeError('params must have one entry per row');
+      const ab = new ArrayBuffer(rows * PARAMS_BYTES);
+      const view = new DataView(ab);
+      for (let r = 0; r < rows; r++) writeParams(view, r * PARAMS_BYTES, packed[r].params);
+      d.rowParams = this._buf('params', ab.byteLength).upload(new Uint8Array(ab)).ptr;
+      d.params = packed[0].params;
+    } else {
+      d.params = packed[0].params;
+    }
+    // history: per-row lists (Array / Uint32Array / Set), or recentIds for every row
+    let hist = opts.history;
+    if (!hist && opts.recentIds) {
+      hist = [];
+      for (let r = 0; r < rows; r++) hist.push(opts.recentIds);
+    }
+    if (hist) {
+      if (hist.length !== rows) throw new RangeError('history must have one list per row');
+      const lists = hist.map(toU32);
+      const offs = new Int32Array(rows + 1);
+      for (let r = 0; r < rows; r++) offs[r + 1] = offs[r] + lists[r].length;
+      const flat = new Uint32Array(Math.max(1, offs[rows]));
+      for (let r = 0; r < rows; r++) flat.set(lists[r], offs[r]);
+      d.histIds = this._buf('hist', flat.byteLength).upload(flat).ptr;
+      d.histOffsets = this._buf('histOffsets', offs.byteLength).upload(offs).ptr;
+    }
+    // uniforms: host-supplied U per row, else the reference GPU sampler's
+    // PCG draw from each row's seed (kernels.js:181, 320)
+    let u = opts.uniforms;
+    if (!u) {
+      u = new Float64Array(rows);
+      const it = orDefault(opts.iteration, 0) >>> 0;
+      for (let r = 0; r < rows; r++) u[r] = addon.pcgUniform(packed[ps ? r : 0].seed, it, r);
+    }
+    if (!(u instanceof Float64Array) || u.length < rows) throw new TypeError('uniforms must be a Float64Array[rows]');
+    d.uniforms = this._buf('uniforms', rows * 8).upload(u).ptr;
+    d.outIds = this._buf('ids', rows * 4).ptr;
+    if (opts.full) {
+      d.outProbs = this._buf('probs', rows * addon.MAX_TOP_K * 8).ptr;
+      d.outCandIds = this._buf('candIds', rows * addon.MAX_TOP_K * 4).ptr;
+      d.outCounts = this._buf('counts', rows * 8).ptr;
+      d.outFlags = this._buf('flags', rows * 4).ptr;
+    }
+    return { desc: d, packed: packed };
+  }
+
+  _collect(opts, packed) {
+    const rows = opts.rows;
+    const ids = this._scratch.ids.download(new Uint32Array(rows));
+    const stopped = [];
+    const stopId = [];
+    for (let r = 0; r < rows; r++) {
+      const set = packed[packed.length > 1 ? r : 0].stopSet;
+      const hit = set.has(ids[r]);
+      stopped.push(hit);
+      stopId.push(hit ? ids[r] : null);
+    }
+    const out = { ids: ids, stopped: stopped, stopId: stopId };
+    if (opts.full) {
+      out.probs = this._scratch.probs.download(new Float64Array(rows * addon.MAX_TOP_K));
+      out.candIds = this._scratch.candIds.download(new Uint32Array(rows * addon.MAX_TOP_K));
+      out.counts = this._scratch.counts.download(new Int32Array(rows * 2));
+      out.flags = this._scratch.flags.download(new Uint32Array(rows));
+    }
+    return out;
+  }
+
+  /**
+   * One token per row.  opts: {logits, rows, vocab, stride?, mask?, params,
+   * history? | recentIds?, uniforms? | seeds via params, iteration?, full?}.
+   * Returns {ids: Uint32Array, stopped, stopId[, probs, candIds, counts, flags]}.
+   */
+  sampleRows(opts) {
+    const r = this._describe(opts);
+    addon.sample(this._handle(), r.desc);
+    return this._collect(opts, r.packed);
+  }
+
+  /** sampleRows with the launch and the wait on a worker thread.  Calls queue. */
+  sampleRowsAsync(opts) {
+    const self = this;
+    const run = function () {
+      const r = self._describe(opts);
+      return addon.sampleAsync(self._handle(), r.desc).then(function () { return self._collect(opts, r.packed); });
+    };
+    const p = this._queue.then(run, run);
+    this._queue = p.then(function () {}, function () {});
+    return p;
+  }
+
+  /**
+   * The reference's sample(cands, opts) signature (tokenizer.js:151): a
+   * candidate list [id, value] interleaved in ids/vals, presence penalty
+   * over opts.recentIds.  Runs on the GPU over a row that holds the
+   * candidates' values (every other id excluded).  opts.uniform replaces
+   * Math.random() when given.
+   */
+  sample(cands, opts) {
+    opts = opts || {};
+    const n = cands.ids.length >> 1;
+    let vocab = 1;
+    for (let i = 0; i < n; i++) vocab = Math.max(vocab, (cands.ids[i * 2] >>> 0) + 1);
+    const row = new Float32Array(vocab).fill(NaN);
+    const words = new Uint32Array(Math.ceil(vocab / 32));
+    for (let i = 0; i < n; i++) {
+      const id = cands.ids[i * 2] >>> 0;
+      row[id] = cands.vals[i * 2 + 1];
+      words[id >> 5] |= (1 << (id & 31)) >>> 0;
+    }
+    const params = {
+      temperature: orDefault(opts.temperature, 0.6),
+      topK: orDefault(opts.topK, 20),
+      topP: orDefault(opts.topP, 0.95),
+      presencePenalty: orDefault(opts.presencePenalty, 0),
+    };
+    const u = new Float64Array([opts.uniform !== undefined ? opts.uniform : Math.random()]);
+    const out = this.sampleRows({
+      logits: row, rows: 1, vocab: vocab, mask: words, params: params,
+      history: opts.recentIds ? [opts.recentIds] : null, uniforms: u,
+    });
+    return out.ids[0];
+  }
+
+  /**
+   * Speculative verify.  opts: {target, draft (DeviceBuffer | Float32Array),
+   * vocab, seqs, draftLen, draftIds (Uint32Array), uniforms (Float64Array
+   * [seqs][draftLen+1][2]), temperature, mask? (Uint32Array words)}.
+   * Returns {tokens: Uint32Array[seqs*(draftLen+1)], accepted: Int32Array}.
+   */
+  verify(opts) {
+    const d = this._describeVerify(opts);
+    addon.verify(this._handle(), d);
+    return this._collectVerify(opts);
+  }
+
+  verifyAsync(opts) {
+    const self = this;
+    const run = function () {
+      const d = self._describeVerify(opts);
+      return addon.verifyAsync(self._handle(), d).then(function () { return self._collectVerify(opts); });
+    };
+    const p = this._queue.then(run, run);
+    this._queue = p.then(function () {}, function () {});
+    return p;
+  }
+
+  _describeVerify(opts) {
+    const self = this;
+    const dev = function (name, x) {
+      if (x instanceof DeviceBuffer) return x.ptr;
+      return self._buf(name, x.byteLength).upload(x).ptr;
+    };
+    const seqs = opts.seqs;
+    const L = opts.draftLen;
+    const nwords = Math.ceil(opts.vocab / 32);
+    const d = {
+      targetLogits: dev('vTarget', opts.target), draftLogits: dev('vDraft', opts.draft),
+      logitsStride: orDefault(opts.stride, opts.vocab), vocab: opts.vocab, seqs: seqs, draftLen: L,
+      draftIds: dev('vIds', toU32(opts.draftIds)), uniforms: dev('vU', opts.uniforms),
+      temperature: orDefault(opts.temperature, 1.0),
+      outTokens: this._buf('vTokens', seqs * (L + 1) * 4).ptr, outAccepted: this._buf('vAcc', seqs * 4).ptr,
+    };
+    if (opts.mask) {
+      d.mask = dev('vMask', opts.mask);
+      d.maskStride = opts.mask.length === nwords ? 0 : orDefault(opts.maskStride, nwords);
+    }
+    return d;
+  }
+
+  _collectVerify(opts) {
+    const n = opts.seqs * (opts.draftLen + 1);
+    return {
+      tokens: this._scratch.vTokens.download(new Uint32Array(n)),
+      accepted: this._scratch.vAcc.download(new Int32Array(opts.seqs)),
+    };
+  }
+}
+
+module.exports = {
+  Sampler: Sampler,
+  DeviceBuffer: DeviceBuffer,
+  updateTokenMaskState: updateTokenMaskState,
+  packSamplerParams: packSamplerParams,
+  maskFromIds: addon.maskFromIds,
+  pcgUniform: addon.pcgUniform,
+  clampParams: addon.clampParams,
+  version: addon.version,
+  MAX_TOP_K: addon.MAX_TOP_K,
+  MAX_DRAFT: addon.MAX_DRAFT,
+  NO_TOKEN: addon.NO_TOKEN,
+  FLAG_EMPTY_ROW: addon.FLAG_EMPTY_ROW,
+  FLAG_TOPP_EDGE: addon.FLAG_TOPP_EDGE,
+  FLAG_DRAW_EDGE: addon.FLAG_DRAW_EDGE,
+  STOP_PAD: STOP_PAD,
+};

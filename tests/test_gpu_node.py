@@ -1,0 +1,96 @@
+"""The Node host layer on the GPU: tests/node/host_gpu.js samples a C3P-shaped
+batch through every entry of the JS API (host and device-resident logits,
+async, per-row params, TokenMask state, the reference's sample(cands, opts)
+signature, verify), and every result is compared with the oracle."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+from shared_amd import Params
+from shared_amd import workloads as W
+from shared_amd._capi import MASK_ALLOW
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _u32(d, name):
+    return np.fromfile(os.path.join(d, name), np.uint32)
+
+
+def test_node_api_end_to_end(tmp_path):
+    if shutil.which("node") is None:
+        pytest.skip("node is not installed")
+    d = str(tmp_path)
+    b = W.c3p(rows=12, seed=91)
+    O.write_case(d, b)
+    rng = np.random.default_rng(5)
+    allow = np.unique(rng.integers(0, b.vocab, 3000)).astype(np.uint32)
+    allow.tofile(os.path.join(d, "tokmask_allow.u32"))
+    # a candidate list as the reference's GPU top-k hands it to sample()
+    cand_ids = rng.choice(b.vocab, 20, replace=False).astype(np.uint32)
+    cand_vals = (rng.standard_normal(20) * 3).astype(np.float32)
+    recent = [int(cand_ids[3]), int(cand_ids[7]), 5]
+    us = [0.0, 0.1, 0.37, 0.5, 0.9, 0.999]
+    cc = {"ids": cand_ids.tolist(), "vals": cand_vals.astype(float).tolist(), "temperature": 0.8, "topK": 12,
+          "topP": 0.9, "presencePenalty": 1.2, "recent": recent, "uniforms": us}
+    with open(os.path.join(d, "cands.json"), "w") as f:
+        json.dump(cc, f)
+    v = W.c5(seqs=4, seed=17)
+    v["target"].tofile(os.path.join(d, "v_target.f32"))
+    v["draft"].tofile(os.path.join(d, "v_draft.f32"))
+    np.ascontiguousarray(v["draft_ids"], np.uint32).tofile(os.path.join(d, "v_ids.u32"))
+    np.ascontiguousarray(v["uniforms"], np.float64).tofile(os.path.join(d, "v_u.f64"))
+    np.ascontiguousarray(v["mask"], np.uint32).tofile(os.path.join(d, "v_mask.u32"))
+    with open(os.path.join(d, "verify.json"), "w") as f:
+        json.dump({"vocab": v["vocab"], "seqs": v["seqs"], "drafts": v["drafts"],
+                   "temperature": v["temperature"]}, f)
+
+    print("[gpu] node host_gpu.js", d, flush=True)
+    proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "host_gpu.js"), d], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-3000:]
+
+    want = O.sample_rows(b)
+    got = _u32(d, "js_sync_ids.u32")
+    assert np.array_equal(got, want["ids"])
+    probs = np.fromfile(os.path.join(d, "js_sync_probs.f64")).reshape(b.rows, -1)
+    assert np.array_equal(probs, want["probs"])
+    assert np.array_equal(_u32(d, "js_sync_cand.u32").reshape(b.rows, -1), want["cand_ids"])
+    for name in ("js_async_ids.u32", "js_dev_ids.u32", "js_rowparams_ids.u32"):
+        assert np.array_equal(_u32(d, name), want["ids"]), name
+
+    m1 = O.mask_from_ids(MASK_ALLOW, allow, b.vocab)
+    bt = W.Batch("tokmask", b.logits, b.params, mask=np.repeat(m1[None, :], b.rows, axis=0),
+                 hist_ids=b.hist_ids, hist_offsets=b.hist_offsets, uniforms=b.uniforms)
+    wt = O.sample_rows(bt)["ids"]
+    assert np.array_equal(_u32(d, "js_tokmask_ids.u32"), wt)
+    assert np.array_equal(_u32(d, "js_tokmask2_ids.u32"), wt)
+
+    cv = int(cand_ids.max()) + 1
+    row = np.full(cv, np.nan, np.float32)
+    row[cand_ids] = cand_vals
+    bits = np.zeros(cv, bool)
+    bits[cand_ids] = True
+    n = len(us)
+    hi, ho = W._csr([np.unique(np.array(recent, np.uint32))] * n)
+    bc = W.Batch("compat", np.repeat(row[None, :], n, axis=0),
+                 Params(temperature=0.8, top_k=12, top_p=0.9, presence_penalty=1.2),
+                 mask=np.repeat(W.pack_bits(bits[None, :]), n, axis=0), hist_ids=hi, hist_offsets=ho,
+                 uniforms=np.array(us))
+    with open(os.path.join(d, "js_compat.json")) as f:
+        compat = json.load(f)
+    assert compat == O.sample_rows(bc)["ids"].tolist()
+
+    ov = O.verify(v)
+    L = v["drafts"]
+    assert np.array_equal(_u32(d, "js_v_tokens.u32").reshape(v["seqs"], L + 1), ov["tokens"])
+    assert np.array_equal(np.fromfile(os.path.join(d, "js_v_acc.i32"), np.int32), ov["accepted"])
+    assert np.array_equal(_u32(d, "js_v2_tokens.u32"), _u32(d, "js_v_tokens.u32"))

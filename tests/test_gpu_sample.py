@@ -208,3 +208,20 @@ def test_argument_errors_are_reported(sampler):
     with pytest.raises(SasError, match="mask_stride"):
         sampler.sample_into(x, ids, mask=torch.zeros((2, 2), dtype=torch.int32, device="cuda"), params=Params())
     sampler.sample_into(x[:0], ids, params=Params())          # zero rows is a no-op
+
+
+def test_one_mask_for_every_row(sampler):
+    """mask_stride 0: one grammar state shared by all rows equals the same
+    words repeated per row."""
+    import torch
+    b = _small_batch(77, rows=9, vocab=50000, params=Params(temperature=0.8, top_k=40, top_p=0.9),
+                     mask_density=0.05)
+    one = b.mask[:1]
+    b.mask = np.ascontiguousarray(np.repeat(one, b.rows, axis=0))
+    lg = to_dev(b.logits)
+    u = to_dev(b.uniforms)
+    shared = to_dev(one, torch.int32).expand(b.rows, one.shape[1])
+    assert shared.stride(0) == 0
+    got = sampler.sample(lg, vocab=b.vocab, mask=shared, uniforms=u, params=b.params).cpu().numpy().view(np.uint32)
+    want = O.sample_rows(b)["ids"]
+    assert np.array_equal(got, want)
