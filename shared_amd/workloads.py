@@ -52,14 +52,17 @@ class Batch:
         return self.logits.shape[1]
 
     def algorithmic_bytes(self) -> int:
-        """Compulsory HBM bytes of one step: logits, mask, history, U, ids."""
+        """Compulsory HBM bytes of one step as the C ABI takes it: the fp32
+        logits, the mask words, the history ids and their row offsets, the
+        float64 uniforms (when some row samples) read once, and the uint32
+        ids written once."""
         b = self.logits.nbytes + 4 * self.rows
         if self.mask is not None:
-            b += self.rows * ((self.vocab + 7) // 8)
+            b += self.rows * ((self.vocab + 31) // 32) * 4
         if self.hist_ids is not None:
-            b += self.hist_ids.nbytes
+            b += self.hist_ids.nbytes + self.hist_offsets.nbytes
         if self.uniforms is not None and self.params.temperature > 0:
-            b += 4 * self.rows
+            b += self.uniforms.nbytes
         return b
 
 
