@@ -17,12 +17,16 @@ struct sas_sampler {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
-  void *recs = nullptr;        // candidate record slots, then their counts
+  void *recs = nullptr;        // candidate record slots of every (row, part)
   size_t recs_cap = 0;
-  uint32_t *ctl = nullptr;     // per-row arrival counters and thresholds, zero between launches
+  uint32_t *ctl = nullptr;     // per-row control blocks: arrivals and thresholds zero between launches
   int32_t ctl_rows = 0;
   void *vscratch = nullptr;   // sas_verify partials
   size_t vscratch_cap = 0;
+  void *pad = nullptr;        // rows of fewer than 4 logits, padded to 4
+  size_t pad_cap = 0;
+  int cus = 0;                 // compute units of the device
+  int resident[8] = {0};       // blocks per CU of each sampling kernel variant (0: not queried)
 };
 
 namespace {
@@ -61,9 +65,8 @@ int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
   return SAS_OK;
 }
 
-int ensure_sample_scratch(sas_sampler *s, int rows, int splits) {
-  int rc = grow(s, &s->recs, &s->recs_cap,
-                sas::sample_rec_bytes(rows, splits) + sas::sample_count_bytes(rows, splits), false);
+int ensure_sample_scratch(sas_sampler *s, int rows, int parts) {
+  int rc = grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, parts), false);
   if (rc) return rc;
   if (rows > s->ctl_rows) {
     size_t cap = (size_t)s->ctl_rows * sas::kCtlStride * 4;
@@ -75,8 +78,6 @@ int ensure_sample_scratch(sas_sampler *s, int rows, int splits) {
   }
   return SAS_OK;
 }
-
-int splits_for(int f4, int vocab) { return (vocab + f4 * 1024 - 1) / (f4 * 1024); }
 
 int set_device(sas_sampler *s) {
   hipError_t e = hipSetDevice(s->device);
@@ -101,6 +102,8 @@ int sas_create(int device, sas_sampler **out) {
   if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
   sas_sampler *s = new sas_sampler();
   s->device = device;
+  if ((e = hipDeviceGetAttribute(&s->cus, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess || s->cus < 1)
+    s->cus = 256;
   if ((e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete s;
     return hip_fail(nullptr, e, "hipStreamCreate");
@@ -116,6 +119,7 @@ void sas_destroy(sas_sampler *s) {
   if (s->recs) (void)hipFree(s->recs);
   if (s->ctl) (void)hipFree(s->ctl);
   if (s->vscratch) (void)hipFree(s->vscratch);
+  if (s->pad) (void)hipFree(s->pad);
   if (s->stream) (void)hipStreamDestroy(s->stream);
   delete s;
 }
@@ -127,10 +131,10 @@ int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab) {
   if (rows < 0 || vocab < 1 || vocab > SAS_MAX_VOCAB)
     return fail(s, SAS_ERR_INVALID, "sas_reserve: rows must be >= 0 and vocab in [1, SAS_MAX_VOCAB]");
   if (int rc = set_device(s)) return rc;
-  // the smallest chunk any batch of <= rows rows may pick
-  int splits = splits_for(2, vocab);
-  if (splits > sas::kMaxSplits) splits = splits_for(sas::choose_f4(1, vocab), vocab);
-  return ensure_sample_scratch(s, rows, splits);
+  // the most parts any batch of <= rows rows may pick
+  int parts = 0, cpp = 0;
+  sas::choose_parts(1, vocab, 0, &parts, &cpp);
+  return ensure_sample_scratch(s, rows, parts);
 }
 
 int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
@@ -150,13 +154,29 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   if (!r->uniforms && !all_greedy)
     return fail(s, SAS_ERR_INVALID, "sas_sample: uniforms are required unless every row is greedy");
   if (int rc = set_device(s)) return rc;
-  const int f4 = sas::choose_f4(r->rows, r->vocab);
-  const int splits = splits_for(f4, r->vocab);
-  if (int rc = ensure_sample_scratch(s, r->rows, splits)) return rc;
+  const bool softcap = r->row_params != nullptr || r->params.softcap > 0.0f;
+  const int variant = (r->mask ? 4 : 0) | (r->hist_ids ? 2 : 0) | (softcap ? 1 : 0);
+  if (s->resident[variant] == 0) {
+    s->resident[variant] = sas::sample_blocks_per_cu(r->mask != nullptr, r->hist_ids != nullptr, softcap);
+    if (s->resident[variant] < 1) s->resident[variant] = 1;
+  }
+  int parts = 0, cpp = 0;
+  sas::choose_parts(r->rows, r->vocab, s->resident[variant] * s->cus, &parts, &cpp);
+  if (int rc = ensure_sample_scratch(s, r->rows, parts)) return rc;
 
   sas::SampleArgs a;
   a.logits = r->logits;
   a.logits_stride = r->logits_stride;
+  if (r->vocab < 4) {
+    // the kernel loads 16 bytes at a time from inside a row: copy rows of
+    // fewer than 4 logits into rows of 4, NaN (never selected) past vocab
+    if (int rc = grow(s, &s->pad, &s->pad_cap, (size_t)r->rows * 16, false)) return rc;
+    hipError_t e = sas::launch_pad_rows(r->logits, r->logits_stride, r->vocab, r->rows,
+                                        reinterpret_cast<float *>(s->pad), pick_stream(s, stream));
+    if (e != hipSuccess) return hip_fail(s, e, "sas_sample pad launch");
+    a.logits = reinterpret_cast<const float *>(s->pad);
+    a.logits_stride = 4;
+  }
   a.mask = r->mask;
   a.mask_stride = r->mask_stride;
   a.hist_ids = r->hist_ids;
@@ -169,19 +189,14 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.out_cand_ids = r->out_cand_ids;
   a.out_counts = r->out_counts;
   a.out_flags = r->out_flags;
-  // record arrays carved from one allocation: values (8-byte) first
-  const size_t slots = (size_t)r->rows * splits * sas::kCapBlock;
-  a.rval = reinterpret_cast<double *>(s->recs);
-  a.rkey = reinterpret_cast<float *>(a.rval + slots);
-  a.rid = reinterpret_cast<uint32_t *>(a.rkey + slots);
-  a.counts = a.rid + slots;
+  a.rec = reinterpret_cast<uint64_t *>(s->recs);
   a.ctl = s->ctl;
   a.vocab = r->vocab;
   a.rows = r->rows;
-  a.splits = splits;
-  a.aligned = (reinterpret_cast<uintptr_t>(r->logits) & 15u) == 0 && (r->logits_stride & 3) == 0;
-  const bool softcap = r->row_params != nullptr || r->params.softcap > 0.0f;
-  hipError_t e = sas::launch_sample(a, f4, softcap, pick_stream(s, stream));
+  a.parts = parts;
+  a.cpp = cpp;
+  a.chunks = (r->vocab + sas::kChunkIds - 1) / sas::kChunkIds;
+  hipError_t e = sas::launch_sample(a, softcap, pick_stream(s, stream));
   if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
   return SAS_OK;
 }

@@ -15,13 +15,13 @@ namespace sas {
 
 constexpr int kThreads = 256;           // 4 wave64s per block
 constexpr int kWaves = kThreads / 64;
-constexpr int kCapBlock = 256;          // records one block may emit
-constexpr int kCapMerge = 512;          // survivors ranked exactly in LDS by the merge
-constexpr int kMaxSplits = 512;         // SAS_MAX_VOCAB / 8192
+constexpr int kCapBlock = 256;          // candidates one exact chunk selection may emit
 constexpr uint32_t kPenFlag = 0x80000000u;
 
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// A float4 that needs 4-byte alignment only (global loads take it as one 16-byte access).
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
 
 __device__ __forceinline__ float qnan() { return __builtin_nanf(""); }
 
@@ -146,8 +146,9 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 // Order-preserving map of an fp32 key to uint32 (larger float, larger
 // uint); NaN maps to 0, which marks "no key".
 __device__ __forceinline__ uint32_t okey(float f) {
-  const uint32_t u = __float_as_uint(f);
+  uint32_t u = __float_as_uint(f);
   if (f != f) return 0u;
+  if (u == 0x80000000u) u = 0u;  // -0 and +0 are one value: one key
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
@@ -205,14 +206,53 @@ __device__ __forceinline__ void wave_best(bool &have, double &v, uint32_t &id) {
 }
 
 // Inclusive prefix sum over the wave.
+// DPP lane moves (GFX9 encodings).  dpp0: lanes whose source lies outside
+// their row (or in a row that row_mask leaves out) read 0; dppx: every
+// source lies inside the row.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ uint32_t dpp0(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kCtrl, kRowMask, 0xF, true);
+}
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dppx(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, kCtrl, 0xF, 0xF, false);
+}
+constexpr int kDppQuad1032 = 0xB1, kDppQuad2301 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+// Inclusive prefix sum over the wave: Hillis-Steele within each row of 16
+// lanes, then the rows' totals broadcast forward.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-    uint32_t y = (uint32_t)__shfl_up((int)x, s, 64);
-    if (lane >= s) x += y;
-  }
+  x += dpp0<kDppRowShr1>(x);
+  x += dpp0<kDppRowShr2>(x);
+  x += dpp0<kDppRowShr4>(x);
+  x += dpp0<kDppRowShr8>(x);
+  x += dpp0<kDppRowBcast15, 0xA>(x);
+  x += dpp0<kDppRowBcast31, 0xC>(x);
   return x;
+}
+
+// Wave-wide reductions: pairs, quads, eights and rows of 16 by DPP, then the
+// four rows' results (wave-uniform).
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t x, Op op) {
+  x = op(x, dppx<kDppQuad1032>(x));
+  x = op(x, dppx<kDppQuad2301>(x));
+  x = op(x, dppx<kDppRowHalfMirror>(x));
+  x = op(x, dppx<kDppRowMirror>(x));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 16),
+                 r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+  return op(op(r0, r1), op(r2, r3));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  return wave_reduce(x, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  return wave_reduce(x, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
+  return wave_reduce(x, [](uint32_t a, uint32_t b) { return a + b; });
 }
 
 }  // namespace sas

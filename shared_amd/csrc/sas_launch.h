@@ -8,9 +8,16 @@
 
 namespace sas {
 
-// Kernel arguments of the split and merge kernels (validated by sas_sample).
-constexpr int kCtlStride = 64;  // words per row: 256 bytes
-constexpr int kCtlThr = 32;     // second 128-byte line
+// Kernel arguments of the sampling kernel (validated by sas_sample).
+//
+// A row's vocabulary is cut into chunks of kChunkIds ids; block (row, part)
+// streams chunks [part * cpp, (part + 1) * cpp) of the row.
+constexpr int kChunkIds = 4096;
+constexpr int kMaxParts = 64;   // blocks per row; the merge holds one count per part
+constexpr int kListCap = 2048;  // record slots of one part in HBM
+constexpr int kCtlStride = 128; // words per row of the control block: 512 bytes
+constexpr int kCtlThr = 32;     // second 128-byte line: the largest published threshold key
+constexpr int kCtlCnt = 64;     // third and fourth lines: records written by each part (<= kMaxParts)
 
 struct SampleArgs {
   const float *logits;
@@ -27,33 +34,36 @@ struct SampleArgs {
   uint32_t *out_cand_ids;
   int32_t *out_counts;
   uint32_t *out_flags;
-  // Candidate records: block (row, split) writes up to kCapBlock records at
-  // recs[(row * splits + split) * kCapBlock] and their number at
-  // counts[row * splits + split]; the merge kernel, next in stream order,
-  // reads them.
-  float *rkey;        // [rows][splits][kCapBlock] fp32 key (round-down of the value)
-  uint32_t *rid;      // [rows][splits][kCapBlock] token id
-  double *rval;       // [rows][splits][kCapBlock] exact value
-  uint32_t *counts;   // [rows][splits]
-  // Per row kCtlStride words, zero between launches: [0] blocks counted in,
-  // [kCtlThr] the largest published threshold key; each on a cache line of
-  // its own so that atomics of different rows never queue on one line.
-  uint32_t *ctl;      // [rows][kCtlStride]
+  // Candidate records: part (row, q) writes its records at
+  // rec[((row * parts + q) * kListCap + j) * 2 + {0, 1}] = {fp32 key bits |
+  // id << 32, exact value bits} and their number at ctl[row][kCtlCnt + q];
+  // the row's last part reads them.
+  uint64_t *rec;
+  // Per row kCtlStride words, [0] and [kCtlThr] zero between launches:
+  // [0] parts counted in, [kCtlThr] the largest published threshold key,
+  // [kCtlCnt + q] records of part q.  Each row has 512 bytes of its own so
+  // that atomics of different rows never queue on one cache line.
+  uint32_t *ctl;
   int32_t vocab;
   int32_t rows;
-  int32_t splits;
-  bool aligned;       // logits rows start 16-byte aligned
+  int32_t parts;   // blocks per row
+  int32_t cpp;     // chunks per part
+  int32_t chunks;  // chunks per row
 };
 
-// float4 loads per thread (chunk = f4 * 1024 ids) for a batch shape.
-int choose_f4(int rows, int vocab);
-// Launches the sampling kernel on `stream`.  softcap:
-// some row may have a softcap (row_params, or params.softcap > 0).
-hipError_t launch_sample(const SampleArgs &a, int f4, bool softcap, hipStream_t stream);
+// Blocks per row and chunks per part for a batch shape, aiming at `target`
+// blocks in all.
+void choose_parts(int rows, int vocab, int target, int *parts, int *cpp);
+// Blocks of the sampling kernel variant that fit on one CU at once.
+int sample_blocks_per_cu(bool mask, bool hist, bool softcap);
+// Launches the sampling kernel on `stream`.  softcap: some row may have a
+// softcap (row_params, or params.softcap > 0).
+hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
 
-// Scratch bytes of the record slots and their counts for a batch shape.
-size_t sample_rec_bytes(int rows, int splits);
-size_t sample_count_bytes(int rows, int splits);
+// Scratch bytes of the record slots for a batch shape.
+size_t sample_rec_bytes(int rows, int parts);
+// Copies rows of vocab < 4 logits into dst[rows][4], NaN past vocab.
+hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows, float *dst, hipStream_t stream);
 
 // ---------------------------------------------------------------- verify --
 // Positions are the rows of target_logits: position p = seq * (L + 1) + j,

@@ -95,6 +95,37 @@ def test_ties_take_lowest_id(sampler):
     assert (g["ids"] == 0).all()
 
 
+def test_signed_zero_ties(sampler):
+    # +0 and -0 are one value: their ties go by id, whatever the sign
+    rng = np.random.default_rng(12)
+    vocab, rows = 50000, 4
+    x = (-1.0 - np.abs(rng.standard_normal((rows, vocab)))).astype(np.float32)
+    zeros = rng.choice(vocab, 300, replace=False)
+    x[:, zeros] = np.float32(0.0)
+    x[:, zeros[::2]] = np.float32(-0.0)
+    x[1, zeros.min()] = np.float32(-0.0)       # the lowest zero id negative
+    x[2, zeros.min()] = np.float32(0.0)        # the lowest zero id positive
+    b = W.Batch("zeros", x, Params(temperature=1.0, top_k=40, top_p=0.5), uniforms=rng.random(rows))
+    g, _ = check(sampler, b, label="zeros")
+    assert np.array_equal(g["cand_ids"][0, :40], np.sort(zeros)[:40])
+    b.params = Params(temperature=0.0)
+    g, _ = check(sampler, b, label="zeros-greedy")
+    assert (g["ids"] == zeros.min()).all()
+
+
+@pytest.mark.parametrize("vocab", [1, 2, 3, 4, 5, 6, 7, 4097, 8191])
+def test_small_and_ragged_vocab(sampler, vocab):
+    # rows of fewer than 4 logits, and rows whose end cuts a float4
+    rng = np.random.default_rng(vocab)
+    rows = 5
+    x = (rng.standard_normal((rows, vocab)) * 2).astype(np.float32)
+    for p in (Params(temperature=0.0), Params(temperature=1.0, top_k=3, top_p=0.9),
+              Params(temperature=0.7, top_k=128, top_p=1.0)):
+        b = W.Batch("ragged", x, p, uniforms=rng.random(rows))
+        print(f"[gpu] ragged vocab={vocab} {p}", flush=True)
+        check(sampler, b, label=f"ragged{vocab}")
+
+
 def test_many_ties_at_threshold(sampler):
     # a few distinct levels, each shared by thousands of ids
     rng = np.random.default_rng(3)
