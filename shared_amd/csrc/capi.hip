@@ -26,7 +26,6 @@ struct sas_sampler {
   void *pad = nullptr;        // rows of fewer than 4 logits, padded to 4
   size_t pad_cap = 0;
   int cus = 0;                 // compute units of the device
-  int resident[8] = {0};       // blocks per CU of each sampling kernel variant (0: not queried)
 };
 
 namespace {
@@ -131,9 +130,9 @@ int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab) {
   if (rows < 0 || vocab < 1 || vocab > SAS_MAX_VOCAB)
     return fail(s, SAS_ERR_INVALID, "sas_reserve: rows must be >= 0 and vocab in [1, SAS_MAX_VOCAB]");
   if (int rc = set_device(s)) return rc;
-  // the most parts any batch of <= rows rows may pick
-  int parts = 0, cpp = 0;
-  sas::choose_parts(1, vocab, 0, &parts, &cpp);
+  // the most parts any batch of <= rows rows may pick (a single row)
+  int parts = 0, span = 0;
+  sas::choose_parts(1, vocab, 2 * s->cus, &parts, &span);
   return ensure_sample_scratch(s, rows, parts);
 }
 
@@ -155,13 +154,9 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
     return fail(s, SAS_ERR_INVALID, "sas_sample: uniforms are required unless every row is greedy");
   if (int rc = set_device(s)) return rc;
   const bool softcap = r->row_params != nullptr || r->params.softcap > 0.0f;
-  const int variant = (r->mask ? 4 : 0) | (r->hist_ids ? 2 : 0) | (softcap ? 1 : 0);
-  if (s->resident[variant] == 0) {
-    s->resident[variant] = sas::sample_blocks_per_cu(r->mask != nullptr, r->hist_ids != nullptr, softcap);
-    if (s->resident[variant] < 1) s->resident[variant] = 1;
-  }
-  int parts = 0, cpp = 0;
-  sas::choose_parts(r->rows, r->vocab, s->resident[variant] * s->cus, &parts, &cpp);
+  // at least two blocks per CU: small batches take shorter parts
+  int parts = 0, span = 0;
+  sas::choose_parts(r->rows, r->vocab, 2 * s->cus, &parts, &span);
   if (int rc = ensure_sample_scratch(s, r->rows, parts)) return rc;
 
   sas::SampleArgs a;
@@ -190,12 +185,13 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.out_counts = r->out_counts;
   a.out_flags = r->out_flags;
   a.rec = reinterpret_cast<uint64_t *>(s->recs);
+  a.xval = reinterpret_cast<double *>(a.rec + (size_t)r->rows * parts * sas::kListCap);
+  a.pinfo = reinterpret_cast<uint64_t *>(a.xval + (size_t)r->rows * parts * sas::kListCap);
   a.ctl = s->ctl;
   a.vocab = r->vocab;
   a.rows = r->rows;
   a.parts = parts;
-  a.cpp = cpp;
-  a.chunks = (r->vocab + sas::kChunkIds - 1) / sas::kChunkIds;
+  a.span = span;
   hipError_t e = sas::launch_sample(a, softcap, pick_stream(s, stream));
   if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
   return SAS_OK;

@@ -8,16 +8,20 @@
 
 namespace sas {
 
-// Kernel arguments of the sampling kernel (validated by sas_sample).
+// Kernel arguments of the sampling kernels (validated by sas_sample).
 //
-// A row's vocabulary is cut into chunks of kChunkIds ids; block (row, part)
-// streams chunks [part * cpp, (part + 1) * cpp) of the row.
-constexpr int kChunkIds = 4096;
-constexpr int kMaxParts = 64;   // blocks per row; the merge holds one count per part
-constexpr int kListCap = 2048;  // record slots of one part in HBM
-constexpr int kCtlStride = 128; // words per row of the control block: 512 bytes
-constexpr int kCtlThr = 32;     // second 128-byte line: the largest published threshold key
-constexpr int kCtlCnt = 64;     // third and fourth lines: records written by each part (<= kMaxParts)
+// A row's vocabulary is cut into parts of `span` ids.  The parts kernel
+// runs block (row, part) over ids [part * span, (part + 1) * span) in passes
+// of kSpanPass ids (8 float4 per thread) and writes the part's candidates
+// (every allowed value at or above the part's bound) as records; the merge
+// kernel, one block per row, selects the row's top k from them and draws.
+constexpr int kSpanPass = 8192;   // ids of one pass of a block
+constexpr int kMaxSpan = 65536;   // ids one part may span (a multiple of kSpanPass above it)
+constexpr int kMaxParts = 64;     // blocks per row
+constexpr int kListCap = 640;     // records one part may write
+constexpr int kCtlStride = 128;   // words per row of the control block: 512 bytes
+constexpr int kCtlThr = 32;       // second 128-byte line: the largest published bound (okey image)
+constexpr int kCtlFlags = 33;     // SAS_FLAG_* bits raised by the row's parts
 
 struct SampleArgs {
   const float *logits;
@@ -34,33 +38,33 @@ struct SampleArgs {
   uint32_t *out_cand_ids;
   int32_t *out_counts;
   uint32_t *out_flags;
-  // Candidate records: part (row, q) writes its records at
-  // rec[((row * parts + q) * kListCap + j) * 2 + {0, 1}] = {fp32 key bits |
-  // id << 32, exact value bits} and their number at ctl[row][kCtlCnt + q];
-  // the row's last part reads them.
+  // Records: part (row, q) writes its candidates, unordered, slot-major:
+  // rec[(row * kListCap + j) * parts + q] = {fp32 key bits, id | flag << 31}
+  // for j < the count in pinfo[row * parts + q] = {count, bound key << 32};
+  // a flagged record's exact value (above its key) is xval at the same index.
   uint64_t *rec;
-  // Per row kCtlStride words, [0] and [kCtlThr] zero between launches:
-  // [0] parts counted in, [kCtlThr] the largest published threshold key,
-  // [kCtlCnt + q] records of part q.  Each row has 512 bytes of its own so
-  // that atomics of different rows never queue on one cache line.
+  double *xval;
+  uint64_t *pinfo;
+  // Per row kCtlStride words; [kCtlThr] and [kCtlFlags] are zero between
+  // launches (the merge kernel resets them): [kCtlThr] the largest bound a
+  // part published, [kCtlFlags] flags of the parts.  Each row has 512 bytes
+  // of its own so that atomics of different rows never queue on one line.
   uint32_t *ctl;
   int32_t vocab;
   int32_t rows;
   int32_t parts;   // blocks per row
-  int32_t cpp;     // chunks per part
-  int32_t chunks;  // chunks per row
+  int32_t span;    // ids per part: a multiple of 1024, and of kSpanPass above it
 };
 
-// Blocks per row and chunks per part for a batch shape, aiming at `target`
-// blocks in all.
-void choose_parts(int rows, int vocab, int target, int *parts, int *cpp);
-// Blocks of the sampling kernel variant that fit on one CU at once.
-int sample_blocks_per_cu(bool mask, bool hist, bool softcap);
-// Launches the sampling kernel on `stream`.  softcap: some row may have a
+// Parts per row and ids per part for a batch shape: spans of one pass
+// (fewer, larger parts) unless the grid would hold fewer than
+// `min_blocks` blocks; at most kMaxParts parts per row.
+void choose_parts(int rows, int vocab, int min_blocks, int *parts, int *span);
+// Launches the parts and merge kernels on `stream`.  softcap: some row may have a
 // softcap (row_params, or params.softcap > 0).
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
 
-// Scratch bytes of the record slots for a batch shape.
+// Scratch bytes of the records and part counts for a batch shape.
 size_t sample_rec_bytes(int rows, int parts);
 // Copies rows of vocab < 4 logits into dst[rows][4], NaN past vocab.
 hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows, float *dst, hipStream_t stream);
