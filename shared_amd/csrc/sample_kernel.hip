@@ -199,6 +199,8 @@ struct MergeLds {
   double t_val[SAS_MAX_TOP_K + 1];  // the ranked top k and the one after
   uint32_t t_id[SAS_MAX_TOP_K + 1];
   uint64_t t_c[SAS_MAX_TOP_K + 1];
+  double t_p[SAS_MAX_TOP_K];        // exp weights (zero past k)
+  double t_q[SAS_MAX_TOP_K];        // weights / sum
   uint32_t m, clash;
 };
 
@@ -211,11 +213,12 @@ struct MergeOut {
 };
 
 // The reference's sample() tail (tokenizer.js:161-177) in double precision
-// over the ranked top kk in ml.t_val / ml.t_id, by wave 0.  Weights and
-// divisions run across lanes (lane i holds candidate i, and i + 64 when
-// kk > 64); each running sum is one chain in the reference's left-to-right
-// order with its operands broadcast from the lanes that hold them.
-__device__ void sample_tail(const MergeLds &ml, int kk, int row, double temperature, double top_p, double u_row,
+// over the ranked top kk in ml.t_val / ml.t_id, by wave 0.  The weights and
+// divisions run across lanes (lane i holds candidates i and i + 64) and are
+// staged in LDS; each running sum is one chain in the reference's
+// left-to-right order, run alike by every lane on operands read 8 at a time
+// (broadcast reads), its 8 partial values kept in registers for the tests.
+__device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, double top_p, double u_row,
                             uint32_t flags, MergeOut o) {
   const int lane = threadIdx.x & 63;
   const bool greedy = !(temperature > 0.0);
@@ -231,9 +234,8 @@ __device__ void sample_tail(const MergeLds &ml, int kk, int row, double temperat
     const double T = temperature;
     const double v0 = ml.t_val[0];
     const bool two = kk > 64;
-    const int n1 = two ? 64 : kk;
     // p_i = exp((v_i - v_0) / T); x / 1 is x, so the division only runs
-    // for other temperatures
+    // for other temperatures.  Weights past kk are zero.
     double p_a = 0.0, p_b = 0.0;
     if (lane < kk) {
       double d = ml.t_val[lane] - v0;
@@ -245,48 +247,93 @@ __device__ void sample_tail(const MergeLds &ml, int kk, int row, double temperat
       if (T != 1.0) d = d / T;
       p_b = fd_exp(d);
     }
+    ml.t_p[lane] = p_a;
+    ml.t_p[lane + 64] = p_b;
+    __builtin_amdgcn_wave_barrier();
+    const int nb = (kk + 7) >> 3;  // batches of 8 (zeros past kk leave every sum as it is)
     // the sum of the weights, left to right
     double run = 0.0;
-    for (int i = 0; i < n1; ++i) run = run + bcast(p_a, i);
-    for (int i = 64; i < kk; ++i) run = run + bcast(p_b, i - 64);
+    for (int b = 0; b < nb; ++b) {
+      double x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = ml.t_p[8 * b + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) run = run + x[u];
+    }
     const double sum = run;
     q_a = p_a / sum;
     if (two) q_b = p_b / sum;
+    ml.t_q[lane] = q_a;
+    ml.t_q[lane + 64] = q_b;
+    __builtin_amdgcn_wave_barrier();
     // top-p cut: the first i with p_0/sum + ... + p_i/sum >= top_p, with
     // the running weight sum beside it (the draw's mass at the cut)
-    double cum = 0.0, pre = 0.0;
-    bool te = false, hit = false;
+    double cum = 0.0, pre = 0.0, sub = 0.0;
+    bool te = false;
     cut = kk;
-    auto cut_step = [&](double pi, double qi, int i) {
-      pre = pre + pi;
-      cum = cum + qi;
-      if (fabs(cum - top_p) < 1e-6) te = true;
-      if (cum >= top_p) {
-        cut = i + 1;
-        hit = true;
+    for (int b = 0; b < nb; ++b) {
+      double xp[8], xq[8], pr[8];
+      uint32_t hit = 0u, edge = 0u;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        xp[u] = ml.t_p[8 * b + u];
+        xq[u] = ml.t_q[8 * b + u];
       }
-    };
-    for (int i = 0; i < n1 && !hit; ++i) cut_step(bcast(p_a, i), bcast(q_a, i), i);
-    for (int i = 64; i < kk && !hit; ++i) cut_step(bcast(p_b, i - 64), bcast(q_b, i - 64), i);
-    const double sub = pre;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        pre = pre + xp[u];
+        cum = cum + xq[u];
+        pr[u] = pre;
+        hit |= (cum >= top_p ? 1u : 0u) << u;
+        edge |= (fabs(cum - top_p) < 1e-6 ? 1u : 0u) << u;
+      }
+      const int left = kk - 8 * b;  // candidates of this batch
+      const uint32_t live = left >= 8 ? 0xFFu : (1u << left) - 1u;
+      hit = uni(hit) & live;
+      edge = uni(edge) & live;
+      if (hit) {
+        const int f = __builtin_ctz(hit);
+        cut = 8 * b + f + 1;
+        te |= (edge & ((2u << f) - 1u)) != 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u == f) sub = pr[u];
+        break;
+      }
+      te |= edge != 0u;
+      sub = pre;
+    }
     // r = U * (p_0 + ... + p_{cut-1}); the first i at which
     // r - p_0 - ... - p_i <= 0 is drawn, else the last of the cut
     double r = u_row * sub;
     int pick = cut - 1;
-    bool de = false, drawn = false;
-    auto draw_step = [&](double pi, int i) {
-      r = r - pi;
-      if (fabs(r) <= 1e-12 * sub) de = true;
-      if (r <= 0.0) {
-        pick = i;
-        drawn = true;
+    bool de = false;
+    const int nc = (cut + 7) >> 3;
+    for (int b = 0; b < nc; ++b) {
+      double xp[8];
+      uint32_t hit = 0u, edge = 0u;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) xp[u] = ml.t_p[8 * b + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        r = r - xp[u];
+        hit |= (r <= 0.0 ? 1u : 0u) << u;
+        edge |= (fabs(r) <= 1e-12 * sub ? 1u : 0u) << u;
       }
-    };
-    const int c1 = cut < 64 ? cut : 64;
-    for (int i = 0; i < c1 && !drawn; ++i) draw_step(bcast(p_a, i), i);
-    for (int i = 64; i < cut && !drawn; ++i) draw_step(bcast(p_b, i - 64), i);
-    if (__ballot(te)) flags |= SAS_FLAG_TOPP_EDGE;
-    if (__ballot(de)) flags |= SAS_FLAG_DRAW_EDGE;
+      const int left = cut - 8 * b;
+      const uint32_t live = left >= 8 ? 0xFFu : (1u << left) - 1u;
+      hit = uni(hit) & live;
+      edge = uni(edge) & live;
+      if (hit) {
+        const int f = __builtin_ctz(hit);
+        pick = 8 * b + f;
+        de |= (edge & ((2u << f) - 1u)) != 0u;
+        break;
+      }
+      de |= edge != 0u;
+    }
+    if (te) flags |= SAS_FLAG_TOPP_EDGE;
+    if (de) flags |= SAS_FLAG_DRAW_EDGE;
     out_id = ml.t_id[pick];
   }
   const uint32_t id_a = lane < kk ? ml.t_id[lane] : SAS_NO_TOKEN;
@@ -419,8 +466,36 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
       }
     }
   };
+  {
+    // first round: each lane's count, a ballot prefix over the count bits,
+    // one LDS atomic per wave, then the lane's own records
+    uint32_t mine = 0u;
 #pragma unroll
-  for (int r = 0; r < kMergeR; ++r) keep_one(key[r], rec[r], tid + kThreads * r);
+    for (int r = 0; r < kMergeR; ++r) mine += key[r] >= bnd ? 1u : 0u;
+    static_assert(kMergeR < 32, "a lane's survivor count fits 5 bits");
+    uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+    for (int bit = 0; bit < 5; ++bit) {
+      const uint64_t bb = __ballot((mine >> bit) & 1u);
+      pre += lanes_below(bb) << bit;
+      tot += (uint32_t)__popcll(bb) << bit;
+    }
+    if (tot) {
+      uint32_t base = 0u;
+      if (lane == 0) base = atomicAdd(&ml.m, tot);
+      uint32_t d = uni(base) + pre;
+#pragma unroll
+      for (int r = 0; r < kMergeR; ++r) {
+        if (key[r] >= bnd) {
+          if (d < (uint32_t)kSurvCap) {
+            ml.m_c[d] = composite((uint32_t)rec[r], (uint32_t)(rec[r] >> 32));
+            ml.m_g[d] = (uint32_t)(tid + kThreads * r);
+          }
+          ++d;
+        }
+      }
+    }
+  }
   // records past the first round (parts with many candidates)
   const int gend = min(NS, (int)maxc * P);
   for (int g0 = kThreads * kMergeR; g0 < gend; g0 += kThreads) {
@@ -475,19 +550,30 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     // ---- rank by composites; the first k + 1 ranks are kept ----------------------
     if ((uint32_t)tid < m8 - m) ml.m_c[m + tid] = 0ull;
     __syncthreads();
-    for (uint32_t i = (uint32_t)tid; i < m; i += kThreads) {
-      const uint64_t c = ml.m_c[i];
+    // 4, 2 or 1 threads per survivor (as m allows), each counting a share
+    // of the others; the shares are summed across the group's lanes
+    const int lg = m <= 64u ? 2 : m <= 128u ? 1 : 0;
+    const uint32_t gsz = 1u << lg;
+    const uint32_t share = ((m8 >> lg) + 7u) & ~7u;  // entries per thread, a multiple of 8
+    for (uint32_t i0 = 0; i0 < m; i0 += (uint32_t)(kThreads >> lg)) {
+      const uint32_t i = i0 + ((uint32_t)tid >> lg);
+      const uint32_t part = (uint32_t)tid & (gsz - 1u);
+      const uint64_t c = i < m ? ml.m_c[i] : ~0ull;
       // a flagged record's exact value: loaded while the rank is counted
-      const double xv = (c & kXFlag) ? xrow[ml.m_g[i]] : (double)fkey((uint32_t)(c >> 32));
+      const bool lead = i < m && part == 0u;
+      const double xv = lead && (c & kXFlag) ? xrow[ml.m_g[i]] : (double)fkey((uint32_t)(c >> 32));
       uint32_t rank = 0u;
-      for (uint32_t j = 0; j < m8; j += 8) {
+      const uint32_t j0 = part * share, j1 = min(j0 + share, m8);
+      for (uint32_t j = j0; j < j1; j += 8) {
         uint64_t o[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) o[u] = ml.m_c[j + u];
 #pragma unroll
         for (int u = 0; u < 8; ++u) rank += o[u] > c ? 1u : 0u;
       }
-      if (rank <= (uint32_t)k) {
+      if (lg >= 1) rank += (uint32_t)__shfl_xor((int)rank, 1, 64);
+      if (lg >= 2) rank += (uint32_t)__shfl_xor((int)rank, 2, 64);
+      if (lead && rank <= (uint32_t)k) {
         ml.t_c[rank] = c;
         ml.t_id[rank] = comp_id(c);
         ml.t_val[rank] = xv;
