@@ -59,6 +59,22 @@ constexpr uint32_t kIdBits = 0x7FFFFFFFu;
 // The value of the wave's first active lane (wave-uniform values).
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// One row's parameters from the per-row array: read as 32-bit words by
+// nontemporal loads, so that the compiler never forms a pointer that may
+// point into the kernel's by-value arguments (which would copy them to
+// scratch memory).
+__device__ __forceinline__ sas_params load_row_params(const sas_params *q) {
+  static_assert(sizeof(sas_params) % 4 == 0, "whole words");
+  union {
+    sas_params p;
+    uint32_t w[sizeof(sas_params) / 4];
+  } u;
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(q);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(sas_params) / 4); ++i) u.w[i] = __builtin_nontemporal_load(src + i);
+  return u.p;
+}
+
 // Lane i's double on every lane (i wave-uniform).
 __device__ __forceinline__ double bcast(double x, int i) {
   const uint64_t b = (uint64_t)__double_as_longlong(x);
@@ -118,7 +134,7 @@ __device__ __forceinline__ bool key_ge(const Key96 &a, const Key96 &b) {
 // taken whole (the bits below stay zero: exactly `need` keys reach the
 // result).  LDS: hist[256], sel[3].  Block-wide; every thread returns it.
 template <typename ForKeys>
-__device__ Key96 block_select96(ForKeys for_keys, uint32_t need, uint32_t *hist, uint32_t *sel) {
+__device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need, uint32_t *hist, uint32_t *sel) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   Key96 res{{0u, 0u, 0u}};
   for (int pass = 0; pass < 12; ++pass) {
@@ -201,7 +217,7 @@ struct MergeLds {
   uint64_t t_c[SAS_MAX_TOP_K + 1];
   double t_p[SAS_MAX_TOP_K];        // exp weights (zero past k)
   double t_q[SAS_MAX_TOP_K];        // weights / sum
-  uint32_t m, clash;
+  uint32_t m, clash, rflags;
 };
 
 struct MergeOut {
@@ -378,8 +394,9 @@ __device__ __forceinline__ uint32_t rank_exact(const double *vals, const uint32_
   return rank;
 }
 
-constexpr int kMergeR = 16;  // record slots per thread in the first round
+constexpr int kMergeR = 20;  // record slots per thread in the first round
 
+template <bool kRowParams>
 __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs a) {
   __shared__ MergeLds ml;
   __shared__ uint32_t s_hist[256];
@@ -387,7 +404,11 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = blockIdx.x;
   const int P = a.parts;
-  const sas_params p = a.row_params ? a.row_params[row] : a.params;
+  // shared parameters come from the kernel arguments (scalar loads, no
+  // wait for a vector load before the first round is issued)
+  sas_params p;
+  if constexpr (kRowParams) p = load_row_params(a.row_params + row);
+  else p = a.params;
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
   const double u_row = greedy ? 0.0 : a.uniforms[row];
@@ -400,7 +421,8 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
 
   // ---- round 1: counts, bounds, flags and records, every load in flight ----
   const uint64_t my_info = lane < P ? pin[lane] : 0ull;
-  const uint32_t rflags_v = ctl[kCtlFlags];
+  // the parts' flags: read and then reset by thread 0 alone
+  const uint32_t rflags_v = tid == 0 ? ctl[kCtlFlags] : 0u;
   uint64_t rec[kMergeR];
 #pragma unroll
   for (int r = 0; r < kMergeR; ++r) {
@@ -412,12 +434,13 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   const uint32_t total = wave_sum_u32(my_cnt);
   const uint32_t maxc = wave_max_u32(my_cnt);
   const uint32_t pbound = wave_max_u32((uint32_t)(my_info >> 32));
-  const uint32_t rflags = uni(rflags_v);
   if (tid == 0) {
     ml.m = 0u;
     ml.clash = 0u;
+    ml.rflags = rflags_v;
   }
   __syncthreads();
+  const uint32_t rflags = ml.rflags;
   if (tid == 0) {
     // read by every part of this launch: reset for the next one
     ctl[kCtlThr] = 0u;
@@ -430,18 +453,27 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   uint32_t key[kMergeR];
   uint32_t kmax = 0u;
   {
+    // every slot's part count read at once (no branch, one LDS wait), then
+    // the keys of the slots that hold a record
+    uint32_t cq[kMergeR];
+    int ss[kMergeR];
     int s = s0, q = q0;
 #pragma unroll
     for (int r = 0; r < kMergeR; ++r) {
-      const bool ok = tid + kThreads * r < NS && (uint32_t)s < ml.cnt[q];
-      key[r] = ok ? okey(__uint_as_float((uint32_t)rec[r])) : 0u;
-      kmax = max(kmax, key[r]);
+      ss[r] = s;
+      cq[r] = ml.cnt[q];
       s += ds;
       q += dq;
-      if (q >= P) {
-        q -= P;
-        ++s;
-      }
+      const bool wrap = q >= P;
+      q = wrap ? q - P : q;
+      s = wrap ? s + 1 : s;
+    }
+#pragma unroll
+    for (int r = 0; r < kMergeR; ++r) {
+      const bool ok = (tid + kThreads * r < NS) & ((uint32_t)ss[r] < cq[r]);
+      const uint32_t kx = okey(__uint_as_float((uint32_t)rec[r]));
+      key[r] = ok ? kx : 0u;
+      kmax = max(kmax, key[r]);
     }
   }
   const int jw = (k + kWaves - 1) / kWaves;
@@ -667,7 +699,8 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   const int lo = part * a.span;
   const int nids = min(a.span, vocab - lo);  // > 0
 
-  const sas_params p = a.row_params ? a.row_params[row] : a.params;
+  sas_params p = a.params;
+  if (a.row_params) p = load_row_params(a.row_params + row);
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
   const float softcap = kSoftcap ? p.softcap : 0.0f;
@@ -724,7 +757,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
     s_nx = 0u;
     s_flags = 0u;
   }
-  auto set_bit = [&](uint32_t id, int base) {
+  auto set_bit = [&](uint32_t id, int base) __attribute__((always_inline)) {
     const uint32_t off = id - (uint32_t)base;
     if (off < (uint32_t)min(kSpanPass, lo + nids - base)) atomicOr(&L.hbits[off >> 5], 1u << (off & 31u));
   };
@@ -736,7 +769,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
     L.hbits[tid] = 0u;
     if (tid == 0) L.hover = 0u;
     lds_barrier();
-    auto insert = [&](uint32_t id) {
+    auto insert = [&](uint32_t id) __attribute__((always_inline)) {
       const uint32_t off = id - (uint32_t)lo;
       if (off >= (uint32_t)nids) return;
       set_bit(id, lo);
@@ -758,7 +791,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
     lds_barrier();
   }
   // occurrences of a history member of the part
-  auto hcount = [&](uint32_t id) -> uint32_t {
+  auto hcount = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
     uint32_t sl = hash_slot(id);
     for (int probe = 0; probe < kHashSlots; ++probe) {
       const uint32_t kk = L.hkey[sl];
@@ -773,7 +806,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   };
   // exact value of a history member: CTRL repetition, then OpenAI frequency
   // and presence (presence alone is tokenizer.js:157)
-  auto hist_value = [&](uint32_t id, float x, uint32_t mw, double &val) -> bool {
+  auto hist_value = [&](uint32_t id, float x, uint32_t mw, double &val) __attribute__((always_inline)) -> bool {
     if (kMask && !((mw >> (id & 31u)) & 1u)) return false;
     if (kSoftcap && softcap > 0.0f) x = softcap_f32(x, softcap);
     if (x != x) return false;
@@ -1048,7 +1081,10 @@ hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) 
     case 6: launch_parts<true, true, false>(a, stream); break;
     default: launch_parts<true, true, true>(a, stream); break;
   }
-  hipLaunchKernelGGL(sample_merge_kernel, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+  if (a.row_params)
+    hipLaunchKernelGGL(sample_merge_kernel<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(sample_merge_kernel<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
