@@ -10,8 +10,9 @@ than 512 MB so the 256 MB Infinity Cache cannot serve them.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C3P]
 
-Prints ONE JSON line (rank 0): rows/s, the roofline of the sampling kernel
-(algorithmic bytes / average launch time, HIP events on the launch stream)
+Prints ONE JSON line (rank 0): rows/s, the roofline of the sampling step
+(its two launches, sas::sample_parts_kernel then sas::sample_merge_kernel:
+algorithmic bytes / average step time, HIP events on the launch stream)
 and the CPU baseline: the Node restatement of the reference's JS sampling
 path timed on this host's cores on a bounded sample of the same workload.
 """
@@ -30,7 +31,7 @@ if ROOT not in sys.path:
 
 METRIC = "rows/s + % HBM peak: 262k-vocab penalties+mask+top-k/top-p, B=128"
 HBM_PEAK_GBPS = 8000.0
-KERNEL = "sample_kernel"
+KERNEL = "sampler_step"  # the profiles/ summaries of the two launches of one step
 WORKLOAD_DOC = {
     "C2": "T0.7 top-k40 top-p0.95, vocab 151936, batch 64, Zipf-biased N(0,3) logits",
     "C3": "bitmask 0.5-20% + top-k50 top-p0.9 T1.0, vocab 262144, batch 128, N(0,4) logits",
@@ -207,7 +208,8 @@ def main() -> int:
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": KERNEL, "algorithmic_bytes_per_launch": set_bytes},
+                     "kernel": "sas::sample_parts_kernel + sas::sample_merge_kernel (one step)",
+                     "algorithmic_bytes_per_launch": set_bytes},
         "cpu_baseline": None,
     }
     if base is not None:
