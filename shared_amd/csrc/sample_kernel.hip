@@ -48,9 +48,8 @@ constexpr int kSlots = kSpanPass / (4 * kThreads);  // float4 per thread per pas
 static_assert(kSlots == 8, "a thread holds 32 values of a pass");
 constexpr int kHashSlots = 512;
 constexpr int kHistPre = 2;                          // history ids per thread loaded before the logits
-constexpr int kWaveCap = 128;                        // entries of one wave's list
-static_assert(kListCap >= kWaves * kWaveCap + SAS_MAX_TOP_K, "a part's records: its four lists and its exact entries");
-static_assert(kWaveCap >= SAS_MAX_TOP_K, "an exact part selection fits one wave's region");
+constexpr int kQuadCap = 64;                         // float4 entries of one wave's candidate list
+static_assert(kQuadCap == 64, "a wave's list is one entry per lane at the end");
 constexpr int kSurvCap = 512;                        // survivors the merge ranks
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kXFlag = 0x80000000u;             // record id flag: the exact value lies above the key
@@ -268,13 +267,20 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
     __builtin_amdgcn_wave_barrier();
     const int nb = (kk + 7) >> 3;  // batches of 8 (zeros past kk leave every sum as it is)
     // the sum of the weights, left to right
+    // (each chain reads the next batch of 8 while it adds the current one)
     double run = 0.0;
-    for (int b = 0; b < nb; ++b) {
-      double x[8];
+    double x[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = ml.t_p[8 * b + u];
+    for (int u = 0; u < 8; ++u) x[u] = ml.t_p[u];
+    for (int b = 0; b < nb; ++b) {
+      const int bn = b + 1 < nb ? b + 1 : b;
+      double y[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) y[u] = ml.t_p[8 * bn + u];
 #pragma unroll
       for (int u = 0; u < 8; ++u) run = run + x[u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = y[u];
     }
     const double sum = run;
     q_a = p_a / sum;
@@ -287,13 +293,20 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
     double cum = 0.0, pre = 0.0, sub = 0.0;
     bool te = false;
     cut = kk;
+    double xp[8], xq[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      xp[u] = ml.t_p[u];
+      xq[u] = ml.t_q[u];
+    }
     for (int b = 0; b < nb; ++b) {
-      double xp[8], xq[8], pr[8];
+      const int bn = b + 1 < nb ? b + 1 : b;
+      double yp[8], yq[8], pr[8];
       uint32_t hit = 0u, edge = 0u;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        xp[u] = ml.t_p[8 * b + u];
-        xq[u] = ml.t_q[8 * b + u];
+        yp[u] = ml.t_p[8 * bn + u];
+        yq[u] = ml.t_q[8 * bn + u];
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -318,6 +331,11 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
       }
       te |= edge != 0u;
       sub = pre;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        xp[u] = yp[u];
+        xq[u] = yq[u];
+      }
     }
     // r = U * (p_0 + ... + p_{cut-1}); the first i at which
     // r - p_0 - ... - p_i <= 0 is drawn, else the last of the cut
@@ -325,11 +343,14 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
     int pick = cut - 1;
     bool de = false;
     const int nc = (cut + 7) >> 3;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) xp[u] = ml.t_p[u];
     for (int b = 0; b < nc; ++b) {
-      double xp[8];
+      const int bn = b + 1 < nc ? b + 1 : b;
+      double yp[8];
       uint32_t hit = 0u, edge = 0u;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) xp[u] = ml.t_p[8 * b + u];
+      for (int u = 0; u < 8; ++u) yp[u] = ml.t_p[8 * bn + u];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         r = r - xp[u];
@@ -347,6 +368,8 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
         break;
       }
       de |= edge != 0u;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) xp[u] = yp[u];
     }
     if (te) flags |= SAS_FLAG_TOPP_EDGE;
     if (de) flags |= SAS_FLAG_DRAW_EDGE;
@@ -596,6 +619,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
       const double xv = lead && (c & kXFlag) ? xrow[ml.m_g[i]] : (double)fkey((uint32_t)(c >> 32));
       uint32_t rank = 0u;
       const uint32_t j0 = part * share, j1 = min(j0 + share, m8);
+#pragma unroll 4
       for (uint32_t j = j0; j < j1; j += 8) {
         uint64_t o[8];
 #pragma unroll
@@ -665,8 +689,8 @@ struct PartLds {
   uint32_t hcnt[kHashSlots];
   uint32_t hbits[kPassWords];   // history membership of the pass's ids
   uint32_t comb[kPassWords];    // the pass's ids to select from: allowed, not history, inside the part
-  uint32_t l_key[kListCap];     // per-wave candidate lists: fp32 value bits, id
-  uint32_t l_id[kListCap];
+  float4 q_val[kWaves * kQuadCap];     // per-wave candidate lists: float4s with a value at the bound
+  uint32_t q_base[kWaves * kQuadCap];  // and the id of their first value
   double x_val[kXCap];          // exact-valued entries: value, id
   uint32_t x_id[kXCap];
   uint32_t hover;               // some history id did not fit in the hash
@@ -678,7 +702,8 @@ static_assert(kHashSlots == 512, "hash_slot yields 9 bits");
 template <bool kMask, bool kHist, bool kSoftcap>
 __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs a) {
   __shared__ PartLds L;
-  __shared__ uint32_t s_nw[kWaves];   // entries of each wave's list (may pass kWaveCap: overflow)
+  __shared__ uint32_t s_nw[kWaves];   // records of each wave's list
+  __shared__ uint32_t s_qover;        // a wave's list overflowed
   __shared__ uint32_t s_thr[kWaves];
   __shared__ uint32_t s_hist[256];
   __shared__ uint32_t s_sel[4];
@@ -753,6 +778,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
 
   // ---- the part's history: (id, count) hash, the first pass's bitmap -----------
   if (tid < kWaves) s_nw[tid] = 0u;
+  if (tid == 0) s_qover = 0u;
   if (tid == 0) {
     s_nx = 0u;
     s_flags = 0u;
@@ -818,7 +844,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   const int jw = (k + kWaves - 1) / kWaves;  // per-wave rank of the bound
   const uint32_t sh = 4u * (uint32_t)(tid & 7);
   uint32_t tkey = 0u;  // the part's bound (okey image; 0 = none)
-  uint32_t n_w = 0u;   // entries of this wave's list
+  uint32_t n_q = 0u;   // float4 entries of this wave's list (may pass kQuadCap: overflow)
   auto run_pass = [&](int base) __attribute__((always_inline)) {
     // the history members of this thread's word: the first one's logit is
     // loaded now, while the pass's loads are in flight
@@ -875,22 +901,21 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
     const uint32_t teff = max(tkey, thr0);
     // keys at or below okey(-inf) (0 or truncated) admit every valid value
     const float tf = teff > 0x007FFFFFu ? fkey(teff) : -__builtin_inff();
+    // whole float4s with a value at or above the bound go to the list (one
+    // ballot per float4); their values are cut to the final bound at the end
 #pragma unroll
     for (int f = 0; f < kSlots; ++f) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x = j == 0 ? v[f].x : j == 1 ? v[f].y : j == 2 ? v[f].z : v[f].w;
-        const bool pass = x >= tf;
-        const uint64_t bb = __ballot(pass);
-        if (bb) {
-          const uint32_t cnt = (uint32_t)__popcll(bb);
-          if (n_w + cnt <= (uint32_t)kWaveCap && pass) {
-            const uint32_t d = (uint32_t)wave * kWaveCap + n_w + lanes_below(bb);
-            L.l_key[d] = __float_as_uint(x);
-            L.l_id[d] = (uint32_t)(base + 1024 * f + 4 * tid + j);
-          }
-          n_w += cnt;
+      const float m4 = fmaxf(fmaxf(v[f].x, v[f].y), fmaxf(v[f].z, v[f].w));
+      const bool pass = m4 >= tf;
+      const uint64_t bb = __ballot(pass);
+      if (bb) {
+        const uint32_t cnt = (uint32_t)__popcll(bb);
+        if (n_q + cnt <= (uint32_t)kQuadCap && pass) {
+          const uint32_t d = (uint32_t)wave * kQuadCap + n_q + lanes_below(bb);
+          L.q_val[d] = v[f];
+          L.q_base[d] = (uint32_t)(base + 1024 * f + 4 * tid);
         }
+        n_q += cnt;
       }
     }
     // the history members of this thread's word: exact penalized values
@@ -928,14 +953,34 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   }
   if (tid == 0 && tkey > thr0)
     __hip_atomic_fetch_max(ctl + kCtlThr, tkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (lane == 0) s_nw[wave] = n_w;
+  // this wave's list, one float4 per lane, cut to the final bound: each
+  // lane's values at or above it, and their places among the wave's records
+  const uint32_t tfin = max(tkey, thr0);
+  const float tff = tfin > 0x007FFFFFu ? fkey(tfin) : -__builtin_inff();
+  const uint32_t qat = (uint32_t)wave * kQuadCap + (uint32_t)lane;
+  const bool qin = (uint32_t)lane < n_q && n_q <= (uint32_t)kQuadCap;
+  const float4 q = qin ? L.q_val[qat] : make_float4(qnan(), qnan(), qnan(), qnan());
+  const uint32_t qid = L.q_base[qat];
+  uint32_t pm = (q.x >= tff ? 1u : 0u) | (q.y >= tff ? 2u : 0u) | (q.z >= tff ? 4u : 0u) | (q.w >= tff ? 8u : 0u);
+  const uint32_t qcnt = (uint32_t)__popc(pm);
+  uint32_t qpre = 0u, qtot = 0u;
+#pragma unroll
+  for (int bit = 0; bit < 3; ++bit) {
+    const uint64_t bb = __ballot((qcnt >> bit) & 1u);
+    qpre += lanes_below(bb) << bit;
+    qtot += (uint32_t)__popcll(bb) << bit;
+  }
+  if (lane == 0) {
+    s_nw[wave] = qtot;
+    if (n_q > (uint32_t)kQuadCap) s_qover = 1u;
+  }
   __syncthreads();
   uint32_t nw[kWaves];
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) nw[w] = s_nw[w];
   uint32_t nx = s_nx;
-  const bool overflow = nw[0] > (uint32_t)kWaveCap || nw[1] > (uint32_t)kWaveCap || nw[2] > (uint32_t)kWaveCap ||
-                        nw[3] > (uint32_t)kWaveCap || nx > (uint32_t)kXCap;
+  const bool overflow = s_qover != 0u || nx > (uint32_t)kXCap ||
+                        nw[0] + nw[1] + nw[2] + nw[3] + min(nx, (uint32_t)kXCap) > (uint32_t)kListCap;
   if (overflow) {
     // more values at or above the bound than the lists hold (ties): the
     // part's exact top k by a radix select over (value, id) keys, every
@@ -993,20 +1038,27 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) nw[w] = s_nw[w];
     nx = s_nx;
+    pm = 0u;
   }
 
-  // ---- records: each wave's list after those of the waves before it, then --
+  // ---- records: each wave's values after those of the waves before it, then
   // the exact-valued entries (record j of this part at row index j * P + part)
   uint32_t off = 0u;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) off += w < wave ? nw[w] : 0u;
-  const uint32_t mine = wave == 0 ? nw[0] : wave == 1 ? nw[1] : wave == 2 ? nw[2] : nw[3];
   const uint32_t nplain = nw[0] + nw[1] + nw[2] + nw[3];
   uint64_t *rrow = a.rec + (int64_t)row * kListCap * P + part;
   double *xrow = a.xval + (int64_t)row * kListCap * P + part;
-  for (uint32_t i = (uint32_t)lane; i < mine; i += 64u) {
-    const uint32_t at = (uint32_t)wave * kWaveCap + i;
-    rrow[(int64_t)(off + i) * P] = (uint64_t)L.l_key[at] | ((uint64_t)L.l_id[at] << 32);
+  {
+    uint32_t j = off + qpre;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if ((pm >> c) & 1u) {
+        const float x = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
+        rrow[(int64_t)j * P] = (uint64_t)__float_as_uint(x) | ((uint64_t)(qid + (uint32_t)c) << 32);
+        ++j;
+      }
+    }
   }
   if ((uint32_t)tid < nx) {
     // an exact value's round-down key, flagged when the value lies above it
