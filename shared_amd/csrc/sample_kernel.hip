@@ -681,7 +681,8 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
 
 constexpr int kPassWords = kSpanPass / 32;  // mask / history words of one pass: one per thread
 static_assert(kPassWords == kThreads, "one word of 32 ids per thread");
-constexpr int kXCap = 128;                  // exact-valued entries of a part
+constexpr int kXCap = 256;                  // exact-valued entries of a part: history members, or an exact selection
+static_assert(kXCap == kThreads, "one exact entry per thread");
 static_assert(kXCap >= SAS_MAX_TOP_K, "an exact part selection fits the exact list");
 
 struct PartLds {
@@ -689,6 +690,7 @@ struct PartLds {
   uint32_t hcnt[kHashSlots];
   uint32_t hbits[kPassWords];   // history membership of the pass's ids
   uint32_t comb[kPassWords];    // the pass's ids to select from: allowed, not history, inside the part
+  uint32_t hmem[kPassWords];    // the pass's allowed history members
   float4 q_val[kWaves * kQuadCap];     // per-wave candidate lists: float4s with a value at the bound
   uint32_t q_base[kWaves * kQuadCap];  // and the id of their first value
   double x_val[kXCap];          // exact-valued entries: value, id
@@ -708,6 +710,8 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   __shared__ uint32_t s_hist[256];
   __shared__ uint32_t s_sel[4];
   __shared__ uint32_t s_nx;           // exact-valued entries (may pass kXCap: overflow)
+  __shared__ uint32_t s_nxk;          // exact-valued entries kept at the end
+  __shared__ uint32_t s_nxw;          // exact-valued records written
   __shared__ uint32_t s_flags;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -781,6 +785,8 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   if (tid == 0) s_qover = 0u;
   if (tid == 0) {
     s_nx = 0u;
+    s_nxk = 0u;
+    s_nxw = 0u;
     s_flags = 0u;
   }
   auto set_bit = [&](uint32_t id, int base) __attribute__((always_inline)) {
@@ -846,16 +852,14 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
   uint32_t tkey = 0u;  // the part's bound (okey image; 0 = none)
   uint32_t n_q = 0u;   // float4 entries of this wave's list (may pass kQuadCap: overflow)
   auto run_pass = [&](int base) __attribute__((always_inline)) {
-    // the history members of this thread's word: the first one's logit is
-    // loaded now, while the pass's loads are in flight
+    // the history members of this thread's word
     const uint32_t hb = has_hist ? L.hbits[tid] : 0u;
-    float hx0 = 0.0f;
-    if (hb) hx0 = lrow[base + 32 * tid + __builtin_ctz(hb)];
     // ids to select from, 32 per word: allowed, not history, inside the part
     {
       const int rem = lo + nids - (base + 32 * tid);
       uint32_t cw = rem >= 32 ? ~0u : rem > 0 ? (1u << rem) - 1u : 0u;
       L.comb[tid] = cw & mword & ~hb;
+      L.hmem[tid] = cw & mword & hb;
     }
     lds_barrier();
     float m = qnan();
@@ -879,6 +883,24 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
         v[f].y = softcap_f32(v[f].y, softcap);
         v[f].z = softcap_f32(v[f].z, softcap);
         v[f].w = softcap_f32(v[f].w, softcap);
+      }
+      if (has_hist) {
+        // allowed history members of this float4: their values (in the
+        // registers now) and ids go to the exact list, penalized after the
+        // passes
+        const uint32_t hn = (L.hmem[32 * f + (tid >> 3)] >> sh) & 0xFu;
+        if (__ballot(hn != 0u)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if ((hn >> j) & 1u) {
+              const uint32_t d = atomicAdd(&s_nx, 1u);
+              if (d < (uint32_t)kXCap) {
+                L.x_val[d] = (double)(j == 0 ? v[f].x : j == 1 ? v[f].y : j == 2 ? v[f].z : v[f].w);
+                L.x_id[d] = (uint32_t)(base + 1024 * f + 4 * tid + j);
+              }
+            }
+          }
+        }
       }
       // bit j of the nibble -> all ones or zero, then one bit-field insert
       // keeps the value or puts a quiet NaN in its place
@@ -916,23 +938,6 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
           L.q_base[d] = (uint32_t)(base + 1024 * f + 4 * tid);
         }
         n_q += cnt;
-      }
-    }
-    // the history members of this thread's word: exact penalized values
-    uint32_t bits = hb;
-    bool first = true;
-    while (bits) {
-      const uint32_t b = (uint32_t)__builtin_ctz(bits);
-      bits &= bits - 1u;
-      const uint32_t id = (uint32_t)(base + 32 * tid) + b;
-      const float x = first ? hx0 : lrow[id];
-      first = false;
-      double val;
-      if (!hist_value(id, x, mword, val) || !(val >= (double)tf)) continue;
-      const uint32_t d = atomicAdd(&s_nx, 1u);
-      if (d < (uint32_t)kXCap) {
-        L.x_val[d] = val;
-        L.x_id[d] = id;
       }
     }
   };
@@ -975,12 +980,21 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
     if (n_q > (uint32_t)kQuadCap) s_qover = 1u;
   }
   __syncthreads();
+  // the history members' exact values, kept at or above the final bound
+  // (NaN ones never are)
+  bool xw = false;  // this thread writes exact entry tid
+  if (has_hist && (uint32_t)tid < min(s_nx, (uint32_t)kXCap)) {
+    const double val = penalize(L.x_val[tid], hcount(L.x_id[tid]), p);
+    L.x_val[tid] = val;
+    xw = val >= (double)tff;
+    if (xw) atomicAdd(&s_nxk, 1u);
+  }
+  __syncthreads();
   uint32_t nw[kWaves];
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) nw[w] = s_nw[w];
-  uint32_t nx = s_nx;
-  const bool overflow = s_qover != 0u || nx > (uint32_t)kXCap ||
-                        nw[0] + nw[1] + nw[2] + nw[3] + min(nx, (uint32_t)kXCap) > (uint32_t)kListCap;
+  uint32_t nx = s_nxk;
+  const bool overflow = s_qover != 0u || s_nx > (uint32_t)kXCap || nw[0] + nw[1] + nw[2] + nw[3] + nx > (uint32_t)kListCap;
   if (overflow) {
     // more values at or above the bound than the lists hold (ties): the
     // part's exact top k by a radix select over (value, id) keys, every
@@ -1038,6 +1052,7 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) nw[w] = s_nw[w];
     nx = s_nx;
+    xw = (uint32_t)tid < nx;
     pm = 0u;
   }
 
@@ -1060,12 +1075,12 @@ __global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs
       }
     }
   }
-  if ((uint32_t)tid < nx) {
+  if (xw) {
     // an exact value's round-down key, flagged when the value lies above it
     const double val = L.x_val[tid];
     const float kf = rd_f32(val);
     const uint32_t idf = L.x_id[tid] | ((double)kf != val ? kXFlag : 0u);
-    const int64_t j = (int64_t)(nplain + tid) * P;
+    const int64_t j = (int64_t)(nplain + atomicAdd(&s_nxw, 1u)) * P;
     rrow[j] = (uint64_t)__float_as_uint(kf) | ((uint64_t)idf << 32);
     if (idf & kXFlag) xrow[j] = val;
   }
