@@ -702,7 +702,7 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t id) { return (id * 265443
 static_assert(kHashSlots == 512, "hash_slot yields 9 bits");
 
 template <bool kMask, bool kHist, bool kSoftcap>
-__global__ __launch_bounds__(kThreads) void sample_parts_kernel(const SampleArgs a) {
+__global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6) void sample_parts_kernel(const SampleArgs a) {
   __shared__ PartLds L;
   __shared__ uint32_t s_nw[kWaves];   // records of each wave's list
   __shared__ uint32_t s_qover;        // a wave's list overflowed
