@@ -308,13 +308,23 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
         yp[u] = ml.t_p[8 * bn + u];
         yq[u] = ml.t_q[8 * bn + u];
       }
+      double cv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         pre = pre + xp[u];
         cum = cum + xq[u];
         pr[u] = pre;
-        hit |= (cum >= top_p ? 1u : 0u) << u;
-        edge |= (fabs(cum - top_p) < 1e-6 ? 1u : 0u) << u;
+        cv[u] = cum;
+      }
+      // the running mass never decreases (zero weights past kk leave it as
+      // it is): a batch whose last value lies 1e-6 or more below top_p holds
+      // neither the cut nor an edge
+      if (cum - top_p > -1e-6) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          hit |= (cv[u] >= top_p ? 1u : 0u) << u;
+          edge |= (fabs(cv[u] - top_p) < 1e-6 ? 1u : 0u) << u;
+        }
       }
       const int left = kk - 8 * b;  // candidates of this batch
       const uint32_t live = left >= 8 ? 0xFFu : (1u << left) - 1u;
@@ -351,11 +361,20 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
       uint32_t hit = 0u, edge = 0u;
 #pragma unroll
       for (int u = 0; u < 8; ++u) yp[u] = ml.t_p[8 * bn + u];
+      double rv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         r = r - xp[u];
-        hit |= (r <= 0.0 ? 1u : 0u) << u;
-        edge |= (fabs(r) <= 1e-12 * sub ? 1u : 0u) << u;
+        rv[u] = r;
+      }
+      // the residual never increases: a batch whose last value lies above
+      // 1e-12 * sub holds neither the draw nor an edge
+      if (r <= 1e-12 * sub) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          hit |= (rv[u] <= 0.0 ? 1u : 0u) << u;
+          edge |= (fabs(rv[u]) <= 1e-12 * sub ? 1u : 0u) << u;
+        }
       }
       const int left = cut - 8 * b;
       const uint32_t live = left >= 8 ? 0xFFu : (1u << left) - 1u;
