@@ -140,7 +140,7 @@ __device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need,
     const int w = pass >> 2;
     const int sh = 24 - 8 * (pass & 3);
     const uint32_t hm = sh == 24 ? 0u : ~0u << (sh + 8);
-    hist[tid] = 0u;
+    for (int i = tid; i < 256; i += (int)blockDim.x) hist[i] = 0u;
     __syncthreads();
     // word w of a key by selects (no indexed registers)
     auto word = [&](const Key96 &x) { return w == 0 ? x.w[0] : w == 1 ? x.w[1] : x.w[2]; };
@@ -204,9 +204,12 @@ __device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need,
 
 // ----------------------------------------------------------------- merge --
 
+constexpr int kMThreads = 256;   // threads of a merge block (more measured no faster)
+constexpr int kMWaves = kMThreads / 64;
+
 struct MergeLds {
   uint32_t cnt[kMaxParts];          // records of each part
-  uint32_t thr[kWaves];
+  uint32_t thr[kMWaves];
   uint64_t m_c[kSurvCap + 8];       // survivors: composites (zero-padded to a multiple of 8)
   uint32_t m_g[kSurvCap];           // their record index in the row
   double m_v[kSurvCap + 8];         // exact values (exact ranking only; sentinel padded)
@@ -439,7 +442,7 @@ __device__ __forceinline__ uint32_t rank_exact(const double *vals, const uint32_
 constexpr int kMergeR = 20;  // record slots per thread in the first round
 
 template <bool kRowParams>
-__global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs a) {
+__global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArgs a) {
   __shared__ MergeLds ml;
   __shared__ uint32_t s_hist[256];
   __shared__ uint32_t s_sel[4];
@@ -468,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   uint64_t rec[kMergeR];
 #pragma unroll
   for (int r = 0; r < kMergeR; ++r) {
-    const int g = tid + kThreads * r;
+    const int g = tid + kMThreads * r;
     rec[r] = g < NS ? __builtin_nontemporal_load(rrow + g) : 0ull;
   }
   const uint32_t my_cnt = (uint32_t)my_info;
@@ -488,9 +491,9 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     ctl[kCtlThr] = 0u;
     ctl[kCtlFlags] = 0u;
   }
-  // slot g = tid + 256 r is record s of part q: (s, q) stepped without division
+  // slot g = tid + kMThreads r is record s of part q: (s, q) stepped without division
   const int s0 = tid / P, q0 = tid - s0 * P;
-  const int ds = kThreads / P, dq = kThreads - ds * P;
+  const int ds = kMThreads / P, dq = kMThreads - ds * P;
   // ---- the bound ----------------------------------------------------------------
   uint32_t key[kMergeR];
   uint32_t kmax = 0u;
@@ -512,17 +515,20 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     }
 #pragma unroll
     for (int r = 0; r < kMergeR; ++r) {
-      const bool ok = (tid + kThreads * r < NS) & ((uint32_t)ss[r] < cq[r]);
+      const bool ok = (tid + kMThreads * r < NS) & ((uint32_t)ss[r] < cq[r]);
       const uint32_t kx = okey(__uint_as_float((uint32_t)rec[r]));
       key[r] = ok ? kx : 0u;
       kmax = max(kmax, key[r]);
     }
   }
-  const int jw = (k + kWaves - 1) / kWaves;
+  const int jw = (k + kMWaves - 1) / kMWaves;
   const uint32_t tw = wave_jth_largest_key16(kmax, jw);
   if (lane == 0) ml.thr[wave] = tw;
   __syncthreads();
-  const uint32_t bnd = max(pbound, max(min(min(ml.thr[0], ml.thr[1]), min(ml.thr[2], ml.thr[3])), 1u));
+  uint32_t tmin = 0xFFFFFFFFu;
+#pragma unroll
+  for (int w = 0; w < kMWaves; ++w) tmin = min(tmin, ml.thr[w]);
+  const uint32_t bnd = max(pbound, max(tmin, 1u));
   // ---- survivors: composites and record indices ----------------------------------
   auto keep_one = [&](uint32_t kk, uint64_t rc, int g) {
     const bool keep = kk >= bnd;
@@ -563,7 +569,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
         if (key[r] >= bnd) {
           if (d < (uint32_t)kSurvCap) {
             ml.m_c[d] = composite((uint32_t)rec[r], (uint32_t)(rec[r] >> 32));
-            ml.m_g[d] = (uint32_t)(tid + kThreads * r);
+            ml.m_g[d] = (uint32_t)(tid + kMThreads * r);
           }
           ++d;
         }
@@ -572,7 +578,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   }
   // records past the first round (parts with many candidates)
   const int gend = min(NS, (int)maxc * P);
-  for (int g0 = kThreads * kMergeR; g0 < gend; g0 += kThreads) {
+  for (int g0 = kMThreads * kMergeR; g0 < gend; g0 += kMThreads) {
     const int g = g0 + tid;
     const int s = g / P;
     const bool ok = g < gend && (uint32_t)s < ml.cnt[g - s * P];
@@ -587,10 +593,10 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     // too many survivors (ties): exact select over every record
     flags |= SAS_FLAG_SLOW_SELECT;
     exact = true;
-    const int rounds = (gend + kThreads - 1) / kThreads;
+    const int rounds = (gend + kMThreads - 1) / kMThreads;
     auto for_recs = [&](auto f) {
       for (int i = 0; i < rounds; ++i) {
-        const int g = i * kThreads + tid;
+        const int g = i * kMThreads + tid;
         const int s = g / P;
         const bool ok = g < gend && (uint32_t)s < ml.cnt[g - s * P];
         double v = 0.0;
@@ -624,12 +630,13 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     // ---- rank by composites; the first k + 1 ranks are kept ----------------------
     if ((uint32_t)tid < m8 - m) ml.m_c[m + tid] = 0ull;
     __syncthreads();
-    // 4, 2 or 1 threads per survivor (as m allows), each counting a share
-    // of the others; the shares are summed across the group's lanes
-    const int lg = m <= 64u ? 2 : m <= 128u ? 1 : 0;
+    // up to 8 threads per survivor (as m allows), each counting a share of
+    // the others; the shares are summed across the group's lanes
+    int lg = 0;
+    while (lg < 3 && (uint32_t)(kMThreads >> (lg + 1)) >= m) ++lg;
     const uint32_t gsz = 1u << lg;
     const uint32_t share = ((m8 >> lg) + 7u) & ~7u;  // entries per thread, a multiple of 8
-    for (uint32_t i0 = 0; i0 < m; i0 += (uint32_t)(kThreads >> lg)) {
+    for (uint32_t i0 = 0; i0 < m; i0 += (uint32_t)(kMThreads >> lg)) {
       const uint32_t i = i0 + ((uint32_t)tid >> lg);
       const uint32_t part = (uint32_t)tid & (gsz - 1u);
       const uint64_t c = i < m ? ml.m_c[i] : ~0ull;
@@ -648,6 +655,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
       }
       if (lg >= 1) rank += (uint32_t)__shfl_xor((int)rank, 1, 64);
       if (lg >= 2) rank += (uint32_t)__shfl_xor((int)rank, 2, 64);
+      if (lg >= 3) rank += (uint32_t)__shfl_xor((int)rank, 4, 64);
       if (lead && rank <= (uint32_t)k) {
         ml.t_c[rank] = c;
         ml.t_id[rank] = comp_id(c);
@@ -666,7 +674,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     if (ml.clash) {
       exact = true;
       flags |= SAS_FLAG_SLOW_SELECT;
-      for (uint32_t i = (uint32_t)tid; i < m; i += kThreads) {
+      for (uint32_t i = (uint32_t)tid; i < m; i += kMThreads) {
         const uint64_t c = ml.m_c[i];
         ml.m_id[i] = comp_id(c);
         ml.m_v[i] = (c & kXFlag) ? xrow[ml.m_g[i]] : (double)fkey((uint32_t)(c >> 32));
@@ -679,7 +687,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
       ml.m_id[m + tid] = kEmpty;
     }
     __syncthreads();
-    for (uint32_t i = (uint32_t)tid; i < m; i += kThreads) {
+    for (uint32_t i = (uint32_t)tid; i < m; i += kMThreads) {
       const double v = ml.m_v[i];
       const uint32_t id = ml.m_id[i];
       const uint32_t rank = rank_exact(ml.m_v, ml.m_id, m8, v, id);
@@ -1168,9 +1176,9 @@ hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) 
     default: launch_parts<true, true, true>(a, stream); break;
   }
   if (a.row_params)
-    hipLaunchKernelGGL(sample_merge_kernel<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(sample_merge_kernel<true>, dim3((unsigned)a.rows), dim3(kMThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(sample_merge_kernel<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(sample_merge_kernel<false>, dim3((unsigned)a.rows), dim3(kMThreads), 0, stream, a);
   return hipGetLastError();
 }
 
