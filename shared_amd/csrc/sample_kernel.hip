@@ -447,7 +447,10 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
   __shared__ uint32_t s_hist[256];
   __shared__ uint32_t s_sel[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = blockIdx.x;
+  // the XCD that ran the row's parts (the parts kernel gives each XCD a
+  // contiguous run of rows): the row's records may still be in its L2
+  int row = blockIdx.x;
+  if ((a.rows & 7) == 0 && ((a.rows * a.parts) & 7) == 0) row = (row & 7) * (a.rows >> 3) + (row >> 3);
   const int P = a.parts;
   // shared parameters come from the kernel arguments (scalar loads, no
   // wait for a vector load before the first round is issued)
