@@ -505,16 +505,27 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
     // the keys of the slots that hold a record
     uint32_t cq[kMergeR];
     int ss[kMergeR];
-    int s = s0, q = q0;
+    if (dq == 0) {
+      // the part count divides the block: every slot of a thread is its one
+      // part's, at records s0, s0 + ds, ...
+      const uint32_t c0 = ml.cnt[q0];
 #pragma unroll
-    for (int r = 0; r < kMergeR; ++r) {
-      ss[r] = s;
-      cq[r] = ml.cnt[q];
-      s += ds;
-      q += dq;
-      const bool wrap = q >= P;
-      q = wrap ? q - P : q;
-      s = wrap ? s + 1 : s;
+      for (int r = 0; r < kMergeR; ++r) {
+        ss[r] = s0 + r * ds;
+        cq[r] = c0;
+      }
+    } else {
+      int s = s0, q = q0;
+#pragma unroll
+      for (int r = 0; r < kMergeR; ++r) {
+        ss[r] = s;
+        cq[r] = ml.cnt[q];
+        s += ds;
+        q += dq;
+        const bool wrap = q >= P;
+        q = wrap ? q - P : q;
+        s = wrap ? s + 1 : s;
+      }
     }
 #pragma unroll
     for (int r = 0; r < kMergeR; ++r) {
