@@ -452,8 +452,21 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
   int row = blockIdx.x;
   if ((a.rows & 7) == 0 && ((a.rows * a.parts) & 7) == 0) row = (row & 7) * (a.rows >> 3) + (row >> 3);
   const int P = a.parts;
-  // shared parameters come from the kernel arguments (scalar loads, no
-  // wait for a vector load before the first round is issued)
+  const uint64_t *pin = a.pinfo + (int64_t)row * P;
+  // record j of part q: index j * P + q of the row
+  const uint64_t *rrow = a.rec + (int64_t)row * kListCap * P;
+  const int NS = kListCap * P;
+
+  // ---- round 1: records and counts first, every load in flight, then the ---
+  // row's parameters, uniform and flags (their scalar loads are not waited
+  // for before the records are requested)
+  uint64_t rec[kMergeR];
+#pragma unroll
+  for (int r = 0; r < kMergeR; ++r) {
+    const int g = tid + kMThreads * r;
+    rec[r] = g < NS ? __builtin_nontemporal_load(rrow + g) : 0ull;
+  }
+  const uint64_t my_info = lane < P ? pin[lane] : 0ull;
   sas_params p;
   if constexpr (kRowParams) p = load_row_params(a.row_params + row);
   else p = a.params;
@@ -461,22 +474,9 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
   const double u_row = greedy ? 0.0 : a.uniforms[row];
   uint32_t *ctl = a.ctl + (int64_t)row * kCtlStride;
-  const uint64_t *pin = a.pinfo + (int64_t)row * P;
-  // record j of part q: index j * P + q of the row
-  const uint64_t *rrow = a.rec + (int64_t)row * kListCap * P;
   const double *xrow = a.xval + (int64_t)row * kListCap * P;
-  const int NS = kListCap * P;
-
-  // ---- round 1: counts, bounds, flags and records, every load in flight ----
-  const uint64_t my_info = lane < P ? pin[lane] : 0ull;
   // the parts' flags: read and then reset by thread 0 alone
   const uint32_t rflags_v = tid == 0 ? ctl[kCtlFlags] : 0u;
-  uint64_t rec[kMergeR];
-#pragma unroll
-  for (int r = 0; r < kMergeR; ++r) {
-    const int g = tid + kMThreads * r;
-    rec[r] = g < NS ? __builtin_nontemporal_load(rrow + g) : 0ull;
-  }
   const uint32_t my_cnt = (uint32_t)my_info;
   if (wave == 0 && lane < P) ml.cnt[lane] = my_cnt;
   const uint32_t total = wave_sum_u32(my_cnt);
