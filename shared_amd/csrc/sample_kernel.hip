@@ -860,7 +860,17 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     };
 #pragma unroll
     for (int j = 0; j < kHistPre; ++j) insert(hpre[j]);
-    for (int i = h0 + kHistPre * kThreads + tid; i < h1; i += kThreads) insert(a.hist_ids[i]);
+    // longer histories: rounds of 8 ids per thread, all 8 loads in flight
+    for (int i0 = h0 + kHistPre * kThreads + tid; i0 < h1; i0 += 8 * kThreads) {
+      uint32_t hb8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * kThreads;
+        hb8[j] = i < h1 ? a.hist_ids[i] : kEmpty;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) insert(hb8[j]);
+    }
     lds_barrier();
   }
   // occurrences of a history member of the part
