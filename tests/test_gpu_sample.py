@@ -176,6 +176,31 @@ def test_history_edge_ids(sampler):
     check(sampler, b, label="hist")
 
 
+def test_dense_and_long_histories(sampler):
+    # history members packed into whole float4s and words, members that stay
+    # in the top k after their penalties, more distinct members in one part
+    # than its exact list holds (the part's exact fallback), and a history
+    # longer than the ids a block loads up front
+    rng = np.random.default_rng(17)
+    vocab, rows = 20000, 5
+    x = (rng.standard_normal((rows, vocab)) * 2).astype(np.float32)
+    x[1, 2048:2348] += 6.0                                   # members that win despite the penalties
+    x[4, :64] = np.float32(9.0)                              # tied members at the top
+    hist = [np.arange(0, 600),                               # 600 distinct ids in the row's first ids
+            np.arange(2048, 2348),                           # contiguous: every id of whole words
+            rng.integers(0, vocab, 5000),                    # long, with repeats
+            np.zeros(0, np.int64),
+            np.concatenate([np.arange(0, 64), np.arange(0, 64)])]
+    hi, ho = W._csr(hist)
+    for p in (Params(temperature=1.0, top_k=40, top_p=0.95, repetition_penalty=1.2, presence_penalty=0.3,
+                     frequency_penalty=0.1),
+              Params(temperature=0.0, repetition_penalty=1.2, presence_penalty=0.3),
+              Params(temperature=0.8, top_k=128, top_p=1.0, repetition_penalty=0.8)):  # penalties that raise
+        b = W.Batch("dense_hist", x, p, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+        print(f"[gpu] dense/long histories {p}", flush=True)
+        check(sampler, b, label="dense_hist")
+
+
 def test_repeated_launches_reset_state(sampler):
     b = W.c3p(rows=32, vocab=50000)
     first = run_gpu(sampler, b)
