@@ -95,8 +95,12 @@ __device__ __forceinline__ double fd_exp(double x) {
   }
   double t = x * x;
   double c = x - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
-  if (k == 0) return 1.0 - ((x * c) / (c - 2.0) - x);
-  double y = 1.0 - ((lo - (x * c) / (2.0 - c)) - hi);
+  // fdlibm's (x*c)/(c-2) and (x*c)/(2-c) are one quotient and its exact
+  // negation (IEEE subtraction and division are sign-symmetric), so both
+  // branches share one division: lo - (x*c)/(2-c) is lo + q to the bit.
+  const double q = (x * c) / (c - 2.0);
+  if (k == 0) return 1.0 - (q - x);
+  double y = 1.0 - ((lo + q) - hi);
   if (k >= -1021) {
     if (k == 1024) return y * 2.0 * 8.988465674311579539e307;
     return y * __longlong_as_double((long long)(uint64_t)(0x3ff00000u + ((uint32_t)k << 20)) << 32);
