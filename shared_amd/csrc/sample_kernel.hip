@@ -14,9 +14,7 @@
 //   3. the bound: every wave finds the j-th largest of its 64 lane maxima
 //      (j = ceil(k / 4)) by a ballot search on order-preserving keys, and the
 //      part's bound is the smallest of the four: at least 4 j >= k values of
-//      the part reach it, so no value below it is in the row's top k.  It is
-//      published to the row (an atomic max), and the largest bound other
-//      parts published earlier is used as well;
+//      the part reach it, so no value below it is in the row's top k;
 //   4. values at or above the bound go to per-wave LDS lists (one ballot per
 //      value slot); the part's history ids are handled one by one with their
 //      exact penalized double values;
@@ -80,10 +78,6 @@ __device__ __forceinline__ double bcast(double x, int i) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, i);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), i);
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-
-__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Barrier over the block's LDS accesses alone: it waits for this wave's LDS
@@ -491,7 +485,6 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
   const uint32_t rflags = ml.rflags;
   if (tid == 0) {
     // read by every part of this launch: reset for the next one
-    ctl[kCtlThr] = 0u;
     ctl[kCtlFlags] = 0u;
   }
   // slot g = tid + kMThreads r is record s of part q: (s, q) stepped without division
@@ -777,8 +770,6 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const float *lrow = a.logits + (int64_t)row * a.logits_stride;
   const uint32_t *mrow = kMask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
   uint32_t *ctl = a.ctl + (int64_t)row * kCtlStride;
-  // the largest bound a part of this row published before this block started
-  const uint32_t thr0 = ld_agent(ctl + kCtlThr);
 
   // ---- history ids (loaded first: the tables fill while the logits load) ----
   int h0 = 0, h1 = 0;
@@ -971,9 +962,8 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     if (lane == 0) s_thr[wave] = tw;
     lds_barrier();
     tkey = max(tkey, min(min(s_thr[0], s_thr[1]), min(s_thr[2], s_thr[3])));
-    const uint32_t teff = max(tkey, thr0);
     // keys at or below okey(-inf) (0 or truncated) admit every valid value
-    const float tf = teff > 0x007FFFFFu ? fkey(teff) : -__builtin_inff();
+    const float tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
     // whole float4s with a value at or above the bound go to the list (one
     // ballot per float4); their values are cut to the final bound at the end
 #pragma unroll
@@ -1007,12 +997,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     lds_barrier();
     run_pass(base);
   }
-  if (tid == 0 && tkey > thr0)
-    __hip_atomic_fetch_max(ctl + kCtlThr, tkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // this wave's list, one float4 per lane, cut to the final bound: each
   // lane's values at or above it, and their places among the wave's records
-  const uint32_t tfin = max(tkey, thr0);
-  const float tff = tfin > 0x007FFFFFu ? fkey(tfin) : -__builtin_inff();
+  const float tff = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
   const uint32_t qat = (uint32_t)wave * kQuadCap + (uint32_t)lane;
   const bool qin = (uint32_t)lane < n_q && n_q <= (uint32_t)kQuadCap;
   const float4 q = qin ? L.q_val[qat] : make_float4(qnan(), qnan(), qnan(), qnan());

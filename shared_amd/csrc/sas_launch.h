@@ -20,8 +20,7 @@ constexpr int kMaxSpan = 65536;   // ids one part may span (a multiple of kSpanP
 constexpr int kMaxParts = 64;     // blocks per row
 constexpr int kListCap = 640;     // records one part may write
 constexpr int kCtlStride = 128;   // words per row of the control block: 512 bytes
-constexpr int kCtlThr = 32;       // second 128-byte line: the largest published bound (okey image)
-constexpr int kCtlFlags = 33;     // SAS_FLAG_* bits raised by the row's parts
+constexpr int kCtlFlags = 32;     // second 128-byte line: SAS_FLAG_* bits raised by the row's parts
 
 struct SampleArgs {
   const float *logits;
@@ -45,10 +44,10 @@ struct SampleArgs {
   uint64_t *rec;
   double *xval;
   uint64_t *pinfo;
-  // Per row kCtlStride words; [kCtlThr] and [kCtlFlags] are zero between
-  // launches (the merge kernel resets them): [kCtlThr] the largest bound a
-  // part published, [kCtlFlags] flags of the parts.  Each row has 512 bytes
-  // of its own so that atomics of different rows never queue on one line.
+  // Per row kCtlStride words; [kCtlFlags], the flags of the row's parts, is
+  // zero between launches (the merge kernel resets it).  Each row has 512
+  // bytes of its own so that atomics of different rows never queue on one
+  // line.
   uint32_t *ctl;
   int32_t vocab;
   int32_t rows;
