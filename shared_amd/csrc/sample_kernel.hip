@@ -1017,9 +1017,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     s_nw[wave] = qtot;
     if (n_q > (uint32_t)kQuadCap) s_qover = 1u;
   }
-  __syncthreads();
   // the history members' exact values, kept at or above the final bound
-  // (NaN ones never are)
+  // (NaN ones never are).  The list is complete: every wave recorded its
+  // members before the last pass's bound barrier.
   bool xw = false;  // this thread writes exact entry tid
   if (has_hist && (uint32_t)tid < min(s_nx, (uint32_t)kXCap)) {
     const double val = penalize(L.x_val[tid], hcount(L.x_id[tid]), p);
