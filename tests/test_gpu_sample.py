@@ -126,6 +126,20 @@ def test_small_and_ragged_vocab(sampler, vocab):
         check(sampler, b, label=f"ragged{vocab}")
 
 
+@pytest.mark.parametrize("vocab,rows", [(524_289, 3), (1_000_003, 3), (2_000_000, 4)])
+def test_multi_pass_parts(sampler, vocab, rows):
+    # vocabularies past 64 parts of 8,192 ids: every part runs 2 or 4 passes
+    # of 8,192 ids (its history bitmap rebuilt per pass, its lists and bound
+    # carried across them); 524,289 leaves a last part of one id, and the
+    # ragged ends cut the row's last float4
+    for i, p in enumerate((Params(temperature=0.8, top_k=100, top_p=0.9, repetition_penalty=1.2,
+                                  presence_penalty=0.4, frequency_penalty=0.2),
+                           Params(temperature=0.0, repetition_penalty=1.3))):
+        b = _small_batch(7 + i, rows=rows, vocab=vocab, params=p, mask_density=[0.3, None][i], hist=2000)
+        print(f"[gpu] multi-pass vocab={vocab} rows={rows} {p}", flush=True)
+        check(sampler, b, label=f"multipass{vocab}")
+
+
 def test_many_ties_at_threshold(sampler):
     # a few distinct levels, each shared by thousands of ids
     rng = np.random.default_rng(3)
