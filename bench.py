@@ -52,6 +52,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work of the baseline sample (0 disables it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--row-params", action="store_true",
+                    help="pass the workload's parameters per row (row_params, with the no-softcap hint) "
+                         "instead of one sas_params for every row")
     ap.add_argument("--calibrate-copy-mb", type=float, default=0.0,
                     help="instead of the benchmark, run device-to-device copies of this many MB (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -147,6 +150,7 @@ def main() -> int:
     import torch
 
     from shared_amd import Sampler
+    from shared_amd._capi import FLAG_TOPP_EDGE
 
     if not torch.cuda.is_available():
         print("bench.py: no HIP device is visible", file=sys.stderr)
@@ -165,11 +169,26 @@ def main() -> int:
                          hist_ids=dev(b.hist_ids, torch.int32), hist_offsets=dev(b.hist_offsets),
                          uniforms=dev(b.uniforms), params=b.params))
     rows, vocab = first.rows, first.vocab
+    if args.row_params:
+        from shared_amd import pack_params
+        from shared_amd.sampler import row_hints
+        plist = [first.params] * rows
+        rp = dev(pack_params(plist).view(np.uint8))
+        for st in sets:
+            st["row_params"] = rp
+            st["row_hints"] = row_hints(plist)
     out_ids = [torch.empty(rows, dtype=torch.int32, device="cuda") for _ in sets]
     stream = torch.cuda.current_stream()
 
     with Sampler(0) as s:
         s.reserve(rows, vocab)
+        # untimed: the rows whose top-p running mass lies within 1e-6 of top_p
+        # (SAS_FLAG_TOPP_EDGE), over every input set
+        flags = torch.empty(rows, dtype=torch.int32, device="cuda")
+        edge_rows = 0
+        for j in range(nsets):
+            s.sample_into(out_ids=out_ids[j], out_flags=flags, stream=stream, **sets[j])
+            edge_rows += int(((flags & FLAG_TOPP_EDGE) != 0).sum().item())
         for i in range(args.warmup):
             j = i % nsets
             s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
@@ -204,7 +223,10 @@ def main() -> int:
         "config": {"workload": f"{args.workload}: {WORKLOAD_DOC[args.workload]}", "rows": rows, "vocab": vocab,
                    "top_k": first.params.top_k, "top_p": first.params.top_p,
                    "temperature": first.params.temperature, "input_sets": nsets,
-                   "rotating_set_mb": round(nsets * set_bytes / 1e6, 1)},
+                   "rotating_set_mb": round(nsets * set_bytes / 1e6, 1),
+                   "params": "per row (row_params)" if args.row_params else "one sas_params for every row"},
+        "topp_edge_rows": {"rows": edge_rows, "of": nsets * rows,
+                           "rule": "top-p running mass within 1e-6 of top_p (SAS_FLAG_TOPP_EDGE)"},
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define SAS_ABI_VERSION 1
+#define SAS_ABI_VERSION 2
 
 /* Largest top_k honoured; the request API accepts 1..128
  * (lib/completions.ts:271).  The reference GPU path caps at 20
@@ -63,6 +63,10 @@ extern "C" {
 #define SAS_FLAG_TOPP_EDGE 2u      /* a running top-p mass was within 1e-6 of top_p */
 #define SAS_FLAG_DRAW_EDGE 4u      /* the draw residual was within 1e-12*mass of 0 */
 #define SAS_FLAG_SLOW_SELECT 8u    /* exact tie-safe fallback selection ran */
+
+/* sas_rows.row_hints bits: facts about row_params the caller vouches for,
+ * so the library can pick a cheaper kernel variant.  0 assumes nothing. */
+#define SAS_HINT_NO_SOFTCAP 1u     /* no row of row_params has softcap > 0 */
 
 /* TokenMask kinds (lib/webgpu-llm/tool-constraint.ts:39-42). */
 #define SAS_MASK_ALL 0
@@ -107,7 +111,10 @@ typedef struct sas_rows {
                                   row uses the same words (one grammar state) */
   const uint32_t *hist_ids;    /* device, all rows' histories back to back, or NULL */
   const int32_t *hist_offsets; /* device [rows + 1]: row r owns
-                                  hist_ids[hist_offsets[r] .. hist_offsets[r+1]) */
+                                  hist_ids[hist_offsets[r] .. hist_offsets[r+1]);
+                                  non-decreasing, each row at most SAS_MAX_HISTORY ids
+                                  (the kernels clamp: a row's range is cut to
+                                  [0, hist_count] and to SAS_MAX_HISTORY ids) */
   const double *uniforms;      /* device [rows], U in [0, 1); may be NULL when every
                                   row is greedy */
   sas_params params;           /* used for every row unless row_params is set */
@@ -119,6 +126,9 @@ typedef struct sas_rows {
                                   top-k candidate ids */
   int32_t *out_counts;         /* device [rows][2] or NULL: {k, cut} (0,0 greedy) */
   uint32_t *out_flags;         /* device [rows] or NULL: SAS_FLAG_* bits */
+  int64_t hist_count;          /* ids in hist_ids, >= 1 when hist_ids is set: no row
+                                  reads past it */
+  uint32_t row_hints;          /* SAS_HINT_* bits about row_params (0 = none) */
 } sas_rows;
 
 /*

@@ -33,6 +33,7 @@ MAX_DRAFT = _header_define("SAS_MAX_DRAFT")
 NO_TOKEN = 0xFFFFFFFF
 OK, ERR_INVALID, ERR_HIP, ERR_NOMEM = 0, 1, 2, 3
 FLAG_EMPTY_ROW, FLAG_TOPP_EDGE, FLAG_DRAW_EDGE, FLAG_SLOW_SELECT = 1, 2, 4, 8
+HINT_NO_SOFTCAP = 1
 MASK_ALL, MASK_ALLOW, MASK_DENY = 0, 1, 2
 
 
@@ -66,6 +67,8 @@ class SasRows(ctypes.Structure):
         ("out_cand_ids", c_void_p),
         ("out_counts", c_void_p),
         ("out_flags", c_void_p),
+        ("hist_count", c_int64),
+        ("row_hints", c_uint32),
     ]
 
 

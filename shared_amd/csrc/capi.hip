@@ -26,6 +26,10 @@ struct sas_sampler {
   void *pad = nullptr;        // rows of fewer than 4 logits, padded to 4
   size_t pad_cap = 0;
   int cus = 0;                 // compute units of the device
+  // The stream of the handle's last launch: a handle's calls are ordered by
+  // the caller, so its scratch is idle once that stream has drained.
+  hipStream_t last_stream = nullptr;
+  bool launched = false;
 };
 
 namespace {
@@ -44,12 +48,19 @@ int hip_fail(sas_sampler *s, hipError_t e, const char *what) {
 
 hipStream_t pick_stream(sas_sampler *, void *stream) { return reinterpret_cast<hipStream_t>(stream); }
 
-// Grow a scratch buffer; waits for queued work before freeing the old one.
+// Wait for the handle's last launch (its scratch may still be in use).
+hipError_t drain(sas_sampler *s) {
+  if (!s->launched) return hipSuccess;
+  return hipStreamSynchronize(s->last_stream);
+}
+
+// Grow a scratch buffer; waits for the handle's queued work before freeing
+// the old one (that stream only: other streams of the process run on).
 int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
   if (need <= *cap) return SAS_OK;
   hipError_t e;
   if (*buf) {
-    if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(s, e, "hipDeviceSynchronize");
+    if ((e = drain(s)) != hipSuccess) return hip_fail(s, e, "hipStreamSynchronize");
     if ((e = hipFree(*buf)) != hipSuccess) return hip_fail(s, e, "hipFree");
     *buf = nullptr;
     *cap = 0;
@@ -87,7 +98,7 @@ int set_device(sas_sampler *s) {
 
 extern "C" {
 
-const char *sas_version(void) { return "shared_amd_sampler 1 gfx950"; }
+const char *sas_version(void) { return "shared_amd_sampler 2 gfx950"; }
 
 int sas_create(int device, sas_sampler **out) {
   if (!out) return fail(nullptr, SAS_ERR_INVALID, "sas_create: out is NULL");
@@ -114,7 +125,7 @@ int sas_create(int device, sas_sampler **out) {
 void sas_destroy(sas_sampler *s) {
   if (!s) return;
   (void)hipSetDevice(s->device);
-  (void)hipDeviceSynchronize();
+  (void)drain(s);
   if (s->recs) (void)hipFree(s->recs);
   if (s->ctl) (void)hipFree(s->ctl);
   if (s->vscratch) (void)hipFree(s->vscratch);
@@ -149,11 +160,16 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
     return fail(s, SAS_ERR_INVALID, "sas_sample: mask_stride must be 0 or >= ceil(vocab / 32)");
   if (r->hist_ids && !r->hist_offsets)
     return fail(s, SAS_ERR_INVALID, "sas_sample: hist_ids requires hist_offsets");
+  if (r->hist_ids && r->hist_count < 1)
+    return fail(s, SAS_ERR_INVALID, "sas_sample: hist_count must be >= 1 with hist_ids");
   const bool all_greedy = !r->row_params && !(r->params.temperature > 0.0);
   if (!r->uniforms && !all_greedy)
     return fail(s, SAS_ERR_INVALID, "sas_sample: uniforms are required unless every row is greedy");
   if (int rc = set_device(s)) return rc;
-  const bool softcap = r->row_params != nullptr || r->params.softcap > 0.0f;
+  // the softcap kernel variants (fewer waves per SIMD) only when some row
+  // may have a softcap
+  const bool softcap =
+      r->row_params ? (r->row_hints & SAS_HINT_NO_SOFTCAP) == 0u : r->params.softcap > 0.0f;
   // at least two blocks per CU: small batches take shorter parts
   int parts = 0, span = 0;
   sas::choose_parts(r->rows, r->vocab, 2 * s->cus, &parts, &span);
@@ -176,6 +192,7 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.mask_stride = r->mask_stride;
   a.hist_ids = r->hist_ids;
   a.hist_offsets = r->hist_ids ? r->hist_offsets : nullptr;
+  a.hist_count = r->hist_ids ? r->hist_count : 0;
   a.uniforms = r->uniforms;
   a.row_params = r->row_params;
   a.params = r->params;
@@ -193,6 +210,8 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.parts = parts;
   a.span = span;
   hipError_t e = sas::launch_sample(a, softcap, pick_stream(s, stream));
+  s->last_stream = pick_stream(s, stream);
+  s->launched = true;
   if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
   return SAS_OK;
 }
@@ -244,6 +263,8 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
   a.aligned = (reinterpret_cast<uintptr_t>(v->target_logits) & 15u) == 0 &&
               (reinterpret_cast<uintptr_t>(v->draft_logits) & 15u) == 0 && (v->logits_stride & 3) == 0;
   hipError_t e = sas::launch_verify(a, pick_stream(s, stream));
+  s->last_stream = pick_stream(s, stream);
+  s->launched = true;
   if (e != hipSuccess) return hip_fail(s, e, "sas_verify launch");
   return SAS_OK;
 }

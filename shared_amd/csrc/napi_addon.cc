@@ -8,12 +8,21 @@
 // is free while the GPU works (the reference awaits mapAsync the same way,
 // lib/webgpu-llm/model.js:724).  Errors throw a JS Error carrying
 // sas_last_error().  Host code only: no HIP header is needed here.
+//
+// A handle is not re-entrant, so every call on it holds the handle's mutex
+// for the whole C call, the async ones on their worker thread included: a
+// synchronous call made while a worker runs waits for it instead of racing
+// it.  destroy() takes the mutex too, marks the handle closed (later calls
+// throw "sampler is closed") and frees the C handle; the wrapper itself
+// lives until the JS external is collected, and queued async work holds a
+// reference to that external, so no worker ever sees freed memory.
 #define NAPI_VERSION 8
 #include <node_api.h>
 
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "shared_amd_sampler.h"
@@ -106,12 +115,30 @@ napi_value make_ptr(napi_env env, const void *p) {
   return v;
 }
 
-sas_sampler *get_handle(napi_env env, napi_value v) {
+// What the JS external holds: the C handle and its call lock.
+struct Handle {
+  sas_sampler *s = nullptr;
+  std::mutex mu;
+  bool closed = false;
+};
+
+Handle *get_wrapper(napi_env env, napi_value v) {
   void *p = nullptr;
   napi_valuetype t;
   if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) return nullptr;
   napi_get_value_external(env, v, &p);
-  return reinterpret_cast<sas_sampler *>(p);
+  return reinterpret_cast<Handle *>(p);
+}
+
+void finalize_handle(napi_env, void *data, void *) {
+  Handle *h = static_cast<Handle *>(data);
+  {
+    std::lock_guard<std::mutex> g(h->mu);
+    if (!h->closed && h->s) sas_destroy(h->s);
+    h->s = nullptr;
+    h->closed = true;
+  }
+  delete h;
 }
 
 bool read_params(napi_env env, napi_value obj, sas_params *p) {
@@ -165,7 +192,10 @@ bool read_rows(napi_env env, napi_value d, sas_rows *r) {
             get_ptr(env, d, "outProbs", (void **)&r->out_probs) &&
             get_ptr(env, d, "outCandIds", (void **)&r->out_cand_ids) &&
             get_ptr(env, d, "outCounts", (void **)&r->out_counts) &&
-            get_ptr(env, d, "outFlags", (void **)&r->out_flags);
+            get_ptr(env, d, "outFlags", (void **)&r->out_flags) && get_i64(env, d, "histCount", &r->hist_count);
+  int64_t hints = 0;
+  ok = ok && get_i64(env, d, "rowHints", &hints);
+  r->row_hints = (uint32_t)hints;
   if (!ok || vocab < INT32_MIN || vocab > INT32_MAX || rows < INT32_MIN || rows > INT32_MAX) return false;
   r->vocab = (int32_t)vocab;
   r->rows = (int32_t)rows;
@@ -219,24 +249,46 @@ napi_value Create(napi_env env, napi_callback_info info) {
   sas_sampler *s = nullptr;
   int rc = sas_create(device, &s);
   if (rc != SAS_OK) return throw_sas(env, nullptr, rc);
+  Handle *h = new Handle();
+  h->s = s;
   napi_value ext;
-  NAPI_OK(napi_create_external(env, s, nullptr, nullptr, &ext));
+  if (napi_create_external(env, h, finalize_handle, nullptr, &ext) != napi_ok) {
+    sas_destroy(s);
+    delete h;
+    return throw_napi(env, "napi_create_external");
+  }
   return ext;
 }
 
 napi_value Destroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!args(env, info, 1, argv)) return throw_napi(env, "arguments");
-  sas_destroy(get_handle(env, argv[0]));
+  Handle *h = get_wrapper(env, argv[0]);
+  if (!h) {
+    napi_throw_type_error(env, nullptr, "sas_napi: expected a sampler handle");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(h->mu);
+  if (!h->closed && h->s) sas_destroy(h->s);
+  h->s = nullptr;
+  h->closed = true;
   return undefined(env);
 }
 
-#define HANDLE_OR_THROW(v, s)                                        \
-  sas_sampler *s = get_handle(env, v);                               \
-  if (!s) {                                                          \
+// Binds `s` to the handle's C sampler with its mutex held until the end of
+// the enclosing scope; throws when the value is no handle or it is closed.
+#define HANDLE_OR_THROW(v, s)                                                   \
+  Handle *s##_w = get_wrapper(env, v);                                          \
+  if (!s##_w) {                                                                 \
     napi_throw_type_error(env, nullptr, "sas_napi: expected a sampler handle"); \
-    return nullptr;                                                  \
-  }
+    return nullptr;                                                             \
+  }                                                                             \
+  std::lock_guard<std::mutex> s##_lock(s##_w->mu);                              \
+  if (s##_w->closed) {                                                          \
+    napi_throw_error(env, nullptr, "sampler is closed");                        \
+    return nullptr;                                                             \
+  }                                                                             \
+  sas_sampler *s = s##_w->s;
 
 napi_value Reserve(napi_env env, napi_callback_info info) {
   napi_value argv[3];
@@ -353,7 +405,8 @@ napi_value Verify(napi_env env, napi_callback_info info) {
 struct AsyncCall {
   napi_async_work work = nullptr;
   napi_deferred deferred = nullptr;
-  sas_sampler *s = nullptr;
+  napi_ref handle_ref = nullptr;  // keeps the handle's external alive until completion
+  Handle *h = nullptr;
   bool verify = false;
   sas_rows rows;
   sas_verify_rows vrows;
@@ -363,13 +416,21 @@ struct AsyncCall {
 
 void async_execute(napi_env, void *data) {
   AsyncCall *c = static_cast<AsyncCall *>(data);
-  c->rc = c->verify ? sas_verify(c->s, &c->vrows, sas_stream(c->s)) : sas_sample(c->s, &c->rows, sas_stream(c->s));
-  if (c->rc == SAS_OK) c->rc = sas_synchronize(c->s, sas_stream(c->s));
-  if (c->rc != SAS_OK) c->err = sas_last_error(c->s);
+  std::lock_guard<std::mutex> g(c->h->mu);
+  if (c->h->closed) {
+    c->rc = SAS_ERR_INVALID;
+    c->err = "sampler is closed";
+    return;
+  }
+  sas_sampler *s = c->h->s;
+  c->rc = c->verify ? sas_verify(s, &c->vrows, sas_stream(s)) : sas_sample(s, &c->rows, sas_stream(s));
+  if (c->rc == SAS_OK) c->rc = sas_synchronize(s, sas_stream(s));
+  if (c->rc != SAS_OK) c->err = sas_last_error(s);
 }
 
 void async_complete(napi_env env, napi_status, void *data) {
   AsyncCall *c = static_cast<AsyncCall *>(data);
+  if (c->handle_ref) napi_delete_reference(env, c->handle_ref);
   if (c->rc == SAS_OK) {
     napi_resolve_deferred(env, c->deferred, undefined(env));
   } else {
@@ -384,48 +445,72 @@ void async_complete(napi_env env, napi_status, void *data) {
   delete c;
 }
 
-napi_value start_async(napi_env env, AsyncCall *c, const char *name) {
+napi_value start_async(napi_env env, AsyncCall *c, napi_value handle, const char *name) {
   napi_value promise, rname;
+  if (napi_create_reference(env, handle, 1, &c->handle_ref) != napi_ok) {
+    delete c;
+    return throw_napi(env, "napi_create_reference");
+  }
   if (napi_create_promise(env, &c->deferred, &promise) != napi_ok) {
+    napi_delete_reference(env, c->handle_ref);
     delete c;
     return throw_napi(env, "napi_create_promise");
   }
   napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &rname);
   if (napi_create_async_work(env, nullptr, rname, async_execute, async_complete, c, &c->work) != napi_ok ||
       napi_queue_async_work(env, c->work) != napi_ok) {
+    napi_delete_reference(env, c->handle_ref);
     delete c;
     return throw_napi(env, "napi_queue_async_work");
   }
   return promise;
 }
 
+// The wrapper of an async call's handle, checked open; the worker takes the
+// mutex itself.
+Handle *open_wrapper(napi_env env, napi_value v) {
+  Handle *h = get_wrapper(env, v);
+  if (!h) {
+    napi_throw_type_error(env, nullptr, "sas_napi: expected a sampler handle");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(h->mu);
+  if (h->closed) {
+    napi_throw_error(env, nullptr, "sampler is closed");
+    return nullptr;
+  }
+  return h;
+}
+
 napi_value SampleAsync(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
-  HANDLE_OR_THROW(argv[0], s);
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
   AsyncCall *c = new AsyncCall();
-  c->s = s;
+  c->h = h;
   if (!read_rows(env, argv[1], &c->rows)) {
     delete c;
     napi_throw_type_error(env, nullptr, "sas_napi: bad sample descriptor");
     return nullptr;
   }
-  return start_async(env, c, "sas_sample");
+  return start_async(env, c, argv[0], "sas_sample");
 }
 
 napi_value VerifyAsync(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
-  HANDLE_OR_THROW(argv[0], s);
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
   AsyncCall *c = new AsyncCall();
-  c->s = s;
+  c->h = h;
   c->verify = true;
   if (!read_verify(env, argv[1], &c->vrows)) {
     delete c;
     napi_throw_type_error(env, nullptr, "sas_napi: bad verify descriptor");
     return nullptr;
   }
-  return start_async(env, c, "sas_verify");
+  return start_async(env, c, argv[0], "sas_verify");
 }
 
 // --------------------------------------------------------- host helpers --
@@ -527,6 +612,7 @@ napi_value Init(napi_env env, napi_value exports) {
                 {"MASK_ALLOW", SAS_MASK_ALLOW},     {"MASK_DENY", SAS_MASK_DENY},
                 {"FLAG_EMPTY_ROW", SAS_FLAG_EMPTY_ROW}, {"FLAG_TOPP_EDGE", SAS_FLAG_TOPP_EDGE},
                 {"FLAG_DRAW_EDGE", SAS_FLAG_DRAW_EDGE}, {"FLAG_SLOW_SELECT", SAS_FLAG_SLOW_SELECT},
+                {"HINT_NO_SOFTCAP", SAS_HINT_NO_SOFTCAP},
                 {"PARAMS_BYTES", (double)sizeof(sas_params)}};
   for (const auto &k : consts) {
     napi_create_double(env, k.value, &c);

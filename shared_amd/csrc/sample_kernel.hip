@@ -774,8 +774,12 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   // ---- history ids (loaded first: the tables fill while the logits load) ----
   int h0 = 0, h1 = 0;
   if (kHist) {
-    h0 = a.hist_offsets[row];
-    h1 = a.hist_offsets[row + 1];
+    // the row's range, clamped into the ids the caller holds and to the
+    // largest window
+    const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
+    const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
+    h0 = (int)o0;
+    h1 = (int)o1;
   }
   const bool has_hist = kHist && h1 > h0;
   uint32_t hpre[kHistPre];

@@ -29,6 +29,7 @@ struct SampleArgs {
   int64_t mask_stride;
   const uint32_t *hist_ids;
   const int32_t *hist_offsets;
+  int64_t hist_count;   // ids in hist_ids: every row's range is clamped into [0, hist_count]
   const double *uniforms;
   const sas_params *row_params;
   sas_params params;

@@ -10,6 +10,12 @@
 //   Sampler#sampleRows                <- the topk + sampler WGSL pair,
 //                                        lib/webgpu-llm/kernels.js:65-201, 1389-1449
 //   Sampler#verify                    <- acceptSpec, lib/webgpu-llm/kernels.js:211-369
+//   Sampler#decodeRows                <- the sampling tail of decodeBatch, lib/webgpu-llm/model.js:656-742,
+//                                        lib/webgpu-llm/gemma-model.js:921-992 ({ids, fed, eos, stopped, stopId})
+//   PenaltyWindow                     <- genIds / recentSet / rewindDecode, lib/webgpu-llm/model.js:386-399,
+//                                        lib/webgpu-llm/gemma-model.js:817-839
+//   requestSamplingParams             <- request defaults and ranges, lib/completions.ts:268-273,
+//                                        lib/gemma-completions.ts:212-217
 //
 // Grammar state stays on the host: a TokenMask becomes the packed u32
 // bitmask (bit id & 31 of word id >> 5 = allowed) once per distinct
@@ -59,16 +65,30 @@ function updateTokenMaskState(state, mask) {
 }
 
 /**
+ * Packer defaults of the two model families.  Qwen (model.js:401-426):
+ * greedy unless a temperature is given, seed 1, and the first stop id is the
+ * end-of-sequence id.  Gemma (gemma-model.js:900-919): temperature 0.6,
+ * top-p 0.95, a random seed, and eos only when eosId is given.
+ */
+const PACKER_DEFAULTS = {
+  qwen: { temperature: 0, topP: 1, topK: 20, seed: 1, eosFromStops: true },
+  gemma: { temperature: 0.6, topP: 0.95, topK: 20, seed: null, eosFromStops: false },
+};
+
+/**
  * The reference packer's validation and clamps (model.js:401-426): stop ids
  * are checked and padded, and every numeric field is clamped by
  * sas_clamp_params.  top_k may go to 128 here (the request API's range,
  * completions.ts:271) where the reference GPU path stopped at 20.
- * Defaults follow model.js (temperature 0 / greedy, topP 1, topK 20); pass
- * defaults = {temperature: 0.6, topP: 0.95} for the Gemma packer.
+ * `defaults` is PACKER_DEFAULTS.qwen (the default) or .gemma, or a partial
+ * object of the same fields.  SampleParams.allowedTokenIds (model.d.ts:15)
+ * is checked and carried through: a non-empty Uint32Array constrains the
+ * draw to those ids; an empty one or none leaves the row unconstrained, as
+ * the reference's allowedCount of 0 does (model.js:660-666).
  */
 function packSamplerParams(sp, defaults) {
   sp = sp || {};
-  defaults = defaults || {};
+  defaults = defaults || PACKER_DEFAULTS.qwen;
   const rawStopIds = sp.stopIds !== undefined ? sp.stopIds
     : (sp.eosId !== undefined ? [sp.eosId] : []);
   if (!Array.isArray(rawStopIds)) throw new Error('stopIds must be an array');
@@ -77,6 +97,10 @@ function packSamplerParams(sp, defaults) {
     if (!Number.isInteger(id)) throw new Error('invalid stop token id: ' + id);
     return id >>> 0;
   });
+  const allowed = sp.allowedTokenIds;
+  if (allowed !== undefined && allowed !== null && !(allowed instanceof Uint32Array)) {
+    throw new TypeError('allowedTokenIds must be a Uint32Array');
+  }
   const pick = function (name, d) { return Number.isFinite(sp[name]) ? sp[name] : orDefault(defaults[name], d); };
   const params = addon.clampParams({
     temperature: pick('temperature', 0),
@@ -87,10 +111,82 @@ function packSamplerParams(sp, defaults) {
     frequencyPenalty: pick('frequencyPenalty', 0),
     softcap: pick('softcap', 0),
   });
-  const seed = sp.seed !== undefined && sp.seed !== null ? sp.seed >>> 0 : orDefault(defaults.seed, 1) >>> 0;
+  let seed;
+  if (sp.seed !== undefined && sp.seed !== null) seed = sp.seed >>> 0;
+  else if (defaults.seed === null) seed = (Math.random() * 0xffffffff) >>> 0;
+  else seed = orDefault(defaults.seed, 1) >>> 0;
   const padded = [];
   for (let i = 0; i < MAX_STOP_IDS; i++) padded.push(i < stopIds.length ? stopIds[i] : STOP_PAD);
-  return { params: params, seed: seed, stopIds: stopIds, paddedStopIds: padded, stopSet: new Set(stopIds) };
+  const eosFromStops = defaults.eosFromStops !== undefined ? defaults.eosFromStops : true;
+  let eosId = null;
+  if (sp.eosId !== undefined) eosId = sp.eosId >>> 0;
+  else if (eosFromStops) eosId = stopIds.length ? stopIds[0] : STOP_PAD;
+  return {
+    params: params, seed: seed, stopIds: stopIds, paddedStopIds: padded, stopSet: new Set(stopIds),
+    eosId: eosId, allowedTokenIds: allowed && allowed.length ? allowed : null,
+  };
+}
+
+/**
+ * The rows' allowedTokenIds lists (null = unconstrained) from packed
+ * params, checked as decodeBatch checks them (model.js:661-664): a list
+ * longer than the vocabulary throws the reference's message.  A list cannot
+ * be combined with a mask (the reference's two model families take one or
+ * the other).
+ */
+function allowedLists(packed, vocab, hasMask) {
+  const lists = packed.map(function (p) { return p.allowedTokenIds; });
+  let any = false;
+  for (let i = 0; i < lists.length; i++) {
+    if (lists[i] === null) continue;
+    any = true;
+    if (lists[i].length > vocab) throw new Error('Tool constraint has too many allowed token IDs.');
+  }
+  if (any && hasMask) throw new Error('allowedTokenIds and mask cannot both be given');
+  return lists;
+}
+
+/**
+ * Request-level sampling defaults and ranges of the completion endpoints:
+ * Qwen (completions.ts:268-273) temperature 0.6 in [0, 2], top_p 0.95 in
+ * [0.05, 1], top_k 20 rounded in [1, 128], presence 1.5 in [0, 2]; Gemma
+ * (gemma-completions.ts:212-217) the same with temperature 1.0 and presence
+ * 0.  Math.min/Math.max as the reference's clamp(), so NaN stays NaN and the
+ * packer then applies its own non-finite defaults.
+ */
+function requestSamplingParams(request, grammar) {
+  request = request || {};
+  const clamp = function (v, lo, hi) { return Math.min(hi, Math.max(lo, v)); };
+  const gemma = grammar === 'gemma';
+  return {
+    temperature: clamp(orDefault(request.temperature, gemma ? 1.0 : 0.6), 0, 2),
+    topP: clamp(orDefault(request.top_p, 0.95), 0.05, 1),
+    topK: Math.round(clamp(orDefault(request.top_k, 20), 1, 128)),
+    presencePenalty: clamp(orDefault(request.presence_penalty, gemma ? 0 : 1.5), 0, 2),
+  };
+}
+
+/**
+ * The penalty window of one sequence: the tokens generated this turn
+ * (model.js:386-389; gemma-model.js:817-827), the last `size` of them as
+ * the history the penalties use (recentSet), and rewindDecode's removal of
+ * discarded tokens (gemma-model.js:834-839).  Stop tokens never enter it.
+ */
+class PenaltyWindow {
+  constructor(size) {
+    this.size = size || 512;
+    this.genIds = [];
+  }
+  reset() { this.genIds = []; }
+  note(id) { this.genIds.push(id >>> 0); }
+  /** The ids the next step penalizes: the last `size` generated tokens. */
+  recent() { return Uint32Array.from(this.genIds.slice(-this.size)); }
+  recentSet() { return new Set(this.genIds.slice(-this.size)); }
+  /** rewindDecode(count, sampledCount): drop the last sampledCount tokens. */
+  rewind(sampledCount) {
+    const n = Math.max(0, Math.floor(sampledCount || 0));
+    if (n) this.genIds.splice(Math.max(0, this.genIds.length - n), n);
+  }
 }
 
 /** sas_params layout: five doubles, a float softcap, an int32 top_k (48 bytes). */
@@ -114,20 +210,20 @@ class DeviceBuffer {
   constructor(sampler, bytes) {
     this.sampler = sampler;
     this.bytes = bytes;
-    this.ptr = addon.alloc(sampler._handle(), bytes);
+    this.ptr = addon.alloc(sampler._idle('alloc'), bytes);
   }
   upload(typed) {
     if (typed.byteLength > this.bytes) throw new RangeError('upload larger than the device buffer');
-    addon.copy(this.sampler._handle(), this.ptr, typed, 0);
+    addon.copy(this.sampler._idle('upload'), this.ptr, typed, 0);
     return this;
   }
   download(typed) {
     if (typed.byteLength > this.bytes) throw new RangeError('download larger than the device buffer');
-    addon.copy(this.sampler._handle(), this.ptr, typed, 1);
+    addon.copy(this.sampler._idle('download'), this.ptr, typed, 1);
     return typed;
   }
   free() {
-    if (this.ptr !== null && this.sampler._h !== null) addon.free(this.sampler._h, this.ptr);
+    if (this.ptr !== null && this.sampler._h !== null) addon.free(this.sampler._idle('free'), this.ptr);
     this.ptr = null;
   }
 }
@@ -138,6 +234,10 @@ class Sampler {
     this._h = addon.create(device || 0);
     this._scratch = {};
     this._queue = Promise.resolve();
+    this._pending = 0;      // async calls queued or running
+    this._running = false;  // the queue is executing one of them now
+    this._inWorker = false; // ... and its launch is on a libuv worker thread
+    this._closing = null;   // close() requested while async calls were pending
   }
 
   _handle() {
@@ -145,21 +245,88 @@ class Sampler {
     return this._h;
   }
 
-  close() {
+  // The handle for a synchronous call.  A handle runs one call at a time
+  // (its scratch and stream are shared): while async calls are pending, a
+  // synchronous one would run beside them, so it throws; after close() was
+  // asked for, every new call throws.  The queued call's own host steps
+  // (before and after its worker) run with _running set and pass.
+  _idle(what) {
+    const h = this._handle();
+    if (this._running && !this._inWorker) return h;
+    if (this._closing) throw new Error('sampler is closed');
+    if (this._pending > 0) {
+      throw new Error('Sampler: ' + what + ' called while an async call is pending; await it first');
+    }
+    return h;
+  }
+
+  // Run an addon async call (a promise from a libuv worker) as the queue's
+  // current job, flagging the worker phase.
+  _worker(promise) {
+    const self = this;
+    this._inWorker = true;
+    return promise.then(function (v) { self._inWorker = false; return v; },
+      function (e) { self._inWorker = false; throw e; });
+  }
+
+  // Queue fn (which returns a promise) behind every earlier async call.
+  _enqueue(fn) {
+    const self = this;
+    this._handle();
+    if (this._closing) throw new Error('sampler is closed');
+    this._pending++;
+    const run = function () {
+      self._running = true;
+      let p;
+      try {
+        p = Promise.resolve(fn());
+      } catch (e) {
+        p = Promise.reject(e);
+      }
+      return p.then(function (v) { self._running = false; self._pending--; return v; },
+        function (e) { self._running = false; self._pending--; throw e; });
+    };
+    const p = this._queue.then(run, run);
+    this._queue = p.then(function () {}, function () {});
+    return p;
+  }
+
+  _destroy() {
     if (this._h === null) return;
     const names = Object.keys(this._scratch);
-    for (let i = 0; i < names.length; i++) this._scratch[names[i]].free();
+    for (let i = 0; i < names.length; i++) {
+      const b = this._scratch[names[i]];
+      if (b.ptr !== null) addon.free(this._h, b.ptr);
+      b.ptr = null;
+    }
     this._scratch = {};
     addon.destroy(this._h);
     this._h = null;
   }
 
-  reserve(rows, vocab) { addon.reserve(this._handle(), rows, vocab); }
+  /**
+   * Release the handle.  With async calls pending, the handle stays alive
+   * until they settle and the returned promise resolves after the release;
+   * new calls throw from now on.
+   */
+  close() {
+    if (this._h === null) return Promise.resolve();
+    if (this._closing) return this._closing;
+    if (this._pending > 0) {
+      const self = this;
+      this._closing = this._queue.then(function () { self._destroy(); });
+      return this._closing;
+    }
+    this._destroy();
+    return Promise.resolve();
+  }
+
+  reserve(rows, vocab) { addon.reserve(this._idle('reserve'), rows, vocab); }
 
   /** Device memory owned by the caller (e.g. the LM head's logits). */
   alloc(bytes) { return new DeviceBuffer(this, bytes); }
 
-  synchronize() { addon.synchronize(this._handle()); }
+  synchronize() { addon.synchronize(this._idle('synchronize')); }
 
   // Grow-only per-name scratch, so steady-state calls allocate nothing.
   _buf(name, bytes) {
@@ -232,6 +399,44 @@ class Sampler {
     const ps = Array.isArray(opts.params) ? opts.params : null;
     const packed = ps ? ps.map(function (p) { return packSamplerParams(p, opts.defaults); })
       : [packSamplerParams(opts.params, opts.defaults)];
+    // SampleParams.allowedTokenIds (the Qwen path, model.js:661-666): each
+    // distinct Uint32Array becomes an allow bitmask once
+    const lists = allowedLists(packed, vocab, d.mask !== undefined);
+    const firstList = lists.find(function (x) { return x !== null; });
+    if (firstList !== undefined) {
+      const shared = lists.every(function (x) { return x === firstList; });
+      if (shared) {
+        let st = this._allowState;
+        if (!st || st.cfg.text.vocab !== vocab) {
+          if (st) st.words.free();
+          st = this._allowState = this.createTokenMaskState(vocab);
+        }
+        updateTokenMaskState(st, { kind: 'allow', tokenIds: firstList });
+        d.mask = st.words.ptr;
+        d.maskStride = 0;
+      } else {
+        // rows with different lists (rows without one are unconstrained)
+        const cache = this._allowWords || (this._allowWords = new WeakMap());
+        const allWords = addon.maskFromIds(addon.MASK_ALL, null, vocab).words;
+        const words = new Uint32Array(rows * nwords);
+        for (let r = 0; r < rows; r++) {
+          const list = lists[r];
+          let w = allWords;
+          if (list !== null) {
+            const hit = cache.get(list);
+            if (hit && hit.vocab === vocab) {
+              w = hit.words;
+            } else {
+              w = addon.maskFromIds(addon.MASK_ALLOW, list, vocab).words;
+              cache.set(list, { vocab: vocab, words: w });
+            }
+          }
+          words.set(w, r * nwords);
+        }
+        d.mask = this._buf('mask', words.byteLength).upload(words).ptr;
+        d.maskStride = nwords;
+      }
+    }
     if (ps) {
       if (ps.length !== rows) throw new RangeError('params must have one entry per row');
       const ab = new ArrayBuffer(rows * PARAMS_BYTES);
@@ -239,23 +444,38 @@ class Sampler {
       for (let r = 0; r < rows; r++) writeParams(view, r * PARAMS_BYTES, packed[r].params);
       d.rowParams = this._buf('params', ab.byteLength).upload(new Uint8Array(ab)).ptr;
       d.params = packed[0].params;
+      // the packer knows every row's values: without a softcap anywhere the
+      // library may use its cheaper kernel variant
+      d.rowHints = packed.every(function (p) { return !(p.params.softcap > 0); }) ? addon.HINT_NO_SOFTCAP : 0;
     } else {
       d.params = packed[0].params;
     }
     // history: per-row lists (Array / Uint32Array / Set), or recentIds for every row
     let hist = opts.history;
+    if (!hist && opts.windows) {
+      if (opts.windows.length !== rows) throw new RangeError('windows must have one PenaltyWindow per row');
+      hist = opts.windows.map(function (w) { return w.recent(); });
+    }
     if (!hist && opts.recentIds) {
       hist = [];
       for (let r = 0; r < rows; r++) hist.push(opts.recentIds);
     }
     if (hist) {
       if (hist.length !== rows) throw new RangeError('history must have one list per row');
-      const lists = hist.map(toU32);
+      const hl = hist.map(toU32);
       const offs = new Int32Array(rows + 1);
-      for (let r = 0; r < rows; r++) offs[r + 1] = offs[r] + lists[r].length;
+      for (let r = 0; r < rows; r++) {
+        if (hl[r].length > addon.MAX_HISTORY) {
+          throw new RangeError('history of row ' + r + ' holds ' + hl[r].length + ' ids; at most ' +
+            addon.MAX_HISTORY + ' are supported');
+        }
+        if (offs[r] + hl[r].length > 0x7FFFFFFF) throw new RangeError('histories exceed 2^31 - 1 ids');
+        offs[r + 1] = offs[r] + hl[r].length;
+      }
       const flat = new Uint32Array(Math.max(1, offs[rows]));
-      for (let r = 0; r < rows; r++) flat.set(lists[r], offs[r]);
+      for (let r = 0; r < rows; r++) flat.set(hl[r], offs[r]);
       d.histIds = this._buf('hist', flat.byteLength).upload(flat).ptr;
+      d.histCount = flat.length;
       d.histOffsets = this._buf('histOffsets', offs.byteLength).upload(offs).ptr;
     }
     // uniforms: host-supplied U per row, else the reference GPU sampler's
@@ -305,21 +525,61 @@ class Sampler {
    * Returns {ids: Uint32Array, stopped, stopId[, probs, candIds, counts, flags]}.
    */
   sampleRows(opts) {
+    this._idle('sampleRows');
     const r = this._describe(opts);
     addon.sample(this._handle(), r.desc);
     return this._collect(opts, r.packed);
   }
 
-  /** sampleRows with the launch and the wait on a worker thread.  Calls queue. */
+  /**
+   * sampleRows with the launch and the wait on a worker thread.  Async calls
+   * queue behind each other; synchronous calls throw until they settle.
+   */
   sampleRowsAsync(opts) {
     const self = this;
-    const run = function () {
+    return this._enqueue(function () {
       const r = self._describe(opts);
-      return addon.sampleAsync(self._handle(), r.desc).then(function () { return self._collect(opts, r.packed); });
-    };
-    const p = this._queue.then(run, run);
-    this._queue = p.then(function () {}, function () {});
-    return p;
+      return self._worker(addon.sampleAsync(self._handle(), r.desc))
+        .then(function () { return self._collect(opts, r.packed); });
+    });
+  }
+
+  // decodeBatch's per-row result for one step (model.js:727-741,
+  // gemma-model.js:976-991), with each window's genIds mirror.
+  _decodeResults(opts, out, packed) {
+    const res = [];
+    for (let r = 0; r < opts.rows; r++) {
+      const pk = packed[packed.length > 1 ? r : 0];
+      const id = out.ids[r];
+      const stopped = pk.stopSet.has(id);
+      if (opts.windows && !stopped && id !== addon.NO_TOKEN) opts.windows[r].note(id);
+      res.push({ ids: [id], fed: 1, eos: stopped && pk.eosId !== null && id === pk.eosId, stopped: stopped,
+        stopId: stopped ? id : null });
+    }
+    return res;
+  }
+
+  /**
+   * One decode step over every row with decodeBatch's result shape
+   * (model.d.ts:23-29): an array of {ids, fed, eos, stopped, stopId}, one
+   * per row.  opts as sampleRows, plus windows: a PenaltyWindow per row whose
+   * last tokens are the row's history and which receives the row's token
+   * unless it is a stop id (model.js:733-734).
+   */
+  decodeRows(opts) {
+    this._idle('decodeRows');
+    const r = this._describe(opts);
+    addon.sample(this._handle(), r.desc);
+    return this._decodeResults(opts, this._collect(opts, r.packed), r.packed);
+  }
+
+  decodeRowsAsync(opts) {
+    const self = this;
+    return this._enqueue(function () {
+      const r = self._describe(opts);
+      return self._worker(addon.sampleAsync(self._handle(), r.desc))
+        .then(function () { return self._decodeResults(opts, self._collect(opts, r.packed), r.packed); });
+    });
   }
 
   /**
@@ -330,6 +590,7 @@ class Sampler {
    * Math.random() when given.
    */
   sample(cands, opts) {
+    this._idle('sample');
     opts = opts || {};
     const n = cands.ids.length >> 1;
     let vocab = 1;
@@ -362,6 +623,7 @@ class Sampler {
    * Returns {tokens: Uint32Array[seqs*(draftLen+1)], accepted: Int32Array}.
    */
   verify(opts) {
+    this._idle('verify');
     const d = this._describeVerify(opts);
     addon.verify(this._handle(), d);
     return this._collectVerify(opts);
@@ -369,13 +631,10 @@ class Sampler {
 
   verifyAsync(opts) {
     const self = this;
-    const run = function () {
+    return this._enqueue(function () {
       const d = self._describeVerify(opts);
-      return addon.verifyAsync(self._handle(), d).then(function () { return self._collectVerify(opts); });
-    };
-    const p = this._queue.then(run, run);
-    this._queue = p.then(function () {}, function () {});
-    return p;
+      return self._worker(addon.verifyAsync(self._handle(), d)).then(function () { return self._collectVerify(opts); });
+    });
   }
 
   _describeVerify(opts) {
@@ -413,8 +672,12 @@ class Sampler {
 module.exports = {
   Sampler: Sampler,
   DeviceBuffer: DeviceBuffer,
+  PenaltyWindow: PenaltyWindow,
   updateTokenMaskState: updateTokenMaskState,
   packSamplerParams: packSamplerParams,
+  requestSamplingParams: requestSamplingParams,
+  allowedLists: allowedLists,
+  PACKER_DEFAULTS: PACKER_DEFAULTS,
   maskFromIds: addon.maskFromIds,
   pcgUniform: addon.pcgUniform,
   clampParams: addon.clampParams,

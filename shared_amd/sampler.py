@@ -73,6 +73,32 @@ def mask_from_ids(kind: int, ids, vocab: int) -> np.ndarray:
     return words
 
 
+def check_history(offsets, count: int) -> None:
+    """Validate CSR history offsets on the host: int32 [rows + 1], starting
+    at >= 0, non-decreasing, ending at <= count ids, each row at most
+    MAX_HISTORY ids.  Raises ValueError naming the first bad row."""
+    o = np.asarray(offsets)
+    if o.ndim != 1 or o.size < 1:
+        raise ValueError("hist_offsets must be a 1-D array of rows + 1 offsets")
+    o = o.astype(np.int64)
+    if o[0] < 0:
+        raise ValueError(f"hist_offsets[0] = {o[0]} is negative")
+    d = np.diff(o)
+    bad = np.nonzero(d < 0)[0]
+    if bad.size:
+        raise ValueError(f"hist_offsets decrease at row {int(bad[0])}")
+    big = np.nonzero(d > _capi.MAX_HISTORY)[0]
+    if big.size:
+        raise ValueError(f"row {int(big[0])} holds {int(d[big[0]])} history ids; at most {_capi.MAX_HISTORY}")
+    if o[-1] > count:
+        raise ValueError(f"hist_offsets end at {int(o[-1])} but hist_ids holds {count} ids")
+
+
+def row_hints(rows: Sequence[Params]) -> int:
+    """SAS_HINT_* bits that hold for every row of a per-row parameter list."""
+    return _capi.HINT_NO_SOFTCAP if all(not (p.softcap > 0) for p in rows) else 0
+
+
 def _ptr(t) -> Optional[int]:
     if t is None:
         return None
@@ -122,8 +148,11 @@ class Sampler:
 
     def sample_into(self, logits, out_ids, *, vocab: Optional[int] = None, mask=None, hist_ids=None,
                     hist_offsets=None, uniforms=None, params: Optional[Params] = None, row_params=None,
-                    out_probs=None, out_cand_ids=None, out_counts=None, out_flags=None, stream=None) -> None:
-        """Launch sas_sample on caller-provided device buffers (no allocation)."""
+                    out_probs=None, out_cand_ids=None, out_counts=None, out_flags=None, stream=None,
+                    row_hints: int = 0) -> None:
+        """Launch sas_sample on caller-provided device buffers (no allocation,
+        no synchronisation: the history offsets are not checked here, the
+        kernels clamp them to hist_ids' length)."""
         rows = logits.shape[0]
         vocab = int(vocab if vocab is not None else logits.shape[1])
         if logits.dtype.itemsize != 4 or logits.stride(1) != 1:
@@ -138,6 +167,8 @@ class Sampler:
             d.mask_stride = mask.stride(0)
         d.hist_ids = _ptr(hist_ids)
         d.hist_offsets = _ptr(hist_offsets)
+        d.hist_count = hist_ids.numel() if hist_ids is not None else 0
+        d.row_hints = int(row_hints)
         d.uniforms = _ptr(uniforms)
         d.params = (params or Params()).to_c()
         d.row_params = _ptr(row_params)
@@ -149,8 +180,13 @@ class Sampler:
         check(self._lib.sas_sample(self._h, ctypes.byref(d), self._stream(stream)), self._h)
 
     def sample(self, logits, *, full: bool = False, **kw):
-        """Allocate outputs and sample; returns ids (and the extras if full)."""
+        """Allocate outputs and sample; returns ids (and the extras if full).
+        The history offsets are checked on the host first."""
         import torch
+        if kw.get("hist_ids") is not None:
+            if kw.get("hist_offsets") is None:
+                raise ValueError("hist_ids requires hist_offsets")
+            check_history(kw["hist_offsets"].cpu().numpy(), kw["hist_ids"].numel())
         rows = logits.shape[0]
         dev = logits.device
         out = {"ids": torch.empty(rows, dtype=torch.int32, device=dev)}

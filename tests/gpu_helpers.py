@@ -29,11 +29,14 @@ def run_gpu(s: Sampler, b, *, logits_dev=None, row_params=None, full=True):
     ho = to_dev(b.hist_offsets) if b.hist_offsets is not None else None
     u = to_dev(b.uniforms) if b.uniforms is not None else None
     rp = None
+    hints = 0
     if row_params is not None:
         from shared_amd import pack_params
+        from shared_amd.sampler import row_hints
         rp = to_dev(pack_params(row_params).view(np.uint8))
+        hints = row_hints(row_params)
     out = s.sample(lg, vocab=b.vocab, mask=mask, hist_ids=hi, hist_offsets=ho, uniforms=u, params=b.params,
-                   row_params=rp, full=full)
+                   row_params=rp, row_hints=hints, full=full)
     torch.cuda.synchronize()
     if not full:
         return {"ids": out.cpu().numpy().view(np.uint32)}

@@ -117,6 +117,70 @@ check('pcg uniform matches the reference hash', function () {
   }
 });
 
+check('allowedTokenIds: checked and carried like decodeBatch (model.js:661-666)', function () {
+  assert.throws(function () { sas.packSamplerParams({ allowedTokenIds: [1, 2] }); },
+    /^TypeError: allowedTokenIds must be a Uint32Array$/);
+  const ids = Uint32Array.of(3, 9);
+  const p = sas.packSamplerParams({ allowedTokenIds: ids });
+  assert.strictEqual(p.allowedTokenIds, ids);                 // identity kept for the upload dedupe
+  assert.strictEqual(sas.packSamplerParams({ allowedTokenIds: new Uint32Array() }).allowedTokenIds, null);
+  assert.strictEqual(sas.packSamplerParams({}).allowedTokenIds, null);
+  // more ids than the vocabulary: the reference's message
+  const big = sas.packSamplerParams({ allowedTokenIds: new Uint32Array(11) });
+  assert.throws(function () { sas.allowedLists([big], 10, false); },
+    /^Error: Tool constraint has too many allowed token IDs\.$/);
+  assert.deepStrictEqual(sas.allowedLists([p, sas.packSamplerParams({})], 10, false), [ids, null]);
+  assert.throws(function () { sas.allowedLists([p], 10, true); }, /cannot both be given/);
+  assert.deepStrictEqual(sas.allowedLists([sas.packSamplerParams({})], 10, true), [null]);
+});
+
+check('eos id: Qwen takes the first stop id, Gemma only an explicit eosId', function () {
+  assert.strictEqual(sas.packSamplerParams({ stopIds: [7, 9] }).eosId, 7);
+  assert.strictEqual(sas.packSamplerParams({}).eosId, sas.STOP_PAD);
+  assert.strictEqual(sas.packSamplerParams({ stopIds: [7, 9], eosId: 9 }).eosId, 9);
+  const g = sas.PACKER_DEFAULTS.gemma;
+  assert.strictEqual(sas.packSamplerParams({ stopIds: [7, 9] }, g).eosId, null);
+  assert.strictEqual(sas.packSamplerParams({ stopIds: [7, 9], eosId: 9 }, g).eosId, 9);
+  const gp = sas.packSamplerParams({}, g);
+  assert.strictEqual(gp.params.temperature, 0.6);
+  assert.strictEqual(gp.params.topP, 0.95);
+  assert.ok(Number.isInteger(gp.seed) && gp.seed >= 0 && gp.seed <= 0xFFFFFFFF);
+});
+
+check('request clamps and defaults (completions.ts:268-273, gemma-completions.ts:212-217)', function () {
+  assert.deepStrictEqual(sas.requestSamplingParams({}),
+    { temperature: 0.6, topP: 0.95, topK: 20, presencePenalty: 1.5 });
+  assert.deepStrictEqual(sas.requestSamplingParams({}, 'gemma'),
+    { temperature: 1.0, topP: 0.95, topK: 20, presencePenalty: 0 });
+  assert.deepStrictEqual(sas.requestSamplingParams({ temperature: 5, top_p: 0.01, top_k: 300.6, presence_penalty: -1 }),
+    { temperature: 2, topP: 0.05, topK: 128, presencePenalty: 0 });
+  assert.strictEqual(sas.requestSamplingParams({ top_k: 0.4 }).topK, 1);
+  assert.strictEqual(sas.requestSamplingParams({ top_k: 40.5 }).topK, 41);   // Math.round
+  assert.ok(Number.isNaN(sas.requestSamplingParams({ temperature: NaN }).temperature));
+  // NaN then meets the packer's non-finite rule: greedy for Qwen, 0.6 for Gemma
+  assert.strictEqual(sas.packSamplerParams(sas.requestSamplingParams({ temperature: NaN })).params.temperature, 0);
+  assert.strictEqual(sas.packSamplerParams(sas.requestSamplingParams({ temperature: NaN }, 'gemma'),
+    sas.PACKER_DEFAULTS.gemma).params.temperature, 0.6);
+});
+
+check('penalty window: last 512, rewind by sampled count (token-mask-state.test.ts:58-70)', function () {
+  const w = new sas.PenaltyWindow();
+  [1, 2, 3, 4, 5].forEach(function (x) { w.note(x); });
+  w.rewind(2);
+  assert.deepStrictEqual(w.genIds, [1, 2, 3]);
+  w.rewind(0);
+  assert.deepStrictEqual(w.genIds, [1, 2, 3]);
+  const big = new sas.PenaltyWindow();
+  for (let i = 0; i < 600; i++) big.note(i);
+  const r = big.recent();
+  assert.strictEqual(r.length, 512);
+  assert.strictEqual(r[0], 88);
+  assert.strictEqual(r[511], 599);
+  assert.ok(big.recentSet().has(599) && !big.recentSet().has(87));
+  big.reset();
+  assert.strictEqual(big.recent().length, 0);
+});
+
 check('a sampler needs a HIP device and says so', function () {
   assert.throws(function () { return new sas.Sampler(0); }, /no HIP device/);
 });

@@ -84,6 +84,65 @@ async function main() {
       step('sampleRows (TokenMask) done');
     }
 
+    if (allow) {
+      // Qwen's SampleParams.allowedTokenIds (model.js:661-666): one list for
+      // every row, then rows with and without one
+      const qp = Object.assign({}, params, { allowedTokenIds: allow });
+      const f = s.sampleRows(Object.assign({}, base, { logits: logits, mask: null, params: qp }));
+      write('js_allowed_ids.u32', f.ids);
+      const mixed = [];
+      for (let r = 0; r < rows; r++) mixed.push(r % 2 ? params : qp);
+      const f2 = s.sampleRows(Object.assign({}, base, { logits: logits, mask: null, params: mixed }));
+      write('js_allowed_mixed_ids.u32', f2.ids);
+      let msg = '';
+      try {
+        s.sampleRows(Object.assign({}, base, { logits: logits, mask: null,
+          params: Object.assign({}, params, { allowedTokenIds: new Uint32Array(vocab + 1) }) }));
+      } catch (e) { msg = e.message; }
+      if (msg !== 'Tool constraint has too many allowed token IDs.') throw new Error('allow-list check: ' + msg);
+      step('sampleRows (allowedTokenIds) done');
+    }
+
+    // decodeBatch's result shape over PenaltyWindows seeded with the history;
+    // the stop ids are two of the tokens the rows draw
+    const want = read('want_ids.u32', Uint32Array);
+    if (want && history) {
+      const windows = history.map(function (h) {
+        const w = new sas.PenaltyWindow(512);
+        for (let i = 0; i < h.length; i++) w.note(h[i]);
+        return w;
+      });
+      const sp = Object.assign({}, params, { stopIds: [want[0], want[1]] });
+      const res = s.decodeRows(Object.assign({}, base, { logits: logits, params: sp, history: null, windows: windows }));
+      fs.writeFileSync(path.join(dir, 'js_decode.json'), JSON.stringify({
+        results: res, lens: windows.map(function (w) { return w.genIds.length; }),
+        last: windows.map(function (w) { return w.genIds[w.genIds.length - 1]; }),
+      }));
+      step('decodeRows done');
+    }
+
+    // a synchronous call while an async one is pending throws; close() after
+    // an async call waits for it, then the handle is closed
+    {
+      const s2 = new sas.Sampler(0);
+      const pend = s2.sampleRowsAsync(Object.assign({ logits: logits }, base));
+      let msg = '';
+      try { s2.sampleRows(Object.assign({ logits: logits }, base)); } catch (e) { msg = e.message; }
+      if (!/pending/.test(msg)) throw new Error('sync during async did not throw: ' + msg);
+      const pend2 = s2.sampleRowsAsync(Object.assign({ logits: logits }, base, { uniforms: uniforms }));
+      const closing = s2.close();
+      msg = '';
+      try { s2.sampleRowsAsync(Object.assign({ logits: logits }, base)); } catch (e) { msg = e.message; }
+      if (msg !== 'sampler is closed') throw new Error('call after close did not throw: ' + msg);
+      const r1 = await pend;
+      const r2 = await pend2;
+      await closing;
+      if (s2._h !== null) throw new Error('handle not released after close');
+      write('js_conc1_ids.u32', r1.ids);
+      write('js_conc2_ids.u32', r2.ids);
+      step('async queue, sync guard and deferred close done');
+    }
+
     const candsPath = path.join(dir, 'cands.json');
     if (fs.existsSync(candsPath)) {
       const cc = JSON.parse(fs.readFileSync(candsPath, 'utf8'));

@@ -137,3 +137,31 @@ def test_handle_calls_fail_loudly_without_a_device():
     with pytest.raises(_capi.SasError):
         from shared_amd import Sampler
         Sampler(0)
+
+
+def test_history_offsets_checked_on_the_host():
+    from shared_amd.sampler import check_history
+    check_history(np.array([0, 3, 3, 7], np.int32), 7)
+    with pytest.raises(ValueError, match="negative"):
+        check_history(np.array([-1, 3], np.int32), 7)
+    with pytest.raises(ValueError, match="decrease at row 1"):
+        check_history(np.array([0, 4, 2], np.int32), 7)
+    with pytest.raises(ValueError, match="hist_ids holds 5 ids"):
+        check_history(np.array([0, 3, 6], np.int32), 5)
+    with pytest.raises(ValueError, match="at most 65535"):
+        check_history(np.array([0, 70000], np.int32), 70000)
+
+
+def test_row_hints_follow_the_rows():
+    from shared_amd.sampler import row_hints
+    assert row_hints([Params(), Params(temperature=1.0)]) == _capi.HINT_NO_SOFTCAP
+    assert row_hints([Params(), Params(softcap=30.0)]) == 0
+
+
+def test_rows_struct_matches_the_header():
+    # the ctypes layout has the fields the header declares, in order
+    import re
+    text = open(_capi.HEADER).read()
+    body = re.search(r"typedef struct sas_rows \{(.*?)\} sas_rows;", text, re.S).group(1)
+    names = re.findall(r"\b([a-z_]+);", re.sub(r"/\*.*?\*/", "", body, flags=re.S))
+    assert names == [f for f, _ in _capi.SasRows._fields_]

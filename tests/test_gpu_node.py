@@ -52,19 +52,22 @@ def test_node_api_end_to_end(tmp_path):
         json.dump({"vocab": v["vocab"], "seqs": v["seqs"], "drafts": v["drafts"],
                    "temperature": v["temperature"]}, f)
 
+    want = O.sample_rows(b)
+    want["ids"].astype(np.uint32).tofile(os.path.join(d, "want_ids.u32"))
+
     print("[gpu] node host_gpu.js", d, flush=True)
     proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "host_gpu.js"), d], stdout=subprocess.PIPE,
                           stderr=subprocess.STDOUT, text=True, timeout=240)
     print(proc.stdout, flush=True)
     assert proc.returncode == 0, proc.stdout[-3000:]
 
-    want = O.sample_rows(b)
     got = _u32(d, "js_sync_ids.u32")
     assert np.array_equal(got, want["ids"])
     probs = np.fromfile(os.path.join(d, "js_sync_probs.f64")).reshape(b.rows, -1)
     assert np.array_equal(probs, want["probs"])
     assert np.array_equal(_u32(d, "js_sync_cand.u32").reshape(b.rows, -1), want["cand_ids"])
-    for name in ("js_async_ids.u32", "js_dev_ids.u32", "js_rowparams_ids.u32"):
+    for name in ("js_async_ids.u32", "js_dev_ids.u32", "js_rowparams_ids.u32", "js_conc1_ids.u32",
+                 "js_conc2_ids.u32"):
         assert np.array_equal(_u32(d, name), want["ids"]), name
 
     m1 = O.mask_from_ids(MASK_ALLOW, allow, b.vocab)
@@ -73,6 +76,31 @@ def test_node_api_end_to_end(tmp_path):
     wt = O.sample_rows(bt)["ids"]
     assert np.array_equal(_u32(d, "js_tokmask_ids.u32"), wt)
     assert np.array_equal(_u32(d, "js_tokmask2_ids.u32"), wt)
+
+    # allowedTokenIds: every row, then the even rows only
+    ba = W.Batch("allowed", b.logits, b.params, mask=np.repeat(m1[None, :], b.rows, axis=0),
+                 hist_ids=b.hist_ids, hist_offsets=b.hist_offsets, uniforms=b.uniforms)
+    assert np.array_equal(_u32(d, "js_allowed_ids.u32"), O.sample_rows(ba)["ids"])
+    full = O.mask_from_ids(0, np.zeros(0, np.uint32), b.vocab)
+    mixed = np.stack([full if r % 2 else m1 for r in range(b.rows)])
+    bm = W.Batch("allowed_mixed", b.logits, b.params, mask=mixed, hist_ids=b.hist_ids,
+                 hist_offsets=b.hist_offsets, uniforms=b.uniforms)
+    assert np.array_equal(_u32(d, "js_allowed_mixed_ids.u32"), O.sample_rows(bm)["ids"])
+
+    # decodeBatch's per-row result: {ids, fed, eos, stopped, stopId}; stops
+    # are the tokens of rows 0 and 1, the first of them the eos id
+    with open(os.path.join(d, "js_decode.json")) as f:
+        dec = json.load(f)
+    stops = [int(want["ids"][0]), int(want["ids"][1])]
+    for r, res in enumerate(dec["results"]):
+        tok = int(want["ids"][r])
+        hit = tok in stops
+        assert res == {"ids": [tok], "fed": 1, "eos": hit and tok == stops[0], "stopped": hit,
+                       "stopId": tok if hit else None}, (r, res)
+        n0 = int(b.hist_offsets[r + 1] - b.hist_offsets[r])
+        assert dec["lens"][r] == n0 + (0 if hit else 1), r
+        if not hit:
+            assert dec["last"][r] == tok
 
     cv = int(cand_ids.max()) + 1
     row = np.full(cv, np.nan, np.float32)

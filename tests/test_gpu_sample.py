@@ -67,6 +67,38 @@ def test_row_params_mixed(sampler):
     check(sampler, b, row_params=plist, label="row_params")
 
 
+def test_penalty_order_closed_form_on_gpu(sampler):
+    # repetition, then frequency, then presence: id 0 (seen twice) becomes
+    # 3 / 2 - 0.5 * 2 - 0.25 = 0.25 and -3 * 2 - 1 - 0.25 = -7.25; the
+    # greedy pick flips exactly at those values (another order gives 0.875
+    # and -8.5)
+    rows = np.array([[3.0, 0.26, 0.1, 0.0], [3.0, 0.24, 0.1, 0.0],
+                     [-3.0, -7.2, -9.0, -9.5], [-3.0, -7.3, -9.0, -9.5]], np.float32)
+    hi, ho = W._csr([np.array([0, 0], np.uint32)] * 4)
+    p = Params(temperature=0.0, repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25)
+    b = W.Batch("penalty_order", rows, p, hist_ids=hi, hist_offsets=ho)
+    g, _ = check(sampler, b)
+    assert g["ids"].tolist() == [1, 0, 1, 0]
+
+
+def test_row_params_full_size_mixed(sampler):
+    # C3P at full size with per-row params: softcap, repetition, frequency,
+    # presence, temperature, top-k and top-p all vary by row
+    b = W.c3p()
+    rng = np.random.default_rng(21)
+    plist = [Params(temperature=float(rng.choice([0.0, 0.7, 1.0, 1.3])), top_k=int(rng.integers(1, 129)),
+                    top_p=float(rng.choice([0.5, 0.9, 1.0])), repetition_penalty=float(rng.choice([1.0, 1.1, 1.3])),
+                    presence_penalty=float(rng.choice([0.0, 0.5])), frequency_penalty=float(rng.choice([0.0, 0.3])),
+                    softcap=float(rng.choice([0.0, 30.0])))
+             for _ in range(b.rows)]
+    print(f"[gpu] row_params full size rows={b.rows} vocab={b.vocab}", flush=True)
+    check(sampler, b, row_params=plist, label="row_params_full")
+    # no row with a softcap: the cheaper kernel variant through the hint
+    for q in plist:
+        q.softcap = 0.0
+    check(sampler, b, row_params=plist, label="row_params_full_nocap")
+
+
 # ------------------------------------------------------------------ edges --
 
 def test_empty_and_single_allowed_rows(sampler):

@@ -150,6 +150,28 @@ def test_repetition_and_frequency_penalties():
     assert _row(LOG4, Params(temperature=0.0, frequency_penalty=0.4), hist=[1, 1]).id == 1
 
 
+def test_penalty_order_closed_form():
+    # repetition first, then frequency, then presence, for positive, negative
+    # and zero logits; operands exact in binary so every result is exact.
+    # Another order gives another value: e.g. v=3 with frequency and
+    # presence first is (3 - 1 - 0.25) / 2 = 0.875, not 0.25.
+    pen = O.lib().orc_penalize
+    p = O.params(Params(repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25))
+    assert pen(3.0, 2, p) == 0.25          # 3 / 2 - 0.5 * 2 - 0.25
+    assert pen(-3.0, 2, p) == -7.25        # -3 * 2 - 1 - 0.25
+    assert pen(0.0, 2, p) == -1.25         # 0 is not > 0: 0 * 2 - 1 - 0.25
+    assert pen(3.0, 1, p) == 0.75          # 1.5 - 0.5 - 0.25
+    q = O.params(Params(repetition_penalty=4.0, frequency_penalty=0.25, presence_penalty=0.5))
+    assert pen(4.0, 4, q) == -0.5          # 4 / 4 - 1 - 0.5
+    assert pen(-0.5, 4, q) == -3.5         # -0.5 * 4 - 1 - 0.5
+    # through a whole row: the penalized id drops below 0.26 but stays above 0.24
+    pp = Params(temperature=0.0, repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25)
+    assert _row([3.0, 0.26, 0.1], pp, hist=[0, 0]).id == 1
+    assert _row([3.0, 0.24, 0.1], pp, hist=[0, 0]).id == 0
+    assert _row([-3.0, -7.2, -9.0], pp, hist=[0, 0]).id == 1
+    assert _row([-3.0, -7.3, -9.0], pp, hist=[0, 0]).id == 0
+
+
 def test_penalty_invariants():
     pen = O.lib().orc_penalize
     rng = np.random.default_rng(1)
