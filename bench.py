@@ -230,7 +230,7 @@ def main() -> int:
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": "sas::sample_parts_kernel + sas::sample_merge_kernel (one step)",
+                     "kernel": "sas::sample_kernel (one launch per step)",
                      "algorithmic_bytes_per_launch": set_bytes},
         "cpu_baseline": None,
     }

@@ -202,8 +202,8 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   a.out_counts = r->out_counts;
   a.out_flags = r->out_flags;
   a.rec = reinterpret_cast<uint64_t *>(s->recs);
-  a.xval = reinterpret_cast<double *>(a.rec + (size_t)r->rows * parts * sas::kListCap);
-  a.pinfo = reinterpret_cast<uint64_t *>(a.xval + (size_t)r->rows * parts * sas::kListCap);
+  a.mrec = reinterpret_cast<uint4 *>(a.rec + (size_t)r->rows * parts * sas::kListCap);
+  a.pinfo = reinterpret_cast<uint64_t *>(a.mrec + (size_t)r->rows * parts * (sas::kListCap / 2));
   a.ctl = s->ctl;
   a.vocab = r->vocab;
   a.rows = r->rows;

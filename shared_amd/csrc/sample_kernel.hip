@@ -18,18 +18,18 @@
 //   4. values at or above the bound go to per-wave LDS lists (one ballot per
 //      value slot); the part's history ids are handled one by one with their
 //      exact penalized double values;
-//   5. the lists are written as records, unordered: {fp32 key, id}, where
-//      the key of a penalized value is its double rounded toward -inf and a
-//      flag marks keys below their exact value (kept beside the record).
+//   5. the lists are written as records to the part's own slots: plain
+//      values as {fp32 value, id}, history members as {round-down key, id,
+//      exact double}.
 // The merge kernel: one block per row.
-//   6. one round of loads brings the parts' counts and bounds and the
-//      records (slot-major: record j of every part back to back, so every
-//      lane holds records of its own part);
+//   6. one round of loads brings every part's counts, bound and records;
 //   7. the bound again, over the records: the largest part bound, and the
 //      j-th largest of each wave's lane maxima, the smallest over the waves;
-//   8. the records at or above it (about k + 20) are ranked exactly by
-//      (value desc, id asc) through 64-bit (key, flag, ~id) composites;
-//   9. the reference's sample() tail in double precision.
+//   8. the records at or above it are ranked exactly by (value desc, id asc)
+//      through 64-bit (key, inexact, ~id) composites;
+//   9. the reference's sample() tail in double precision: a parallel scan
+//      of the weights decides the top-p cut and the draw whenever rounding
+//      cannot change them, else the reference's sequential chains run.
 //
 // A part list that overflows (heavy ties) or a merge with too many survivors
 // takes an exact radix select over (value, id) keys (SAS_FLAG_SLOW_SELECT).
@@ -48,10 +48,7 @@ constexpr int kHashSlots = 512;
 constexpr int kHistPre = 2;                          // history ids per thread loaded before the logits
 constexpr int kQuadCap = 64;                         // float4 entries of one wave's candidate list
 static_assert(kQuadCap == 64, "a wave's list is one entry per lane at the end");
-constexpr int kSurvCap = 512;                        // survivors the merge ranks
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
-constexpr uint32_t kXFlag = 0x80000000u;             // record id flag: the exact value lies above the key
-constexpr uint32_t kIdBits = 0x7FFFFFFFu;
 
 // The value of the wave's first active lane (wave-uniform values).
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -93,15 +90,6 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ bool before(double va, uint32_t ia, double vb, uint32_t ib) {
   return va > vb || (va == vb && ia < ib);
 }
-
-// Record composite: larger = ranks first.  An unflagged value equals its key;
-// a flagged one lies strictly between its key and the next float, so it
-// ranks after every larger key and before the unflagged values of its own
-// key.  Only two flagged records of one key need their exact values.
-__device__ __forceinline__ uint64_t composite(uint32_t keybits, uint32_t idf) {
-  return ((uint64_t)okey(__uint_as_float(keybits)) << 32) | (idf & kXFlag) | (kIdBits - (idf & kIdBits));
-}
-__device__ __forceinline__ uint32_t comp_id(uint64_t c) { return kIdBits - ((uint32_t)c & kIdBits); }
 
 // 96-bit key of (value, id), larger = ranks first: an order-preserving
 // image of the double (-0 and +0 one value), then the id reversed.
@@ -197,23 +185,32 @@ __device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need,
 }
 
 // ----------------------------------------------------------------- merge --
+//
+// The block that finishes a row's last part merges the row: it loads every
+// part's records, bounds the row's k-th largest key by the j-th largest of
+// each wave's lane maxima, ranks the records at or above the bound exactly
+// by (value desc, id asc) and runs the reference's sample() tail.
 
-constexpr int kMThreads = 256;   // threads of a merge block (more measured no faster)
-constexpr int kMWaves = kMThreads / 64;
+constexpr int kMR = 12;           // plain record slots per thread loaded before the counts are known
+constexpr int kSurvCap = 512;     // survivors the merge ranks
+constexpr int kMemSlots = kListCap / 2;  // member records (16 bytes) of a part
+constexpr uint32_t kInexact = 0x80000000u;  // composite bit: the exact value lies above the key
+constexpr uint32_t kPinfoSlow = 0x80000000u;  // pinfo bit: the part took the exact slow selection
 
 struct MergeLds {
-  uint32_t cnt[kMaxParts];          // records of each part
-  uint32_t thr[kMWaves];
-  uint64_t m_c[kSurvCap + 8];       // survivors: composites (zero-padded to a multiple of 8)
-  uint32_t m_g[kSurvCap];           // their record index in the row
-  double m_v[kSurvCap + 8];         // exact values (exact ranking only; sentinel padded)
-  uint32_t m_id[kSurvCap + 8];
-  double t_val[SAS_MAX_TOP_K + 1];  // the ranked top k and the one after
+  uint32_t wred[kWaves][4];          // per-wave partial results
+  uint64_t s_c[kSurvCap + 8];        // survivors: rank composites (zero padded to a multiple of 8)
+  double s_v[kSurvCap];              // and exact values
+  uint32_t s_rank[kSurvCap];
+  double t_val[SAS_MAX_TOP_K + 1];   // the ranked top k (and the one after)
   uint32_t t_id[SAS_MAX_TOP_K + 1];
   uint64_t t_c[SAS_MAX_TOP_K + 1];
-  double t_p[SAS_MAX_TOP_K];        // exp weights (zero past k)
-  double t_q[SAS_MAX_TOP_K];        // weights / sum
-  uint32_t m, clash, rflags;
+  double t_p[SAS_MAX_TOP_K + 8];     // weights exp((v_i - v_0) / T), zero past k
+  double t_q[SAS_MAX_TOP_K + 8];     // weights / their sum, zero past k
+  double t_pre[SAS_MAX_TOP_K + 8];   // running weight sums
+  double t_cum[SAS_MAX_TOP_K + 8];   // running top-p masses
+  double t_r[SAS_MAX_TOP_K + 8];     // running draw residuals
+  uint32_t m, clash;
 };
 
 struct MergeOut {
@@ -224,16 +221,100 @@ struct MergeOut {
   uint32_t *flags;
 };
 
-// The reference's sample() tail (tokenizer.js:161-177) in double precision
-// over the ranked top kk in ml.t_val / ml.t_id, by wave 0.  The weights and
-// divisions run across lanes (lane i holds candidates i and i + 64) and are
-// staged in LDS; each running sum is one chain in the reference's
-// left-to-right order, run alike by every lane on operands read 8 at a time
-// (broadcast reads), its 8 partial values kept in registers for the tests.
-__device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, double top_p, double u_row,
-                            uint32_t flags, MergeOut o) {
+// A member record: {fp32 key bits of the penalized value (rounded toward
+// -inf), id, the penalized double (low word, high word)}.
+__device__ __forceinline__ double member_value(const uint4 &mr) {
+  return __longlong_as_double((long long)(((uint64_t)mr.w << 32) | mr.z));
+}
+
+// Rank composite, larger = ranks first: the key, then whether the exact
+// value lies above it (strictly between the key and the next float, so it
+// ranks after every larger key and before the exact values of its own
+// key), then the id reversed.  Only two inexact values of one key need
+// their doubles to be ordered.
+__device__ __forceinline__ uint64_t composite(uint32_t key, bool inexact, uint32_t id) {
+  return ((uint64_t)key << 32) | (inexact ? kInexact : 0u) | (0x7FFFFFFFu - id);
+}
+__device__ __forceinline__ uint32_t comp_id(uint64_t c) { return 0x7FFFFFFFu - ((uint32_t)c & 0x7FFFFFFFu); }
+
+// One running chain in the reference's left-to-right order, run by the
+// calling lane alone: dst[i] = init (+ or -) src[0] ... (+ or -) src[i] for
+// every i < n (and a few past it, over the zero padding).  Each step is one
+// add and one LDS store; the operands arrive 8 at a time, the next batch in
+// flight.
+template <bool kSub>
+__device__ __forceinline__ void chain(const double *src, double *dst, int n, double init) {
+  double run = init;
+  double x[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) x[u] = src[u];
+  for (int i = 0; i < n; i += 8) {
+    const int in = i + 8 < n ? i + 8 : i;
+    double y[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) y[u] = src[in + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      run = kSub ? run - x[u] : run + x[u];
+      dst[i + u] = run;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = y[u];
+  }
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The first index (lanes 0..63 of `lo`, then 64..127 of `hi`) below n whose
+// condition holds, or n.
+__device__ __forceinline__ int first_true(bool c_lo, bool c_hi, int n) {
   const int lane = threadIdx.x & 63;
-  const bool greedy = !(temperature > 0.0);
+  const uint64_t a = __ballot(c_lo && lane < n), b = __ballot(c_hi && lane + 64 < n);
+  if (a) return __builtin_ctzll(a);
+  if (b) return 64 + __builtin_ctzll(b);
+  return n;
+}
+
+// Inclusive prefix sum of a double over the wave (a tree of depth 6).
+__device__ __forceinline__ double wave_scan_d(double x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double y = __shfl_up(x, o, 64);
+    if (lane >= o) x = x + y;
+  }
+  return x;
+}
+
+// The reference's sample() tail (tokenizer.js:161-177) in double precision
+// over the ranked top kk in ml.t_val / ml.t_id, by wave 0 (lane i holds
+// candidate i and i + 64).
+//
+// The reference runs three sequential chains: the weight sum s_i (each
+// addition rounded), the top-p mass cum_i = sum of fl(p_j / s_{k-1}), and
+// the draw residual r_i = fl(U * s_{cut-1}) - p_0 - ... - p_i.  The token
+// depends only on the signs of cum_i - top_p (up to the cut) and of r_i
+// (up to the draw).  A parallel scan t_i of the same weights decides those
+// signs wherever they are clear by a margin, with rounding-error bounds
+// (n <= 128 terms, u = 2^-53, S_i = exact sum p_0..p_i >= 1 = p_0):
+//   |s_i - S_i| <= 128u/(1-128u) S_i <= 1.43e-14 S_i   (sequential, any order)
+//   |t_i - S_i| <= 8u S_i <= 1e-15 S_i                  (scan: depth <= 8)
+//   cum_i = (S_i / S_{k-1})(1 + e), |e| <= 2.9e-14, so with
+//   D_i = t_i - fl(top_p t_{k-1}):  |S_{k-1}(cum_i - top_p) - D_i| <= 3.3e-14 S_{k-1}
+//   |r_i - (fl(U t_{cut-1}) - t_i)| <= 3.2e-14 S_{cut-1}
+// A row is taken from the scan when every D_i up to the cut is clear of 0
+// by 1e-13 t_{k-1} and also of the top-p edge test (|cum_i - top_p| < 1e-6),
+// and every residual up to the draw is clear of 0 and of the draw edge test
+// (|r_i| <= 1e-12 s_{cut-1}) by 1e-13 t_{cut-1}: then the sequential chains
+// give the same cut, draw and flags.  Other rows run the chains.
+__device__ __forceinline__ void sample_tail(MergeLds &ml, int kk, int row, double T, double top_p, double u_row,
+                                            uint32_t flags, const MergeOut &o) {
+  const int lane = threadIdx.x & 63;
+  const bool greedy = !(T > 0.0);
   const bool draw = !greedy && kk > 0;
   uint32_t out_id = SAS_NO_TOKEN;
   int cut = 0;
@@ -243,156 +324,82 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
   } else if (greedy) {
     out_id = ml.t_id[0];
   } else {
-    const double T = temperature;
     const double v0 = ml.t_val[0];
-    const bool two = kk > 64;
-    // p_i = exp((v_i - v_0) / T); x / 1 is x, so the division only runs
-    // for other temperatures.  Weights past kk are zero.
+    // p_i = exp((v_i - v_0) / T), zero past kk (x / 1 is x)
     double p_a = 0.0, p_b = 0.0;
     if (lane < kk) {
       double d = ml.t_val[lane] - v0;
       if (T != 1.0) d = d / T;
       p_a = fd_exp(d);
     }
-    if (two && lane + 64 < kk) {
+    if (lane + 64 < kk) {
       double d = ml.t_val[lane + 64] - v0;
       if (T != 1.0) d = d / T;
       p_b = fd_exp(d);
     }
     ml.t_p[lane] = p_a;
     ml.t_p[lane + 64] = p_b;
-    __builtin_amdgcn_wave_barrier();
-    const int nb = (kk + 7) >> 3;  // batches of 8 (zeros past kk leave every sum as it is)
-    // the sum of the weights, left to right
-    // (each chain reads the next batch of 8 while it adds the current one)
-    double run = 0.0;
-    double x[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = ml.t_p[u];
-    for (int b = 0; b < nb; ++b) {
-      const int bn = b + 1 < nb ? b + 1 : b;
-      double y[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) y[u] = ml.t_p[8 * bn + u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) run = run + x[u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = y[u];
+    if (lane < 8) ml.t_p[128 + lane] = 0.0;
+    // ---- the scan ----
+    const double ta = wave_scan_d(p_a);
+    const double tot_a = bcast(ta, 63);
+    const double tb = kk > 64 ? tot_a + wave_scan_d(p_b) : tot_a;
+    const double tk = kk > 64 ? bcast(tb, 63) : tot_a;  // t_{k-1}: the weights past kk are zero
+    const double tp = top_p * tk;
+    const double da = ta - tp, db = tb - tp;
+    int c = min(first_true(da >= 0.0, db >= 0.0, kk) + 1, kk);
+    const double mc = (1e-6 + 1e-13) * tk;
+    bool fast = __ballot((lane < c && fabs(da) < mc) || (lane + 64 < c && fabs(db) < mc)) == 0ull;
+    int pk = 0;
+    if (fast) {
+      const double sub = c - 1 < 64 ? bcast(ta, c - 1) : bcast(tb, c - 65);
+      const double us = u_row * sub;
+      const double ra = us - ta, rb = us - tb;
+      pk = min(first_true(ra <= 0.0, rb <= 0.0, c), c - 1);
+      const double md = (1e-12 + 1e-13) * sub;
+      fast = __ballot((lane <= pk && fabs(ra) <= md) || (lane + 64 <= pk && fabs(rb) <= md)) == 0ull;
     }
-    const double sum = run;
-    q_a = p_a / sum;
-    if (two) q_b = p_b / sum;
-    ml.t_q[lane] = q_a;
-    ml.t_q[lane + 64] = q_b;
-    __builtin_amdgcn_wave_barrier();
-    // top-p cut: the first i with p_0/sum + ... + p_i/sum >= top_p, with
-    // the running weight sum beside it (the draw's mass at the cut)
-    double cum = 0.0, pre = 0.0, sub = 0.0;
-    bool te = false;
-    cut = kk;
-    double xp[8], xq[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      xp[u] = ml.t_p[u];
-      xq[u] = ml.t_q[u];
-    }
-    for (int b = 0; b < nb; ++b) {
-      const int bn = b + 1 < nb ? b + 1 : b;
-      double yp[8], yq[8], pr[8];
-      uint32_t hit = 0u, edge = 0u;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        yp[u] = ml.t_p[8 * bn + u];
-        yq[u] = ml.t_q[8 * bn + u];
-      }
-      double cv[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        pre = pre + xp[u];
-        cum = cum + xq[u];
-        pr[u] = pre;
-        cv[u] = cum;
-      }
-      // the running mass never decreases (zero weights past kk leave it as
-      // it is): a batch whose last value lies 1e-6 or more below top_p holds
-      // neither the cut nor an edge
-      if (cum - top_p > -1e-6) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          hit |= (cv[u] >= top_p ? 1u : 0u) << u;
-          edge |= (fabs(cv[u] - top_p) < 1e-6 ? 1u : 0u) << u;
-        }
-      }
-      const int left = kk - 8 * b;  // candidates of this batch
-      const uint32_t live = left >= 8 ? 0xFFu : (1u << left) - 1u;
-      hit = uni(hit) & live;
-      edge = uni(edge) & live;
-      if (hit) {
-        const int f = __builtin_ctz(hit);
-        cut = 8 * b + f + 1;
-        te |= (edge & ((2u << f) - 1u)) != 0u;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (u == f) sub = pr[u];
-        break;
-      }
-      te |= edge != 0u;
-      sub = pre;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        xp[u] = yp[u];
-        xq[u] = yq[u];
+    wave_lds_sync();
+    if (fast && !o.probs) {
+      cut = c;
+      out_id = ml.t_id[pk];
+    } else {
+      // the weight sum and its prefixes (tokenizer.js:164-167)
+      if (lane == 0) chain<false>(ml.t_p, ml.t_pre, kk, 0.0);
+      wave_lds_sync();
+      const double sum = ml.t_pre[kk - 1];
+      q_a = p_a / sum;
+      q_b = p_b / sum;
+      if (fast) {
+        cut = c;
+        out_id = ml.t_id[pk];
+      } else {
+        ml.t_q[lane] = q_a;
+        ml.t_q[lane + 64] = q_b;
+        if (lane < 8) ml.t_q[128 + lane] = 0.0;
+        wave_lds_sync();
+        // top-p (tokenizer.js:169-174): the first i with q_0 + ... + q_i >= top_p
+        if (lane == 0) chain<false>(ml.t_q, ml.t_cum, kk, 0.0);
+        wave_lds_sync();
+        const double c_a = ml.t_cum[lane], c_b = ml.t_cum[lane + 64];
+        cut = min(first_true(c_a >= top_p, c_b >= top_p, kk) + 1, kk);
+        const bool te = __ballot((lane < cut && fabs(c_a - top_p) < 1e-6) ||
+                                 (lane + 64 < cut && fabs(c_b - top_p) < 1e-6)) != 0ull;
+        // the draw (tokenizer.js:175-177): r = U * (p_0 + ... + p_{cut-1}),
+        // minus p_0, p_1, ... until it reaches 0; else the last of the cut
+        const double sub = ml.t_pre[cut - 1];
+        if (lane == 0) chain<true>(ml.t_p, ml.t_r, cut, u_row * sub);
+        wave_lds_sync();
+        const double r_a = ml.t_r[lane], r_b = ml.t_r[lane + 64];
+        const int pick = min(first_true(r_a <= 0.0, r_b <= 0.0, cut), cut - 1);
+        const double eps = 1e-12 * sub;
+        const bool de = __ballot((lane <= pick && fabs(r_a) <= eps) || (lane + 64 <= pick && fabs(r_b) <= eps)) != 0ull;
+        if (te) flags |= SAS_FLAG_TOPP_EDGE;
+        if (de) flags |= SAS_FLAG_DRAW_EDGE;
+        out_id = ml.t_id[pick];
       }
     }
-    // r = U * (p_0 + ... + p_{cut-1}); the first i at which
-    // r - p_0 - ... - p_i <= 0 is drawn, else the last of the cut
-    double r = u_row * sub;
-    int pick = cut - 1;
-    bool de = false;
-    const int nc = (cut + 7) >> 3;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) xp[u] = ml.t_p[u];
-    for (int b = 0; b < nc; ++b) {
-      const int bn = b + 1 < nc ? b + 1 : b;
-      double yp[8];
-      uint32_t hit = 0u, edge = 0u;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) yp[u] = ml.t_p[8 * bn + u];
-      double rv[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        r = r - xp[u];
-        rv[u] = r;
-      }
-      // the residual never increases: a batch whose last value lies above
-      // 1e-12 * sub holds neither the draw nor an edge
-      if (r <= 1e-12 * sub) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          hit |= (rv[u] <= 0.0 ? 1u : 0u) << u;
-          edge |= (fabs(rv[u]) <= 1e-12 * sub ? 1u : 0u) << u;
-        }
-      }
-      const int left = cut - 8 * b;
-      const uint32_t live = left >= 8 ? 0xFFu : (1u << left) - 1u;
-      hit = uni(hit) & live;
-      edge = uni(edge) & live;
-      if (hit) {
-        const int f = __builtin_ctz(hit);
-        pick = 8 * b + f;
-        de |= (edge & ((2u << f) - 1u)) != 0u;
-        break;
-      }
-      de |= edge != 0u;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) xp[u] = yp[u];
-    }
-    if (te) flags |= SAS_FLAG_TOPP_EDGE;
-    if (de) flags |= SAS_FLAG_DRAW_EDGE;
-    out_id = ml.t_id[pick];
   }
-  const uint32_t id_a = lane < kk ? ml.t_id[lane] : SAS_NO_TOKEN;
-  const uint32_t id_b = lane + 64 < kk ? ml.t_id[lane + 64] : SAS_NO_TOKEN;
   if (lane == 0) {
     o.ids[row] = out_id;
     if (o.counts) {
@@ -409,214 +416,198 @@ __device__ void sample_tail(MergeLds &ml, int kk, int row, double temperature, d
   }
   if (o.cand_ids) {
     uint32_t *oc = o.cand_ids + (int64_t)row * SAS_MAX_TOP_K;
-    oc[lane] = lane < np ? id_a : SAS_NO_TOKEN;
-    oc[lane + 64] = lane + 64 < np ? id_b : SAS_NO_TOKEN;
+    oc[lane] = lane < np ? ml.t_id[lane] : SAS_NO_TOKEN;
+    oc[lane + 64] = lane + 64 < np ? ml.t_id[lane + 64] : SAS_NO_TOKEN;
   }
 }
 
-// Rank of (v, id) among n entries of LDS arrays (value desc, id asc); the
-// arrays hold sentinels (-inf, kEmpty) up to a multiple of 8 past n.
-__device__ __forceinline__ uint32_t rank_exact(const double *vals, const uint32_t *ids, uint32_t n8, double v,
-                                               uint32_t id) {
-  uint32_t rank = 0u;
-  for (uint32_t j = 0; j < n8; j += 8) {
-    double vv[8];
-    uint32_t ii[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      vv[u] = vals[j + u];
-      ii[u] = ids[j + u];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) rank += before(vv[u], ii[u], v, id) ? 1u : 0u;
-  }
-  return rank;
+// Loads of the records the row's parts published.  A record line is written
+// only by its part (whole lines per part and per row of part counts) and read
+// only by the row's merging block, after the part counted itself: the reading
+// CU and its L2 hold no earlier copy of the line.
+__device__ __forceinline__ uint64_t load_rec(const uint64_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint4 load_rec4(const uint4 *p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-constexpr int kMergeR = 20;  // record slots per thread in the first round
-
-template <bool kRowParams>
-__global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArgs a) {
-  __shared__ MergeLds ml;
-  __shared__ uint32_t s_hist[256];
-  __shared__ uint32_t s_sel[4];
+// Merge of row `row`: one block.
+__device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int row, const sas_params &p,
+                                          uint32_t *s_hist, uint32_t *s_sel) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // the XCD that ran the row's parts (the parts kernel gives each XCD a
-  // contiguous run of rows): the row's records may still be in its L2
-  int row = blockIdx.x;
-  if ((a.rows & 7) == 0 && ((a.rows * a.parts) & 7) == 0) row = (row & 7) * (a.rows >> 3) + (row >> 3);
   const int P = a.parts;
-  const uint64_t *pin = a.pinfo + (int64_t)row * P;
-  // record j of part q: index j * P + q of the row
-  const uint64_t *rrow = a.rec + (int64_t)row * kListCap * P;
-  const int NS = kListCap * P;
-
-  // ---- round 1: records and counts first, every load in flight, then the ---
-  // row's parameters, uniform and flags (their scalar loads are not waited
-  // for before the records are requested)
-  uint64_t rec[kMergeR];
-#pragma unroll
-  for (int r = 0; r < kMergeR; ++r) {
-    const int g = tid + kMThreads * r;
-    rec[r] = g < NS ? __builtin_nontemporal_load(rrow + g) : 0ull;
-  }
-  const uint64_t my_info = lane < P ? pin[lane] : 0ull;
-  sas_params p;
-  if constexpr (kRowParams) p = load_row_params(a.row_params + row);
-  else p = a.params;
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
+  // G threads per part; thread (q, sub) reads plain records sub, sub + G,
+  // ... and member record sub of part q
+  const int G = kThreads / P;
+  const int q = tid / G, sub = tid - q * G;
+  const bool qok = q < P;
+  const int64_t pq = (int64_t)row * P + (qok ? q : 0);
+  const uint64_t *rq = a.rec + pq * kListCap;
+  const uint4 *mq = a.mrec + pq * kMemSlots;
+
+  // ---- loads: the part's counts and bound, its first kMR * G plain and
+  // first G member records, all in flight at once ----
+  uint64_t rec[kMR];
+#pragma unroll
+  for (int r = 0; r < kMR; ++r) {
+    const int j = sub + G * r;
+    rec[r] = qok && j < kListCap ? load_rec(rq + j) : 0ull;
+  }
+  const uint4 mr = qok ? load_rec4(mq + sub) : make_uint4(0u, 0u, 0u, 0u);
+  const uint64_t info = qok ? load_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + q) : 0ull;
   const double u_row = greedy ? 0.0 : a.uniforms[row];
-  uint32_t *ctl = a.ctl + (int64_t)row * kCtlStride;
-  const double *xrow = a.xval + (int64_t)row * kListCap * P;
-  // the parts' flags: read and then reset by thread 0 alone
-  const uint32_t rflags_v = tid == 0 ? ctl[kCtlFlags] : 0u;
-  const uint32_t my_cnt = (uint32_t)my_info;
-  if (wave == 0 && lane < P) ml.cnt[lane] = my_cnt;
-  const uint32_t total = wave_sum_u32(my_cnt);
-  const uint32_t maxc = wave_max_u32(my_cnt);
-  const uint32_t pbound = wave_max_u32((uint32_t)(my_info >> 32));
+  for (int i = tid; i < kSurvCap + 8; i += kThreads) ml.s_c[i] = 0ull;  // padding: ranks after everything
+  ml.s_rank[tid] = 0u;
+  ml.s_rank[tid + kThreads] = 0u;
   if (tid == 0) {
     ml.m = 0u;
     ml.clash = 0u;
-    ml.rflags = rflags_v;
   }
-  __syncthreads();
-  const uint32_t rflags = ml.rflags;
-  if (tid == 0) {
-    // read by every part of this launch: reset for the next one
-    ctl[kCtlFlags] = 0u;
-  }
-  // slot g = tid + kMThreads r is record s of part q: (s, q) stepped without division
-  const int s0 = tid / P, q0 = tid - s0 * P;
-  const int ds = kMThreads / P, dq = kMThreads - ds * P;
-  // ---- the bound ----------------------------------------------------------------
-  uint32_t key[kMergeR];
-  uint32_t kmax = 0u;
-  {
-    // every slot's part count read at once (no branch, one LDS wait), then
-    // the keys of the slots that hold a record
-    uint32_t cq[kMergeR];
-    int ss[kMergeR];
-    if (dq == 0) {
-      // the part count divides the block: every slot of a thread is its one
-      // part's, at records s0, s0 + ds, ...
-      const uint32_t c0 = ml.cnt[q0];
-#pragma unroll
-      for (int r = 0; r < kMergeR; ++r) {
-        ss[r] = s0 + r * ds;
-        cq[r] = c0;
-      }
-    } else {
-      int s = s0, q = q0;
-#pragma unroll
-      for (int r = 0; r < kMergeR; ++r) {
-        ss[r] = s;
-        cq[r] = ml.cnt[q];
-        s += ds;
-        q += dq;
-        const bool wrap = q >= P;
-        q = wrap ? q - P : q;
-        s = wrap ? s + 1 : s;
-      }
+  const uint32_t np = qok ? (uint32_t)info & 0x7FFFu : 0u;          // plain records of part q
+  const uint32_t nm = qok ? ((uint32_t)info >> 16) & 0x7FFFu : 0u;  // member records
+  const bool pslow = ((uint32_t)info & kPinfoSlow) != 0u;
+  const uint32_t bq = (uint32_t)(info >> 32);                       // the part's bound key
+  const int nfast = min((int)np, G * kMR);
+  // records past the first kMR * G plain or G member ones of a part (rarely
+  // any) are read again where they are used: f(key, composite, exact value)
+  auto for_extra = [&](auto f) __attribute__((always_inline)) {
+    for (int j = sub + G * kMR; j < (int)np; j += G) {
+      const uint64_t rc = load_rec(rq + j);
+      const float x = __uint_as_float((uint32_t)rc);
+      const uint32_t kx = okey(x);
+      f(kx, composite(kx, false, (uint32_t)(rc >> 32)), (double)x);
     }
-#pragma unroll
-    for (int r = 0; r < kMergeR; ++r) {
-      const bool ok = (tid + kMThreads * r < NS) & ((uint32_t)ss[r] < cq[r]);
-      const uint32_t kx = okey(__uint_as_float((uint32_t)rec[r]));
-      key[r] = ok ? kx : 0u;
-      kmax = max(kmax, key[r]);
-    }
-  }
-  const int jw = (k + kMWaves - 1) / kMWaves;
-  const uint32_t tw = wave_jth_largest_key16(kmax, jw);
-  if (lane == 0) ml.thr[wave] = tw;
-  __syncthreads();
-  uint32_t tmin = 0xFFFFFFFFu;
-#pragma unroll
-  for (int w = 0; w < kMWaves; ++w) tmin = min(tmin, ml.thr[w]);
-  const uint32_t bnd = max(pbound, max(tmin, 1u));
-  // ---- survivors: composites and record indices ----------------------------------
-  auto keep_one = [&](uint32_t kk, uint64_t rc, int g) {
-    const bool keep = kk >= bnd;
-    const uint64_t bb = __ballot(keep);
-    if (bb) {
-      uint32_t base = 0u;
-      if (lane == 0) base = atomicAdd(&ml.m, (uint32_t)__popcll(bb));
-      base = uni(base);
-      if (keep) {
-        const uint32_t d = base + lanes_below(bb);
-        if (d < (uint32_t)kSurvCap) {
-          ml.m_c[d] = composite((uint32_t)rc, (uint32_t)(rc >> 32));
-          ml.m_g[d] = (uint32_t)g;
-        }
-      }
+    for (int j = sub + G; j < (int)nm; j += G) {
+      const uint4 m4 = load_rec4(mq + j);
+      const uint32_t kx = okey(__uint_as_float(m4.x));
+      const double v = member_value(m4);
+      f(kx, composite(kx, (double)__uint_as_float(m4.x) != v, m4.y), v);
     }
   };
-  {
-    // first round: each lane's count, a ballot prefix over the count bits,
-    // one LDS atomic per wave, then the lane's own records
-    uint32_t mine = 0u;
+  // a plain record's value is fkey(key): keep (key, id) pairs
+  uint32_t key[kMR], rid[kMR];
+  uint32_t kmax = 0u;
 #pragma unroll
-    for (int r = 0; r < kMergeR; ++r) mine += key[r] >= bnd ? 1u : 0u;
-    static_assert(kMergeR < 32, "a lane's survivor count fits 5 bits");
+  for (int r = 0; r < kMR; ++r) {
+    key[r] = sub + G * r < nfast ? okey(__uint_as_float((uint32_t)rec[r])) : 0u;
+    rid[r] = (uint32_t)(rec[r] >> 32);
+    kmax = max(kmax, key[r]);
+  }
+  const uint32_t mkey = (uint32_t)sub < nm ? okey(__uint_as_float(mr.x)) : 0u;
+  kmax = max(kmax, mkey);
+  for_extra([&](uint32_t kx, uint64_t, double) { kmax = max(kmax, kx); });
+  // ---- the bound: at least jw lanes of every wave hold a key at or above
+  // the wave's result, so k keys reach the smallest; and every part's bound
+  // certifies k values of its own ----
+  const int jw = (k + kWaves - 1) / kWaves;
+  {
+    const uint32_t tw = wave_jth_largest_key16(kmax, jw), wb = wave_max_u32(bq);
+    const uint32_t ws = __ballot(pslow) ? 1u : 0u;
+    if (lane == 0) {
+      ml.wred[wave][0] = tw;
+      ml.wred[wave][1] = wb;
+      ml.wred[wave][2] = ws;
+    }
+  }
+  __syncthreads();
+  uint32_t lo = 0xFFFFFFFFu, pb = 0u;
+  bool slow = false;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    lo = min(lo, ml.wred[w][0]);
+    pb = max(pb, ml.wred[w][1]);
+    slow = slow || ml.wred[w][2] != 0u;
+  }
+  lo = max(max(lo, pb), 1u);  // key 0: no value
+  // ---- survivors: composites and exact values of the keys at or above lo,
+  // one LDS atomic per wave ----
+  {
+    uint32_t mine = (mkey >= lo) ? 1u : 0u;
+#pragma unroll
+    for (int r = 0; r < kMR; ++r) mine += key[r] >= lo ? 1u : 0u;
+    static_assert(kMR + 1 < 16, "a lane's survivor count fits 4 bits");
     uint32_t pre = 0u, tot = 0u;
 #pragma unroll
-    for (int bit = 0; bit < 5; ++bit) {
+    for (int bit = 0; bit < 4; ++bit) {
       const uint64_t bb = __ballot((mine >> bit) & 1u);
       pre += lanes_below(bb) << bit;
       tot += (uint32_t)__popcll(bb) << bit;
     }
-    if (tot) {
-      uint32_t base = 0u;
-      if (lane == 0) base = atomicAdd(&ml.m, tot);
-      uint32_t d = uni(base) + pre;
+    uint32_t base = 0u;
+    if (lane == 0 && tot) base = atomicAdd(&ml.m, tot);
+    uint32_t d = uni(base) + pre;
 #pragma unroll
-      for (int r = 0; r < kMergeR; ++r) {
-        if (key[r] >= bnd) {
-          if (d < (uint32_t)kSurvCap) {
-            ml.m_c[d] = composite((uint32_t)rec[r], (uint32_t)(rec[r] >> 32));
-            ml.m_g[d] = (uint32_t)(tid + kMThreads * r);
-          }
-          ++d;
+    for (int r = 0; r < kMR; ++r) {
+      const bool kp = key[r] >= lo;
+      if (kp && d < (uint32_t)kSurvCap) {
+        ml.s_c[d] = composite(key[r], false, rid[r]);
+        ml.s_v[d] = (double)fkey(key[r]);
+      }
+      d += kp ? 1u : 0u;
+    }
+    if (mkey >= lo && d < (uint32_t)kSurvCap) {
+      const double v = member_value(mr);
+      ml.s_c[d] = composite(mkey, (double)__uint_as_float(mr.x) != v, mr.y);
+      ml.s_v[d] = v;
+    }
+    for_extra([&](uint32_t kx, uint64_t c, double v) {
+      if (kx >= lo) {
+        const uint32_t e = atomicAdd(&ml.m, 1u);
+        if (e < (uint32_t)kSurvCap) {
+          ml.s_c[e] = c;
+          ml.s_v[e] = v;
         }
       }
-    }
-  }
-  // records past the first round (parts with many candidates)
-  const int gend = min(NS, (int)maxc * P);
-  for (int g0 = kMThreads * kMergeR; g0 < gend; g0 += kMThreads) {
-    const int g = g0 + tid;
-    const int s = g / P;
-    const bool ok = g < gend && (uint32_t)s < ml.cnt[g - s * P];
-    const uint64_t rc = ok ? rrow[g] : 0ull;
-    keep_one(ok ? okey(__uint_as_float((uint32_t)rc)) : 0u, rc, g);
+    });
   }
   __syncthreads();
   uint32_t m = ml.m;
-  uint32_t flags = rflags;
-  bool exact = false;  // rank by exact doubles (m_v, m_id) instead of composites
+  uint32_t flags = slow ? SAS_FLAG_SLOW_SELECT : 0u;
+  bool exact = false;  // rank by exact doubles (ties of inexact keys, or the slow path)
   if (m > (uint32_t)kSurvCap) {
-    // too many survivors (ties): exact select over every record
+    // too many survivors (ties): the exact k-th largest (value, id) over
+    // every record, then the records at or above it
     flags |= SAS_FLAG_SLOW_SELECT;
     exact = true;
-    const int rounds = (gend + kMThreads - 1) / kMThreads;
     auto for_recs = [&](auto f) {
+      const int rounds = (kListCap + G - 1) / G;
       for (int i = 0; i < rounds; ++i) {
-        const int g = i * kMThreads + tid;
-        const int s = g / P;
-        const bool ok = g < gend && (uint32_t)s < ml.cnt[g - s * P];
+        const int j = sub + G * i;
+        const bool ok = j < (int)np;
         double v = 0.0;
         uint32_t id = 0u;
         if (ok) {
-          const uint64_t rc = rrow[g];
-          id = (uint32_t)(rc >> 32) & kIdBits;
-          v = ((uint32_t)(rc >> 32) & kXFlag) ? xrow[g] : (double)__uint_as_float((uint32_t)rc);
+          const uint64_t rc = load_rec(rq + j);
+          v = (double)__uint_as_float((uint32_t)rc);
+          id = (uint32_t)(rc >> 32);
+        }
+        f(key96(v, id), ok, v, id);
+      }
+      const int mrounds = (kMemSlots + G - 1) / G;
+      for (int i = 0; i < mrounds; ++i) {
+        const int j = sub + G * i;
+        const bool ok = j < (int)nm;
+        double v = 0.0;
+        uint32_t id = 0u;
+        if (ok) {
+          const uint4 m4 = load_rec4(mq + j);
+          v = member_value(m4);
+          id = m4.y;
         }
         f(key96(v, id), ok, v, id);
       }
     };
-    const uint32_t need = min(total, (uint32_t)k);
+    uint32_t tot = 0u;
+    for_recs([&](const Key96 &, bool ok, double, uint32_t) { tot += ok ? 1u : 0u; });
+    if (tid == 0) ml.m = 0u;
+    __syncthreads();
+    atomicAdd(&ml.m, tot);
+    __syncthreads();
+    const uint32_t need = min(ml.m, (uint32_t)k);
+    __syncthreads();
     const Key96 kth = block_select96(
         [&](auto f) { for_recs([&](const Key96 &kx, bool ok, double, uint32_t) { f(kx, ok); }); }, need, s_hist,
         s_sel);
@@ -624,83 +615,88 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
     __syncthreads();
     for_recs([&](const Key96 &kx, bool ok, double v, uint32_t id) {
       if (ok && key_ge(kx, kth)) {
-        const uint32_t d = atomicAdd(&ml.m, 1u);
-        ml.m_v[d] = v;
-        ml.m_id[d] = id;
+        const uint32_t e = atomicAdd(&ml.m, 1u);
+        if (e < (uint32_t)kSurvCap) {
+          ml.s_c[e] = composite(0u, false, id);  // the id; the value is s_v
+          ml.s_v[e] = v;
+        }
       }
     });
     __syncthreads();
-    m = ml.m;
+    m = min(ml.m, (uint32_t)kSurvCap);
   }
   const uint32_t m8 = (m + 7u) & ~7u;
+  const uint32_t m64 = (m + 63u) & ~63u;
+  const uint32_t groups = m64 >= (uint32_t)kThreads ? 1u : (uint32_t)kThreads / max(m64, 64u);
+  const uint32_t per = (uint32_t)kThreads / groups;
+  const uint32_t share = ((m8 + groups - 1u) / groups + 7u) & ~7u;
   if (!exact) {
-    // ---- rank by composites; the first k + 1 ranks are kept ----------------------
-    if ((uint32_t)tid < m8 - m) ml.m_c[m + tid] = 0ull;
-    __syncthreads();
-    // up to 8 threads per survivor (as m allows), each counting a share of
-    // the others; the shares are summed across the group's lanes
-    int lg = 0;
-    while (lg < 3 && (uint32_t)(kMThreads >> (lg + 1)) >= m) ++lg;
-    const uint32_t gsz = 1u << lg;
-    const uint32_t share = ((m8 >> lg) + 7u) & ~7u;  // entries per thread, a multiple of 8
-    for (uint32_t i0 = 0; i0 < m; i0 += (uint32_t)(kMThreads >> lg)) {
-      const uint32_t i = i0 + ((uint32_t)tid >> lg);
-      const uint32_t part = (uint32_t)tid & (gsz - 1u);
-      const uint64_t c = i < m ? ml.m_c[i] : ~0ull;
-      // a flagged record's exact value: loaded while the rank is counted
-      const bool lead = i < m && part == 0u;
-      const double xv = lead && (c & kXFlag) ? xrow[ml.m_g[i]] : (double)fkey((uint32_t)(c >> 32));
-      uint32_t rank = 0u;
-      const uint32_t j0 = part * share, j1 = min(j0 + share, m8);
-#pragma unroll 4
-      for (uint32_t j = j0; j < j1; j += 8) {
-        uint64_t o[8];
+    // ---- rank by composites; the first k + 1 ranks are kept ----
+    for (uint32_t i0 = 0; i0 < m; i0 += per) {
+      const uint32_t i = i0 + (uint32_t)tid % per;
+      const uint32_t g = (uint32_t)tid / per;
+      if (i < m) {
+        const uint64_t c = ml.s_c[i];
+        uint32_t rank = 0u;
+        const uint32_t j0 = g * share, j1 = min(j0 + share, m8);
+        for (uint32_t j = j0; j < j1; j += 8) {
+          uint64_t o8[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) o[u] = ml.m_c[j + u];
+          for (int u = 0; u < 8; ++u) o8[u] = ml.s_c[j + u];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) rank += o[u] > c ? 1u : 0u;
-      }
-      if (lg >= 1) rank += (uint32_t)__shfl_xor((int)rank, 1, 64);
-      if (lg >= 2) rank += (uint32_t)__shfl_xor((int)rank, 2, 64);
-      if (lg >= 3) rank += (uint32_t)__shfl_xor((int)rank, 4, 64);
-      if (lead && rank <= (uint32_t)k) {
-        ml.t_c[rank] = c;
-        ml.t_id[rank] = comp_id(c);
-        ml.t_val[rank] = xv;
+          for (int u = 0; u < 8; ++u) rank += o8[u] > c ? 1u : 0u;
+        }
+        if (groups == 1u) ml.s_rank[i] = rank;
+        else atomicAdd(&ml.s_rank[i], rank);
       }
     }
     __syncthreads();
-    // Two flagged records of one key rank next to each other, by id: if
-    // such a pair lies within the first k + 1 ranks, rank by exact values.
+    for (uint32_t i = (uint32_t)tid; i < m; i += kThreads) {
+      const uint32_t rank = ml.s_rank[i];
+      if (rank <= (uint32_t)k) {
+        const uint64_t c = ml.s_c[i];
+        ml.t_c[rank] = c;
+        ml.t_val[rank] = ml.s_v[i];
+        ml.t_id[rank] = comp_id(c);
+      }
+    }
+    __syncthreads();
+    // two inexact values of one key within the first k + 1 ranks: their
+    // order needs the doubles
     const uint32_t nt = min(m, (uint32_t)k + 1u);
     if ((uint32_t)tid + 1u < nt) {
       const uint64_t x = ml.t_c[tid], y = ml.t_c[tid + 1];
-      if ((x & kXFlag) && (y & kXFlag) && (x >> 32) == (y >> 32)) ml.clash = 1u;
+      if ((x & kInexact) && (y & kInexact) && (x >> 32) == (y >> 32)) ml.clash = 1u;
     }
     __syncthreads();
     if (ml.clash) {
       exact = true;
       flags |= SAS_FLAG_SLOW_SELECT;
-      for (uint32_t i = (uint32_t)tid; i < m; i += kMThreads) {
-        const uint64_t c = ml.m_c[i];
-        ml.m_id[i] = comp_id(c);
-        ml.m_v[i] = (c & kXFlag) ? xrow[ml.m_g[i]] : (double)fkey((uint32_t)(c >> 32));
-      }
+      for (uint32_t i = (uint32_t)tid; i < kSurvCap; i += kThreads) ml.s_rank[i] = 0u;
+      __syncthreads();
     }
   }
   if (exact) {
-    if ((uint32_t)tid < m8 - m) {
-      ml.m_v[m + tid] = -__builtin_inf();
-      ml.m_id[m + tid] = kEmpty;
+    // ---- rank by exact (value, id) ----
+    for (uint32_t i0 = 0; i0 < m; i0 += per) {
+      const uint32_t i = i0 + (uint32_t)tid % per;
+      const uint32_t g = (uint32_t)tid / per;
+      if (i < m) {
+        const double v = ml.s_v[i];
+        const uint32_t id = comp_id(ml.s_c[i]);
+        uint32_t rank = 0u;
+        const uint32_t j0 = g * share, j1 = min(j0 + share, m);
+        for (uint32_t j = j0; j < j1; ++j) rank += before(ml.s_v[j], comp_id(ml.s_c[j]), v, id) ? 1u : 0u;
+        if (groups == 1u) ml.s_rank[i] = rank;
+        else atomicAdd(&ml.s_rank[i], rank);
+      }
     }
     __syncthreads();
-    for (uint32_t i = (uint32_t)tid; i < m; i += kMThreads) {
-      const double v = ml.m_v[i];
-      const uint32_t id = ml.m_id[i];
-      const uint32_t rank = rank_exact(ml.m_v, ml.m_id, m8, v, id);
+    for (uint32_t i = (uint32_t)tid; i < m; i += kThreads) {
+      const uint32_t rank = ml.s_rank[i];
       if (rank < (uint32_t)k) {
-        ml.t_val[rank] = v;
-        ml.t_id[rank] = id;
+        ml.t_val[rank] = ml.s_v[i];
+        ml.t_id[rank] = comp_id(ml.s_c[i]);
       }
     }
     __syncthreads();
@@ -711,6 +707,21 @@ __global__ __launch_bounds__(kMThreads) void sample_merge_kernel(const SampleArg
   sample_tail(ml, kk, row, p.temperature, p.top_p, u_row, flags, o);
 }
 
+// One block per row, after the parts kernel (stream order makes every record
+// visible).  Block b takes the row whose parts ran on its XCD (the parts
+// kernel gives each XCD a contiguous run of rows), so the records come from
+// that XCD's L2.
+__global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs a) {
+  __shared__ MergeLds ml;
+  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_sel[4];
+  int row = blockIdx.x;
+  if ((a.rows & 7) == 0 && ((a.rows * a.parts) & 7) == 0) row = (row & 7) * (a.rows >> 3) + (row >> 3);
+  sas_params p = a.params;
+  if (a.row_params) p = load_row_params(a.row_params + row);
+  merge_row(a, ml, row, p, s_hist, s_sel);
+}
+
 // ------------------------------------------------------------------ parts --
 
 constexpr int kPassWords = kSpanPass / 32;  // mask / history words of one pass: one per thread
@@ -718,6 +729,9 @@ static_assert(kPassWords == kThreads, "one word of 32 ids per thread");
 constexpr int kXCap = 256;                  // exact-valued entries of a part: history members, or an exact selection
 static_assert(kXCap == kThreads, "one exact entry per thread");
 static_assert(kXCap >= SAS_MAX_TOP_K, "an exact part selection fits the exact list");
+
+// x_id bit of an exact-selection entry that is a history member
+constexpr uint32_t kXMem = 0x80000000u;
 
 struct PartLds {
   uint32_t hkey[kHashSlots];    // (id, count) open-addressing hash of the part's history ids
@@ -727,13 +741,17 @@ struct PartLds {
   uint32_t hmem[kPassWords];    // the pass's allowed history members
   float4 q_val[kWaves * kQuadCap];     // per-wave candidate lists: float4s with a value at the bound
   uint32_t q_base[kWaves * kQuadCap];  // and the id of their first value
-  double x_val[kXCap];          // exact-valued entries: value, id
+  double x_val[kXCap];          // exact-valued entries: value, id (| kXMem for a member)
   uint32_t x_id[kXCap];
   uint32_t hover;               // some history id did not fit in the hash
 };
 
 __device__ __forceinline__ uint32_t hash_slot(uint32_t id) { return (id * 2654435761u) >> 23; }
 static_assert(kHashSlots == 512, "hash_slot yields 9 bits");
+
+// A record store: the merge kernel reads it after the launch boundary, on
+// the same XCD (rows stay on one XCD), so from L2.
+__device__ __forceinline__ void put_rec(uint64_t *p, uint64_t v) { *p = v; }
 
 template <bool kMask, bool kHist, bool kSoftcap>
 __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6) void sample_parts_kernel(const SampleArgs a) {
@@ -745,7 +763,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   __shared__ uint32_t s_sel[4];
   __shared__ uint32_t s_nx;           // exact-valued entries (may pass kXCap: overflow)
   __shared__ uint32_t s_nxk;          // exact-valued entries kept at the end
-  __shared__ uint32_t s_nxw;          // exact-valued records written
+  __shared__ uint32_t s_nxw;          // exact-valued plain records written
+  __shared__ uint32_t s_nmw;          // member records written
+  __shared__ uint32_t s_nxm;          // members among an exact selection's entries
   __shared__ uint32_t s_flags;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -769,7 +789,6 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const float softcap = kSoftcap ? p.softcap : 0.0f;
   const float *lrow = a.logits + (int64_t)row * a.logits_stride;
   const uint32_t *mrow = kMask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
-  uint32_t *ctl = a.ctl + (int64_t)row * kCtlStride;
 
   // ---- history ids (loaded first: the tables fill while the logits load) ----
   int h0 = 0, h1 = 0;
@@ -823,6 +842,8 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     s_nx = 0u;
     s_nxk = 0u;
     s_nxw = 0u;
+    s_nmw = 0u;
+    s_nxm = 0u;
     s_flags = 0u;
   }
   auto set_bit = [&](uint32_t id, int base) __attribute__((always_inline)) {
@@ -882,16 +903,6 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       for (int i = h0; i < h1; ++i) c += a.hist_ids[i] == id ? 1u : 0u;
     return c;
   };
-  // exact value of a history member: CTRL repetition, then OpenAI frequency
-  // and presence (presence alone is tokenizer.js:157)
-  auto hist_value = [&](uint32_t id, float x, uint32_t mw, double &val) __attribute__((always_inline)) -> bool {
-    if (kMask && !((mw >> (id & 31u)) & 1u)) return false;
-    if (kSoftcap && softcap > 0.0f) x = softcap_f32(x, softcap);
-    if (x != x) return false;
-    val = penalize((double)x, hcount(id), p);
-    return val == val;
-  };
-
   // ---- passes: values, the bound, the lists ---------------------------------
   const int jw = (k + kWaves - 1) / kWaves;  // per-wave rank of the bound
   const uint32_t sh = 4u * (uint32_t)(tid & 7);
@@ -1023,12 +1034,16 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   }
   // the history members' exact values, kept at or above the final bound
   // (NaN ones never are).  The list is complete: every wave recorded its
-  // members before the last pass's bound barrier.
-  bool xw = false;  // this thread writes exact entry tid
+  // members before the last pass's bound barrier.  A member's record holds
+  // the round-down key of its penalized value and the double itself.
+  bool xw = false;   // this thread writes exact entry tid
+  bool xmem = true;  // ... as a member record
+  uint32_t xid = 0u;
+  double xv = 0.0;
   if (has_hist && (uint32_t)tid < min(s_nx, (uint32_t)kXCap)) {
-    const double val = penalize(L.x_val[tid], hcount(L.x_id[tid]), p);
-    L.x_val[tid] = val;
-    xw = val >= (double)tff;
+    xid = L.x_id[tid];
+    xv = penalize(L.x_val[tid], hcount(xid), p);
+    xw = xv >= (double)tff;
     if (xw) atomicAdd(&s_nxk, 1u);
   }
   __syncthreads();
@@ -1036,6 +1051,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) nw[w] = s_nw[w];
   uint32_t nx = s_nxk;
+  uint32_t nxm = nx;  // exact entries that are members (all of them unless the slow selection ran)
   const bool overflow = s_qover != 0u || s_nx > (uint32_t)kXCap || nw[0] + nw[1] + nw[2] + nw[3] + nx > (uint32_t)kListCap;
   if (overflow) {
     // more values at or above the bound than the lists hold (ties): the
@@ -1047,25 +1063,24 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
         const uint32_t off = (uint32_t)(i * kThreads + tid);
         const uint32_t id = (uint32_t)lo + off;
         bool ok = off < (uint32_t)nids;
+        uint32_t cnt = 0u;
+        float x = 0.0f;
         double val = 0.0;
         if (ok) {
           const uint32_t mw = kMask ? mrow[id >> 5] : ~0u;
-          float x = lrow[id];
-          const uint32_t cnt = has_hist ? hcount(id) : 0u;
-          if (cnt) {
-            ok = hist_value(id, x, mw, val);
-          } else {
-            ok = !kMask || ((mw >> (id & 31u)) & 1u);
-            if (kSoftcap && softcap > 0.0f) x = softcap_f32(x, softcap);
-            ok = ok && x == x;
-            val = (double)x;
-          }
+          x = lrow[id];
+          cnt = has_hist ? hcount(id) : 0u;
+          ok = !kMask || ((mw >> (id & 31u)) & 1u);
+          if (kSoftcap && softcap > 0.0f) x = softcap_f32(x, softcap);
+          ok = ok && x == x;
+          val = cnt ? penalize((double)x, cnt, p) : (double)x;
+          ok = ok && val == val;
         }
-        f(key96(val, id), ok, val, id);
+        f(key96(val, id), ok, val, id | (cnt ? kXMem : 0u), x, cnt);
       }
     };
     uint32_t nval = 0u;
-    for_elems([&](const Key96 &, bool ok, double, uint32_t) { nval += ok ? 1u : 0u; });
+    for_elems([&](const Key96 &, bool ok, double, uint32_t, float, uint32_t) { nval += ok ? 1u : 0u; });
     if (tid == 0) s_sel[3] = 0u;
     __syncthreads();
     atomicAdd(&s_sel[3], nval);
@@ -1079,14 +1094,17 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     }
     if (need > 0u) {
       const Key96 kth = block_select96(
-          [&](auto f) { for_elems([&](const Key96 &kx, bool ok, double, uint32_t) { f(kx, ok); }); }, need, s_hist,
-          s_sel);
+          [&](auto f) {
+            for_elems([&](const Key96 &kx, bool ok, double, uint32_t, float, uint32_t) { f(kx, ok); });
+          },
+          need, s_hist, s_sel);
       // exactly need <= kXCap entries
-      for_elems([&](const Key96 &kx, bool ok, double val, uint32_t id) {
+      for_elems([&](const Key96 &kx, bool ok, double val, uint32_t idm, float x, uint32_t cnt) {
         if (ok && key_ge(kx, kth)) {
           const uint32_t d = atomicAdd(&s_nx, 1u);
           L.x_val[d] = val;
-          L.x_id[d] = id;
+          L.x_id[d] = idm;
+          if (cnt) atomicAdd(&s_nxm, 1u);
         }
       });
     }
@@ -1096,40 +1114,51 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     nx = s_nx;
     xw = (uint32_t)tid < nx;
     pm = 0u;
+    nxm = s_nxm;
+    if (xw) {
+      // an exact entry: a plain value, or a member with its penalized double
+      xv = L.x_val[tid];
+      const uint32_t xi = L.x_id[tid];
+      xmem = (xi & kXMem) != 0u;
+      xid = xi & ~kXMem;
+    }
   }
 
   // ---- records: each wave's values after those of the waves before it, then
-  // the exact-valued entries (record j of this part at row index j * P + part)
+  // the exact plain values, in the part's own kListCap slots; the members in
+  // the part's own member slots
   uint32_t off = 0u;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) off += w < wave ? nw[w] : 0u;
   const uint32_t nplain = nw[0] + nw[1] + nw[2] + nw[3];
-  uint64_t *rrow = a.rec + (int64_t)row * kListCap * P + part;
-  double *xrow = a.xval + (int64_t)row * kListCap * P + part;
+  uint64_t *rrow = a.rec + ((int64_t)row * P + part) * kListCap;
+  uint4 *mrow4 = a.mrec + ((int64_t)row * P + part) * kMemSlots;
   {
     uint32_t j = off + qpre;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if ((pm >> c) & 1u) {
         const float x = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
-        rrow[(int64_t)j * P] = (uint64_t)__float_as_uint(x) | ((uint64_t)(qid + (uint32_t)c) << 32);
+        put_rec(rrow + j, (uint64_t)__float_as_uint(x) | ((uint64_t)(qid + (uint32_t)c) << 32));
         ++j;
       }
     }
   }
   if (xw) {
-    // an exact value's round-down key, flagged when the value lies above it
-    const double val = L.x_val[tid];
-    const float kf = rd_f32(val);
-    const uint32_t idf = L.x_id[tid] | ((double)kf != val ? kXFlag : 0u);
-    const int64_t j = (int64_t)(nplain + atomicAdd(&s_nxw, 1u)) * P;
-    rrow[j] = (uint64_t)__float_as_uint(kf) | ((uint64_t)idf << 32);
-    if (idf & kXFlag) xrow[j] = val;
+    if (xmem) {
+      const uint32_t j = atomicAdd(&s_nmw, 1u);
+      uint64_t *d = reinterpret_cast<uint64_t *>(mrow4 + j);
+      put_rec(d, (uint64_t)__float_as_uint(rd_f32(xv)) | ((uint64_t)xid << 32));
+      put_rec(d + 1, (uint64_t)__double_as_longlong(xv));
+    } else {
+      const uint32_t j = nplain + atomicAdd(&s_nxw, 1u);
+      put_rec(rrow + j, (uint64_t)__float_as_uint((float)xv) | ((uint64_t)xid << 32));
+    }
   }
-  if (tid == 0) {
-    a.pinfo[(int64_t)row * P + part] = (uint64_t)(nplain + nx) | ((uint64_t)tkey << 32);
-    if (s_flags) __hip_atomic_fetch_or(ctl + kCtlFlags, s_flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // the part's counts, bound and slow-selection flag
+  if (tid == 0)
+    put_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + part,
+            (uint64_t)((nplain + nx - nxm) | (nxm << 16) | (s_flags ? kPinfoSlow : 0u)) | ((uint64_t)tkey << 32));
 }
 
 // Parts per row and ids per part: one pass per part (8192 ids), more
@@ -1156,7 +1185,9 @@ void choose_parts(int rows, int vocab, int min_blocks, int *parts, int *span) {
   *parts = (int)pc;
 }
 
-size_t sample_rec_bytes(int rows, int parts) { return (size_t)rows * parts * (kListCap * 16 + 8); }
+size_t sample_rec_bytes(int rows, int parts) {
+  return (size_t)rows * parts * kListCap * 16 + (size_t)rows * pinfo_stride(parts) * 8;
+}
 
 __global__ __launch_bounds__(kThreads) void pad_rows_kernel(const float *src, int64_t stride, int vocab, int rows,
                                                            float *dst) {
@@ -1174,26 +1205,23 @@ hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows
 }
 
 template <bool kMask, bool kHist, bool kSoftcap>
-static void launch_parts(const SampleArgs &a, hipStream_t stream) {
-  hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap>), dim3((unsigned)(a.rows * a.parts)), dim3(kThreads),
-                     0, stream, a);
+static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
+  hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap>), dim3((unsigned)(a.rows * a.parts)),
+                     dim3(kThreads), 0, stream, a);
 }
 
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) {
   switch ((a.mask ? 4 : 0) | (a.hist_ids ? 2 : 0) | (softcap ? 1 : 0)) {
-    case 0: launch_parts<false, false, false>(a, stream); break;
-    case 1: launch_parts<false, false, true>(a, stream); break;
-    case 2: launch_parts<false, true, false>(a, stream); break;
-    case 3: launch_parts<false, true, true>(a, stream); break;
-    case 4: launch_parts<true, false, false>(a, stream); break;
-    case 5: launch_parts<true, false, true>(a, stream); break;
-    case 6: launch_parts<true, true, false>(a, stream); break;
-    default: launch_parts<true, true, true>(a, stream); break;
+    case 0: launch_kernel<false, false, false>(a, stream); break;
+    case 1: launch_kernel<false, false, true>(a, stream); break;
+    case 2: launch_kernel<false, true, false>(a, stream); break;
+    case 3: launch_kernel<false, true, true>(a, stream); break;
+    case 4: launch_kernel<true, false, false>(a, stream); break;
+    case 5: launch_kernel<true, false, true>(a, stream); break;
+    case 6: launch_kernel<true, true, false>(a, stream); break;
+    default: launch_kernel<true, true, true>(a, stream); break;
   }
-  if (a.row_params)
-    hipLaunchKernelGGL(sample_merge_kernel<true>, dim3((unsigned)a.rows), dim3(kMThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL(sample_merge_kernel<false>, dim3((unsigned)a.rows), dim3(kMThreads), 0, stream, a);
+  hipLaunchKernelGGL(sample_merge_kernel, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -55,6 +55,19 @@ __device__ __forceinline__ double penalize(double v, uint32_t count, const sas_p
 // approximate exp(r) with the degree-5 Remez rational form, scale by 2^k.
 // V8's Math.exp is this algorithm, so probabilities come out bit-identical
 // to the reference's JS sample().
+//
+// Written without branches (lanes of a wave take different paths): every
+// path is computed and the result selected.  The paths fdlibm keeps apart
+// are one formula here, bit for bit:
+//   - |x| in (ln2/2, 1.5 ln2) uses k = +-1, hi = x -+ ln2_hi, lo = +-ln2_lo,
+//     which is k*ln2_hi and k*ln2_lo for k = +-1 (exact products);
+//   - |x| <= ln2/2 uses k = 0 and no reduction: with k = 0, hi = x - 0 = x,
+//     lo = 0, and 1 - ((0 + q) - x) is fdlibm's 1 - (q - x);
+//   - fdlibm's (x*c)/(c-2) and (x*c)/(2-c) are one quotient and its exact
+//     negation (IEEE subtraction and division are sign-symmetric), so
+//     lo - (x*c)/(2-c) is lo + q to the bit.
+// Specials (NaN, infinities, overflow, underflow, |x| < 2^-28, x == 1)
+// are selected last, as fdlibm returns them before the reduction.
 __device__ __forceinline__ double fd_exp(double x) {
   const double inv_ln2 = 1.44269504088896338700e+00;
   const double ln2_hi = 6.93147180369123816490e-01, ln2_lo = 1.90821492927058770002e-10;
@@ -63,50 +76,33 @@ __device__ __forceinline__ double fd_exp(double x) {
                P5 = 4.13813679705723846039e-08;
   const double over = 7.09782712893383973096e+02, under = -7.45133219101941108420e+02;
   const double two_m1000 = 9.33263618503218878990e-302;
-  uint64_t bits = (uint64_t)__double_as_longlong(x);
-  uint32_t hx = (uint32_t)(bits >> 32);
-  const int neg = (int)(hx >> 31);
-  hx &= 0x7fffffffu;
-  double hi = 0.0, lo = 0.0;
-  int k = 0;
-  if (hx >= 0x40862E42u) {
-    if (hx >= 0x7ff00000u) {
-      if (((hx & 0xfffffu) | (uint32_t)bits) != 0u) return x + x;
-      return neg ? 0.0 : x;
-    }
-    if (x > over) return __longlong_as_double(0x7ff0000000000000ll);
-    if (x < under) return 0.0;
-  }
-  if (hx > 0x3fd62e42u) {
-    if (hx < 0x3FF0A2B2u) {
-      if (x == 1.0) return 2.718281828459045;
-      hi = neg ? x + ln2_hi : x - ln2_hi;
-      lo = neg ? -ln2_lo : ln2_lo;
-      k = neg ? -1 : 1;
-    } else {
-      k = (int)(inv_ln2 * x + (neg ? -0.5 : 0.5));
-      double t = (double)k;
-      hi = x - t * ln2_hi;
-      lo = t * ln2_lo;
-    }
-    x = hi - lo;
-  } else if (hx < 0x3e300000u) {
-    return 1.0 + x;
-  }
-  double t = x * x;
-  double c = x - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
-  // fdlibm's (x*c)/(c-2) and (x*c)/(2-c) are one quotient and its exact
-  // negation (IEEE subtraction and division are sign-symmetric), so both
-  // branches share one division: lo - (x*c)/(2-c) is lo + q to the bit.
-  const double q = (x * c) / (c - 2.0);
-  if (k == 0) return 1.0 - (q - x);
-  double y = 1.0 - ((lo + q) - hi);
-  if (k >= -1021) {
-    if (k == 1024) return y * 2.0 * 8.988465674311579539e307;
-    return y * __longlong_as_double((long long)(uint64_t)(0x3ff00000u + ((uint32_t)k << 20)) << 32);
-  }
-  return y * __longlong_as_double((long long)(uint64_t)(0x3ff00000u + ((uint32_t)(k + 1000) << 20)) << 32) *
-         two_m1000;
+  const uint64_t bits = (uint64_t)__double_as_longlong(x);
+  const uint32_t hx = (uint32_t)(bits >> 32) & 0x7fffffffu;
+  const bool neg = (bits >> 63) != 0u;
+  const bool reduce = hx > 0x3fd62e42u;   // |x| > ln2 / 2
+  const bool one = hx < 0x3FF0A2B2u;      // |x| < 1.5 ln2
+  // clamped so the conversion is defined for every x; |x| <= 745 is unchanged
+  const double xc = fmin(fmax(x, -1100.0), 1100.0);
+  const int kg = (int)(inv_ln2 * xc + (neg ? -0.5 : 0.5));
+  const int k = reduce ? (one ? (neg ? -1 : 1) : kg) : 0;
+  const double t = (double)k;
+  const double hi = x - t * ln2_hi;
+  const double lo = t * ln2_lo;
+  const double r = hi - lo;
+  const double rr = r * r;
+  const double c = r - rr * (P1 + rr * (P2 + rr * (P3 + rr * (P4 + rr * P5))));
+  const double q = (r * c) / (c - 2.0);
+  const double y = 1.0 - ((lo + q) - hi);
+  const int ke = k >= -1021 ? k : k + 1000;
+  const double scale = __longlong_as_double((long long)((uint64_t)((0x3ffu + (uint32_t)ke) & 0x7ffu) << 52));
+  double res = k >= -1021 ? y * scale : y * scale * two_m1000;
+  if (k == 1024) res = y * 2.0 * 8.988465674311579539e307;
+  if (reduce && one && x == 1.0) res = 2.718281828459045;
+  if (hx < 0x3e300000u) res = 1.0 + x;    // |x| < 2^-28
+  if (x < under) res = 0.0;
+  if (x > over) res = __longlong_as_double(0x7ff0000000000000ll);
+  if (hx >= 0x7ff00000u) res = (((hx & 0xfffffu) | (uint32_t)bits) != 0u) ? x + x : (neg ? 0.0 : x);
+  return res;
 }
 
 // tanh of an fp32 value, rounded once to fp32 from a double-precision

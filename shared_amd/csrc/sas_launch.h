@@ -8,19 +8,21 @@
 
 namespace sas {
 
-// Kernel arguments of the sampling kernels (validated by sas_sample).
+// Kernel arguments of the sampling kernel (validated by sas_sample).
 //
-// A row's vocabulary is cut into parts of `span` ids.  The parts kernel
-// runs block (row, part) over ids [part * span, (part + 1) * span) in passes
-// of kSpanPass ids (8 float4 per thread) and writes the part's candidates
-// (every allowed value at or above the part's bound) as records; the merge
-// kernel, one block per row, selects the row's top k from them and draws.
+// A row's vocabulary is cut into parts of `span` ids.  Block (row, part)
+// runs over ids [part * span, (part + 1) * span) in passes of kSpanPass ids
+// (8 float4 per thread) and writes the part's candidates (every allowed
+// value at or above the part's bound) as records; the block that finishes
+// its row last selects the row's top k from every part's records and draws.
 constexpr int kSpanPass = 8192;   // ids of one pass of a block
 constexpr int kMaxSpan = 65536;   // ids one part may span (a multiple of kSpanPass above it)
 constexpr int kMaxParts = 64;     // blocks per row
 constexpr int kListCap = 640;     // records one part may write
 constexpr int kCtlStride = 128;   // words per row of the control block: 512 bytes
-constexpr int kCtlFlags = 32;     // second 128-byte line: SAS_FLAG_* bits raised by the row's parts
+
+// Part counts of a row (pinfo) per 128-byte line: rows never share a line.
+__host__ __device__ constexpr int pinfo_stride(int parts) { return (parts + 15) & ~15; }
 
 struct SampleArgs {
   const float *logits;
@@ -38,17 +40,20 @@ struct SampleArgs {
   uint32_t *out_cand_ids;
   int32_t *out_counts;
   uint32_t *out_flags;
-  // Records: part (row, q) writes its candidates, unordered, slot-major:
-  // rec[(row * kListCap + j) * parts + q] = {fp32 key bits, id | flag << 31}
-  // for j < the count in pinfo[row * parts + q] = {count, bound key << 32};
-  // a flagged record's exact value (above its key) is xval at the same index.
+  // Records: part (row, q) writes its candidates, unordered, to its own
+  // slots: plain values rec[(row * parts + q) * kListCap + j] = {fp32 value
+  // bits, id} (the value after the mask and softcap), and history members
+  // mrec[(row * parts + q) * (kListCap / 2) + j] = {fp32 bits of the
+  // penalized value rounded toward -inf, id, the penalized double}; pinfo[row * pinfo_stride(parts) + q] =
+  // {plain count | member count << 16, bound key << 32}.
   uint64_t *rec;
-  double *xval;
+  uint4 *mrec;
   uint64_t *pinfo;
-  // Per row kCtlStride words; [kCtlFlags], the flags of the row's parts, is
-  // zero between launches (the merge kernel resets it).  Each row has 512
-  // bytes of its own so that atomics of different rows never queue on one
-  // line.
+  // Per row kCtlStride words, zero between launches: word 0 counts the
+  // row's finished parts (low 16 bits) and the parts that took the exact
+  // slow selection (high 16 bits); the row's last block resets it.  Each row
+  // has 512 bytes of its own so that atomics of different rows never queue
+  // on one line.
   uint32_t *ctl;
   int32_t vocab;
   int32_t rows;
@@ -60,7 +65,7 @@ struct SampleArgs {
 // (fewer, larger parts) unless the grid would hold fewer than
 // `min_blocks` blocks; at most kMaxParts parts per row.
 void choose_parts(int rows, int vocab, int min_blocks, int *parts, int *span);
-// Launches the parts and merge kernels on `stream`.  softcap: some row may have a
+// Launches the sampling kernel on `stream`.  softcap: some row may have a
 // softcap (row_params, or params.softcap > 0).
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
 
