@@ -182,6 +182,24 @@ int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab);
  * calls concurrently. */
 int sas_sample(sas_sampler *s, const sas_rows *rows, void *stream);
 
+/* Bytes of the static scratch of sas_sample_noalloc on each device. */
+#define SAS_NOALLOC_SCRATCH_BYTES (48u << 20)
+
+/*
+ * sas_sample without any allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory during the call (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same kernels and results as sas_sample, on HIP device `device`, with
+ * their scratch in a static device array of SAS_NOALLOC_SCRATCH_BYTES per
+ * device, held until the process ends (its address is resolved by sas_create
+ * on that device, or by the first call).  A batch whose records need more
+ * (rows x parts x 10 KiB; 128 rows of 262,144 ids take 40 MiB) fails with
+ * SAS_ERR_INVALID.  Every call on one device shares that device's array:
+ * calls that overlap on one GPU (other streams, other threads) race.
+ * Errors: sas_last_error(NULL) on the calling thread.
+ */
+int sas_sample_noalloc(int device, const sas_rows *rows, void *stream);
+
 /* Speculative accept/resample, stream-ordered like sas_sample. */
 int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
 

@@ -30,6 +30,7 @@ MAX_TOP_K = _header_define("SAS_MAX_TOP_K")
 MAX_VOCAB = _header_define("SAS_MAX_VOCAB")
 MAX_HISTORY = _header_define("SAS_MAX_HISTORY")
 MAX_DRAFT = _header_define("SAS_MAX_DRAFT")
+NOALLOC_SCRATCH_BYTES = _header_define("SAS_NOALLOC_SCRATCH_BYTES")
 NO_TOKEN = 0xFFFFFFFF
 OK, ERR_INVALID, ERR_HIP, ERR_NOMEM = 0, 1, 2, 3
 FLAG_EMPTY_ROW, FLAG_TOPP_EDGE, FLAG_DRAW_EDGE, FLAG_SLOW_SELECT = 1, 2, 4, 8
@@ -98,6 +99,7 @@ SIGNATURES = {
     "sas_last_error": (c_char_p, [c_void_p]),
     "sas_reserve": (c_int, [c_void_p, c_int32, c_int32]),
     "sas_sample": (c_int, [c_void_p, POINTER(SasRows), c_void_p]),
+    "sas_sample_noalloc": (c_int, [c_int, POINTER(SasRows), c_void_p]),
     "sas_verify": (c_int, [c_void_p, POINTER(SasVerifyRows), c_void_p]),
     "sas_clamp_params": (c_int, [POINTER(SasParams), POINTER(SasParams)]),
     "sas_mask_from_ids": (c_int64, [c_int32, POINTER(c_uint32), c_size_t, c_int32, POINTER(c_uint32), c_int64]),

@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "sas_device.h"
@@ -19,8 +20,6 @@ struct sas_sampler {
   std::string err;
   void *recs = nullptr;        // candidate record slots of every (row, part)
   size_t recs_cap = 0;
-  uint32_t *ctl = nullptr;     // per-row control blocks: arrivals and thresholds zero between launches
-  int32_t ctl_rows = 0;
   void *vscratch = nullptr;   // sas_verify partials
   size_t vscratch_cap = 0;
   void *pad = nullptr;        // rows of fewer than 4 logits, padded to 4
@@ -76,22 +75,94 @@ int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
 }
 
 int ensure_sample_scratch(sas_sampler *s, int rows, int parts) {
-  int rc = grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, parts), false);
-  if (rc) return rc;
-  if (rows > s->ctl_rows) {
-    size_t cap = (size_t)s->ctl_rows * sas::kCtlStride * 4;
-    void *p = s->ctl;
-    rc = grow(s, &p, &cap, (size_t)rows * sas::kCtlStride * 4, true);
-    s->ctl = reinterpret_cast<uint32_t *>(p);
-    if (rc) return rc;
-    s->ctl_rows = (int32_t)(cap / (sas::kCtlStride * 4));
-  }
-  return SAS_OK;
+  return grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, parts), false);
 }
 
 int set_device(sas_sampler *s) {
   hipError_t e = hipSetDevice(s->device);
   return e == hipSuccess ? SAS_OK : hip_fail(s, e, "hipSetDevice");
+}
+
+// The checks of a sas_rows descriptor shared by sas_sample and
+// sas_sample_noalloc: nullptr when it is valid, else the message (after
+// `who`).  rows == 0 is valid (nothing to do).
+const char *check_rows(const sas_rows *r) {
+  if (!r) return "rows descriptor is NULL";
+  if (r->rows < 0) return "rows must be >= 0";
+  if (r->vocab < 1 || r->vocab > SAS_MAX_VOCAB) return "vocab must be in [1, SAS_MAX_VOCAB]";
+  if (r->rows == 0) return nullptr;
+  if (!r->logits || !r->out_ids) return "logits and out_ids are required";
+  if (r->logits_stride < r->vocab) return "logits_stride < vocab";
+  if (r->mask && r->mask_stride != 0 && r->mask_stride < ((int64_t)r->vocab + 31) / 32)
+    return "mask_stride must be 0 or >= ceil(vocab / 32)";
+  if (r->hist_ids && !r->hist_offsets) return "hist_ids requires hist_offsets";
+  if (r->hist_ids && r->hist_count < 1) return "hist_count must be >= 1 with hist_ids";
+  const bool all_greedy = !r->row_params && !(r->params.temperature > 0.0);
+  if (!r->uniforms && !all_greedy) return "uniforms are required unless every row is greedy";
+  return nullptr;
+}
+
+// The softcap kernel variants (fewer waves per SIMD) only when some row may
+// have a softcap.
+bool any_softcap(const sas_rows *r) {
+  return r->row_params ? (r->row_hints & SAS_HINT_NO_SOFTCAP) == 0u : r->params.softcap > 0.0f;
+}
+
+// Kernel arguments for a valid descriptor whose record scratch is `recs`
+// (sas::sample_rec_bytes(rows, parts) bytes) and whose logits have already
+// been padded when vocab < 4.
+void fill_args(const sas_rows *r, const float *logits, int64_t logits_stride, int parts, int span, void *recs,
+               sas::SampleArgs *a) {
+  a->logits = logits;
+  a->logits_stride = logits_stride;
+  a->mask = r->mask;
+  a->mask_stride = r->mask_stride;
+  a->hist_ids = r->hist_ids;
+  a->hist_offsets = r->hist_ids ? r->hist_offsets : nullptr;
+  a->hist_count = r->hist_ids ? r->hist_count : 0;
+  a->uniforms = r->uniforms;
+  a->row_params = r->row_params;
+  a->params = r->params;
+  a->out_ids = r->out_ids;
+  a->out_probs = r->out_probs;
+  a->out_cand_ids = r->out_cand_ids;
+  a->out_counts = r->out_counts;
+  a->out_flags = r->out_flags;
+  a->rec = reinterpret_cast<uint64_t *>(recs);
+  a->mrec = reinterpret_cast<uint4 *>(a->rec + (size_t)r->rows * parts * sas::kListCap);
+  a->pinfo = reinterpret_cast<uint64_t *>(a->mrec + (size_t)r->rows * parts * (sas::kListCap / 2));
+  a->vocab = r->vocab;
+  a->rows = r->rows;
+  a->parts = parts;
+  a->span = span;
+}
+
+// ---- the scratch of sas_sample_noalloc: one array per device, for the
+// life of the process.  Host code never uses the array's name as an
+// address: its device address comes from hipGetSymbolAddress, once per
+// device, with that device current.
+constexpr size_t kStaticScratch = SAS_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratch];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+int g_scratch_cus[kMaxDevices];
+
+// The device address of `device`'s scratch (the device must be current).
+hipError_t static_scratch(int device, void **ptr, int *cus) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n < 1) n = 256;
+    g_scratch_ptr[device] = p;
+    g_scratch_cus[device] = n;
+  }
+  *ptr = g_scratch_ptr[device];
+  *cus = g_scratch_cus[device];
+  return hipSuccess;
 }
 
 }  // namespace
@@ -118,6 +189,13 @@ int sas_create(int device, sas_sampler **out) {
     delete s;
     return hip_fail(nullptr, e, "hipStreamCreate");
   }
+  // sas_sample_noalloc's scratch address on this device, while it is
+  // current (a failure is reported by sas_sample_noalloc itself)
+  if (device < kMaxDevices) {
+    void *p = nullptr;
+    int n = 0;
+    (void)static_scratch(device, &p, &n);
+  }
   *out = s;
   return SAS_OK;
 }
@@ -127,7 +205,6 @@ void sas_destroy(sas_sampler *s) {
   (void)hipSetDevice(s->device);
   (void)drain(s);
   if (s->recs) (void)hipFree(s->recs);
-  if (s->ctl) (void)hipFree(s->ctl);
   if (s->vscratch) (void)hipFree(s->vscratch);
   if (s->pad) (void)hipFree(s->pad);
   if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -149,35 +226,15 @@ int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab) {
 
 int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_sample: handle is NULL");
-  if (!r) return fail(s, SAS_ERR_INVALID, "sas_sample: rows descriptor is NULL");
-  if (r->rows < 0) return fail(s, SAS_ERR_INVALID, "sas_sample: rows must be >= 0");
-  if (r->vocab < 1 || r->vocab > SAS_MAX_VOCAB)
-    return fail(s, SAS_ERR_INVALID, "sas_sample: vocab must be in [1, SAS_MAX_VOCAB]");
+  if (const char *m = check_rows(r)) return fail(s, SAS_ERR_INVALID, std::string("sas_sample: ") + m);
   if (r->rows == 0) return SAS_OK;
-  if (!r->logits || !r->out_ids) return fail(s, SAS_ERR_INVALID, "sas_sample: logits and out_ids are required");
-  if (r->logits_stride < r->vocab) return fail(s, SAS_ERR_INVALID, "sas_sample: logits_stride < vocab");
-  if (r->mask && r->mask_stride != 0 && r->mask_stride < ((int64_t)r->vocab + 31) / 32)
-    return fail(s, SAS_ERR_INVALID, "sas_sample: mask_stride must be 0 or >= ceil(vocab / 32)");
-  if (r->hist_ids && !r->hist_offsets)
-    return fail(s, SAS_ERR_INVALID, "sas_sample: hist_ids requires hist_offsets");
-  if (r->hist_ids && r->hist_count < 1)
-    return fail(s, SAS_ERR_INVALID, "sas_sample: hist_count must be >= 1 with hist_ids");
-  const bool all_greedy = !r->row_params && !(r->params.temperature > 0.0);
-  if (!r->uniforms && !all_greedy)
-    return fail(s, SAS_ERR_INVALID, "sas_sample: uniforms are required unless every row is greedy");
   if (int rc = set_device(s)) return rc;
-  // the softcap kernel variants (fewer waves per SIMD) only when some row
-  // may have a softcap
-  const bool softcap =
-      r->row_params ? (r->row_hints & SAS_HINT_NO_SOFTCAP) == 0u : r->params.softcap > 0.0f;
   // at least two blocks per CU: small batches take shorter parts
   int parts = 0, span = 0;
   sas::choose_parts(r->rows, r->vocab, 2 * s->cus, &parts, &span);
   if (int rc = ensure_sample_scratch(s, r->rows, parts)) return rc;
-
-  sas::SampleArgs a;
-  a.logits = r->logits;
-  a.logits_stride = r->logits_stride;
+  const float *logits = r->logits;
+  int64_t stride = r->logits_stride;
   if (r->vocab < 4) {
     // the kernel loads 16 bytes at a time from inside a row: copy rows of
     // fewer than 4 logits into rows of 4, NaN (never selected) past vocab
@@ -185,34 +242,52 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
     hipError_t e = sas::launch_pad_rows(r->logits, r->logits_stride, r->vocab, r->rows,
                                         reinterpret_cast<float *>(s->pad), pick_stream(s, stream));
     if (e != hipSuccess) return hip_fail(s, e, "sas_sample pad launch");
-    a.logits = reinterpret_cast<const float *>(s->pad);
-    a.logits_stride = 4;
+    logits = reinterpret_cast<const float *>(s->pad);
+    stride = 4;
   }
-  a.mask = r->mask;
-  a.mask_stride = r->mask_stride;
-  a.hist_ids = r->hist_ids;
-  a.hist_offsets = r->hist_ids ? r->hist_offsets : nullptr;
-  a.hist_count = r->hist_ids ? r->hist_count : 0;
-  a.uniforms = r->uniforms;
-  a.row_params = r->row_params;
-  a.params = r->params;
-  a.out_ids = r->out_ids;
-  a.out_probs = r->out_probs;
-  a.out_cand_ids = r->out_cand_ids;
-  a.out_counts = r->out_counts;
-  a.out_flags = r->out_flags;
-  a.rec = reinterpret_cast<uint64_t *>(s->recs);
-  a.mrec = reinterpret_cast<uint4 *>(a.rec + (size_t)r->rows * parts * sas::kListCap);
-  a.pinfo = reinterpret_cast<uint64_t *>(a.mrec + (size_t)r->rows * parts * (sas::kListCap / 2));
-  a.ctl = s->ctl;
-  a.vocab = r->vocab;
-  a.rows = r->rows;
-  a.parts = parts;
-  a.span = span;
-  hipError_t e = sas::launch_sample(a, softcap, pick_stream(s, stream));
+  sas::SampleArgs a;
+  fill_args(r, logits, stride, parts, span, s->recs, &a);
+  hipError_t e = sas::launch_sample(a, any_softcap(r), pick_stream(s, stream));
   s->last_stream = pick_stream(s, stream);
   s->launched = true;
   if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
+  return SAS_OK;
+}
+
+int sas_sample_noalloc(int device, const sas_rows *r, void *stream) {
+  if (const char *m = check_rows(r)) return fail(nullptr, SAS_ERR_INVALID, std::string("sas_sample_noalloc: ") + m);
+  if (r->rows == 0) return SAS_OK;
+  if (device < 0 || device >= kMaxDevices)
+    return fail(nullptr, SAS_ERR_INVALID, "sas_sample_noalloc: device index out of range");
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "sas_sample_noalloc: hipSetDevice");
+  void *base = nullptr;
+  int cus = 0;
+  if ((e = static_scratch(device, &base, &cus)) != hipSuccess)
+    return hip_fail(nullptr, e, "sas_sample_noalloc: hipGetSymbolAddress of the static scratch");
+  int parts = 0, span = 0;
+  sas::choose_parts(r->rows, r->vocab, 2 * cus, &parts, &span);
+  const size_t recs = (sas::sample_rec_bytes(r->rows, parts) + 255) & ~size_t(255);
+  const size_t pad = r->vocab < 4 ? (size_t)r->rows * 16 : 0;
+  if (recs + pad > kStaticScratch)
+    return fail(nullptr, SAS_ERR_INVALID,
+                "sas_sample_noalloc: this batch needs " + std::to_string(recs + pad) +
+                    " bytes of scratch; the static scratch holds " + std::to_string(kStaticScratch) +
+                    " (SAS_NOALLOC_SCRATCH_BYTES): use sas_sample");
+  const float *logits = r->logits;
+  int64_t stride = r->logits_stride;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (pad) {
+    float *dst = reinterpret_cast<float *>(static_cast<unsigned char *>(base) + recs);
+    e = sas::launch_pad_rows(r->logits, r->logits_stride, r->vocab, r->rows, dst, st);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "sas_sample_noalloc pad launch");
+    logits = dst;
+    stride = 4;
+  }
+  sas::SampleArgs a;
+  fill_args(r, logits, stride, parts, span, base, &a);
+  e = sas::launch_sample(a, any_softcap(r), st);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "sas_sample_noalloc launch");
   return SAS_OK;
 }
 

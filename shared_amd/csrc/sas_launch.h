@@ -19,7 +19,6 @@ constexpr int kSpanPass = 8192;   // ids of one pass of a block
 constexpr int kMaxSpan = 65536;   // ids one part may span (a multiple of kSpanPass above it)
 constexpr int kMaxParts = 64;     // blocks per row
 constexpr int kListCap = 640;     // records one part may write
-constexpr int kCtlStride = 128;   // words per row of the control block: 512 bytes
 
 // Part counts of a row (pinfo) per 128-byte line: rows never share a line.
 __host__ __device__ constexpr int pinfo_stride(int parts) { return (parts + 15) & ~15; }
@@ -49,12 +48,6 @@ struct SampleArgs {
   uint64_t *rec;
   uint4 *mrec;
   uint64_t *pinfo;
-  // Per row kCtlStride words, zero between launches: word 0 counts the
-  // row's finished parts (low 16 bits) and the parts that took the exact
-  // slow selection (high 16 bits); the row's last block resets it.  Each row
-  // has 512 bytes of its own so that atomics of different rows never queue
-  // on one line.
-  uint32_t *ctl;
   int32_t vocab;
   int32_t rows;
   int32_t parts;   // blocks per row

@@ -109,6 +109,51 @@ def _ptr(t) -> Optional[int]:
     return t.data_ptr()
 
 
+def _stream(stream):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+def rows_descriptor(logits, out_ids, *, vocab: Optional[int] = None, mask=None, hist_ids=None, hist_offsets=None,
+                    uniforms=None, params: Optional[Params] = None, row_params=None, out_probs=None,
+                    out_cand_ids=None, out_counts=None, out_flags=None, row_hints: int = 0) -> SasRows:
+    """The sas_rows descriptor of torch device tensors."""
+    rows = logits.shape[0]
+    vocab = int(vocab if vocab is not None else logits.shape[1])
+    if logits.dtype.itemsize != 4 or logits.stride(1) != 1:
+        raise ValueError("logits must be fp32 with unit element stride")
+    d = SasRows()
+    d.logits = logits.data_ptr()
+    d.logits_stride = logits.stride(0)
+    d.vocab = vocab
+    d.rows = rows
+    if mask is not None:
+        d.mask = _ptr(mask)
+        d.mask_stride = mask.stride(0)
+    d.hist_ids = _ptr(hist_ids)
+    d.hist_offsets = _ptr(hist_offsets)
+    d.hist_count = hist_ids.numel() if hist_ids is not None else 0
+    d.row_hints = int(row_hints)
+    d.uniforms = _ptr(uniforms)
+    d.params = (params or Params()).to_c()
+    d.row_params = _ptr(row_params)
+    d.out_ids = _ptr(out_ids)
+    d.out_probs = _ptr(out_probs)
+    d.out_cand_ids = _ptr(out_cand_ids)
+    d.out_counts = _ptr(out_counts)
+    d.out_flags = _ptr(out_flags)
+    return d
+
+
+def sample_noalloc_into(device: int, logits, out_ids, *, stream=None, **kw) -> None:
+    """sas_sample_noalloc on caller-provided device buffers: no allocation
+    at all (the scratch is the library's static device array)."""
+    d = rows_descriptor(logits, out_ids, **kw)
+    check(load().sas_sample_noalloc(int(device), ctypes.byref(d), _stream(stream)), None)
+
+
 class Sampler:
     """A sas_sampler handle bound to one device."""
 
@@ -140,44 +185,13 @@ class Sampler:
     def reserve(self, rows: int, vocab: int) -> None:
         check(self._lib.sas_reserve(self._h, int(rows), int(vocab)), self._h)
 
-    def _stream(self, stream):
-        import torch
-        if stream is None:
-            stream = torch.cuda.current_stream()
-        return ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
 
-    def sample_into(self, logits, out_ids, *, vocab: Optional[int] = None, mask=None, hist_ids=None,
-                    hist_offsets=None, uniforms=None, params: Optional[Params] = None, row_params=None,
-                    out_probs=None, out_cand_ids=None, out_counts=None, out_flags=None, stream=None,
-                    row_hints: int = 0) -> None:
+    def sample_into(self, logits, out_ids, *, stream=None, **kw) -> None:
         """Launch sas_sample on caller-provided device buffers (no allocation,
         no synchronisation: the history offsets are not checked here, the
         kernels clamp them to hist_ids' length)."""
-        rows = logits.shape[0]
-        vocab = int(vocab if vocab is not None else logits.shape[1])
-        if logits.dtype.itemsize != 4 or logits.stride(1) != 1:
-            raise ValueError("logits must be fp32 with unit element stride")
-        d = SasRows()
-        d.logits = logits.data_ptr()
-        d.logits_stride = logits.stride(0)
-        d.vocab = vocab
-        d.rows = rows
-        if mask is not None:
-            d.mask = _ptr(mask)
-            d.mask_stride = mask.stride(0)
-        d.hist_ids = _ptr(hist_ids)
-        d.hist_offsets = _ptr(hist_offsets)
-        d.hist_count = hist_ids.numel() if hist_ids is not None else 0
-        d.row_hints = int(row_hints)
-        d.uniforms = _ptr(uniforms)
-        d.params = (params or Params()).to_c()
-        d.row_params = _ptr(row_params)
-        d.out_ids = _ptr(out_ids)
-        d.out_probs = _ptr(out_probs)
-        d.out_cand_ids = _ptr(out_cand_ids)
-        d.out_counts = _ptr(out_counts)
-        d.out_flags = _ptr(out_flags)
-        check(self._lib.sas_sample(self._h, ctypes.byref(d), self._stream(stream)), self._h)
+        d = rows_descriptor(logits, out_ids, **kw)
+        check(self._lib.sas_sample(self._h, ctypes.byref(d), _stream(stream)), self._h)
 
     def sample(self, logits, *, full: bool = False, **kw):
         """Allocate outputs and sample; returns ids (and the extras if full).
@@ -219,7 +233,7 @@ class Sampler:
         d.temperature = float(temperature)
         d.out_tokens = _ptr(out_tokens)
         d.out_accepted = _ptr(out_accepted)
-        check(self._lib.sas_verify(self._h, ctypes.byref(d), self._stream(stream)), self._h)
+        check(self._lib.sas_verify(self._h, ctypes.byref(d), _stream(stream)), self._h)
 
     def verify(self, target, draft, draft_ids, uniforms, **kw):
         import torch

@@ -1,0 +1,72 @@
+"""sas_sample_noalloc, the entry point that allocates nothing (its scratch is
+a static device array), against sas_sample on the same inputs: bit-exact ids,
+ranked candidates, probabilities, counts and flags, on two calls in a row
+(the second with a smaller batch), and its size limit."""
+import numpy as np
+import pytest
+
+from gpu_helpers import to_dev
+from shared_amd import _capi
+from shared_amd import workloads as W
+from shared_amd._capi import SasError
+from shared_amd.sampler import sample_noalloc_into
+
+pytestmark = pytest.mark.gpu
+
+
+def _outputs(rows):
+    import torch
+    return {"out_ids": torch.empty(rows, dtype=torch.int32, device="cuda"),
+            "out_probs": torch.empty((rows, _capi.MAX_TOP_K), dtype=torch.float64, device="cuda"),
+            "out_cand_ids": torch.empty((rows, _capi.MAX_TOP_K), dtype=torch.int32, device="cuda"),
+            "out_counts": torch.empty((rows, 2), dtype=torch.int32, device="cuda"),
+            "out_flags": torch.empty(rows, dtype=torch.int32, device="cuda")}
+
+
+def _inputs(b):
+    import torch
+    return dict(vocab=b.vocab, mask=to_dev(b.mask, torch.int32) if b.mask is not None else None,
+                hist_ids=to_dev(b.hist_ids, torch.int32) if b.hist_ids is not None else None,
+                hist_offsets=to_dev(b.hist_offsets) if b.hist_offsets is not None else None,
+                uniforms=to_dev(b.uniforms) if b.uniforms is not None else None, params=b.params)
+
+
+def _host(out):
+    return {k: v.cpu().numpy() for k, v in out.items()}
+
+
+def test_noalloc_matches_sample_on_two_calls(request):
+    import torch
+    batches = [W.c3p(seed=71), W.c3(rows=24, vocab=W.QWEN_VOCAB, seed=72)]
+    got = []
+    # the static path first: in a fresh process its first call resolves the
+    # scratch address itself
+    for b in batches:
+        print(f"[gpu] noalloc rows={b.rows} vocab={b.vocab}", flush=True)
+        lg = to_dev(b.logits)
+        out = _outputs(b.rows)
+        ids = out.pop("out_ids")
+        sample_noalloc_into(0, lg, ids, **_inputs(b), **out)
+        torch.cuda.synchronize()
+        out["out_ids"] = ids
+        got.append(_host(out))
+    sampler = request.getfixturevalue("sampler")
+    for b, g in zip(batches, got):
+        lg = to_dev(b.logits)
+        out = _outputs(b.rows)
+        ids = out.pop("out_ids")
+        sampler.sample_into(lg, ids, **_inputs(b), **out)
+        torch.cuda.synchronize()
+        out["out_ids"] = ids
+        want = _host(out)
+        for k in want:
+            assert np.array_equal(g[k].view(np.uint8), want[k].view(np.uint8)), f"{b.name} rows={b.rows}: {k} differ"
+
+
+def test_noalloc_rejects_batches_past_its_scratch():
+    import torch
+    rows, vocab = 256, W.GEMMA_VOCAB     # 256 x 32 parts x 10 KiB of records: past 48 MiB
+    lg = torch.zeros((rows, vocab), dtype=torch.float32, device="cuda")
+    ids = torch.empty(rows, dtype=torch.int32, device="cuda")
+    with pytest.raises(SasError, match="static scratch holds"):
+        sample_noalloc_into(0, lg, ids, vocab=vocab)
