@@ -38,7 +38,10 @@ WORKLOAD_DOC = {
     "C3P": "C3 + repetition 1.1 / presence 0.5 / frequency 0.3 over 512 history ids, vocab 262144, batch 128",
     "C4": "repetition 1.15 / presence 0.5 / frequency 0.3 over 4096 Zipf history ids, greedy, vocab 262144, "
           "batch 256",
+    "C5": "speculative verify (rejection sampling): 32 sequences x (4 drafts + 1 bonus), vocab 151936, draft "
+          "logits 0.8-correlated with the target, 5% mask on both",
 }
+CPU_THREADS = 16  # the GPU box's CPU share for one GPU (its nproc may show more)
 
 
 def parse_args():
@@ -78,11 +81,11 @@ def calibrate_copy(mb: float, steps: int) -> int:
     return 0
 
 
-def traffic_from_profiles(workload: str):
+def traffic_from_profiles(workload: str, kernel: str = KERNEL):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
     scaled by the copy-kernel calibration), if a summary for this workload is
     committed under profiles/."""
-    path = os.path.join(ROOT, "profiles", f"{KERNEL}_{workload}_pmc.md")
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.md")
     try:
         with open(path) as f:
             for line in f:
@@ -97,21 +100,36 @@ def traffic_from_profiles(workload: str):
 def cpu_baseline(batch, target_s: float) -> dict:
     """Time the Node restatement of the reference JS path (oracle/sample_js.js)
     on a bounded sample of the same workload: the first set's rows, repeated
-    until about target_s seconds of single-thread work.  Falls back to the C
-    restatement when Node is absent."""
+    until about target_s seconds of single-thread work (the reference samples
+    on one JS thread), then the same rows split over worker_threads on the
+    box's CPU share, and configuration C1 (the case the reference runs on the
+    CPU) single-threaded.  Falls back to the C restatement when Node is
+    absent."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import oracle as O
+    from shared_amd import workloads as W
 
     if O.node_binary() is not None:
         with tempfile.TemporaryDirectory(prefix="sas_cpu_") as tmp:
             _, probe = O.run_node(batch, threads=1, repeat=1, workdir=tmp)
             repeat = max(1, min(50, int(round(target_s / max(probe["median_s"], 1e-3)))))
             out, t = O.run_node(batch, threads=1, repeat=repeat, workdir=tmp)
+            threads = max(1, min(CPU_THREADS, os.cpu_count() or 1))
+            _, tp = O.run_node(batch, threads=threads, repeat=max(3, repeat // 2), workdir=tmp)
+        c1 = W.c1()
+        with tempfile.TemporaryDirectory(prefix="sas_cpu_c1_") as tmp:
+            _, t1 = O.run_node(c1, threads=1, repeat=20, workdir=tmp)
         return {"value": batch.rows / t["median_s"], "unit": "rows/s", "cores": 1, "kind": "port",
                 "sample": f"{batch.rows} rows of the first input set, {repeat} timed passes (median), "
                           f"Node {t['node']} single thread on {t['cpu_model']} ({t['host_cpus']} host cpus)",
+                "parallel": {"value": batch.rows / tp["median_s"], "unit": "rows/s", "cores": tp["threads"],
+                             "sample": f"the same rows split over {tp['threads']} worker_threads, "
+                                       f"{tp['repeat']} passes (median)"},
+                "c1": {"value": 1.0 / t1["median_s"], "unit": "rows/s", "ms_per_row": t1["median_s"] * 1e3,
+                       "cores": 1, "sample": "configuration C1 (greedy + repetition 1.1, vocab 151936, one row, "
+                                             "512 history ids), 20 passes (median)"},
                 "ids": out["ids"]}
     import time
     t0 = time.perf_counter()
@@ -120,6 +138,103 @@ def cpu_baseline(batch, target_s: float) -> dict:
     return {"value": batch.rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
             "sample": f"{batch.rows} rows of the first input set, C restatement single thread (Node absent)",
             "ids": np.asarray(o["ids"])}
+
+
+def verify_bytes(inp) -> int:
+    """Compulsory HBM bytes of one verify step as the C ABI takes it: every
+    target and draft logit row once, one mask row per position (read once,
+    it applies to the target and the draft row of that position), the draft
+    ids and the two uniforms per position, the tokens and the accepted counts
+    written once."""
+    seqs, L, vocab = inp["seqs"], inp["drafts"], inp["vocab"]
+    b = inp["target"].nbytes + inp["draft"].nbytes
+    if inp.get("mask") is not None:
+        b += seqs * (L + 1) * ((vocab + 31) // 32) * 4
+    return b + seqs * (L * 4 + (L + 1) * 16 + (L + 1) * 4 + 4)
+
+
+def bench_verify(args) -> int:
+    """C5: sas_verify steps (three launches each) over rotating input sets."""
+    import time
+
+    import numpy as np
+    import torch
+
+    from shared_amd import Sampler
+    from shared_amd import workloads as W
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    first = W.c5()
+    set_bytes = verify_bytes(first)
+    nsets = max(2, int(np.ceil(args.min_set_mb * 1e6 / set_bytes)))
+    sets_h = [first] + [W.c5(seed=1000 + i) for i in range(1, nsets)]
+    base = None
+    if not args.no_cpu_baseline and args.cpu_seconds > 0:
+        import oracle as O
+        t0 = time.perf_counter()
+        O.verify(first)
+        one = time.perf_counter() - t0
+        reps = max(1, min(20, int(round(args.cpu_seconds / max(one, 1e-3)))))
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            O.verify(first)
+            times.append(time.perf_counter() - t0)
+        med = sorted(times)[len(times) // 2]
+        base = {"value": first["seqs"] / med, "unit": "sequences/s", "cores": 1, "kind": "port",
+                "sample": f"the first input set ({first['seqs']} sequences), {reps} passes (median), the C "
+                          "restatement of rejection sampling (oracle/sampler_oracle.c), single thread"}
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device is visible", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+
+    def dev(a, view=None):
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        return (t.view(view) if view is not None else t).cuda()
+
+    sets = []
+    for inp in sets_h:
+        sets.append(dict(target=dev(inp["target"]), draft=dev(inp["draft"]),
+                         draft_ids=dev(np.ascontiguousarray(inp["draft_ids"], np.uint32), torch.int32),
+                         uniforms=dev(np.ascontiguousarray(inp["uniforms"], np.float64)),
+                         mask=dev(np.ascontiguousarray(inp["mask"], np.uint32), torch.int32)))
+    seqs, L, vocab = first["seqs"], first["drafts"], first["vocab"]
+    toks = [torch.empty((seqs, L + 1), dtype=torch.int32, device="cuda") for _ in sets]
+    acc = [torch.empty(seqs, dtype=torch.int32, device="cuda") for _ in sets]
+    stream = torch.cuda.current_stream()
+    with Sampler(0) as s:
+        def step(j):
+            st = sets[j]
+            s.verify_into(st["target"], st["draft"], st["draft_ids"], st["uniforms"], toks[j], acc[j],
+                          temperature=first["temperature"], mask=st["mask"], vocab=vocab, stream=stream)
+        for i in range(args.warmup):
+            step(i % nsets)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(args.steps):
+            step(i % nsets)
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms_total = start.elapsed_time(end)
+    ms_step = ms_total / args.steps
+    achieved = set_bytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": seqs * args.steps / (ms_total / 1e3), "unit": "sequences/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"C5: {WORKLOAD_DOC['C5']}", "sequences": seqs, "drafts": L, "vocab": vocab,
+                   "input_sets": nsets, "rotating_set_mb": round(nsets * set_bytes / 1e6, 1)},
+        "gbps": achieved,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles("C5", "verify_step"),
+                     "kernel": "sas::verify_stats_kernel + verify_decide_kernel + verify_draw_kernel (one step)",
+                     "algorithmic_bytes_per_launch": set_bytes},
+        "cpu_baseline": base,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -131,6 +246,8 @@ def main() -> int:
         return 2
     if args.calibrate_copy_mb > 0:
         return calibrate_copy(args.calibrate_copy_mb, min(args.steps, 50))
+    if args.workload == "C5":
+        return bench_verify(args)
 
     import numpy as np
 
@@ -230,7 +347,7 @@ def main() -> int:
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": "sas::sample_kernel (one launch per step)",
+                     "kernel": "sas::sample_parts_kernel + sas::sample_merge_kernel (one step: two launches)",
                      "algorithmic_bytes_per_launch": set_bytes},
         "cpu_baseline": None,
     }

@@ -182,6 +182,42 @@ int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab);
  * calls concurrently. */
 int sas_sample(sas_sampler *s, const sas_rows *rows, void *stream);
 
+/*
+ * In-graph token feedback for consecutive decode steps with no host round
+ * trip (the reference's sampler tail, lib/webgpu-llm/kernels.js:184-199, and
+ * the penalty window it appends to, lib/webgpu-llm/model.js:386-399,
+ * 649-742).  Each sas_sample_step call is one step of every row:
+ *   - a row whose state says it already sampled a stop id emits its first
+ *     stop id (SAS_STOP_PAD when it has none) and reads no logits;
+ *   - any other row samples as sas_sample does, its history being its ring
+ *     (the last ring_len tokens it generated), its uniform uniforms[row] or,
+ *     with seeds, the reference's (pcg(seed ^ it * 0x9E3779B9) & 0xFFFFFF) / 2^24;
+ *   - the token goes to out_ids[row], sampled[row][it] and next_tokens[row]
+ *     (the next step's input token), and the iteration advances;
+ *   - a stop id (or SAS_NO_TOKEN, an empty row) freezes the row; any other
+ *     token of a live row is appended to its ring.
+ * All arrays are device memory owned by the caller and persist across calls;
+ * a batch of steps starts from zeroed state and a ring seeded by the caller
+ * (count = ids in it, which may exceed ring_len: the last ring_len are kept).
+ */
+#define SAS_STOP_PAD 0xFFFFFFFFu   /* stop_ids padding: never matches a token */
+
+typedef struct sas_step {
+  uint32_t *state;            /* device [rows][2] = {stopped, iteration} */
+  uint32_t *sampled;          /* device [rows][max_steps] or NULL */
+  int32_t max_steps;          /* columns of sampled (steps past it are not recorded) */
+  uint32_t *next_tokens;      /* device [rows] or NULL */
+  uint32_t *ring;             /* device [rows][1 + ring_len] = {count, ids[ring_len]}:
+                                 id i of the window at ids[i % ring_len] */
+  int32_t ring_len;           /* 1..SAS_MAX_HISTORY (the reference uses 512) */
+  const uint32_t *stop_ids;   /* device [rows][4], SAS_STOP_PAD padded, or NULL (no stops) */
+  const uint32_t *seeds;      /* device [rows] or NULL (then rows->uniforms) */
+} sas_step;
+
+/* One decode step with in-graph feedback.  rows->hist_ids must be NULL
+ * (the ring is the history); everything else as sas_sample. */
+int sas_sample_step(sas_sampler *s, const sas_rows *rows, const sas_step *step, void *stream);
+
 /* Bytes of the static scratch of sas_sample_noalloc on each device. */
 #define SAS_NOALLOC_SCRATCH_BYTES (48u << 20)
 

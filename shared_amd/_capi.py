@@ -32,6 +32,7 @@ MAX_HISTORY = _header_define("SAS_MAX_HISTORY")
 MAX_DRAFT = _header_define("SAS_MAX_DRAFT")
 NOALLOC_SCRATCH_BYTES = _header_define("SAS_NOALLOC_SCRATCH_BYTES")
 NO_TOKEN = 0xFFFFFFFF
+STOP_PAD = 0xFFFFFFFF
 OK, ERR_INVALID, ERR_HIP, ERR_NOMEM = 0, 1, 2, 3
 FLAG_EMPTY_ROW, FLAG_TOPP_EDGE, FLAG_DRAW_EDGE, FLAG_SLOW_SELECT = 1, 2, 4, 8
 HINT_NO_SOFTCAP = 1
@@ -73,6 +74,19 @@ class SasRows(ctypes.Structure):
     ]
 
 
+class SasStep(ctypes.Structure):
+    _fields_ = [
+        ("state", c_void_p),
+        ("sampled", c_void_p),
+        ("max_steps", c_int32),
+        ("next_tokens", c_void_p),
+        ("ring", c_void_p),
+        ("ring_len", c_int32),
+        ("stop_ids", c_void_p),
+        ("seeds", c_void_p),
+    ]
+
+
 class SasVerifyRows(ctypes.Structure):
     _fields_ = [
         ("target_logits", c_void_p),
@@ -100,6 +114,7 @@ SIGNATURES = {
     "sas_reserve": (c_int, [c_void_p, c_int32, c_int32]),
     "sas_sample": (c_int, [c_void_p, POINTER(SasRows), c_void_p]),
     "sas_sample_noalloc": (c_int, [c_int, POINTER(SasRows), c_void_p]),
+    "sas_sample_step": (c_int, [c_void_p, POINTER(SasRows), POINTER(SasStep), c_void_p]),
     "sas_verify": (c_int, [c_void_p, POINTER(SasVerifyRows), c_void_p]),
     "sas_clamp_params": (c_int, [POINTER(SasParams), POINTER(SasParams)]),
     "sas_mask_from_ids": (c_int64, [c_int32, POINTER(c_uint32), c_size_t, c_int32, POINTER(c_uint32), c_int64]),

@@ -86,7 +86,7 @@ int set_device(sas_sampler *s) {
 // The checks of a sas_rows descriptor shared by sas_sample and
 // sas_sample_noalloc: nullptr when it is valid, else the message (after
 // `who`).  rows == 0 is valid (nothing to do).
-const char *check_rows(const sas_rows *r) {
+const char *check_rows(const sas_rows *r, bool seeded = false) {
   if (!r) return "rows descriptor is NULL";
   if (r->rows < 0) return "rows must be >= 0";
   if (r->vocab < 1 || r->vocab > SAS_MAX_VOCAB) return "vocab must be in [1, SAS_MAX_VOCAB]";
@@ -98,7 +98,7 @@ const char *check_rows(const sas_rows *r) {
   if (r->hist_ids && !r->hist_offsets) return "hist_ids requires hist_offsets";
   if (r->hist_ids && r->hist_count < 1) return "hist_count must be >= 1 with hist_ids";
   const bool all_greedy = !r->row_params && !(r->params.temperature > 0.0);
-  if (!r->uniforms && !all_greedy) return "uniforms are required unless every row is greedy";
+  if (!r->uniforms && !all_greedy && !seeded) return "uniforms are required unless every row is greedy";
   return nullptr;
 }
 
@@ -165,6 +165,54 @@ hipError_t static_scratch(int device, void **ptr, int *cus) {
   return hipSuccess;
 }
 
+// The checks of a sas_step: nullptr when it is valid, else the message.
+const char *check_step(const sas_rows *r, const sas_step *st) {
+  if (!st->state) return "state is required";
+  if (r->hist_ids) return "hist_ids must be NULL: the step's ring is the history";
+  if (st->ring && (st->ring_len < 1 || st->ring_len > SAS_MAX_HISTORY))
+    return "ring_len must be in [1, SAS_MAX_HISTORY]";
+  if (st->sampled && st->max_steps < 1) return "max_steps must be >= 1 with sampled";
+  return nullptr;
+}
+
+// sas_sample and sas_sample_step: `st` (checked) or nullptr.
+int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char *who, void *stream) {
+  if (int rc = set_device(s)) return rc;
+  // at least two blocks per CU: small batches take shorter parts
+  int parts = 0, span = 0;
+  sas::choose_parts(r->rows, r->vocab, 2 * s->cus, &parts, &span);
+  if (int rc = ensure_sample_scratch(s, r->rows, parts)) return rc;
+  const float *logits = r->logits;
+  int64_t stride = r->logits_stride;
+  if (r->vocab < 4) {
+    // the kernel loads 16 bytes at a time from inside a row: copy rows of
+    // fewer than 4 logits into rows of 4, NaN (never selected) past vocab
+    if (int rc = grow(s, &s->pad, &s->pad_cap, (size_t)r->rows * 16, false)) return rc;
+    hipError_t e = sas::launch_pad_rows(r->logits, r->logits_stride, r->vocab, r->rows,
+                                        reinterpret_cast<float *>(s->pad), pick_stream(s, stream));
+    if (e != hipSuccess) return hip_fail(s, e, "sas_sample pad launch");
+    logits = reinterpret_cast<const float *>(s->pad);
+    stride = 4;
+  }
+  sas::SampleArgs a{};
+  fill_args(r, logits, stride, parts, span, s->recs, &a);
+  if (st) {
+    a.st_state = st->state;
+    a.st_sampled = st->sampled;
+    a.st_max_steps = st->sampled ? st->max_steps : 0;
+    a.st_next = st->next_tokens;
+    a.ring = st->ring;
+    a.ring_len = st->ring ? st->ring_len : 0;
+    a.stop_ids = st->stop_ids;
+    a.seeds = st->seeds;
+  }
+  hipError_t e = sas::launch_sample(a, any_softcap(r), pick_stream(s, stream));
+  s->last_stream = pick_stream(s, stream);
+  s->launched = true;
+  if (e != hipSuccess) return hip_fail(s, e, (std::string(who) + " launch").c_str());
+  return SAS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -228,30 +276,16 @@ int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
   if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_sample: handle is NULL");
   if (const char *m = check_rows(r)) return fail(s, SAS_ERR_INVALID, std::string("sas_sample: ") + m);
   if (r->rows == 0) return SAS_OK;
-  if (int rc = set_device(s)) return rc;
-  // at least two blocks per CU: small batches take shorter parts
-  int parts = 0, span = 0;
-  sas::choose_parts(r->rows, r->vocab, 2 * s->cus, &parts, &span);
-  if (int rc = ensure_sample_scratch(s, r->rows, parts)) return rc;
-  const float *logits = r->logits;
-  int64_t stride = r->logits_stride;
-  if (r->vocab < 4) {
-    // the kernel loads 16 bytes at a time from inside a row: copy rows of
-    // fewer than 4 logits into rows of 4, NaN (never selected) past vocab
-    if (int rc = grow(s, &s->pad, &s->pad_cap, (size_t)r->rows * 16, false)) return rc;
-    hipError_t e = sas::launch_pad_rows(r->logits, r->logits_stride, r->vocab, r->rows,
-                                        reinterpret_cast<float *>(s->pad), pick_stream(s, stream));
-    if (e != hipSuccess) return hip_fail(s, e, "sas_sample pad launch");
-    logits = reinterpret_cast<const float *>(s->pad);
-    stride = 4;
-  }
-  sas::SampleArgs a;
-  fill_args(r, logits, stride, parts, span, s->recs, &a);
-  hipError_t e = sas::launch_sample(a, any_softcap(r), pick_stream(s, stream));
-  s->last_stream = pick_stream(s, stream);
-  s->launched = true;
-  if (e != hipSuccess) return hip_fail(s, e, "sas_sample launch");
-  return SAS_OK;
+  return sample_on(s, r, nullptr, "sas_sample", stream);
+}
+
+int sas_sample_step(sas_sampler *s, const sas_rows *r, const sas_step *st, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_sample_step: handle is NULL");
+  if (!st) return fail(s, SAS_ERR_INVALID, "sas_sample_step: step descriptor is NULL");
+  if (const char *m = check_rows(r, st->seeds != nullptr)) return fail(s, SAS_ERR_INVALID, std::string("sas_sample_step: ") + m);
+  if (const char *m = check_step(r, st)) return fail(s, SAS_ERR_INVALID, std::string("sas_sample_step: ") + m);
+  if (r->rows == 0) return SAS_OK;
+  return sample_on(s, r, st, "sas_sample_step", stream);
 }
 
 int sas_sample_noalloc(int device, const sas_rows *r, void *stream) {
@@ -284,7 +318,7 @@ int sas_sample_noalloc(int device, const sas_rows *r, void *stream) {
     logits = dst;
     stride = 4;
   }
-  sas::SampleArgs a;
+  sas::SampleArgs a{};
   fill_args(r, logits, stride, parts, span, base, &a);
   e = sas::launch_sample(a, any_softcap(r), st);
   if (e != hipSuccess) return hip_fail(nullptr, e, "sas_sample_noalloc launch");

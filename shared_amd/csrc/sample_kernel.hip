@@ -311,8 +311,8 @@ __device__ __forceinline__ double wave_scan_d(double x) {
 // and every residual up to the draw is clear of 0 and of the draw edge test
 // (|r_i| <= 1e-12 s_{cut-1}) by 1e-13 t_{cut-1}: then the sequential chains
 // give the same cut, draw and flags.  Other rows run the chains.
-__device__ __forceinline__ void sample_tail(MergeLds &ml, int kk, int row, double T, double top_p, double u_row,
-                                            uint32_t flags, const MergeOut &o) {
+__device__ __forceinline__ uint32_t sample_tail(MergeLds &ml, int kk, int row, double T, double top_p,
+                                                double u_row, uint32_t flags, const MergeOut &o) {
   const int lane = threadIdx.x & 63;
   const bool greedy = !(T > 0.0);
   const bool draw = !greedy && kk > 0;
@@ -419,6 +419,40 @@ __device__ __forceinline__ void sample_tail(MergeLds &ml, int kk, int row, doubl
     oc[lane] = lane < np ? ml.t_id[lane] : SAS_NO_TOKEN;
     oc[lane + 64] = lane + 64 < np ? ml.t_id[lane + 64] : SAS_NO_TOKEN;
   }
+  return out_id;
+}
+
+// The reference GPU sampler's uniform (kernels.js:91-95, 181).
+__device__ __forceinline__ double pcg_uniform(uint32_t seed, uint32_t it) {
+  uint32_t h = (seed ^ (it * 0x9E3779B9u)) * 747796405u + 2891336453u;
+  h = ((h >> ((h >> 28u) + 4u)) ^ h) * 277803737u;
+  h = (h >> 22u) ^ h;
+  return (double)(h & 0xFFFFFFu) / 16777216.0;
+}
+
+// The step's bookkeeping after a row's token is known (kernels.js:189-199):
+// record it, hand it to the next step, advance the iteration; a stop id or
+// no token freezes the row, any other token joins the row's penalty ring.
+// One thread.
+__device__ __forceinline__ void step_feedback(const SampleArgs &a, int row, uint32_t tok, bool frozen) {
+  uint32_t *st = a.st_state + 2 * row;
+  const uint32_t it = st[1];
+  if (a.st_sampled && it < (uint32_t)a.st_max_steps) a.st_sampled[(int64_t)row * a.st_max_steps + it] = tok;
+  if (a.st_next) a.st_next[row] = tok;
+  st[1] = it + 1u;
+  bool stop = tok == SAS_NO_TOKEN;
+  if (a.stop_ids) {
+    const uint32_t *sp = a.stop_ids + 4 * row;
+    stop = stop || tok == sp[0] || tok == sp[1] || tok == sp[2] || tok == sp[3];
+  }
+  if (stop) {
+    st[0] = 1u;
+  } else if (!frozen && a.ring) {
+    uint32_t *rg = a.ring + (int64_t)row * (a.ring_len + 1);
+    const uint32_t c = rg[0];
+    rg[1 + c % (uint32_t)a.ring_len] = tok;
+    rg[0] = c + 1u;
+  }
 }
 
 // Loads of the records the row's parts published.  A record line is written
@@ -458,7 +492,8 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   }
   const uint4 mr = qok ? load_rec4(mq + sub) : make_uint4(0u, 0u, 0u, 0u);
   const uint64_t info = qok ? load_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + q) : 0ull;
-  const double u_row = greedy ? 0.0 : a.uniforms[row];
+  const double u_row =
+      greedy ? 0.0 : (a.seeds ? pcg_uniform(a.seeds[row], a.st_state[2 * row + 1]) : a.uniforms[row]);
   for (int i = tid; i < kSurvCap + 8; i += kThreads) ml.s_c[i] = 0ull;  // padding: ranks after everything
   ml.s_rank[tid] = 0u;
   ml.s_rank[tid + kThreads] = 0u;
@@ -704,7 +739,8 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   if (wave != 0) return;
   const int kk = (int)min(m, (uint32_t)k);
   const MergeOut o{a.out_ids, a.out_probs, a.out_cand_ids, a.out_counts, a.out_flags};
-  sample_tail(ml, kk, row, p.temperature, p.top_p, u_row, flags, o);
+  const uint32_t tok = sample_tail(ml, kk, row, p.temperature, p.top_p, u_row, flags, o);
+  if (a.st_state && lane == 0) step_feedback(a, row, tok, false);
 }
 
 // One block per row, after the parts kernel (stream order makes every record
@@ -717,6 +753,25 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   __shared__ uint32_t s_sel[4];
   int row = blockIdx.x;
   if ((a.rows & 7) == 0 && ((a.rows * a.parts) & 7) == 0) row = (row & 7) * (a.rows >> 3) + (row >> 3);
+  if (a.st_state && a.st_state[2 * row] != 0u) {
+    // a frozen row emits its first stop id (kernels.js:184-185) and no candidates
+    const int tid = threadIdx.x;
+    const uint32_t tok = a.stop_ids ? a.stop_ids[4 * row] : SAS_STOP_PAD;
+    if (tid == 0) {
+      a.out_ids[row] = tok;
+      if (a.out_counts) {
+        a.out_counts[2 * row] = 0;
+        a.out_counts[2 * row + 1] = 0;
+      }
+      if (a.out_flags) a.out_flags[row] = 0u;
+      step_feedback(a, row, tok, true);
+    }
+    if (tid < SAS_MAX_TOP_K) {
+      if (a.out_probs) a.out_probs[(int64_t)row * SAS_MAX_TOP_K + tid] = 0.0;
+      if (a.out_cand_ids) a.out_cand_ids[(int64_t)row * SAS_MAX_TOP_K + tid] = SAS_NO_TOKEN;
+    }
+    return;
+  }
   sas_params p = a.params;
   if (a.row_params) p = load_row_params(a.row_params + row);
   merge_row(a, ml, row, p, s_hist, s_sel);
@@ -782,6 +837,8 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const int lo = part * a.span;
   const int nids = min(a.span, vocab - lo);  // > 0
 
+  // a row that already sampled a stop id (sas_sample_step) reads nothing
+  if (a.st_state && a.st_state[2 * row] != 0u) return;
   sas_params p = a.params;
   if (a.row_params) p = load_row_params(a.row_params + row);
   const bool greedy = !(p.temperature > 0.0);
@@ -791,21 +848,29 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const uint32_t *mrow = kMask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
 
   // ---- history ids (loaded first: the tables fill while the logits load) ----
+  const uint32_t *hid = a.hist_ids;
   int h0 = 0, h1 = 0;
   if (kHist) {
-    // the row's range, clamped into the ids the caller holds and to the
-    // largest window
-    const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
-    const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
-    h0 = (int)o0;
-    h1 = (int)o1;
+    if (a.ring) {
+      // the row's penalty ring: its first min(count, ring_len) slots
+      const uint32_t *rg = a.ring + (int64_t)row * (a.ring_len + 1);
+      hid = rg + 1;
+      h1 = (int)min(rg[0], (uint32_t)a.ring_len);
+    } else {
+      // the row's range, clamped into the ids the caller holds and to the
+      // largest window
+      const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
+      const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
+      h0 = (int)o0;
+      h1 = (int)o1;
+    }
   }
   const bool has_hist = kHist && h1 > h0;
   uint32_t hpre[kHistPre];
 #pragma unroll
   for (int j = 0; j < kHistPre; ++j) {
     const int i = h0 + j * kThreads + tid;
-    hpre[j] = has_hist && i < h1 ? a.hist_ids[i] : kEmpty;
+    hpre[j] = has_hist && i < h1 ? hid[i] : kEmpty;
   }
 
   // ---- loads of one pass --------------------------------------------------------
@@ -882,7 +947,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int i = i0 + j * kThreads;
-        hb8[j] = i < h1 ? a.hist_ids[i] : kEmpty;
+        hb8[j] = i < h1 ? hid[i] : kEmpty;
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) insert(hb8[j]);
@@ -900,7 +965,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     }
     uint32_t c = 0u;
     if (L.hover)
-      for (int i = h0; i < h1; ++i) c += a.hist_ids[i] == id ? 1u : 0u;
+      for (int i = h0; i < h1; ++i) c += hid[i] == id ? 1u : 0u;
     return c;
   };
   // ---- passes: values, the bound, the lists ---------------------------------
@@ -1007,7 +1072,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     if (has_hist) {
       L.hbits[tid] = 0u;
       lds_barrier();
-      for (int i = h0 + tid; i < h1; i += kThreads) set_bit(a.hist_ids[i], base);
+      for (int i = h0 + tid; i < h1; i += kThreads) set_bit(hid[i], base);
     }
     lds_barrier();
     run_pass(base);
@@ -1211,7 +1276,7 @@ static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) {
-  switch ((a.mask ? 4 : 0) | (a.hist_ids ? 2 : 0) | (softcap ? 1 : 0)) {
+  switch ((a.mask ? 4 : 0) | (a.hist_ids || a.ring ? 2 : 0) | (softcap ? 1 : 0)) {
     case 0: launch_kernel<false, false, false>(a, stream); break;
     case 1: launch_kernel<false, false, true>(a, stream); break;
     case 2: launch_kernel<false, true, false>(a, stream); break;

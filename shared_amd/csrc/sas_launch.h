@@ -48,6 +48,18 @@ struct SampleArgs {
   uint64_t *rec;
   uint4 *mrec;
   uint64_t *pinfo;
+  // In-graph feedback (sas_sample_step), all null for sas_sample: per-row
+  // {stopped, iteration}, the sampled matrix, the next input tokens, the
+  // penalty ring {count, ids[ring_len]} (the history when set), stop ids
+  // [rows][4] and PCG seeds.
+  uint32_t *st_state;
+  uint32_t *st_sampled;
+  uint32_t *st_next;
+  uint32_t *ring;
+  const uint32_t *stop_ids;
+  const uint32_t *seeds;
+  int32_t st_max_steps;
+  int32_t ring_len;
   int32_t vocab;
   int32_t rows;
   int32_t parts;   // blocks per row

@@ -154,6 +154,55 @@ def sample_noalloc_into(device: int, logits, out_ids, *, stream=None, **kw) -> N
     check(load().sas_sample_noalloc(int(device), ctypes.byref(d), _stream(stream)), None)
 
 
+class DecodeState:
+    """The caller-owned device state of sas_sample_step for `rows` sequences:
+    {stopped, iteration} per row, the sampled tokens, the next input token,
+    the penalty ring, the stop ids and the seeds (kernels.js:63-200 keeps the
+    same state for one sequence)."""
+
+    def __init__(self, rows: int, *, max_steps: int, ring_len: int = 512, stop_ids=None, seeds=None,
+                 history=None, device=0):
+        import torch
+        if not 1 <= ring_len <= _capi.MAX_HISTORY:
+            raise ValueError("ring_len must be in [1, SAS_MAX_HISTORY]")
+        dev = torch.device("cuda", device) if isinstance(device, int) else device
+        self.rows, self.max_steps, self.ring_len = rows, max_steps, ring_len
+        self.state = torch.zeros((rows, 2), dtype=torch.int32, device=dev)
+        self.sampled = torch.full((rows, max_steps), -1, dtype=torch.int32, device=dev)
+        self.next_tokens = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+        ring = np.zeros((rows, 1 + ring_len), dtype=np.uint32)
+        for r, h in enumerate(history or []):
+            # the last ring_len ids of the row's window, id i at slot i % ring_len
+            h = [int(x) for x in h]
+            for i in range(max(0, len(h) - ring_len), len(h)):
+                ring[r, 1 + i % ring_len] = h[i]
+            ring[r, 0] = len(h)
+        self.ring = torch.from_numpy(ring.view(np.int32)).to(dev)
+        self.stop_ids = None
+        if stop_ids is not None:
+            st = np.full((rows, 4), _capi.STOP_PAD, dtype=np.uint32)
+            for r, ids in enumerate(stop_ids):
+                ids = list(ids)[:4]
+                st[r, :len(ids)] = ids
+            self.stop_ids = torch.from_numpy(st.view(np.int32)).to(dev)
+        self.seeds = None
+        if seeds is not None:
+            self.seeds = torch.from_numpy(np.asarray(seeds, dtype=np.uint32).view(np.int32)).to(dev)
+
+    def descriptor(self):
+        from ._capi import SasStep
+        d = SasStep()
+        d.state = self.state.data_ptr()
+        d.sampled = self.sampled.data_ptr()
+        d.max_steps = self.max_steps
+        d.next_tokens = self.next_tokens.data_ptr()
+        d.ring = self.ring.data_ptr()
+        d.ring_len = self.ring_len
+        d.stop_ids = _ptr(self.stop_ids)
+        d.seeds = _ptr(self.seeds)
+        return d
+
+
 class Sampler:
     """A sas_sampler handle bound to one device."""
 
@@ -212,6 +261,16 @@ class Sampler:
         self.sample_into(logits, out["ids"], out_probs=out.get("probs"), out_cand_ids=out.get("cand_ids"),
                          out_counts=out.get("counts"), out_flags=out.get("flags"), **kw)
         return out if full else out["ids"]
+
+    def sample_step_into(self, logits, out_ids, state: DecodeState, *, stream=None, **kw) -> None:
+        """One decode step with in-graph feedback (sas_sample_step): the
+        rows' history is `state`'s ring, their uniforms come from its seeds
+        (or `uniforms`), and the token is written back into `state`."""
+        if kw.get("hist_ids") is not None:
+            raise ValueError("sample_step_into takes its history from the state's ring")
+        d = rows_descriptor(logits, out_ids, **kw)
+        st = state.descriptor()
+        check(self._lib.sas_sample_step(self._h, ctypes.byref(d), ctypes.byref(st), _stream(stream)), self._h)
 
     def verify_into(self, target, draft, draft_ids, uniforms, out_tokens, out_accepted, *, temperature=1.0,
                     mask=None, vocab: Optional[int] = None, stream=None) -> None:

@@ -1,0 +1,232 @@
+"""GPU parity of sas_sample_step, the decode step with in-graph feedback
+(the reference's sampler kernel, lib/webgpu-llm/kernels.js:63-200), against
+a step-by-step oracle loop: every step's token, candidates and probabilities
+bit-exact, and the state it leaves (stop flags, iterations, sampled tokens,
+next tokens, penalty rings) equal to the loop's."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+from shared_amd import DecodeState, Params, SasError
+from shared_amd._capi import MAX_TOP_K, NO_TOKEN, STOP_PAD, SasStep, load
+from shared_amd.sampler import pack_params, row_hints
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_steps(xs, prm, *, mask=None, stop_ids=None, seeds=None, uniforms=None, history=None, ring_len=512):
+    """The reference's loop (kernels.js:174-199) for each row on the CPU."""
+    steps, rows, _ = xs.shape
+    stop_ids = stop_ids or [[] for _ in range(rows)]
+    window = [list(h) for h in (history or [[] for _ in range(rows)])]
+    stopped = [False] * rows
+    it = [0] * rows
+    outs = []
+    for t in range(steps):
+        step = {"ids": np.zeros(rows, np.uint32), "counts": np.zeros((rows, 2), np.int32),
+                "probs": np.zeros((rows, MAX_TOP_K)), "cand_ids": np.full((rows, MAX_TOP_K), NO_TOKEN, np.uint32)}
+        for r in range(rows):
+            frozen = stopped[r]
+            if frozen:
+                tok = stop_ids[r][0] if stop_ids[r] else STOP_PAD
+            else:
+                u = O.lib().orc_pcg_uniform(int(seeds[r]), it[r], 0) if seeds is not None else uniforms[t][r]
+                h = window[r][-ring_len:] if ring_len else []
+                res = O.sample_row(xs[t, r], prm[r], mask=None if mask is None else mask[r],
+                                   hist=np.array(h, np.uint32) if h else None, uniform=u)
+                tok = res.id
+                n = res.k  # the ranked candidates (0 for a greedy row)
+                step["counts"][r] = (res.k, res.cut)
+                step["probs"][r, :n] = np.array(res.probs)[:n]
+                step["cand_ids"][r, :n] = np.array(res.cand_ids, np.uint32)[:n]
+            step["ids"][r] = tok
+            it[r] += 1
+            if tok == NO_TOKEN or tok in stop_ids[r]:
+                stopped[r] = True
+            elif not frozen:
+                window[r].append(tok)
+        outs.append(step)
+    return outs, stopped, it, window
+
+
+def ring_of(window, ring_len):
+    ring = np.zeros(1 + ring_len, np.uint32)
+    for i in range(max(0, len(window) - ring_len), len(window)):
+        ring[1 + i % ring_len] = window[i]
+    ring[0] = len(window)
+    return ring
+
+
+def spiky_logits(rng, steps, rows, vocab, spikes, height=6.0):
+    """Noise plus a few tall ids shared by every step: penalties decide
+    which of them wins, so the history each step sees matters."""
+    xs = (rng.standard_normal((steps, rows, vocab)) * 1.5).astype(np.float32)
+    for j, sid in enumerate(spikes):
+        xs[:, :, sid] += np.float32(height - 0.25 * j)
+    return xs
+
+
+def run_steps(sampler, xs, prm, state, *, mask=None, uniforms=None):
+    import torch
+    steps, rows, vocab = xs.shape
+    dev = torch.device("cuda", 0)
+    xd = torch.from_numpy(xs).to(dev)
+    rp = torch.from_numpy(pack_params(prm).view(np.uint8)).to(dev)
+    md = None if mask is None else torch.from_numpy(mask.view(np.int32)).to(dev)
+    ids = torch.empty(rows, dtype=torch.int32, device=dev)
+    probs = torch.empty((rows, MAX_TOP_K), dtype=torch.float64, device=dev)
+    cand = torch.empty((rows, MAX_TOP_K), dtype=torch.int32, device=dev)
+    counts = torch.empty((rows, 2), dtype=torch.int32, device=dev)
+    got = []
+    for t in range(steps):
+        u = None if uniforms is None else torch.from_numpy(np.asarray(uniforms[t], np.float64)).to(dev)
+        sampler.sample_step_into(xd[t], ids, state, mask=md, uniforms=u, row_params=rp, row_hints=row_hints(prm),
+                                 out_probs=probs, out_cand_ids=cand, out_counts=counts)
+        torch.cuda.synchronize()
+        got.append({"ids": ids.cpu().numpy().view(np.uint32).copy(), "probs": probs.cpu().numpy().copy(),
+                    "cand_ids": cand.cpu().numpy().view(np.uint32).copy(), "counts": counts.cpu().numpy().copy()})
+    return got
+
+
+def assert_steps(got, want, label):
+    for t, (g, o) in enumerate(zip(got, want)):
+        bad = np.nonzero(g["ids"] != o["ids"])[0]
+        assert bad.size == 0, f"{label} step {t}: rows {bad} gpu {g['ids'][bad]} oracle {o['ids'][bad]}"
+        assert np.array_equal(g["counts"], o["counts"]), f"{label} step {t}: k/cut differ"
+        assert np.array_equal(g["cand_ids"], o["cand_ids"]), f"{label} step {t}: candidates differ"
+        assert np.array_equal(g["probs"].view(np.uint64), o["probs"].view(np.uint64)), f"{label} step {t}: probs"
+
+
+def assert_state(state, want_stopped, want_it, want_window, got_steps, ring_len, label):
+    st = state.state.cpu().numpy()
+    assert st[:, 0].tolist() == [int(s) for s in want_stopped], f"{label}: stop flags"
+    assert st[:, 1].tolist() == want_it, f"{label}: iterations"
+    sampled = state.sampled.cpu().numpy().view(np.uint32)
+    steps = len(got_steps)
+    for r in range(st.shape[0]):
+        seq = [int(g["ids"][r]) for g in got_steps]
+        n = min(steps, state.max_steps)
+        assert sampled[r, :n].tolist() == seq[:n], f"{label}: sampled row {r}"
+    assert np.array_equal(state.next_tokens.cpu().numpy().view(np.uint32), got_steps[-1]["ids"]), label
+    ring = state.ring.cpu().numpy().view(np.uint32)
+    for r, w in enumerate(want_window):
+        assert np.array_equal(ring[r], ring_of(w, ring_len)), f"{label}: ring row {r}"
+
+
+def _params(rows):
+    kinds = [Params(),  # greedy
+             Params(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.3, presence_penalty=0.7),
+             Params(temperature=1.1, top_k=64, top_p=0.9, frequency_penalty=0.6),
+             Params(temperature=0.7, top_k=8, top_p=1.0, repetition_penalty=1.2, presence_penalty=1.5,
+                    frequency_penalty=0.3),
+             Params(repetition_penalty=1.5, presence_penalty=2.0)]  # greedy with penalties
+    return [kinds[r % len(kinds)] for r in range(rows)]
+
+
+@pytest.mark.parametrize("vocab,ring_len,seeded", [(50_000, 3, True), (262_144, 512, True), (32_000, 5, False)])
+def test_steps_match_oracle_loop(sampler, vocab, ring_len, seeded):
+    rows, steps = 10, 7
+    print(f"[gpu] sample_step vocab={vocab} ring_len={ring_len} seeded={seeded}", flush=True)
+    rng = np.random.default_rng(vocab + ring_len)
+    spikes = [11, 4_097, 20_011, 8_191, 30_000 % vocab]
+    xs = spiky_logits(rng, steps, rows, vocab, spikes)
+    prm = _params(rows)
+    stop_ids = [[] for _ in range(rows)]
+    # row 2 stops when it meets id 77 (planted at step 3); row 4 on a spike
+    # id or on 5 (never drawn); row 7 has two stop ids, the second planted
+    xs[3, 2, 77] = np.float32(60.0)
+    stop_ids[2] = [77]
+    stop_ids[4] = [5, spikes[1]]
+    xs[2, 7, 123] = np.float32(60.0)
+    stop_ids[7] = [9, 123, 4, 3]
+    # row 9 allows nothing: no token at step 0, then its first stop id
+    mask = np.full((rows, (vocab + 31) // 32), 0xFFFFFFFF, np.uint32)
+    mask[9] = 0
+    stop_ids[9] = [42]
+    # row 1 starts with a history longer than the ring
+    history = [[] for _ in range(rows)]
+    history[1] = [spikes[0]] * 4 + [spikes[1], 7, 8]
+    history[3] = [spikes[0], spikes[2]]
+    seeds = rng.integers(0, 2**32, rows, dtype=np.uint64).astype(np.uint32) if seeded else None
+    uniforms = None if seeded else rng.random((steps, rows))
+    state = DecodeState(rows, max_steps=steps - 2, ring_len=ring_len, stop_ids=stop_ids, seeds=seeds,
+                        history=history)
+    got = run_steps(sampler, xs, prm, state, mask=mask, uniforms=uniforms)
+    want, stopped, it, window = oracle_steps(xs, prm, mask=mask, stop_ids=stop_ids, seeds=seeds, uniforms=uniforms,
+                                             history=history, ring_len=ring_len)
+    label = f"step v{vocab} ring{ring_len}"
+    assert_steps(got, want, label)
+    assert_state(state, stopped, it, window, got, ring_len, label)
+    # the planted stops and the empty row froze; the rest of row 9 is filler
+    assert stopped[2] and stopped[7] and stopped[9]
+    assert [int(g["ids"][9]) for g in got] == [NO_TOKEN] + [42] * (steps - 1)
+    assert all(int(g["ids"][2]) == 77 for g in got[3:])
+    # penalties moved some row off its first choice: the ring is exercised
+    assert any(len(set(int(g["ids"][r]) for g in got)) > 1 for r in (0, 4))
+
+
+def test_step_without_stops_or_ring(sampler):
+    """No stop ids (filler SAS_STOP_PAD never needed), no ring (no history),
+    no sampled/next buffers: only the state advances."""
+    import torch
+    rows, vocab, steps = 6, 40_000, 4
+    rng = np.random.default_rng(5)
+    xs = spiky_logits(rng, steps, rows, vocab, [3, 9])
+    prm = [Params(temperature=0.9, top_k=20, top_p=0.9)] * rows
+    seeds = np.arange(rows, dtype=np.uint32) * 7919
+    dev = torch.device("cuda", 0)
+    state = torch.zeros((rows, 2), dtype=torch.int32, device=dev)
+    sd = torch.from_numpy(seeds.view(np.int32)).to(dev)
+    st = SasStep()
+    st.state = state.data_ptr()
+    st.seeds = sd.data_ptr()
+    xd = torch.from_numpy(xs).to(dev)
+    ids = torch.empty(rows, dtype=torch.int32, device=dev)
+    from shared_amd.sampler import _stream, rows_descriptor
+    want, _, _, _ = oracle_steps(xs, prm, seeds=seeds, ring_len=0)
+    rp = torch.from_numpy(pack_params(prm).view(np.uint8)).to(dev)
+    for t in range(steps):
+        d = rows_descriptor(xd[t], ids, row_params=rp, row_hints=row_hints(prm))
+        rc = load().sas_sample_step(sampler._h, ctypes.byref(d), ctypes.byref(st), _stream(None))
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy().view(np.uint32), want[t]["ids"]), f"step {t}"
+    assert state.cpu().numpy().tolist() == [[0, steps]] * rows
+
+
+def test_step_rejects_bad_descriptors(sampler):
+    import torch
+    from shared_amd._capi import check
+    from shared_amd.sampler import _stream, rows_descriptor
+    rows, vocab = 2, 1000
+    dev = torch.device("cuda", 0)
+    x = torch.zeros((rows, vocab), dtype=torch.float32, device=dev)
+    ids = torch.empty(rows, dtype=torch.int32, device=dev)
+    st = DecodeState(rows, max_steps=4, ring_len=8, seeds=[1, 2], device=0)
+    hist = torch.zeros(4, dtype=torch.int32, device=dev)
+    off = torch.zeros(rows + 1, dtype=torch.int32, device=dev)
+
+    def call(d, s):
+        check(load().sas_sample_step(sampler._h, ctypes.byref(d), s if s is None else ctypes.byref(s),
+                                     _stream(None)), sampler._h)
+
+    with pytest.raises(ValueError):
+        sampler.sample_step_into(x, ids, st, hist_ids=hist, hist_offsets=off)
+    with pytest.raises(SasError, match="hist_ids"):
+        call(rows_descriptor(x, ids, hist_ids=hist, hist_offsets=off), st.descriptor())
+    d = rows_descriptor(x, ids, params=Params(temperature=1.0))
+    cases = [("state", None, "state"), ("ring_len", 0, "ring_len"), ("ring_len", 100_000, "ring_len"),
+             ("max_steps", 0, "max_steps"), ("seeds", None, "uniforms")]
+    for field, value, msg in cases:
+        s = st.descriptor()
+        setattr(s, field, value)
+        with pytest.raises(SasError, match=msg):
+            call(d, s)
+    with pytest.raises(SasError, match="step descriptor"):
+        call(d, None)
+    # rows == 0 does nothing; nothing above launched
+    call(rows_descriptor(x[:0], ids, params=Params(temperature=1.0)), st.descriptor())
+    torch.cuda.synchronize()
+    assert st.state.cpu().numpy().tolist() == [[0, 0]] * rows
