@@ -387,6 +387,36 @@ napi_value Sample(napi_env env, napi_callback_info info) {
   return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
 }
 
+// A sas_step descriptor: {state, sampled?, maxSteps?, nextTokens?, ring?,
+// ringLen?, stopIds?, seeds?} of device addresses (BigInt) and sizes.
+bool read_step(napi_env env, napi_value d, sas_step *st) {
+  std::memset(st, 0, sizeof *st);
+  int64_t max_steps = 0, ring_len = 0;
+  const bool ok = get_ptr(env, d, "state", (void **)&st->state) && get_ptr(env, d, "sampled", (void **)&st->sampled) &&
+                  get_i64(env, d, "maxSteps", &max_steps) &&
+                  get_ptr(env, d, "nextTokens", (void **)&st->next_tokens) &&
+                  get_ptr(env, d, "ring", (void **)&st->ring) && get_i64(env, d, "ringLen", &ring_len) &&
+                  get_ptr(env, d, "stopIds", (void **)&st->stop_ids) && get_ptr(env, d, "seeds", (void **)&st->seeds);
+  if (!ok || max_steps < 0 || max_steps > INT32_MAX || ring_len < 0 || ring_len > INT32_MAX) return false;
+  st->max_steps = (int32_t)max_steps;
+  st->ring_len = (int32_t)ring_len;
+  return true;
+}
+
+napi_value SampleStep(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_rows r;
+  sas_step st;
+  if (!read_rows(env, argv[1], &r) || !read_step(env, argv[2], &st)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad sample step descriptor");
+    return nullptr;
+  }
+  int rc = sas_sample_step(s, &r, &st, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
 napi_value Verify(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
@@ -408,7 +438,9 @@ struct AsyncCall {
   napi_ref handle_ref = nullptr;  // keeps the handle's external alive until completion
   Handle *h = nullptr;
   bool verify = false;
+  bool step = false;
   sas_rows rows;
+  sas_step srow;
   sas_verify_rows vrows;
   int rc = SAS_OK;
   std::string err;
@@ -423,7 +455,9 @@ void async_execute(napi_env, void *data) {
     return;
   }
   sas_sampler *s = c->h->s;
-  c->rc = c->verify ? sas_verify(s, &c->vrows, sas_stream(s)) : sas_sample(s, &c->rows, sas_stream(s));
+  c->rc = c->verify ? sas_verify(s, &c->vrows, sas_stream(s))
+          : c->step ? sas_sample_step(s, &c->rows, &c->srow, sas_stream(s))
+                    : sas_sample(s, &c->rows, sas_stream(s));
   if (c->rc == SAS_OK) c->rc = sas_synchronize(s, sas_stream(s));
   if (c->rc != SAS_OK) c->err = sas_last_error(s);
 }
@@ -495,6 +529,22 @@ napi_value SampleAsync(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   return start_async(env, c, argv[0], "sas_sample");
+}
+
+napi_value SampleStepAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
+  AsyncCall *c = new AsyncCall();
+  c->h = h;
+  c->step = true;
+  if (!read_rows(env, argv[1], &c->rows) || !read_step(env, argv[2], &c->srow)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad sample step descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, argv[0], "sas_sample_step");
 }
 
 napi_value VerifyAsync(napi_env env, napi_callback_info info) {
@@ -595,6 +645,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"synchronize", nullptr, Synchronize, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sampleAsync", nullptr, SampleAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sampleStep", nullptr, SampleStep, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sampleStepAsync", nullptr, SampleStepAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verify", nullptr, Verify, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verifyAsync", nullptr, VerifyAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"clampParams", nullptr, ClampParams, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
@@ -612,7 +664,7 @@ napi_value Init(napi_env env, napi_value exports) {
                 {"MASK_ALLOW", SAS_MASK_ALLOW},     {"MASK_DENY", SAS_MASK_DENY},
                 {"FLAG_EMPTY_ROW", SAS_FLAG_EMPTY_ROW}, {"FLAG_TOPP_EDGE", SAS_FLAG_TOPP_EDGE},
                 {"FLAG_DRAW_EDGE", SAS_FLAG_DRAW_EDGE}, {"FLAG_SLOW_SELECT", SAS_FLAG_SLOW_SELECT},
-                {"HINT_NO_SOFTCAP", SAS_HINT_NO_SOFTCAP},
+                {"HINT_NO_SOFTCAP", SAS_HINT_NO_SOFTCAP}, {"STOP_PAD", (double)SAS_STOP_PAD},
                 {"PARAMS_BYTES", (double)sizeof(sas_params)}};
   for (const auto &k : consts) {
     napi_create_double(env, k.value, &c);

@@ -20,6 +20,16 @@ export interface SampleParams {
   eosId?: number;
   stopIds?: number[];
   seed?: number;
+  /** Whitelist (model.d.ts:15): the draw is restricted to these ids. */
+  allowedTokenIds?: Uint32Array;
+}
+
+export interface PackerDefaults {
+  temperature?: number;
+  topP?: number;
+  topK?: number;
+  seed?: number | null;
+  eosFromStops?: boolean;
 }
 
 export interface ClampedParams {
@@ -38,6 +48,29 @@ export interface PackedParams {
   stopIds: number[];
   paddedStopIds: number[];
   stopSet: Set<number>;
+  eosId: number | null;
+  allowedTokenIds: Uint32Array | null;
+}
+
+/** The generated-token window of one sequence (model.js:386-389). */
+export declare class PenaltyWindow {
+  constructor(size?: number);
+  readonly size: number;
+  genIds: number[];
+  reset(): void;
+  note(id: number): void;
+  recent(): Uint32Array;
+  recentSet(): Set<number>;
+  rewind(sampledCount: number): void;
+}
+
+/** decodeBatch's result (model.d.ts:23-29). */
+export interface DecodeBatchResult {
+  ids: number[];
+  fed: number;
+  eos: boolean;
+  stopped: boolean;
+  stopId: number | null;
 }
 
 export interface TokenMaskState {
@@ -67,12 +100,30 @@ export interface SampleRowsOptions {
   mask?: TokenMaskState | TokenMask | Uint32Array | DeviceBuffer;
   maskStride?: number;
   params?: SampleParams | SampleParams[];
-  defaults?: Partial<SampleParams>;
+  defaults?: PackerDefaults;
   history?: Array<number[] | Uint32Array | Set<number>>;
+  windows?: PenaltyWindow[];
   recentIds?: Set<number> | number[];
   uniforms?: Float64Array;
   iteration?: number;
   full?: boolean;
+}
+
+export interface DecodeStepsOptions {
+  /** Step i's logits [rows][stride], computed from the tokens in nextTokens. */
+  logits(i: number, nextTokens: DeviceBuffer): DeviceBuffer | Float32Array | Promise<DeviceBuffer | Float32Array>;
+  rows: number;
+  vocab: number;
+  k: number;
+  stride?: number;
+  mask?: TokenMaskState | TokenMask | Uint32Array | DeviceBuffer;
+  maskStride?: number;
+  params?: SampleParams | SampleParams[];
+  defaults?: PackerDefaults;
+  /** The tokens fed at step 0 (decodeBatch's firstTok per row). */
+  firstTokens?: Uint32Array | number[];
+  windows?: PenaltyWindow[];
+  windowSize?: number;
 }
 
 export interface SampleRowsResult {
@@ -106,13 +157,17 @@ export interface VerifyResult {
 
 export declare class Sampler {
   constructor(device?: number);
-  close(): void;
+  close(): Promise<void>;
   reserve(rows: number, vocab: number): void;
   alloc(bytes: number): DeviceBuffer;
   synchronize(): void;
   createTokenMaskState(vocab: number): TokenMaskState;
   sampleRows(opts: SampleRowsOptions): SampleRowsResult;
   sampleRowsAsync(opts: SampleRowsOptions): Promise<SampleRowsResult>;
+  decodeRows(opts: SampleRowsOptions): DecodeBatchResult[];
+  decodeRowsAsync(opts: SampleRowsOptions): Promise<DecodeBatchResult[]>;
+  decodeSteps(opts: DecodeStepsOptions): DecodeBatchResult[];
+  decodeStepsAsync(opts: DecodeStepsOptions): Promise<DecodeBatchResult[]>;
   sample(
     cands: { ids: ArrayLike<number>; vals: ArrayLike<number> },
     opts?: {
@@ -133,7 +188,15 @@ export declare function updateTokenMaskState(
            allowedCount: number; upload(words: Uint32Array): void },
   mask: TokenMask | undefined | null
 ): void;
-export declare function packSamplerParams(sp?: SampleParams, defaults?: Partial<SampleParams>): PackedParams;
+export declare function packSamplerParams(sp?: SampleParams, defaults?: PackerDefaults): PackedParams;
+export declare const PACKER_DEFAULTS: { qwen: PackerDefaults; gemma: PackerDefaults };
+/** Request defaults and ranges (completions.ts:268-273, gemma-completions.ts:212-217). */
+export declare function requestSamplingParams(
+  request?: { temperature?: number; top_p?: number; top_k?: number; presence_penalty?: number },
+  grammar?: "qwen" | "gemma"
+): { temperature: number; topP: number; topK: number; presencePenalty: number };
+export declare function allowedLists(packed: PackedParams[], vocab: number, hasMask: boolean):
+  Array<Uint32Array | null>;
 export declare function maskFromIds(kind: number, ids: Uint32Array | null, vocab: number):
   { words: Uint32Array; allowed: number };
 export declare function pcgUniform(seed: number, it: number, row: number): number;

@@ -358,13 +358,19 @@ class Sampler {
     };
   }
 
-  _describe(opts) {
+  // The sas_rows descriptor of opts.  With `step` the history (the device
+  // ring) and the uniforms (the device draw from each row's seed) are left
+  // out: sas_sample_step brings them.
+  _describe(opts, step) {
     const rows = opts.rows;
     const vocab = opts.vocab;
     const stride = orDefault(opts.stride, vocab);
     const d = { rows: rows, vocab: vocab, logitsStride: stride };
     // logits: device buffer (resident), or a host Float32Array staged up
-    if (opts.logits instanceof DeviceBuffer) {
+    // (a step loop sets them per step)
+    if (step) {
+      d.logits = null;
+    } else if (opts.logits instanceof DeviceBuffer) {
       d.logits = opts.logits.ptr;
     } else if (opts.logits instanceof Float32Array) {
       d.logits = this._buf('logits', opts.logits.byteLength).upload(opts.logits).ptr;
@@ -449,6 +455,10 @@ class Sampler {
       d.rowHints = packed.every(function (p) { return !(p.params.softcap > 0); }) ? addon.HINT_NO_SOFTCAP : 0;
     } else {
       d.params = packed[0].params;
+    }
+    if (step) {
+      d.outIds = this._buf('ids', rows * 4).ptr;
+      return { desc: d, packed: packed };
     }
     // history: per-row lists (Array / Uint32Array / Set), or recentIds for every row
     let hist = opts.history;
@@ -579,6 +589,126 @@ class Sampler {
       const r = self._describe(opts);
       return self._worker(addon.sampleAsync(self._handle(), r.desc))
         .then(function () { return self._decodeResults(opts, self._collect(opts, r.packed), r.packed); });
+    });
+  }
+
+  // The device state of a k-step loop (kernels.js:63-200 per row): zeroed
+  // {stopped, iteration}, the sampled tokens, the fed-back tokens (seeded
+  // with opts.firstTokens), the penalty rings (seeded from opts.windows as
+  // model.js:391-399 seeds its ring), the padded stop ids and the seeds.
+  _stepState(opts, packed, k) {
+    const rows = opts.rows;
+    const W = Math.floor(orDefault(opts.windowSize, opts.windows && opts.windows.length ? opts.windows[0].size : 512));
+    if (!(W >= 1 && W <= addon.MAX_HISTORY)) throw new RangeError('windowSize must be in [1, ' + addon.MAX_HISTORY + ']');
+    const pk = function (r) { return packed[packed.length > 1 ? r : 0]; };
+    const ring = new Uint32Array(rows * (1 + W));
+    if (opts.windows) {
+      if (opts.windows.length !== rows) throw new RangeError('windows must have one PenaltyWindow per row');
+      for (let r = 0; r < rows; r++) {
+        const g = opts.windows[r].genIds;
+        const n = g.length;
+        const base = r * (1 + W);
+        ring[base] = n;
+        for (let i = Math.max(0, n - W); i < n; i++) ring[base + 1 + (i % W)] = g[i];
+      }
+    }
+    const stops = new Uint32Array(rows * 4);
+    const seeds = new Uint32Array(rows);
+    for (let r = 0; r < rows; r++) {
+      stops.set(pk(r).paddedStopIds, r * 4);
+      seeds[r] = pk(r).seed;
+    }
+    const next = new Uint32Array(rows);
+    if (opts.firstTokens) {
+      const f = toU32(opts.firstTokens);
+      if (f.length !== rows) throw new RangeError('firstTokens must have one id per row');
+      next.set(f);
+    }
+    return {
+      state: this._buf('stState', rows * 8).upload(new Uint32Array(rows * 2)).ptr,
+      sampled: this._buf('stSampled', rows * k * 4).ptr, maxSteps: k,
+      nextTokens: this._buf('stNext', rows * 4).upload(next).ptr,
+      ring: this._buf('stRing', ring.byteLength).upload(ring).ptr, ringLen: W,
+      stopIds: this._buf('stStops', stops.byteLength).upload(stops).ptr,
+      seeds: this._buf('stSeeds', seeds.byteLength).upload(seeds).ptr,
+    };
+  }
+
+  // The logits of step i from the caller's producer (a DeviceBuffer or a
+  // host Float32Array of [rows][stride]).
+  _stepLogits(d, logits) {
+    if (logits instanceof DeviceBuffer) d.logits = logits.ptr;
+    else if (logits instanceof Float32Array) d.logits = this._buf('logits', logits.byteLength).upload(logits).ptr;
+    else throw new TypeError('the logits producer must return a DeviceBuffer or a Float32Array');
+  }
+
+  // decodeBatch's result for each row after k steps (model.js:727-741): the
+  // ids through the first stop, how many were fed, eos/stopped/stopId; the
+  // windows receive the non-stop tokens as the device ring did.
+  _stepResults(opts, packed, k) {
+    const rows = opts.rows;
+    const sampled = this._scratch.stSampled.download(new Uint32Array(rows * k));
+    const res = [];
+    for (let r = 0; r < rows; r++) {
+      const pk = packed[packed.length > 1 ? r : 0];
+      const ids = Array.from(sampled.subarray(r * k, (r + 1) * k));
+      const stopAt = ids.findIndex(function (id) { return pk.stopSet.has(id) || id === addon.NO_TOKEN; });
+      const stopped = stopAt >= 0;
+      const stopId = stopped ? ids[stopAt] : null;
+      if (opts.windows) {
+        const kept = stopped ? ids.slice(0, stopAt) : ids;
+        for (let i = 0; i < kept.length; i++) opts.windows[r].note(kept[i]);
+      }
+      res.push({ ids: stopped ? ids.slice(0, stopAt + 1) : ids, fed: stopped ? stopAt + 1 : k,
+        eos: stopped && pk.eosId !== null && stopId === pk.eosId, stopped: stopped, stopId: stopId });
+    }
+    return res;
+  }
+
+  /**
+   * decodeBatch's k-step loop (model.js:649-742) for opts.rows sequences,
+   * each token fed back on the device: step i samples every live row from
+   * opts.logits(i, nextTokens), the logits ([rows][stride], a DeviceBuffer
+   * or a Float32Array) the caller's model computed from the tokens in
+   * nextTokens (a DeviceBuffer of rows uint32: opts.firstTokens at step 0,
+   * then the last step's tokens).  A row that samples one of its stop ids
+   * freezes and emits its first stop id from then on; other tokens join its
+   * device penalty ring (the last windowSize tokens, seeded from
+   * opts.windows).  Draws use each row's seed at the row's iteration
+   * (kernels.js:181).  opts as sampleRows otherwise, with k (>= 1) and no
+   * history/uniforms.  Returns per row {ids, fed, eos, stopped, stopId}.
+   */
+  decodeSteps(opts) {
+    this._idle('decodeSteps');
+    const k = Math.floor(opts.k);
+    if (!(k >= 1)) throw new RangeError('k must be >= 1');
+    const r = this._describe(opts, true);
+    const st = this._stepState(opts, r.packed, k);
+    const next = this._scratch.stNext;
+    for (let i = 0; i < k; i++) {
+      this._stepLogits(r.desc, opts.logits(i, next));
+      addon.sampleStep(this._handle(), r.desc, st);
+    }
+    return this._stepResults(opts, r.packed, k);
+  }
+
+  /** decodeSteps with each launch and wait on a worker thread; opts.logits may return a promise. */
+  decodeStepsAsync(opts) {
+    const self = this;
+    return this._enqueue(function () {
+      const k = Math.floor(opts.k);
+      if (!(k >= 1)) throw new RangeError('k must be >= 1');
+      const r = self._describe(opts, true);
+      const st = self._stepState(opts, r.packed, k);
+      const next = self._scratch.stNext;
+      let chain = Promise.resolve();
+      for (let i = 0; i < k; i++) {
+        chain = chain.then(function () { return opts.logits(i, next); }).then(function (lg) {
+          self._stepLogits(r.desc, lg);
+          return self._worker(addon.sampleStepAsync(self._handle(), r.desc, st));
+        });
+      }
+      return chain.then(function () { return self._stepResults(opts, r.packed, k); });
     });
   }
 

@@ -6,7 +6,7 @@ import numpy as np
 
 import oracle as O
 from shared_amd import Sampler
-from shared_amd._capi import FLAG_DRAW_EDGE, FLAG_EMPTY_ROW, FLAG_TOPP_EDGE
+from shared_amd._capi import FLAG_DRAW_EDGE, FLAG_EMPTY_ROW, FLAG_TOPP_EDGE, MAX_TOP_K, NO_TOKEN, STOP_PAD
 
 ORACLE_FLAGS = FLAG_EMPTY_ROW | FLAG_TOPP_EDGE | FLAG_DRAW_EDGE
 
@@ -55,3 +55,46 @@ def assert_parity(g: dict, o: dict, label: str = "") -> None:
         # probabilities: identical double arithmetic, so bitwise equal
         assert np.array_equal(g["probs"].view(np.uint64), o["probs"].view(np.uint64)), f"{label}: probs differ"
         assert np.array_equal(g["flags"] & ORACLE_FLAGS, o["flags"] & ORACLE_FLAGS), f"{label}: flags differ"
+
+
+def oracle_steps(xs, prm, *, mask=None, stop_ids=None, seeds=None, uniforms=None, history=None, ring_len=512):
+    """The reference's loop (kernels.js:174-199) for each row on the CPU."""
+    steps, rows, _ = xs.shape
+    stop_ids = stop_ids or [[] for _ in range(rows)]
+    window = [list(h) for h in (history or [[] for _ in range(rows)])]
+    stopped = [False] * rows
+    it = [0] * rows
+    outs = []
+    for t in range(steps):
+        step = {"ids": np.zeros(rows, np.uint32), "counts": np.zeros((rows, 2), np.int32),
+                "probs": np.zeros((rows, MAX_TOP_K)), "cand_ids": np.full((rows, MAX_TOP_K), NO_TOKEN, np.uint32)}
+        for r in range(rows):
+            frozen = stopped[r]
+            if frozen:
+                tok = stop_ids[r][0] if stop_ids[r] else STOP_PAD
+            else:
+                u = O.lib().orc_pcg_uniform(int(seeds[r]), it[r], 0) if seeds is not None else uniforms[t][r]
+                h = window[r][-ring_len:] if ring_len else []
+                res = O.sample_row(xs[t, r], prm[r], mask=None if mask is None else mask[r],
+                                   hist=np.array(h, np.uint32) if h else None, uniform=u)
+                tok = res.id
+                n = res.k  # the ranked candidates (0 for a greedy row)
+                step["counts"][r] = (res.k, res.cut)
+                step["probs"][r, :n] = np.array(res.probs)[:n]
+                step["cand_ids"][r, :n] = np.array(res.cand_ids, np.uint32)[:n]
+            step["ids"][r] = tok
+            it[r] += 1
+            if tok == NO_TOKEN or tok in stop_ids[r]:
+                stopped[r] = True
+            elif not frozen:
+                window[r].append(tok)
+        outs.append(step)
+    return outs, stopped, it, window
+
+
+def ring_of(window, ring_len):
+    ring = np.zeros(1 + ring_len, np.uint32)
+    for i in range(max(0, len(window) - ring_len), len(window)):
+        ring[1 + i % ring_len] = window[i]
+    ring[0] = len(window)
+    return ring

@@ -122,3 +122,62 @@ def test_node_api_end_to_end(tmp_path):
     assert np.array_equal(_u32(d, "js_v_tokens.u32").reshape(v["seqs"], L + 1), ov["tokens"])
     assert np.array_equal(np.fromfile(os.path.join(d, "js_v_acc.i32"), np.int32), ov["accepted"])
     assert np.array_equal(_u32(d, "js_v2_tokens.u32"), _u32(d, "js_v_tokens.u32"))
+
+
+def test_node_decode_steps(tmp_path):
+    """decodeSteps / decodeStepsAsync against the oracle stepped the same way
+    (kernels.js:174-199 per row; decodeBatch's result, model.js:727-741)."""
+    if shutil.which("node") is None:
+        pytest.skip("node is not installed")
+    from gpu_helpers import oracle_steps
+    d = str(tmp_path)
+    rows, vocab, k, wsize = 6, 60_000, 6, 4
+    rng = np.random.default_rng(23)
+    xs = (rng.standard_normal((k, rows, vocab)) * 1.5).astype(np.float32)
+    for j, sid in enumerate([17, 2_049, 40_000]):
+        xs[:, :, sid] += np.float32(6.0 - 0.3 * j)
+    js = [dict(temperature=0.9, topK=30, topP=0.9, repetitionPenalty=1.3, presencePenalty=0.8, frequencyPenalty=0.2,
+               softcap=0, seed=int(rng.integers(1, 2**31))) for _ in range(rows)]
+    js[1].update(temperature=0)  # greedy: the penalties alone move it off the spikes
+    prm = [Params(temperature=p["temperature"], top_k=p["topK"], top_p=p["topP"],
+                  repetition_penalty=p["repetitionPenalty"], presence_penalty=p["presencePenalty"],
+                  frequency_penalty=p["frequencyPenalty"]) for p in js]
+    seeds = np.array([p["seed"] for p in js], np.uint32)
+    hist = [[17, 17, 5, 2_049, 9], [], [40_000], [], [1, 2, 3], [17]]
+    free, _, _, _ = oracle_steps(xs, prm, seeds=seeds, history=hist, ring_len=wsize)
+    # stops: row 0 at its third token (also its eos), row 2 on its first
+    # token as a second stop id, row 4 on an id it never draws
+    stops = [[int(free[2]["ids"][0])], [], [3, int(free[0]["ids"][2])], [], [7], []]
+    for r, st in enumerate(stops):
+        if st:
+            js[r]["stopIds"] = st
+    want, _, _, window = oracle_steps(xs, prm, seeds=seeds, stop_ids=stops, history=hist, ring_len=wsize)
+    xs.tofile(os.path.join(d, "step_logits.f32"))
+    first = np.arange(rows, dtype=np.uint32) + 1000
+    first.tofile(os.path.join(d, "first.u32"))
+    with open(os.path.join(d, "steps.json"), "w") as f:
+        json.dump({"rows": rows, "vocab": vocab, "k": k, "params": js, "windows": hist, "windowSize": wsize}, f)
+    print("[gpu] node steps_gpu.js", d, flush=True)
+    proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "steps_gpu.js"), d], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-3000:]
+    seqs = [[int(w["ids"][r]) for w in want] for r in range(rows)]
+    expect = []
+    for r in range(rows):
+        ids = seqs[r]
+        at = next((i for i, t in enumerate(ids) if t in stops[r]), -1)
+        hit = at >= 0
+        expect.append({"ids": ids[:at + 1] if hit else ids, "fed": at + 1 if hit else k,
+                       "eos": hit and ids[at] == stops[r][0], "stopped": hit, "stopId": ids[at] if hit else None})
+    assert expect[0]["stopped"] and expect[0]["eos"] and expect[2]["stopped"] and not expect[2]["eos"]
+    for name in ("js_steps.json", "js_steps_async.json"):
+        with open(os.path.join(d, name)) as f:
+            got = json.load(f)
+        assert got["results"] == expect, name
+        assert got["windows"] == window, name
+    with open(os.path.join(d, "js_steps.json")) as f:
+        fed = json.load(f)["fed"]
+    assert fed[0] == first.tolist()
+    for i in range(1, k):
+        assert fed[i] == [int(x) for x in want[i - 1]["ids"]], i
