@@ -161,6 +161,47 @@ typedef struct sas_verify_rows {
   int32_t *out_accepted;       /* device [seqs]: number of accepted drafts */
 } sas_verify_rows;
 
+/*
+ * The reference's speculative acceptance (kernels.js:211-369, driven by
+ * model.js:867-1008): drafts are the argmax of the draft head
+ * (argmaxMerge, kernels.js:373-401), every verify row is sampled on its own
+ * and a draft is accepted iff the verify row before it sampled exactly it
+ * (the cascade, kernels.js:328-339).  Sequence s has draft_len drafts and
+ * draft_len + 1 verify rows; verify row j is sampled as sas_sample samples a
+ * row (the sequence's params, its history, mask row s * (draft_len + 1) + j)
+ * with the uniform (pcg(seed ^ round * 0x9E3779B9 ^ j * 0x85EBCA6B) &
+ * 0xFFFFFF) / 2^24 (kernels.js:320).  Then a = 1 and next = pick[0]; while
+ * a <= draft_len, pick[a - 1] equals draft a - 1 and is not a stop id,
+ * a grows by one and next = pick[a - 1].  The sequence commits pick[0 .. a).
+ */
+typedef struct sas_spec_rows {
+  const float *target_logits;   /* device [seqs * (draft_len + 1)][logits_stride]: verify rows */
+  const float *draft_logits;    /* device [seqs * draft_len][logits_stride] (the draft head's
+                                   logits), or NULL when draft_ids are given */
+  int64_t logits_stride;
+  int32_t vocab;
+  int32_t seqs;
+  int32_t draft_len;            /* 1..SAS_MAX_DRAFT (the reference uses 2) */
+  uint32_t *draft_ids;          /* device [seqs][draft_len]: written with the argmax of each
+                                   draft row (lowest id among equals) when draft_logits is
+                                   set, else read */
+  const uint32_t *mask;         /* device [seqs * (draft_len + 1)][mask_stride] or NULL: the
+                                   verify rows' masks, laid out as in sas_rows */
+  int64_t mask_stride;
+  const uint32_t *hist_ids;     /* each sequence's history, as in sas_rows with one range */
+  const int32_t *hist_offsets;  /* per sequence: device [seqs + 1] */
+  int64_t hist_count;
+  sas_params params;            /* every sequence, unless seq_params */
+  const sas_params *seq_params; /* device [seqs] or NULL */
+  const uint32_t *seeds;        /* device [seqs] */
+  uint32_t round;               /* the round number the draws use */
+  uint32_t row_hints;           /* SAS_HINT_* (with seq_params) */
+  const uint32_t *stop_ids;     /* device [seqs][4], SAS_STOP_PAD padded, or NULL */
+  uint32_t *out_picks;          /* device [seqs][draft_len + 1]: each verify row's token */
+  int32_t *out_accepted;        /* device [seqs]: a, the tokens committed (1..draft_len + 1) */
+  uint32_t *out_next;           /* device [seqs]: pick[a - 1], the next input token, or NULL */
+} sas_spec_rows;
+
 typedef struct sas_sampler sas_sampler;
 
 /* Library version string ("shared_amd_sampler <abi> gfx950"). */
@@ -238,6 +279,10 @@ int sas_sample_noalloc(int device, const sas_rows *rows, void *stream);
 
 /* Speculative accept/resample, stream-ordered like sas_sample. */
 int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
+
+/* The reference's exact-match speculative round (kernels.js:211-401),
+ * stream-ordered like sas_sample. */
+int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream);
 
 /* Host: clamp parameters with the reference packer's rules
  * (model.js:418-423): non-finite or negative temperature -> 0 (greedy),

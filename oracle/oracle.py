@@ -68,6 +68,10 @@ def lib() -> ctypes.CDLL:
         L.orc_verify.restype = None
         L.orc_verify.argtypes = [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_int64,
                                  c_void_p, c_double, c_void_p, c_void_p, c_void_p]
+        L.orc_spec_exact.restype = None
+        L.orc_spec_exact.argtypes = [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                     c_int64, c_void_p, c_void_p, POINTER(OrcParams), c_void_p, c_void_p, c_uint32,
+                                     c_void_p, c_void_p, c_void_p, c_void_p]
         _lib = L
     return _lib
 
@@ -135,6 +139,35 @@ def verify(inp: dict) -> dict:
     lib().orc_verify(_p(t), _p(d), vocab, vocab, seqs, L, _p(ids), _p(m), 0 if m is None else m.shape[1], _p(u),
                      float(inp["temperature"]), _p(toks), _p(acc), _p(ratio))
     return {"tokens": toks, "accepted": acc, "ratio": ratio}
+
+
+def spec_exact(inp: dict) -> dict:
+    """The exact-match speculative round (orc_spec_exact) for the fields of
+    shared_amd.workloads.spec_case: target [seqs*(L+1)][V], draft [seqs*L][V]
+    or None (then draft_ids), mask, CSR history per sequence, params or
+    seq_params, seeds, round, stop_ids."""
+    seqs, L, vocab = inp["seqs"], inp["drafts"], inp["vocab"]
+    t = np.ascontiguousarray(inp["target"], np.float32)
+    d = inp.get("draft")
+    d = None if d is None else np.ascontiguousarray(d, np.float32)
+    ids = (np.zeros((seqs, L), np.uint32) if d is not None
+           else np.ascontiguousarray(inp["draft_ids"], np.uint32).copy())
+    m = None if inp.get("mask") is None else np.ascontiguousarray(inp["mask"], np.uint32)
+    hi = None if inp.get("hist_ids") is None else np.ascontiguousarray(inp["hist_ids"], np.uint32)
+    ho = None if inp.get("hist_offsets") is None else np.ascontiguousarray(inp["hist_offsets"], np.int32)
+    sp = None
+    if inp.get("seq_params") is not None:
+        sp = (OrcParams * seqs)(*[params(q) for q in inp["seq_params"]])
+    seeds = np.ascontiguousarray(inp["seeds"], np.uint32)
+    st = None if inp.get("stop_ids") is None else np.ascontiguousarray(inp["stop_ids"], np.uint32)
+    picks = np.zeros((seqs, L + 1), np.uint32)
+    acc = np.zeros(seqs, np.int32)
+    nxt = np.zeros(seqs, np.uint32)
+    lib().orc_spec_exact(_p(t), _p(d), vocab, vocab, seqs, L, _p(ids), _p(m), 0 if m is None else m.shape[1],
+                         _p(hi), _p(ho), ctypes.byref(params(inp.get("params") or {})),
+                         None if sp is None else ctypes.cast(sp, c_void_p), _p(seeds), int(inp.get("round", 0)),
+                         _p(st), _p(picks), _p(acc), _p(nxt))
+    return {"draft_ids": ids, "picks": picks, "accepted": acc, "next": nxt}
 
 
 # ------------------------------------------------------------ Node driver --

@@ -40,6 +40,14 @@
  *                      kernels.js:328-339): textbook rejection sampling;
  *                      pinned by distribution tests (empirical marginal = p,
  *                      q = p accepts always, one-hot q accepts w.p. p(d)).
+ *   orc_spec_exact     acceptSpec kernels.js:211-369 on A.2 semantics: each
+ *                      verify row sampled on its own with the uniform of
+ *                      kernels.js:320, the cascade of kernels.js:328-339
+ *                      (a stop id never extends it); drafts from
+ *                      argmaxMerge kernels.js:373-401 (lowest id among equal
+ *                      maxima).  Pinned by closed forms: drafts = first
+ *                      np.argmax over the non-NaN values, planted picks with
+ *                      hand-derived accept counts, and a stop-id draft.
  */
 #include "sampler_oracle.h"
 
@@ -476,4 +484,62 @@ void orc_verify(const float *target, const float *draft, int64_t stride,
   }
   free(wp);
   free(wq);
+}
+
+/* ------------------------------------------------ exact-match spec round -- */
+
+void orc_spec_exact(const float *target, const float *draft, int64_t stride,
+                    int32_t vocab, int32_t seqs, int32_t draft_len,
+                    uint32_t *draft_ids, const uint32_t *mask,
+                    int64_t mask_stride, const uint32_t *hist_ids,
+                    const int32_t *hist_offsets, const orc_params *params,
+                    const orc_params *seq_params, const uint32_t *seeds,
+                    uint32_t round, const uint32_t *stop_ids,
+                    uint32_t *out_picks, int32_t *out_accepted,
+                    uint32_t *out_next) {
+  const int32_t L = draft_len;
+  orc_params greedy;
+  memset(&greedy, 0, sizeof greedy);
+  greedy.top_p = 1.0;
+  greedy.repetition_penalty = 1.0;
+  greedy.top_k = 1;
+  orc_result res;
+  for (int32_t s = 0; s < seqs; s++) {
+    /* drafts: the top-1 of each draft row (argmaxMerge, kernels.js:373-401) */
+    if (draft) {
+      for (int32_t j = 0; j < L; j++) {
+        orc_sample_row(draft + ((int64_t)s * L + j) * stride, vocab, NULL, NULL, 0, &greedy, 0.0, 0, &res);
+        draft_ids[(int64_t)s * L + j] = res.id;
+      }
+    }
+    const orc_params *p = seq_params ? &seq_params[s] : params;
+    const uint32_t *h = NULL;
+    int32_t hn = 0;
+    if (hist_ids) {
+      h = hist_ids + hist_offsets[s];
+      hn = hist_offsets[s + 1] - hist_offsets[s];
+    }
+    /* every verify row on its own, history as of the round's start
+     * (kernels.js:255-327) */
+    uint32_t *pk = out_picks + (int64_t)s * (L + 1);
+    for (int32_t j = 0; j <= L; j++) {
+      const int64_t row = (int64_t)s * (L + 1) + j;
+      const uint32_t *m = mask ? mask + (mask_stride ? row * mask_stride : 0) : NULL;
+      orc_sample_row(target + row * stride, vocab, m, h, hn, p, orc_pcg_uniform(seeds[s], round, (uint32_t)j), 0,
+                     &res);
+      pk[j] = res.id;
+    }
+    /* the cascade (kernels.js:328-339) */
+    int32_t a = 1;
+    while (a <= L) {
+      const uint32_t t = pk[a - 1];
+      int stop = 0;
+      if (stop_ids)
+        for (int i = 0; i < 4; i++) stop |= t == stop_ids[4 * s + i];
+      if (t != draft_ids[(int64_t)s * L + a - 1] || stop) break;
+      a++;
+    }
+    out_accepted[s] = a;
+    if (out_next) out_next[s] = pk[a - 1];
+  }
 }

@@ -82,4 +82,19 @@ void orc_verify(const float *target, const float *draft, int64_t stride,
                 double temperature, uint32_t *out_tokens,
                 int32_t *out_accepted, double *out_ratio);
 
+/* The reference's exact-match speculative round for `seqs` sequences
+ * (layout as sas_spec_rows): argmax drafts when `draft` is set (written to
+ * draft_ids), verify row j of sequence s sampled by orc_sample_row with the
+ * sequence's params and history and uniform orc_pcg_uniform(seed, round,
+ * j), then the cascade.  stop_ids: [seqs][4] or NULL; out_next may be NULL. */
+void orc_spec_exact(const float *target, const float *draft, int64_t stride,
+                    int32_t vocab, int32_t seqs, int32_t draft_len,
+                    uint32_t *draft_ids, const uint32_t *mask,
+                    int64_t mask_stride, const uint32_t *hist_ids,
+                    const int32_t *hist_offsets, const orc_params *params,
+                    const orc_params *seq_params, const uint32_t *seeds,
+                    uint32_t round, const uint32_t *stop_ids,
+                    uint32_t *out_picks, int32_t *out_accepted,
+                    uint32_t *out_next);
+
 #endif

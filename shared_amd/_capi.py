@@ -105,6 +105,32 @@ class SasVerifyRows(ctypes.Structure):
     ]
 
 
+class SasSpecRows(ctypes.Structure):
+    _fields_ = [
+        ("target_logits", c_void_p),
+        ("draft_logits", c_void_p),
+        ("logits_stride", c_int64),
+        ("vocab", c_int32),
+        ("seqs", c_int32),
+        ("draft_len", c_int32),
+        ("draft_ids", c_void_p),
+        ("mask", c_void_p),
+        ("mask_stride", c_int64),
+        ("hist_ids", c_void_p),
+        ("hist_offsets", c_void_p),
+        ("hist_count", c_int64),
+        ("params", SasParams),
+        ("seq_params", c_void_p),
+        ("seeds", c_void_p),
+        ("round", c_uint32),
+        ("row_hints", c_uint32),
+        ("stop_ids", c_void_p),
+        ("out_picks", c_void_p),
+        ("out_accepted", c_void_p),
+        ("out_next", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); every function declared in the header.
 SIGNATURES = {
     "sas_version": (c_char_p, []),
@@ -116,6 +142,7 @@ SIGNATURES = {
     "sas_sample_noalloc": (c_int, [c_int, POINTER(SasRows), c_void_p]),
     "sas_sample_step": (c_int, [c_void_p, POINTER(SasRows), POINTER(SasStep), c_void_p]),
     "sas_verify": (c_int, [c_void_p, POINTER(SasVerifyRows), c_void_p]),
+    "sas_spec_exact": (c_int, [c_void_p, POINTER(SasSpecRows), c_void_p]),
     "sas_clamp_params": (c_int, [POINTER(SasParams), POINTER(SasParams)]),
     "sas_mask_from_ids": (c_int64, [c_int32, POINTER(c_uint32), c_size_t, c_int32, POINTER(c_uint32), c_int64]),
     "sas_pcg_uniform": (c_double, [c_uint32, c_uint32, c_uint32]),

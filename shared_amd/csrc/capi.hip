@@ -176,7 +176,18 @@ const char *check_step(const sas_rows *r, const sas_step *st) {
 }
 
 // sas_sample and sas_sample_step: `st` (checked) or nullptr.
-int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char *who, void *stream) {
+// The verify rows of an exact-match speculative round: groups of `group`
+// rows share a sequence's history, params and seed.
+struct SpecDraw {
+  const uint32_t *seeds;
+  uint32_t round;
+  int group;
+};
+
+// sas_sample, sas_sample_step (st) and the sampling of sas_spec_exact (sp):
+// one checked descriptor's launches.
+int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char *who, void *stream,
+              const SpecDraw *sp = nullptr) {
   if (int rc = set_device(s)) return rc;
   // at least two blocks per CU: small batches take shorter parts
   int parts = 0, span = 0;
@@ -205,6 +216,11 @@ int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char 
     a.ring_len = st->ring ? st->ring_len : 0;
     a.stop_ids = st->stop_ids;
     a.seeds = st->seeds;
+  }
+  if (sp) {
+    a.spec_seeds = sp->seeds;
+    a.spec_round = sp->round;
+    a.group = sp->group;
   }
   hipError_t e = sas::launch_sample(a, any_softcap(r), pick_stream(s, stream));
   s->last_stream = pick_stream(s, stream);
@@ -322,6 +338,59 @@ int sas_sample_noalloc(int device, const sas_rows *r, void *stream) {
   fill_args(r, logits, stride, parts, span, base, &a);
   e = sas::launch_sample(a, any_softcap(r), st);
   if (e != hipSuccess) return hip_fail(nullptr, e, "sas_sample_noalloc launch");
+  return SAS_OK;
+}
+
+int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_spec_exact: handle is NULL");
+  if (!r) return fail(s, SAS_ERR_INVALID, "sas_spec_exact: descriptor is NULL");
+  if (r->seqs < 0) return fail(s, SAS_ERR_INVALID, "sas_spec_exact: seqs must be >= 0");
+  if (r->draft_len < 1 || r->draft_len > SAS_MAX_DRAFT)
+    return fail(s, SAS_ERR_INVALID, "sas_spec_exact: draft_len must be in [1, SAS_MAX_DRAFT]");
+  if (r->seqs == 0) return SAS_OK;
+  if ((int64_t)r->seqs * (r->draft_len + 1) > INT32_MAX)
+    return fail(s, SAS_ERR_INVALID, "sas_spec_exact: too many verify rows");
+  if (!r->draft_ids || !r->seeds || !r->out_picks || !r->out_accepted)
+    return fail(s, SAS_ERR_INVALID, "sas_spec_exact: draft_ids, seeds, out_picks and out_accepted are required");
+  hipStream_t stream_h = pick_stream(s, stream);
+  const int L = r->draft_len;
+  // the drafts: the argmax of every draft row (argmaxMerge, kernels.js:373-401)
+  if (r->draft_logits) {
+    sas_rows d{};
+    d.logits = r->draft_logits;
+    d.logits_stride = r->logits_stride;
+    d.vocab = r->vocab;
+    d.rows = r->seqs * L;
+    d.params.temperature = 0.0;
+    d.params.top_p = 1.0;
+    d.params.repetition_penalty = 1.0;
+    d.params.top_k = 1;
+    d.out_ids = r->draft_ids;
+    if (const char *m = check_rows(&d)) return fail(s, SAS_ERR_INVALID, std::string("sas_spec_exact: drafts: ") + m);
+    if (int rc = sample_on(s, &d, nullptr, "sas_spec_exact drafts", stream)) return rc;
+  }
+  // every verify row, sampled on its own (kernels.js:255-327)
+  sas_rows v{};
+  v.logits = r->target_logits;
+  v.logits_stride = r->logits_stride;
+  v.vocab = r->vocab;
+  v.rows = r->seqs * (L + 1);
+  v.mask = r->mask;
+  v.mask_stride = r->mask_stride;
+  v.hist_ids = r->hist_ids;
+  v.hist_offsets = r->hist_offsets;
+  v.hist_count = r->hist_count;
+  v.params = r->params;
+  v.row_params = r->seq_params;
+  v.row_hints = r->row_hints;
+  v.out_ids = r->out_picks;
+  if (const char *m = check_rows(&v, true)) return fail(s, SAS_ERR_INVALID, std::string("sas_spec_exact: ") + m);
+  const SpecDraw sp{r->seeds, r->round, L + 1};
+  if (int rc = sample_on(s, &v, nullptr, "sas_spec_exact", stream, &sp)) return rc;
+  // the cascade (kernels.js:328-339)
+  hipError_t e = sas::launch_spec_cascade(r->out_picks, r->draft_ids, r->stop_ids, r->seqs, L, r->out_accepted,
+                                          r->out_next, stream_h);
+  if (e != hipSuccess) return hip_fail(s, e, "sas_spec_exact cascade launch");
   return SAS_OK;
 }
 

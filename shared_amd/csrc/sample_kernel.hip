@@ -422,9 +422,10 @@ __device__ __forceinline__ uint32_t sample_tail(MergeLds &ml, int kk, int row, d
   return out_id;
 }
 
-// The reference GPU sampler's uniform (kernels.js:91-95, 181).
-__device__ __forceinline__ double pcg_uniform(uint32_t seed, uint32_t it) {
-  uint32_t h = (seed ^ (it * 0x9E3779B9u)) * 747796405u + 2891336453u;
+// The reference GPU samplers' uniform (kernels.js:91-95, 181, 320): the
+// in-graph step draws with j = 0, verify row j of a speculative round with j.
+__device__ __forceinline__ double pcg_uniform(uint32_t seed, uint32_t it, uint32_t j) {
+  uint32_t h = (seed ^ (it * 0x9E3779B9u) ^ (j * 0x85EBCA6Bu)) * 747796405u + 2891336453u;
   h = ((h >> ((h >> 28u) + 4u)) ^ h) * 277803737u;
   h = (h >> 22u) ^ h;
   return (double)(h & 0xFFFFFFu) / 16777216.0;
@@ -492,8 +493,11 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   }
   const uint4 mr = qok ? load_rec4(mq + sub) : make_uint4(0u, 0u, 0u, 0u);
   const uint64_t info = qok ? load_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + q) : 0ull;
-  const double u_row =
-      greedy ? 0.0 : (a.seeds ? pcg_uniform(a.seeds[row], a.st_state[2 * row + 1]) : a.uniforms[row]);
+  const int srow = a.group > 1 ? row / a.group : row;
+  const double u_row = greedy        ? 0.0
+                       : a.spec_seeds ? pcg_uniform(a.spec_seeds[srow], a.spec_round, (uint32_t)(row - srow * a.group))
+                       : a.seeds      ? pcg_uniform(a.seeds[row], a.st_state[2 * row + 1], 0u)
+                                      : a.uniforms[row];
   for (int i = tid; i < kSurvCap + 8; i += kThreads) ml.s_c[i] = 0ull;  // padding: ranks after everything
   ml.s_rank[tid] = 0u;
   ml.s_rank[tid + kThreads] = 0u;
@@ -773,8 +777,40 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
     return;
   }
   sas_params p = a.params;
-  if (a.row_params) p = load_row_params(a.row_params + row);
+  if (a.row_params) p = load_row_params(a.row_params + (a.group > 1 ? row / a.group : row));
   merge_row(a, ml, row, p, s_hist, s_sel);
+}
+
+// The exact-match cascade (kernels.js:328-339): a = 1, next = pick[0];
+// each draft equal to the pick before it that is not a stop id accepts one
+// more pick.
+__global__ __launch_bounds__(kThreads) void spec_cascade_kernel(const uint32_t *picks, const uint32_t *drafts,
+                                                                const uint32_t *stop_ids, int seqs, int L,
+                                                                int32_t *accepted, uint32_t *next) {
+  const int s = (int)(blockIdx.x * kThreads + threadIdx.x);
+  if (s >= seqs) return;
+  const uint32_t *pk = picks + (int64_t)s * (L + 1);
+  const uint32_t *dr = drafts + (int64_t)s * L;
+  uint32_t st[4] = {SAS_STOP_PAD, SAS_STOP_PAD, SAS_STOP_PAD, SAS_STOP_PAD};
+  if (stop_ids)
+    for (int i = 0; i < 4; ++i) st[i] = stop_ids[4 * s + i];
+  int n = 1;
+  while (n <= L) {
+    const uint32_t t = pk[n - 1];
+    const bool stop = t == st[0] || t == st[1] || t == st[2] || t == st[3];
+    if (t != dr[n - 1] || stop) break;
+    ++n;
+  }
+  accepted[s] = n;
+  if (next) next[s] = pk[n - 1];
+}
+
+hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, const uint32_t *stop_ids, int seqs,
+                               int L, int32_t *accepted, uint32_t *next, hipStream_t stream) {
+  if (seqs <= 0) return hipSuccess;
+  hipLaunchKernelGGL(spec_cascade_kernel, dim3((unsigned)((seqs + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     stream, picks, drafts, stop_ids, seqs, L, accepted, next);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ parts --
@@ -839,8 +875,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
 
   // a row that already sampled a stop id (sas_sample_step) reads nothing
   if (a.st_state && a.st_state[2 * row] != 0u) return;
+  const int srow = a.group > 1 ? row / a.group : row;  // the row's sequence
   sas_params p = a.params;
-  if (a.row_params) p = load_row_params(a.row_params + row);
+  if (a.row_params) p = load_row_params(a.row_params + srow);
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
   const float softcap = kSoftcap ? p.softcap : 0.0f;
@@ -859,8 +896,8 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     } else {
       // the row's range, clamped into the ids the caller holds and to the
       // largest window
-      const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
-      const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
+      const int64_t o0 = min(max((int64_t)a.hist_offsets[srow], (int64_t)0), a.hist_count);
+      const int64_t o1 = min(max((int64_t)a.hist_offsets[srow + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
       h0 = (int)o0;
       h1 = (int)o1;
     }
@@ -888,6 +925,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   uint32_t mword = ~0u;
   auto load_pass = [&](int base) __attribute__((always_inline)) {
     const int nrem = lo + nids - base;
+    // the mask word first: the pass's id words are built from it while the
+    // logits still arrive, and the slots are then taken in load order
+    if (kMask) mword = mrow[min((base >> 5) + tid, last_word)];
 #pragma unroll
     for (int f = 0; f < kSlots; ++f) {
       const int e = base + 1024 * f + 4 * tid;
@@ -896,7 +936,6 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       const f32x4u t = __builtin_nontemporal_load(reinterpret_cast<const f32x4u *>(lrow + ec));
       v[f] = make_float4(t.x, t.y, t.z, t.w);
     }
-    if (kMask) mword = mrow[min((base >> 5) + tid, last_word)];
   };
   load_pass(lo);
 

@@ -60,6 +60,14 @@ struct SampleArgs {
   const uint32_t *seeds;
   int32_t st_max_steps;
   int32_t ring_len;
+  // Exact-match speculative rounds (sas_spec_exact): `group` consecutive
+  // rows (a sequence's verify rows) share one history range, one row of
+  // row_params and one seed; row j of a group draws with
+  // pcg(spec_seeds[seq] ^ spec_round * 0x9E3779B9 ^ j * 0x85EBCA6B).
+  // group 0 or 1: every row is its own.
+  const uint32_t *spec_seeds;
+  uint32_t spec_round;
+  int32_t group;
   int32_t vocab;
   int32_t rows;
   int32_t parts;   // blocks per row
@@ -73,6 +81,11 @@ void choose_parts(int rows, int vocab, int min_blocks, int *parts, int *span);
 // Launches the sampling kernel on `stream`.  softcap: some row may have a
 // softcap (row_params, or params.softcap > 0).
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
+
+// The exact-match cascade of sas_spec_exact, one thread per sequence:
+// picks [seqs][L + 1], drafts [seqs][L], stop ids [seqs][4] or null.
+hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, const uint32_t *stop_ids, int seqs,
+                               int L, int32_t *accepted, uint32_t *next, hipStream_t stream);
 
 // Scratch bytes of the records and part counts for a batch shape.
 size_t sample_rec_bytes(int rows, int parts);

@@ -13,7 +13,7 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import _capi
-from ._capi import SasParams, SasRows, SasVerifyRows, check, load
+from ._capi import SasParams, SasRows, SasSpecRows, SasVerifyRows, check, load
 
 
 @dataclass
@@ -271,6 +271,46 @@ class Sampler:
         d = rows_descriptor(logits, out_ids, **kw)
         st = state.descriptor()
         check(self._lib.sas_sample_step(self._h, ctypes.byref(d), ctypes.byref(st), _stream(stream)), self._h)
+
+    def spec_exact_into(self, target, draft_ids, seeds, out_picks, out_accepted, *, draft_logits=None,
+                        out_next=None, round: int = 0, vocab: Optional[int] = None, mask=None, hist_ids=None,
+                        hist_offsets=None, params: Optional[Params] = None, seq_params=None, row_hints: int = 0,
+                        stop_ids=None, stream=None) -> None:
+        """sas_spec_exact: the reference's exact-match speculative round
+        (argmax drafts when draft_logits is given, every verify row sampled
+        on its own, the cascade) on caller-provided device buffers."""
+        seqs, L = draft_ids.shape
+        if target.shape[0] != seqs * (L + 1):
+            raise ValueError("target must hold seqs * (draft_len + 1) rows")
+        if target.dtype.itemsize != 4 or target.stride(1) != 1:
+            raise ValueError("target logits must be fp32 with unit element stride")
+        d = SasSpecRows()
+        d.target_logits = target.data_ptr()
+        d.logits_stride = target.stride(0)
+        if draft_logits is not None:
+            if draft_logits.shape[0] != seqs * L or draft_logits.stride(0) != target.stride(0):
+                raise ValueError("draft_logits must hold seqs * draft_len rows of the target's stride")
+            d.draft_logits = draft_logits.data_ptr()
+        d.vocab = int(vocab if vocab is not None else target.shape[1])
+        d.seqs = seqs
+        d.draft_len = L
+        d.draft_ids = _ptr(draft_ids)
+        if mask is not None:
+            d.mask = _ptr(mask)
+            d.mask_stride = mask.stride(0)
+        d.hist_ids = _ptr(hist_ids)
+        d.hist_offsets = _ptr(hist_offsets)
+        d.hist_count = hist_ids.numel() if hist_ids is not None else 0
+        d.params = (params or Params()).to_c()
+        d.seq_params = _ptr(seq_params)
+        d.seeds = _ptr(seeds)
+        d.round = int(round) & 0xFFFFFFFF
+        d.row_hints = int(row_hints)
+        d.stop_ids = _ptr(stop_ids)
+        d.out_picks = _ptr(out_picks)
+        d.out_accepted = _ptr(out_accepted)
+        d.out_next = _ptr(out_next)
+        check(self._lib.sas_spec_exact(self._h, ctypes.byref(d), _stream(stream)), self._h)
 
     def verify_into(self, target, draft, draft_ids, uniforms, out_tokens, out_accepted, *, temperature=1.0,
                     mask=None, vocab: Optional[int] = None, stream=None) -> None:

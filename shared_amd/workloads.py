@@ -198,4 +198,34 @@ def c5(seqs: int = 32, vocab: int = QWEN_VOCAB, seed: int = 5, drafts: int = 4, 
             "temperature": 1.0, "vocab": vocab, "seqs": seqs, "drafts": L}
 
 
+def spec_case(seqs: int = 32, vocab: int = QWEN_VOCAB, seed: int = 6, drafts: int = 2, hist: int = 512,
+              greedy_every: int = 3, mask: bool = False):
+    """Exact-match speculative round inputs (the reference's mode: argmax
+    drafts, kernels.js:211-401): dict of host arrays.  The draft head's rows
+    are the target rows they predict plus noise, so drafts often equal the
+    target's argmax; every greedy_every-th sequence is greedy (its verify
+    rows then accept every draft that is the target's argmax)."""
+    rng = _rng(seed)
+    L = drafts
+    target = _normal(rng, seqs * (L + 1), vocab, 3.0)
+    tview = target.reshape(seqs, L + 1, vocab)
+    draft = np.ascontiguousarray(
+        (tview[:, :L, :] + _normal(rng, seqs * L, vocab, 0.3).reshape(seqs, L, vocab)).reshape(seqs * L, vocab),
+        dtype=np.float32)
+    sp = []
+    for s in range(seqs):
+        if greedy_every and s % greedy_every == 0:
+            sp.append(Params(temperature=0.0, presence_penalty=0.5))
+        else:
+            sp.append(Params(temperature=0.6, top_k=20, top_p=0.95, presence_penalty=1.5,
+                             repetition_penalty=1.05))
+    ids, offs = _csr([rng.integers(0, vocab, hist) for _ in range(seqs)]) if hist else (None, None)
+    m = random_mask(rng, seqs * (L + 1), vocab, 0.3, 0.9) if mask else None
+    stop = np.full((seqs, 4), 0xFFFFFFFF, np.uint32)
+    stop[:, 0] = 151645  # Qwen's <|im_end|>
+    return {"target": target, "draft": draft, "mask": m, "hist_ids": ids, "hist_offsets": offs,
+            "seq_params": sp, "seeds": rng.integers(0, 2**32, seqs, dtype=np.uint64).astype(np.uint32),
+            "round": int(rng.integers(0, 1000)), "stop_ids": stop, "vocab": vocab, "seqs": seqs, "drafts": L}
+
+
 CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C3P": c3p, "C4": c4}

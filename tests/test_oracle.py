@@ -361,3 +361,96 @@ def test_verify_output_marginal_equals_target():
                 tok = O.verify(_verify_inp(t, dl, [d], [[1.0 - 1e-12, u2], [0.5, 0.5]]))["tokens"][0, 0]
                 marg[tok] += q[d] * (1.0 - acc) / g
     assert np.abs(marg - p).max() < 4.0 / g
+
+
+# ------------------------------------------ exact-match speculative round --
+
+def _spec_inp(target, L, *, draft=None, draft_ids=None, stop=None, seeds=None, rnd=0, params=None, hist=None):
+    seqs = target.shape[0] // (L + 1)
+    inp = {"target": target, "draft": draft, "draft_ids": draft_ids, "vocab": target.shape[1], "seqs": seqs,
+           "drafts": L, "seeds": np.zeros(seqs, np.uint32) if seeds is None else np.asarray(seeds, np.uint32),
+           "round": rnd, "params": params or Params()}
+    if stop is not None:
+        st = np.full((seqs, 4), 0xFFFFFFFF, np.uint32)
+        for s, ids in enumerate(stop):
+            st[s, :len(ids)] = ids
+        inp["stop_ids"] = st
+    if hist is not None:
+        inp["hist_ids"], inp["hist_offsets"] = W._csr(hist)
+    return inp
+
+
+def test_spec_drafts_are_the_first_argmax():
+    """argmaxMerge (kernels.js:373-401): the draft is the largest value of
+    the draft row, the lowest id among equal maxima, NaNs never chosen."""
+    rng = np.random.default_rng(3)
+    L, V = 3, 700
+    draft = rng.standard_normal((L, V)).astype(np.float32)
+    draft[0, [9, 4, 600]] = 8.0           # a three-way tie: id 4
+    draft[1, 17] = np.nan
+    draft[1, 30] = 9.0
+    draft[2, :] = np.nan
+    draft[2, [650, 651]] = [-1.0, 2.0]    # only two real values
+    target = rng.standard_normal((L + 1, V)).astype(np.float32)
+    o = O.spec_exact(_spec_inp(target, L, draft=draft))
+    want = []
+    for j in range(L):
+        z = np.where(np.isnan(draft[j]), -np.inf, draft[j])
+        want.append(int(np.argmax(z)))  # numpy returns the first maximum
+    assert o["draft_ids"][0].tolist() == want == [4, 30, 651]
+
+
+def test_spec_cascade_closed_form():
+    """kernels.js:328-339: a = 1, next = pick 0; each draft equal to the
+    pick before it (and not a stop id) accepts the next pick."""
+    L, V = 3, 256
+    picks = [5, 6, 7, 8]
+    target = np.zeros(((L + 1) * 4, V), np.float32)
+    for s in range(4):
+        for j, t in enumerate(picks):
+            target[s * (L + 1) + j, t] = 50.0   # every draw takes this id
+    drafts = np.array([[5, 6, 9], [1, 6, 7], [5, 6, 7], [5, 6, 7]], np.uint32)
+    stop = [[], [], [], [6]]
+    p = Params(temperature=1.0, top_k=10, top_p=0.9)
+    o = O.spec_exact(_spec_inp(target, L, draft_ids=drafts, stop=stop, params=p, seeds=[1, 2, 3, 4], rnd=7))
+    assert o["picks"].tolist() == [picks] * 4
+    # accepted drafts 5, 6 then 9 != 7; none; all three (bonus 8); 6 is a stop id
+    assert o["accepted"].tolist() == [3, 1, 4, 2]
+    assert o["next"].tolist() == [7, 5, 8, 6]
+
+
+def test_spec_draws_use_the_row_uniform():
+    """Verify row j draws with (pcg(seed ^ round 0x9E3779B9 ^ j 0x85EBCA6B)
+    & 0xFFFFFF) / 2^24 (kernels.js:320): between two equal logits at
+    T = 1 the lower id is drawn iff U <= 1/2."""
+    def pcg(x):
+        h = (x * 747796405 + 2891336453) & 0xFFFFFFFF
+        h = (((h >> ((h >> 28) + 4)) ^ h) * 277803737) & 0xFFFFFFFF
+        return ((h >> 22) ^ h) & 0xFFFFFFFF
+
+    L, V, seqs = 2, 64, 40
+    target = np.full((seqs * (L + 1), V), -30.0, np.float32)
+    target[:, [10, 20]] = 1.0
+    seeds = (np.arange(seqs, dtype=np.uint64) * 2654435761 % (2**32)).astype(np.uint32)
+    rnd = 11
+    o = O.spec_exact(_spec_inp(target, L, draft_ids=np.zeros((seqs, L), np.uint32), seeds=seeds, rnd=rnd,
+                               params=Params(temperature=1.0, top_k=2, top_p=1.0)))
+    for s in range(seqs):
+        for j in range(L + 1):
+            x = (int(seeds[s]) ^ ((rnd * 0x9E3779B9) & 0xFFFFFFFF) ^ ((j * 0x85EBCA6B) & 0xFFFFFFFF)) & 0xFFFFFFFF
+            u = (pcg(x) & 0xFFFFFF) / 16777216.0
+            assert o["picks"][s, j] == (10 if u <= 0.5 else 20), (s, j, u)
+
+
+def test_spec_history_is_the_rounds_start_for_every_row():
+    """Every verify row is penalized by the sequence's history as it was at
+    the round's start (kernels.js:279-290): a presence penalty moves all
+    three rows off the history id alike."""
+    L, V = 2, 128
+    target = np.zeros((L + 1, V), np.float32)
+    target[:, 3] = 5.0
+    target[:, 4] = 4.5
+    p = Params(temperature=0.0, presence_penalty=1.0)
+    o = O.spec_exact(_spec_inp(target, L, draft_ids=np.array([[4, 4]], np.uint32), params=p, hist=[[3, 3, 9]]))
+    assert o["picks"].tolist() == [[4, 4, 4]]
+    assert o["accepted"].tolist() == [3]
