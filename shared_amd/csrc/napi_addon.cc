@@ -224,6 +224,35 @@ bool read_verify(napi_env env, napi_value d, sas_verify_rows *v) {
   return true;
 }
 
+bool read_spec(napi_env env, napi_value d, sas_spec_rows *r) {
+  std::memset(r, 0, sizeof *r);
+  int64_t vocab = 0, seqs = 0, L = 0, round = 0, hints = 0;
+  napi_value pv;
+  bool ok = get_ptr(env, d, "targetLogits", (void **)&r->target_logits) &&
+            get_ptr(env, d, "draftLogits", (void **)&r->draft_logits) &&
+            get_i64(env, d, "logitsStride", &r->logits_stride) && get_i64(env, d, "vocab", &vocab) &&
+            get_i64(env, d, "seqs", &seqs) && get_i64(env, d, "draftLen", &L) &&
+            get_ptr(env, d, "draftIds", (void **)&r->draft_ids) && get_ptr(env, d, "mask", (void **)&r->mask) &&
+            get_i64(env, d, "maskStride", &r->mask_stride) && get_ptr(env, d, "histIds", (void **)&r->hist_ids) &&
+            get_ptr(env, d, "histOffsets", (void **)&r->hist_offsets) &&
+            get_i64(env, d, "histCount", &r->hist_count) &&
+            get_ptr(env, d, "seqParams", (void **)&r->seq_params) && get_ptr(env, d, "seeds", (void **)&r->seeds) &&
+            get_i64(env, d, "round", &round) && get_i64(env, d, "rowHints", &hints) &&
+            get_ptr(env, d, "stopIds", (void **)&r->stop_ids) && get_ptr(env, d, "outPicks", (void **)&r->out_picks) &&
+            get_ptr(env, d, "outAccepted", (void **)&r->out_accepted) &&
+            get_ptr(env, d, "outNext", (void **)&r->out_next);
+  if (!ok || vocab < INT32_MIN || vocab > INT32_MAX || seqs < INT32_MIN || seqs > INT32_MAX || L < INT32_MIN ||
+      L > INT32_MAX || round < 0 || round > UINT32_MAX)
+    return false;
+  r->vocab = (int32_t)vocab;
+  r->seqs = (int32_t)seqs;
+  r->draft_len = (int32_t)L;
+  r->round = (uint32_t)round;
+  r->row_hints = (uint32_t)hints;
+  if (has(env, d, "params", &pv) && !read_params(env, pv, &r->params)) return false;
+  return true;
+}
+
 bool args(napi_env env, napi_callback_info info, size_t want, napi_value *argv) {
   size_t argc = want;
   if (napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr) != napi_ok) return false;
@@ -430,6 +459,19 @@ napi_value Verify(napi_env env, napi_callback_info info) {
   return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
 }
 
+napi_value SpecExact(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_spec_rows r;
+  if (!read_spec(env, argv[1], &r)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad spec descriptor");
+    return nullptr;
+  }
+  int rc = sas_spec_exact(s, &r, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
 // --------------------------------------------------------------- async --
 
 struct AsyncCall {
@@ -439,6 +481,8 @@ struct AsyncCall {
   Handle *h = nullptr;
   bool verify = false;
   bool step = false;
+  bool spec = false;
+  sas_spec_rows srows;
   sas_rows rows;
   sas_step srow;
   sas_verify_rows vrows;
@@ -457,6 +501,7 @@ void async_execute(napi_env, void *data) {
   sas_sampler *s = c->h->s;
   c->rc = c->verify ? sas_verify(s, &c->vrows, sas_stream(s))
           : c->step ? sas_sample_step(s, &c->rows, &c->srow, sas_stream(s))
+          : c->spec ? sas_spec_exact(s, &c->srows, sas_stream(s))
                     : sas_sample(s, &c->rows, sas_stream(s));
   if (c->rc == SAS_OK) c->rc = sas_synchronize(s, sas_stream(s));
   if (c->rc != SAS_OK) c->err = sas_last_error(s);
@@ -545,6 +590,22 @@ napi_value SampleStepAsync(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   return start_async(env, c, argv[0], "sas_sample_step");
+}
+
+napi_value SpecExactAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
+  AsyncCall *c = new AsyncCall();
+  c->h = h;
+  c->spec = true;
+  if (!read_spec(env, argv[1], &c->srows)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad spec descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, argv[0], "sas_spec_exact");
 }
 
 napi_value VerifyAsync(napi_env env, napi_callback_info info) {
@@ -649,6 +710,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"sampleStepAsync", nullptr, SampleStepAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verify", nullptr, Verify, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verifyAsync", nullptr, VerifyAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"specExact", nullptr, SpecExact, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"specExactAsync", nullptr, SpecExactAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"clampParams", nullptr, ClampParams, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"maskFromIds", nullptr, MaskFromIds, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"pcgUniform", nullptr, PcgUniform, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

@@ -150,6 +150,38 @@ export interface VerifyOptions {
   maskStride?: number;
 }
 
+export interface SpecExactOptions {
+  /** Verify rows [seqs * (draftLen + 1)][stride]. */
+  target: DeviceBuffer | Float32Array;
+  /** The draft head's rows [seqs * draftLen][stride] (drafts = their argmax), or draftIds. */
+  draft?: DeviceBuffer | Float32Array;
+  draftIds?: Uint32Array | number[];
+  vocab: number;
+  stride?: number;
+  seqs: number;
+  draftLen: number;
+  params?: SampleParams | SampleParams[];
+  defaults?: PackerDefaults;
+  round?: number;
+  history?: Array<number[] | Uint32Array | Set<number>>;
+  windows?: PenaltyWindow[];
+  mask?: DeviceBuffer | Uint32Array;
+  maskStride?: number;
+}
+
+/** One sequence's round (the reference's SpecRound, model.d.ts, plus the picks). */
+export interface SpecExactResult {
+  a: number;
+  next: number;
+  picks: number[];
+  drafts: number[];
+  d0?: number;
+  d1?: number;
+  stopped: boolean;
+  stopId: number | null;
+  eos: boolean;
+}
+
 export interface VerifyResult {
   tokens: Uint32Array;
   accepted: Int32Array;
@@ -179,6 +211,8 @@ export declare class Sampler {
       uniform?: number;
     }
   ): number;
+  specExact(opts: SpecExactOptions): SpecExactResult[];
+  specExactAsync(opts: SpecExactOptions): Promise<SpecExactResult[]>;
   verify(opts: VerifyOptions): VerifyResult;
   verifyAsync(opts: VerifyOptions): Promise<VerifyResult>;
 }

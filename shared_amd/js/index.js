@@ -470,24 +470,7 @@ class Sampler {
       hist = [];
       for (let r = 0; r < rows; r++) hist.push(opts.recentIds);
     }
-    if (hist) {
-      if (hist.length !== rows) throw new RangeError('history must have one list per row');
-      const hl = hist.map(toU32);
-      const offs = new Int32Array(rows + 1);
-      for (let r = 0; r < rows; r++) {
-        if (hl[r].length > addon.MAX_HISTORY) {
-          throw new RangeError('history of row ' + r + ' holds ' + hl[r].length + ' ids; at most ' +
-            addon.MAX_HISTORY + ' are supported');
-        }
-        if (offs[r] + hl[r].length > 0x7FFFFFFF) throw new RangeError('histories exceed 2^31 - 1 ids');
-        offs[r + 1] = offs[r] + hl[r].length;
-      }
-      const flat = new Uint32Array(Math.max(1, offs[rows]));
-      for (let r = 0; r < rows; r++) flat.set(hl[r], offs[r]);
-      d.histIds = this._buf('hist', flat.byteLength).upload(flat).ptr;
-      d.histCount = flat.length;
-      d.histOffsets = this._buf('histOffsets', offs.byteLength).upload(offs).ptr;
-    }
+    if (hist) this._history(d, hist, rows, 'row');
     // uniforms: host-supplied U per row, else the reference GPU sampler's
     // PCG draw from each row's seed (kernels.js:181, 320)
     let u = opts.uniforms;
@@ -506,6 +489,26 @@ class Sampler {
       d.outFlags = this._buf('flags', rows * 4).ptr;
     }
     return { desc: d, packed: packed };
+  }
+
+  // Per-row (or per-sequence) id lists as the CSR history of descriptor d.
+  _history(d, hist, rows, what) {
+    if (hist.length !== rows) throw new RangeError('history must have one list per ' + what);
+    const hl = hist.map(toU32);
+    const offs = new Int32Array(rows + 1);
+    for (let r = 0; r < rows; r++) {
+      if (hl[r].length > addon.MAX_HISTORY) {
+        throw new RangeError('history of ' + what + ' ' + r + ' holds ' + hl[r].length + ' ids; at most ' +
+          addon.MAX_HISTORY + ' are supported');
+      }
+      if (offs[r] + hl[r].length > 0x7FFFFFFF) throw new RangeError('histories exceed 2^31 - 1 ids');
+      offs[r + 1] = offs[r] + hl[r].length;
+    }
+    const flat = new Uint32Array(Math.max(1, offs[rows]));
+    for (let r = 0; r < rows; r++) flat.set(hl[r], offs[r]);
+    d.histIds = this._buf('hist', flat.byteLength).upload(flat).ptr;
+    d.histCount = flat.length;
+    d.histOffsets = this._buf('histOffsets', offs.byteLength).upload(offs).ptr;
   }
 
   _collect(opts, packed) {
@@ -765,6 +768,115 @@ class Sampler {
       const d = self._describeVerify(opts);
       return self._worker(addon.verifyAsync(self._handle(), d)).then(function () { return self._collectVerify(opts); });
     });
+  }
+
+  /**
+   * The reference's exact-match speculative round (specChain's acceptSpec,
+   * kernels.js:211-401) for opts.seqs sequences: drafts are the argmax of
+   * opts.draft (the draft head's rows [seqs*draftLen][stride]) or given in
+   * opts.draftIds; verify row j of a sequence (opts.target
+   * [seqs*(draftLen+1)][stride]) is sampled with the sequence's params
+   * (opts.params, one or one per sequence, with seed and stop ids), its
+   * history (opts.windows or opts.history, as of the round's start) and the
+   * draw of (seed, opts.round, j); a draft is accepted iff the verify row
+   * before it drew exactly it and it is not a stop id.  Returns per sequence
+   * {a, next, picks, drafts, d0, d1, stopped, stopId, eos}; each window
+   * receives the committed picks that are not stop ids (model.js:994-996).
+   */
+  specExact(opts) {
+    this._idle('specExact');
+    const r = this._describeSpec(opts);
+    addon.specExact(this._handle(), r.desc);
+    return this._collectSpec(opts, r.packed);
+  }
+
+  specExactAsync(opts) {
+    const self = this;
+    return this._enqueue(function () {
+      const r = self._describeSpec(opts);
+      return self._worker(addon.specExactAsync(self._handle(), r.desc))
+        .then(function () { return self._collectSpec(opts, r.packed); });
+    });
+  }
+
+  _describeSpec(opts) {
+    const self = this;
+    const dev = function (name, x) {
+      if (x instanceof DeviceBuffer) return x.ptr;
+      return self._buf(name, x.byteLength).upload(x).ptr;
+    };
+    const seqs = opts.seqs;
+    const L = opts.draftLen;
+    const vocab = opts.vocab;
+    const nwords = Math.ceil(vocab / 32);
+    const ps = Array.isArray(opts.params) ? opts.params : null;
+    if (ps && ps.length !== seqs) throw new RangeError('params must have one entry per sequence');
+    const packed = ps ? ps.map(function (p) { return packSamplerParams(p, opts.defaults); })
+      : [packSamplerParams(opts.params, opts.defaults)];
+    const pk = function (q) { return packed[ps ? q : 0]; };
+    const d = {
+      targetLogits: dev('sTarget', opts.target), logitsStride: orDefault(opts.stride, vocab), vocab: vocab,
+      seqs: seqs, draftLen: L, round: (orDefault(opts.round, 0)) >>> 0, params: packed[0].params,
+      outPicks: this._buf('sPicks', seqs * (L + 1) * 4).ptr, outAccepted: this._buf('sAcc', seqs * 4).ptr,
+      outNext: this._buf('sNext', seqs * 4).ptr,
+    };
+    if (opts.draft) {
+      d.draftLogits = dev('sDraft', opts.draft);
+      d.draftIds = this._buf('sIds', seqs * L * 4).ptr;
+    } else {
+      const ids = toU32(opts.draftIds);
+      if (ids.length !== seqs * L) throw new RangeError('draftIds must hold seqs * draftLen ids');
+      d.draftIds = this._buf('sIds', ids.byteLength).upload(ids).ptr;
+    }
+    if (opts.mask) {
+      d.mask = dev('sMask', opts.mask);
+      d.maskStride = opts.mask.length === nwords ? 0 : orDefault(opts.maskStride, nwords);
+    }
+    let hist = opts.history;
+    if (!hist && opts.windows) {
+      if (opts.windows.length !== seqs) throw new RangeError('windows must have one PenaltyWindow per sequence');
+      hist = opts.windows.map(function (w) { return w.recent(); });
+    }
+    if (hist) this._history(d, hist, seqs, 'sequence');
+    if (ps) {
+      const ab = new ArrayBuffer(seqs * PARAMS_BYTES);
+      const view = new DataView(ab);
+      for (let q = 0; q < seqs; q++) writeParams(view, q * PARAMS_BYTES, packed[q].params);
+      d.seqParams = this._buf('sParams', ab.byteLength).upload(new Uint8Array(ab)).ptr;
+      d.rowHints = packed.every(function (p) { return !(p.params.softcap > 0); }) ? addon.HINT_NO_SOFTCAP : 0;
+    }
+    const seeds = new Uint32Array(seqs);
+    const stops = new Uint32Array(seqs * 4);
+    for (let q = 0; q < seqs; q++) {
+      seeds[q] = pk(q).seed;
+      stops.set(pk(q).paddedStopIds, q * 4);
+    }
+    d.seeds = this._buf('sSeeds', seeds.byteLength).upload(seeds).ptr;
+    d.stopIds = this._buf('sStops', stops.byteLength).upload(stops).ptr;
+    return { desc: d, packed: packed };
+  }
+
+  _collectSpec(opts, packed) {
+    const seqs = opts.seqs;
+    const L = opts.draftLen;
+    const picks = this._scratch.sPicks.download(new Uint32Array(seqs * (L + 1)));
+    const acc = this._scratch.sAcc.download(new Int32Array(seqs));
+    const drafts = this._scratch.sIds.download(new Uint32Array(seqs * L));
+    const res = [];
+    for (let q = 0; q < seqs; q++) {
+      const pk = packed[packed.length > 1 ? q : 0];
+      const a = acc[q];
+      const pq = Array.from(picks.subarray(q * (L + 1), (q + 1) * (L + 1)));
+      const dq = Array.from(drafts.subarray(q * L, (q + 1) * L));
+      const next = pq[a - 1];
+      const stopped = pk.stopSet.has(next);
+      if (opts.windows) {
+        for (let i = 0; i < a; i++) if (!pk.stopSet.has(pq[i])) opts.windows[q].note(pq[i]);
+      }
+      res.push({ a: a, next: next, picks: pq, drafts: dq, d0: dq[0], d1: dq[1], stopped: stopped,
+        stopId: stopped ? next : null, eos: stopped && pk.eosId !== null && next === pk.eosId });
+    }
+    return res;
   }
 
   _describeVerify(opts) {

@@ -181,3 +181,44 @@ def test_node_decode_steps(tmp_path):
     assert fed[0] == first.tolist()
     for i in range(1, k):
         assert fed[i] == [int(x) for x in want[i - 1]["ids"]], i
+
+
+def test_node_spec_exact(tmp_path):
+    """specExact / specExactAsync against the oracle's exact-match round
+    (kernels.js:211-401), with the windows mirroring the commits
+    (model.js:994-996)."""
+    if shutil.which("node") is None:
+        pytest.skip("node is not installed")
+    d = str(tmp_path)
+    c = W.spec_case(seqs=10, vocab=W.QWEN_VOCAB, drafts=2, hist=40, seed=8)
+    hist = [c["hist_ids"][c["hist_offsets"][q]:c["hist_offsets"][q + 1]].tolist() for q in range(c["seqs"])]
+    js = []
+    for q, p in enumerate(c["seq_params"]):
+        stops = [int(x) for x in c["stop_ids"][q] if x != 0xFFFFFFFF]
+        js.append(dict(temperature=p.temperature, topK=p.top_k, topP=p.top_p, presencePenalty=p.presence_penalty,
+                       repetitionPenalty=p.repetition_penalty, frequencyPenalty=p.frequency_penalty, softcap=0,
+                       seed=int(c["seeds"][q]), stopIds=stops))
+    c["target"].tofile(os.path.join(d, "spec_target.f32"))
+    c["draft"].tofile(os.path.join(d, "spec_draft.f32"))
+    with open(os.path.join(d, "spec.json"), "w") as f:
+        json.dump({"vocab": c["vocab"], "seqs": c["seqs"], "drafts": c["drafts"], "round": c["round"],
+                   "params": js, "history": hist}, f)
+    print("[gpu] node spec_gpu.js", d, flush=True)
+    proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "spec_gpu.js"), d], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-3000:]
+    o = O.spec_exact(c)
+    stops = [set(int(x) for x in c["stop_ids"][q]) for q in range(c["seqs"])]
+    for name in ("js_spec.json", "js_spec_async.json"):
+        with open(os.path.join(d, name)) as f:
+            got = json.load(f)
+        for q, r in enumerate(got["results"]):
+            a = int(o["accepted"][q])
+            assert r["a"] == a and r["next"] == int(o["next"][q]), (name, q, r)
+            assert r["picks"] == o["picks"][q].tolist() and r["drafts"] == o["draft_ids"][q].tolist(), (name, q)
+            assert r["stopped"] == (r["next"] in stops[q]), (name, q)
+        if "windows" in got:
+            for q in range(c["seqs"]):
+                kept = [t for t in o["picks"][q][:int(o["accepted"][q])].tolist() if t not in stops[q]]
+                assert got["windows"][q] == hist[q] + kept, q
