@@ -7,7 +7,8 @@
 // the first failure.
 const assert = require('assert');
 const path = require('path');
-const sas = require(path.join(__dirname, '..', '..', 'shared_amd', 'js'));
+// SAS_JS_DIR: another build of the module (the sanitizer build in tests/sanitize)
+const sas = require(process.env.SAS_JS_DIR || path.join(__dirname, '..', '..', 'shared_amd', 'js'));
 
 function check(name, fn) {
   fn();
