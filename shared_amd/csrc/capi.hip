@@ -24,6 +24,8 @@ struct sas_sampler {
   size_t vscratch_cap = 0;
   void *pad = nullptr;        // rows of fewer than 4 logits, padded to 4
   size_t pad_cap = 0;
+  void *hb = nullptr;         // long histories bucketed by part
+  size_t hb_cap = 0;
   int cus = 0;                 // compute units of the device
   // The stream of the handle's last launch: a handle's calls are ordered by
   // the caller, so its scratch is idle once that stream has drained.
@@ -222,6 +224,16 @@ int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char 
     a.spec_round = sp->round;
     a.group = sp->group;
   }
+  // long histories: bucket them by part first, so a part reads its own ids
+  const int hrows = sp && sp->group > 1 ? r->rows / sp->group : r->rows;
+  const bool ring = a.ring != nullptr;
+  const int64_t hist_ids = ring ? (int64_t)hrows * a.ring_len : (r->hist_ids ? r->hist_count : 0);
+  if (hist_ids >= sas::kBucketMinIds * hrows && hist_ids > 0) {
+    const size_t ids_bytes = ((size_t)hist_ids * 4 + 255) & ~size_t(255);
+    if (int rc = grow(s, &s->hb, &s->hb_cap, ids_bytes + (size_t)hrows * (parts + 1) * 4, false)) return rc;
+    a.hb_ids = reinterpret_cast<uint32_t *>(s->hb);
+    a.hb_offs = reinterpret_cast<int32_t *>(static_cast<char *>(s->hb) + ids_bytes);
+  }
   hipError_t e = sas::launch_sample(a, any_softcap(r), pick_stream(s, stream));
   s->last_stream = pick_stream(s, stream);
   s->launched = true;
@@ -269,6 +281,7 @@ void sas_destroy(sas_sampler *s) {
   (void)hipSetDevice(s->device);
   (void)drain(s);
   if (s->recs) (void)hipFree(s->recs);
+  if (s->hb) (void)hipFree(s->hb);
   if (s->vscratch) (void)hipFree(s->vscratch);
   if (s->pad) (void)hipFree(s->pad);
   if (s->stream) (void)hipStreamDestroy(s->stream);

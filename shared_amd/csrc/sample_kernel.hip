@@ -888,7 +888,13 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const uint32_t *hid = a.hist_ids;
   int h0 = 0, h1 = 0;
   if (kHist) {
-    if (a.ring) {
+    if (a.hb_offs) {
+      // this part's own ids, bucketed by hist_bucket_kernel
+      const int32_t *bo = a.hb_offs + (int64_t)srow * (P + 1) + part;
+      hid = a.hb_ids;
+      h0 = bo[0];
+      h1 = bo[1];
+    } else if (a.ring) {
       // the row's penalty ring: its first min(count, ring_len) slots
       const uint32_t *rg = a.ring + (int64_t)row * (a.ring_len + 1);
       hid = rg + 1;
@@ -1308,6 +1314,53 @@ hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows
   return hipGetLastError();
 }
 
+// Buckets each history row's ids by part (one block per history row): a
+// counting sort over the row's parts, ids past the vocabulary dropped.  The
+// buckets take the row's own index range of hb_ids (its CSR range, or
+// ring_len slots of a ring row).
+__global__ __launch_bounds__(kThreads) void hist_bucket_kernel(const SampleArgs a) {
+  __shared__ uint32_t s_cnt[kMaxParts + 1];
+  __shared__ uint32_t s_cur[kMaxParts + 1];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int P = a.parts;
+  const uint32_t *ids;
+  int64_t o0, o1, base;
+  if (a.ring) {
+    const uint32_t *rg = a.ring + (int64_t)h * (a.ring_len + 1);
+    ids = rg + 1;
+    o0 = 0;
+    o1 = min(rg[0], (uint32_t)a.ring_len);
+    base = (int64_t)h * a.ring_len;
+  } else {
+    ids = a.hist_ids;
+    o0 = min(max((int64_t)a.hist_offsets[h], (int64_t)0), a.hist_count);
+    o1 = min(max((int64_t)a.hist_offsets[h + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
+    base = o0;
+  }
+  const uint32_t span = (uint32_t)a.span, vocab = (uint32_t)a.vocab;
+  for (int q = tid; q <= P; q += kThreads) s_cnt[q] = 0u;
+  __syncthreads();
+  for (int64_t i = o0 + tid; i < o1; i += kThreads) {
+    const uint32_t id = ids[i];
+    atomicAdd(&s_cnt[id < vocab ? id / span : (uint32_t)P], 1u);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int64_t run = base;
+    int32_t *bo = a.hb_offs + (int64_t)h * (P + 1);
+    for (int q = 0; q <= P; ++q) {
+      s_cur[q] = (uint32_t)(run - base);
+      bo[q] = (int32_t)run;
+      run += q < P ? s_cnt[q] : 0u;
+    }
+  }
+  __syncthreads();
+  for (int64_t i = o0 + tid; i < o1; i += kThreads) {
+    const uint32_t id = ids[i];
+    if (id < vocab) a.hb_ids[base + atomicAdd(&s_cur[id / span], 1u)] = id;
+  }
+}
+
 template <bool kMask, bool kHist, bool kSoftcap>
 static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
   hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap>), dim3((unsigned)(a.rows * a.parts)),
@@ -1315,6 +1368,10 @@ static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) {
+  if (a.hb_offs) {
+    const int hrows = a.group > 1 ? a.rows / a.group : a.rows;
+    hipLaunchKernelGGL(hist_bucket_kernel, dim3((unsigned)hrows), dim3(kThreads), 0, stream, a);
+  }
   switch ((a.mask ? 4 : 0) | (a.hist_ids || a.ring ? 2 : 0) | (softcap ? 1 : 0)) {
     case 0: launch_kernel<false, false, false>(a, stream); break;
     case 1: launch_kernel<false, false, true>(a, stream); break;

@@ -68,6 +68,12 @@ struct SampleArgs {
   const uint32_t *spec_seeds;
   uint32_t spec_round;
   int32_t group;
+  // Long histories bucketed by part before the parts kernel: the ids of
+  // history row h (a row, or a group's sequence) that fall in part q are
+  // hb_ids[hb_offs[h * (parts + 1) + q] .. hb_offs[h * (parts + 1) + q + 1]).
+  // Null: every part scans its row's whole history.
+  uint32_t *hb_ids;
+  int32_t *hb_offs;
   int32_t vocab;
   int32_t rows;
   int32_t parts;   // blocks per row
@@ -86,6 +92,10 @@ hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
 // picks [seqs][L + 1], drafts [seqs][L], stop ids [seqs][4] or null.
 hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, const uint32_t *stop_ids, int seqs,
                                int L, int32_t *accepted, uint32_t *next, hipStream_t stream);
+
+// Histories of at least this many ids per row on average are bucketed by
+// part first (one more launch): each part then reads its own ids only.
+constexpr int64_t kBucketMinIds = 1024;
 
 // Scratch bytes of the records and part counts for a batch shape.
 size_t sample_rec_bytes(int rows, int parts);

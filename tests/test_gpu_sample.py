@@ -214,7 +214,8 @@ def test_history_edge_ids(sampler):
     x = rng.standard_normal((rows, vocab)).astype(np.float32) * 2
     top = np.argsort(-x, axis=1)[:, :5]
     hist = [np.concatenate([top[0], top[0], [vocab + 10, 0xFFFFFFF0]]),  # duplicates + out-of-range ids
-            np.zeros(0, np.int64), np.repeat(top[2, :1], 3000)]          # empty; one id many times
+            np.zeros(0, np.int64), np.repeat(top[2, :1], 3100)]          # empty; one id many times
+    # (over 1,024 ids per row on average: the history is bucketed by part)
     hi, ho = W._csr(hist)
     b = W.Batch("hist", x, Params(temperature=1.0, top_k=10, top_p=1.0, repetition_penalty=1.3,
                                   presence_penalty=0.7, frequency_penalty=0.01),

@@ -83,7 +83,8 @@ def _params(rows):
     return [kinds[r % len(kinds)] for r in range(rows)]
 
 
-@pytest.mark.parametrize("vocab,ring_len,seeded", [(50_000, 3, True), (262_144, 512, True), (32_000, 5, False)])
+@pytest.mark.parametrize("vocab,ring_len,seeded", [(50_000, 3, True), (262_144, 512, True), (32_000, 5, False),
+                                                    (90_000, 2048, True)])  # a ring long enough to be bucketed
 def test_steps_match_oracle_loop(sampler, vocab, ring_len, seeded):
     rows, steps = 10, 7
     print(f"[gpu] sample_step vocab={vocab} ring_len={ring_len} seeded={seeded}", flush=True)
