@@ -1317,7 +1317,10 @@ hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows
 // Buckets each history row's ids by part (one block per history row): a
 // counting sort over the row's parts, ids past the vocabulary dropped.  The
 // buckets take the row's own index range of hb_ids (its CSR range, or
-// ring_len slots of a ring row).
+// ring_len slots of a ring row).  Each round holds kBucketPer ids per
+// thread, all loaded before any is counted.
+constexpr int kBucketPer = 16;
+
 __global__ __launch_bounds__(kThreads) void hist_bucket_kernel(const SampleArgs a) {
   __shared__ uint32_t s_cnt[kMaxParts + 1];
   __shared__ uint32_t s_cur[kMaxParts + 1];
@@ -1337,27 +1340,72 @@ __global__ __launch_bounds__(kThreads) void hist_bucket_kernel(const SampleArgs 
     o1 = min(max((int64_t)a.hist_offsets[h + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
     base = o0;
   }
+  // spans are multiples of 1024, in practice powers of two: a shift
   const uint32_t span = (uint32_t)a.span, vocab = (uint32_t)a.vocab;
+  const bool pow2 = (span & (span - 1u)) == 0u;
+  const uint32_t shift = (uint32_t)__builtin_ctz(span);
+  auto part_of = [&](uint32_t id) -> uint32_t {
+    return id < vocab ? (pow2 ? id >> shift : id / span) : (uint32_t)P;
+  };
+  // one round of kBucketPer ids per thread (the first round's ids stay in
+  // registers for the scatter)
+  uint32_t v[kBucketPer];
+  auto load_round = [&](int64_t r0) {
+#pragma unroll
+    for (int j = 0; j < kBucketPer; ++j) {
+      const int64_t i = r0 + (int64_t)j * kThreads + tid;
+      v[j] = i < o1 ? ids[i] : 0xFFFFFFFFu;
+    }
+  };
+  constexpr int64_t kRound = (int64_t)kBucketPer * kThreads;
   for (int q = tid; q <= P; q += kThreads) s_cnt[q] = 0u;
+  load_round(o0);
   __syncthreads();
-  for (int64_t i = o0 + tid; i < o1; i += kThreads) {
-    const uint32_t id = ids[i];
-    atomicAdd(&s_cnt[id < vocab ? id / span : (uint32_t)P], 1u);
+  for (int64_t r0 = o0; r0 < o1; r0 += kRound) {
+    if (r0 != o0) load_round(r0);
+#pragma unroll
+    for (int j = 0; j < kBucketPer; ++j)
+      if (r0 + (int64_t)j * kThreads + tid < o1) atomicAdd(&s_cnt[part_of(v[j])], 1u);
   }
   __syncthreads();
-  if (tid == 0) {
-    int64_t run = base;
+  // offsets: an exclusive scan of the counts by the first wave
+  if (tid < 64) {
+    const int lane = tid;
+    uint32_t c0 = lane < P ? s_cnt[lane] : 0u;
+    uint32_t c1 = lane + 64 < P ? s_cnt[lane + 64] : 0u;
+    uint32_t x0 = c0, x1 = c1;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y0 = __shfl_up(x0, d), y1 = __shfl_up(x1, d);
+      if (lane >= d) {
+        x0 += y0;
+        x1 += y1;
+      }
+    }
+    const uint32_t tot0 = __shfl(x0, 63);
+    x1 += tot0;
+    // exclusive: inclusive minus own count
+    const uint32_t e0 = x0 - c0, e1 = x1 - c1;
     int32_t *bo = a.hb_offs + (int64_t)h * (P + 1);
-    for (int q = 0; q <= P; ++q) {
-      s_cur[q] = (uint32_t)(run - base);
-      bo[q] = (int32_t)run;
-      run += q < P ? s_cnt[q] : 0u;
+    if (lane <= P) {
+      s_cur[lane] = e0;
+      bo[lane] = (int32_t)(base + e0);
+    }
+    if (lane + 64 <= P) {
+      s_cur[lane + 64] = e1;
+      bo[lane + 64] = (int32_t)(base + e1);
     }
   }
   __syncthreads();
-  for (int64_t i = o0 + tid; i < o1; i += kThreads) {
-    const uint32_t id = ids[i];
-    if (id < vocab) a.hb_ids[base + atomicAdd(&s_cur[id / span], 1u)] = id;
+  // v still holds the first round when there was only one
+  const bool reload = o1 - o0 > kRound;
+  for (int64_t r0 = o0; r0 < o1; r0 += kRound) {
+    if (reload) load_round(r0);
+#pragma unroll
+    for (int j = 0; j < kBucketPer; ++j) {
+      const uint32_t q = part_of(v[j]);
+      if (r0 + (int64_t)j * kThreads + tid < o1 && q < (uint32_t)P) a.hb_ids[base + atomicAdd(&s_cur[q], 1u)] = v[j];
+    }
   }
 }
 
