@@ -441,6 +441,7 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
   a.draft_ids = v->draft_ids;
   a.uniforms = v->uniforms;
   a.temperature = v->temperature;
+  a.inv_t = 1.0 / v->temperature;
   a.out_tokens = v->out_tokens;
   a.out_accepted = v->out_accepted;
   a.vocab = v->vocab;

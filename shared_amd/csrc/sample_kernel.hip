@@ -263,12 +263,6 @@ __device__ __forceinline__ void chain(const double *src, double *dst, int n, dou
   }
 }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // The first index (lanes 0..63 of `lo`, then 64..127 of `hi`) below n whose
 // condition holds, or n.
 __device__ __forceinline__ int first_true(bool c_lo, bool c_hi, int n) {

@@ -105,6 +105,36 @@ __device__ __forceinline__ double fd_exp(double x) {
   return res;
 }
 
+// e^x for sums of many weights, where the order of the additions already
+// differs from a sequential loop: within 2 ulp of the exact value, with no
+// division.  x = k ln2 + r (|r| <= ln2 / 2, ln2 split in two parts), e^r by
+// its Taylor series to degree 13 (truncation below 2^-60 relative), scaled
+// by 2^k with ldexp (subnormal results included).  x = -inf gives 0; x past
+// 709.78 overflows to +inf; NaN stays NaN.
+__device__ __forceinline__ double exp_sum(double x) {
+  const double inv_ln2 = 1.44269504088896338700e+00;
+  const double ln2_hi = 6.93147180369123816490e-01, ln2_lo = 1.90821492927058770002e-10;
+  const double xc = fmin(fmax(x, -1100.0), 1100.0);
+  const double k = rint(xc * inv_ln2);
+  const double r = fma(-k, ln2_lo, fma(-k, ln2_hi, xc));
+  double p = 1.0 / 6227020800.0;  // 1/13!
+  p = fma(p, r, 1.0 / 479001600.0);
+  p = fma(p, r, 1.0 / 39916800.0);
+  p = fma(p, r, 1.0 / 3628800.0);
+  p = fma(p, r, 1.0 / 362880.0);
+  p = fma(p, r, 1.0 / 40320.0);
+  p = fma(p, r, 1.0 / 5040.0);
+  p = fma(p, r, 1.0 / 720.0);
+  p = fma(p, r, 1.0 / 120.0);
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  const double res = __builtin_amdgcn_ldexp(p, (int)k);
+  return x == x ? res : x;
+}
+
 // tanh of an fp32 value, rounded once to fp32 from a double-precision
 // evaluation: an odd Taylor polynomial below 2^-9, (e^2x - 1)/(e^2x + 1)
 // with the fdlibm exp above, 1 from 9.5 on.  Only correctly rounded double
@@ -136,6 +166,13 @@ __device__ __forceinline__ float softcap_f32(float x, float cap) {
 // over an id-ascending candidate list (tokenizer.js:160).
 __device__ __forceinline__ bool ranks_before(double va, uint32_t ia, double vb, uint32_t ib) {
   return va > vb || (va == vb && ia < ib);
+}
+
+// LDS writes of a wave visible to the wave's other lanes.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {

@@ -117,6 +117,7 @@ struct VerifyArgs {
   const uint32_t *draft_ids; // [seqs][L]
   const double *uniforms;    // [seqs][L + 1][2]
   double temperature;
+  double inv_t;              // 1 / temperature: the weights of the sums use x * inv_t
   uint32_t *out_tokens;      // [seqs][L + 1]
   int32_t *out_accepted;     // [seqs]
   // Scratch, each written before it is read within one call:

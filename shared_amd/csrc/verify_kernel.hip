@@ -30,8 +30,12 @@
 //      U2 * total falls, scans that chunk's ids in ascending order, and
 //      writes the tokens.
 //
-// Weights are fdlibm exp (fd_exp) of double differences, as the host oracle
-// computes them; only the order of the sums differs from a sequential loop.
+// The weights that are summed (softmax normalizers, residual and target
+// masses, the draw's running sums) are exp_sum of (x - max) * (1 / T) and
+// products with reciprocals of the normalizers: within a few ulp of the
+// host oracle's fdlibm exp and divisions, a difference of the same order as
+// that of the summation order, which differs from a sequential loop anyway.
+// The acceptance test p(d) >= U1 q(d) uses fdlibm exp and divisions.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -117,42 +121,14 @@ __device__ __forceinline__ uint32_t allow_strided(const uint32_t *mrow, int64_t 
   return bits;
 }
 
+// A wave's allowed values of one side, packed, when they are few.
+constexpr int kCompact = 256;
+
 struct StatsLds {
   float m[kWaves][2];
   double z[kWaves][2];
+  float cv[kWaves][2][kCompact];
 };
-
-// Masked max and sum of exp((x - max) / T) of one chunk; thread 0's results
-// are the block's.
-__device__ __forceinline__ void chunk_stats(const float x[kPerThread], uint32_t ok, double T, int side,
-                                            StatsLds &l, double &m_out, double &z_out) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int i = 0; i < kPerThread; ++i)
-    if ((ok >> i) & 1u) m = fmaxf(m, x[i]);
-  m = wave_max(m);
-  if (lane == 0) l.m[wave][side] = m;
-  __syncthreads();
-  float bm = l.m[0][side];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) bm = fmaxf(bm, l.m[w][side]);
-  const double M = (double)bm;
-  double z = 0.0;
-#pragma unroll
-  for (int i = 0; i < kPerThread; ++i)
-    if ((ok >> i) & 1u) z += fd_exp(((double)x[i] - M) / T);
-  z = wave_sum_d(z);
-  if (lane == 0) l.z[wave][side] = z;
-  __syncthreads();
-  if (tid == 0) {
-    double t = l.z[0][side];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) t += l.z[w][side];
-    m_out = M;
-    z_out = t;
-  }
-}
 
 __device__ __forceinline__ uint32_t nan_free(const float x[kPerThread], uint32_t ok) {
 #pragma unroll
@@ -161,10 +137,44 @@ __device__ __forceinline__ uint32_t nan_free(const float x[kPerThread], uint32_t
   return ok;
 }
 
+// Sum over the wave of exp((x - M) / T) for the allowed values of one side:
+// packed into the wave's LDS slots first when at most kCompact of the
+// wave's 1,024 are allowed (a sparse mask), so that only those are
+// exponentiated; every lane's result is the wave's.
+__device__ __forceinline__ double side_sum(const float x[kPerThread], uint32_t ok, double M, double inv_t,
+                                           float *cv) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t n = (uint32_t)__popc(ok);
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t bb = __ballot((n >> bit) & 1u);
+    pre += lanes_below(bb) << bit;
+    tot += (uint32_t)__popcll(bb) << bit;
+  }
+  double z = 0.0;
+  if (tot <= (uint32_t)kCompact) {
+    uint32_t j = pre;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i)
+      if ((ok >> i) & 1u) cv[j++] = x[i];
+    wave_lds_sync();
+    for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) z += exp_sum(((double)cv[e] - M) * inv_t);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const double w = exp_sum(((double)x[i] - M) * inv_t);
+      z += ((ok >> i) & 1u) ? w : 0.0;
+    }
+  }
+  return wave_sum_d(z);
+}
+
 template <bool kMask>
 __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
   __shared__ StatsLds l;
   const int c = blockIdx.x, pos = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int P1 = a.L + 1;
   const int s = pos / P1, j = pos - s * P1;
   const int64_t base = (int64_t)c * kVChunk;
@@ -173,15 +183,48 @@ __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
   load_strided(a.target + (int64_t)pos * a.stride, base, a.vocab, a.aligned, xt);
   if (has_draft) load_strided(a.draft + ((int64_t)s * a.L + j) * a.stride, base, a.vocab, a.aligned, xq);
   const uint32_t ok = allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr, base, a.vocab);
-  double mt = 0.0, zt = 0.0, mq = dneg_inf(), zq = 0.0;
-  chunk_stats(xt, nan_free(xt, ok), a.temperature, 0, l, mt, zt);
-  if (has_draft) chunk_stats(xq, nan_free(xq, ok), a.temperature, 1, l, mq, zq);
-  if (threadIdx.x == 0) {
+  const uint32_t okt = nan_free(xt, ok), okq = has_draft ? nan_free(xq, ok) : 0u;
+  // the chunk's masked maxima of both rows
+  float mt = -__builtin_inff(), mq = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    if ((okt >> i) & 1u) mt = fmaxf(mt, xt[i]);
+    if ((okq >> i) & 1u) mq = fmaxf(mq, xq[i]);
+  }
+  mt = wave_max(mt);
+  mq = wave_max(mq);
+  if (lane == 0) {
+    l.m[wave][0] = mt;
+    l.m[wave][1] = mq;
+  }
+  __syncthreads();
+  float bt = l.m[0][0], bq = l.m[0][1];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    bt = fmaxf(bt, l.m[w][0]);
+    bq = fmaxf(bq, l.m[w][1]);
+  }
+  // sums of exp((x - max) / T)
+  const double Mt = (double)bt, Mq = (double)bq;
+  const double zt = side_sum(xt, okt, Mt, a.inv_t, l.cv[wave][0]);
+  const double zq = has_draft ? side_sum(xq, okq, Mq, a.inv_t, l.cv[wave][1]) : 0.0;
+  if (lane == 0) {
+    l.z[wave][0] = zt;
+    l.z[wave][1] = zq;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double t = l.z[0][0], q = l.z[0][1];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      t += l.z[w][0];
+      q += l.z[w][1];
+    }
     double *o = a.stats + ((int64_t)pos * a.chunks + c) * 4;
-    o[0] = mt;
-    o[1] = zt;
-    o[2] = mq;
-    o[3] = zq;
+    o[0] = Mt;
+    o[1] = t;
+    o[2] = has_draft ? Mq : dneg_inf();
+    o[3] = q;
   }
 }
 
@@ -195,6 +238,8 @@ struct DecideLds {
   double z[SAS_MAX_DRAFT + 1][2];
   int acc[SAS_MAX_DRAFT];
   double red[kWaves][2];
+  float ct[kWaves][kCompact];  // a wave's allowed target values, packed
+  float cq[kWaves][kCompact];  // and the draft values of the same ids
 };
 
 // Softmax statistics of every position of sequence s from the chunk
@@ -212,7 +257,7 @@ __device__ Decided decide(const VerifyArgs &a, int s, DecideLds &l) {
       double z = 0.0;
       for (int c = lane; c < a.chunks; c += 64) {
         const double zc = st[c * 4 + side * 2 + 1];
-        if (zc > 0.0) z += zc * fd_exp((st[c * 4 + side * 2] - m) / T);
+        if (zc > 0.0) z += zc * exp_sum((st[c * 4 + side * 2] - m) * a.inv_t);
       }
       z = wave_sum_d(z);
       if (lane == 0) {
@@ -256,16 +301,16 @@ __device__ Decided decide(const VerifyArgs &a, int s, DecideLds &l) {
 }
 
 // Residual weight max(0, p - q) and target weight exp((x - M) / T) of one
-// id whose target value is allowed and not NaN.
+// id whose target value is allowed and not NaN.  izt, izq: 1 / zt, 1 / zq.
 struct Weights {
-  double mt, zt, mq, zq, T;
+  double mt, izt, mq, izq, inv_t;
   bool resid;
   __device__ __forceinline__ void at(float xt, float xq, bool q_ok, double &wt, double &r) const {
-    wt = fd_exp(((double)xt - mt) / T);
+    wt = exp_sum(((double)xt - mt) * inv_t);
     r = 0.0;
     if (resid) {
-      const double wq = q_ok ? fd_exp(((double)xq - mq) / T) : 0.0;
-      const double d = wt / zt - wq / zq;
+      const double wq = q_ok ? exp_sum(((double)xq - mq) * inv_t) : 0.0;
+      const double d = wt * izt - wq * izq;
       r = d > 0.0 ? d : 0.0;
     }
   }
@@ -286,16 +331,44 @@ __global__ __launch_bounds__(kThreads) void verify_decide_kernel(VerifyArgs a) {
   if (resid) load_strided(a.draft + ((int64_t)s * a.L + d.a) * a.stride, base, a.vocab, a.aligned, xq);
   const uint32_t ok = nan_free(xt, allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr,
                                                          base, a.vocab));
-  const Weights w{d.mt, d.zt, d.mq, d.zq, a.temperature, resid};
+  const Weights w{d.mt, 1.0 / d.zt, d.mq, resid ? 1.0 / d.zq : 0.0, a.inv_t, resid};
   double pm = 0.0, rs = 0.0;
+  // the allowed ids' values, packed per wave when few (a sparse mask)
+  const uint32_t n = (uint32_t)__popc(ok);
+  uint32_t pre = 0u, tot = 0u;
 #pragma unroll
-  for (int i = 0; i < kPerThread; ++i)
-    if ((ok >> i) & 1u) {
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t bb = __ballot((n >> bit) & 1u);
+    pre += lanes_below(bb) << bit;
+    tot += (uint32_t)__popcll(bb) << bit;
+  }
+  if (tot <= (uint32_t)kCompact) {
+    uint32_t jj = pre;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i)
+      if ((ok >> i) & 1u) {
+        l.ct[wave][jj] = xt[i];
+        l.cq[wave][jj] = resid ? xq[i] : 0.0f;
+        ++jj;
+      }
+    wave_lds_sync();
+    for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
+      const float vq = l.cq[wave][e];
       double wt, r;
-      w.at(xt[i], resid ? xq[i] : 0.0f, resid && xq[i] == xq[i], wt, r);
+      w.at(l.ct[wave][e], vq, resid && vq == vq, wt, r);
       pm += wt;
       rs += r;
     }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i)
+      if ((ok >> i) & 1u) {
+        double wt, r;
+        w.at(xt[i], resid ? xq[i] : 0.0f, resid && xq[i] == xq[i], wt, r);
+        pm += wt;
+        rs += r;
+      }
+  }
   pm = wave_sum_d(pm);
   rs = wave_sum_d(rs);
   if (lane == 0) {
@@ -333,6 +406,11 @@ struct DrawLds {
   double target;
   uint32_t found;
   uint32_t last;
+  uint32_t wcnt[kWaves];
+  float pt[kVChunk];     // the drawing chunk's allowed ids, ascending: target value,
+  float pq[kVChunk];     // draft value,
+  uint16_t pid[kVChunk]; // offset in the chunk,
+  double pw[kVChunk];    // and weight
 };
 
 template <bool kMask>
@@ -430,7 +508,10 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
   const double target = l.target, before = l.before;
   const bool last_mode = l.last_mode != 0;
 
-  // Contiguous layout: thread t owns ids chunk*4096 + 16t .. +15.
+  // The chunk's allowed ids in ascending order, packed: thread t reads ids
+  // chunk*4096 + 16t .. +15, and entry e of the packed list goes to thread
+  // e / per (per = ceil(entries / 256)), so every thread holds a run of
+  // consecutive ids.
   const int64_t id0 = (int64_t)chunk * kVChunk + (int64_t)tid * kPerThread;
   const float *trow = a.target + (int64_t)pos * a.stride;
   const float *drow = resid ? a.draft + ((int64_t)s * L + acc) * a.stride : nullptr;
@@ -440,21 +521,55 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
     const int64_t left = a.vocab - id0;
     if (left < kPerThread) bits &= (1u << left) - 1u;
   }
-  const Weights w{q[1], q[2], q[3], q[4], a.temperature, resid};
-  double wv[kPerThread];
-  double mine = 0.0;
+  float vt[kPerThread], vq[kPerThread];
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
-    wv[i] = 0.0;
-    if ((bits >> i) & 1u) {
-      const float xt = trow[id0 + i];
-      if (xt != xt) continue;
-      const float xq = resid ? drow[id0 + i] : 0.0f;
-      double wt, r;
-      w.at(xt, xq, resid && xq == xq, wt, r);
-      wv[i] = resid ? r : wt;
-      mine += wv[i];
-    }
+    vt[i] = (bits >> i) & 1u ? trow[id0 + i] : 0.0f;
+    vq[i] = resid && ((bits >> i) & 1u) ? drow[id0 + i] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if (vt[i] != vt[i]) bits &= ~(1u << i);
+  // block-wide exclusive prefix of the per-thread counts (thread order)
+  const uint32_t n = (uint32_t)__popc(bits);
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t bb = __ballot((n >> bit) & 1u);
+    pre += lanes_below(bb) << bit;
+    tot += (uint32_t)__popcll(bb) << bit;
+  }
+  if (lane == 0) l.wcnt[wave] = tot;
+  __syncthreads();
+  uint32_t start_e = pre, total_e = 0u;
+#pragma unroll
+  for (int v = 0; v < kWaves; ++v) {
+    start_e += v < wave ? l.wcnt[v] : 0u;
+    total_e += l.wcnt[v];
+  }
+  {
+    uint32_t e = start_e;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i)
+      if ((bits >> i) & 1u) {
+        l.pt[e] = vt[i];
+        l.pq[e] = vq[i];
+        l.pid[e] = (uint16_t)(tid * kPerThread + i);
+        ++e;
+      }
+  }
+  __syncthreads();
+  const Weights w{q[1], 1.0 / q[2], q[3], resid ? 1.0 / q[4] : 0.0, a.inv_t, resid};
+  const uint32_t per = (total_e + kThreads - 1) / kThreads;
+  const uint32_t e0 = min((uint32_t)tid * per, total_e), e1 = min(e0 + per, total_e);
+  double mine = 0.0;
+  for (uint32_t e = e0; e < e1; ++e) {
+    const float xq = l.pq[e];
+    double wt, r;
+    w.at(l.pt[e], xq, resid && xq == xq, wt, r);
+    const double wv = resid ? r : wt;
+    l.pw[e] = wv;
+    mine += wv;
   }
   // exclusive prefix of the per-thread sums in thread order
   const double incl = wave_incl_scan_d(mine);
@@ -468,14 +583,16 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
   uint32_t found = SAS_NO_TOKEN, last = 0;
   bool any = false;
   double cum = start;
-#pragma unroll
-  for (int i = 0; i < kPerThread; ++i)
-    if (wv[i] > 0.0) {
+  for (uint32_t e = e0; e < e1; ++e) {
+    const double wv = l.pw[e];
+    if (wv > 0.0) {
+      const uint32_t id = (uint32_t)((int64_t)chunk * kVChunk + l.pid[e]);
       any = true;
-      last = (uint32_t)(id0 + i);
-      cum += wv[i];
-      if (found == SAS_NO_TOKEN && cum > target) found = (uint32_t)(id0 + i);
+      last = id;
+      cum += wv;
+      if (found == SAS_NO_TOKEN && cum > target) found = id;
     }
+  }
   if (!last_mode && found != SAS_NO_TOKEN) atomicMin(&l.found, found);
   if (any) atomicMax(&l.last, last + 1u);
   __syncthreads();
