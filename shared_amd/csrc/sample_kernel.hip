@@ -191,7 +191,7 @@ __device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need,
 // each wave's lane maxima, ranks the records at or above the bound exactly
 // by (value desc, id asc) and runs the reference's sample() tail.
 
-constexpr int kMR = 12;           // plain record slots per thread loaded before the counts are known
+constexpr int kMR = 16;           // plain record slots per thread loaded before the counts are known
 constexpr int kSurvCap = 512;     // survivors the merge ranks
 constexpr int kMemSlots = kListCap / 2;  // member records (16 bytes) of a part
 constexpr uint32_t kInexact = 0x80000000u;  // composite bit: the exact value lies above the key
@@ -561,10 +561,10 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
     uint32_t mine = (mkey >= lo) ? 1u : 0u;
 #pragma unroll
     for (int r = 0; r < kMR; ++r) mine += key[r] >= lo ? 1u : 0u;
-    static_assert(kMR + 1 < 16, "a lane's survivor count fits 4 bits");
+    static_assert(kMR + 1 < 32, "a lane's survivor count fits 5 bits");
     uint32_t pre = 0u, tot = 0u;
 #pragma unroll
-    for (int bit = 0; bit < 4; ++bit) {
+    for (int bit = 0; bit < 5; ++bit) {
       const uint64_t bb = __ballot((mine >> bit) & 1u);
       pre += lanes_below(bb) << bit;
       tot += (uint32_t)__popcll(bb) << bit;
