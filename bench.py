@@ -58,6 +58,8 @@ def parse_args():
     ap.add_argument("--row-params", action="store_true",
                     help="pass the workload's parameters per row (row_params, with the no-softcap hint) "
                          "instead of one sas_params for every row")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="time sas_probe_read: the parts kernel's loads alone over one C3P step's bytes")
     ap.add_argument("--calibrate-copy-mb", type=float, default=0.0,
                     help="instead of the benchmark, run device-to-device copies of this many MB (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -78,6 +80,47 @@ def calibrate_copy(mb: float, steps: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "copy", "bytes_read_per_launch": src.numel() * 4,
                       "bytes_written_per_launch": dst.numel() * 4, "launches": steps}), flush=True)
+    return 0
+
+
+def stream_probe(args) -> int:
+    """The streaming bound of the sampling kernels: sas_probe_read reads the
+    C3P step's algorithmic bytes with the parts kernel's access pattern and
+    nothing else, over rotating buffers (more bytes than the caches hold),
+    for several grid sizes.  Prints one JSON line."""
+    import ctypes
+
+    import torch
+
+    from shared_amd import Sampler
+    from shared_amd import workloads as W
+    from shared_amd._capi import check
+
+    set_bytes = W.c3p().algorithmic_bytes() // 16 * 16  # one C3P step
+    nsets = max(2, int(-(-args.min_set_mb * 1e6 // set_bytes)))
+    bufs = [torch.empty(set_bytes // 4, dtype=torch.float32, device="cuda").uniform_() for _ in range(nsets)]
+    res = {}
+    with Sampler(0) as s:
+        stream = torch.cuda.current_stream()
+        for blocks in (1024, 2048, 4096, 8192):
+            def launch(i):
+                check(s._lib.sas_probe_read(s._h, ctypes.c_void_p(bufs[i % nsets].data_ptr()), set_bytes, blocks,
+                                            ctypes.c_void_p(stream.cuda_stream)), s._h)
+            for i in range(args.warmup):
+                launch(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(args.steps):
+                launch(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / args.steps
+            res[blocks] = {"us_per_launch": us, "gbps": set_bytes / us / 1e3}
+    best = max(res.values(), key=lambda r: r["gbps"])
+    print(json.dumps({"probe": "streaming read (sas_probe_read)", "bytes_per_launch": set_bytes, "sets": nsets,
+                      "by_blocks": res, "best_us": best["us_per_launch"], "best_gbps": best["gbps"],
+                      "frac": best["gbps"] / HBM_PEAK_GBPS}), flush=True)
     return 0
 
 
@@ -246,6 +289,8 @@ def main() -> int:
         return 2
     if args.calibrate_copy_mb > 0:
         return calibrate_copy(args.calibrate_copy_mb, min(args.steps, 50))
+    if args.stream_probe:
+        return stream_probe(args)
     if args.workload == "C5":
         return bench_verify(args)
 

@@ -315,6 +315,13 @@ int sas_synchronize(sas_sampler *s, void *stream);
  * binding of their own (the N-API addon passes it to every call). */
 void *sas_stream(sas_sampler *s);
 
+/* Measurement helper, no reference counterpart: one launch that reads
+ * `bytes` (a multiple of 16, at `src`, 16-byte aligned) with the sampling
+ * kernel's access pattern and nothing else: `blocks` blocks of 256 threads,
+ * each a contiguous share, 16-byte nontemporal loads, eight per thread in
+ * flight.  Its time is the streaming bound of the sampling kernels. */
+int sas_probe_read(sas_sampler *s, const void *src, size_t bytes, int32_t blocks, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -151,6 +151,7 @@ SIGNATURES = {
     "sas_memcpy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_void_p]),
     "sas_synchronize": (c_int, [c_void_p, c_void_p]),
     "sas_stream": (c_void_p, [c_void_p]),
+    "sas_probe_read": (c_int, [c_void_p, c_void_p, c_size_t, c_int32, c_void_p]),
 }
 
 _lib = None

@@ -559,4 +559,18 @@ int sas_synchronize(sas_sampler *s, void *stream) {
 
 void *sas_stream(sas_sampler *s) { return s ? reinterpret_cast<void *>(s->stream) : nullptr; }
 
+int sas_probe_read(sas_sampler *s, const void *src, size_t bytes, int32_t blocks, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_probe_read: handle is NULL");
+  if (!src || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16 || blocks < 1)
+    return fail(s, SAS_ERR_INVALID, "sas_probe_read: src must be 16-byte aligned, bytes a multiple of 16, blocks >= 1");
+  if (int rc = set_device(s)) return rc;
+  // the sink: the pad scratch (never read)
+  if (int rc = grow(s, &s->pad, &s->pad_cap, 1024, false)) return rc;
+  hipError_t e = sas::launch_probe_read(src, (int64_t)(bytes / 16), blocks, reinterpret_cast<float *>(s->pad),
+                                        pick_stream(s, stream));
+  s->last_stream = pick_stream(s, stream);
+  s->launched = true;
+  return e == hipSuccess ? SAS_OK : hip_fail(s, e, "sas_probe_read launch");
+}
+
 }  // extern "C"
