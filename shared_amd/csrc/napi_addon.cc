@@ -640,6 +640,74 @@ napi_value ClampParams(napi_env env, napi_callback_info info) {
 }
 
 // maskFromIds(kind, Uint32Array ids, vocab) -> {words: Uint32Array, allowed: number}
+// A content key of a Uint32Array (id list or mask words): FNV-1a style
+// 64-bit hashes of its 32-bit values in four interleaved chains, folded
+// with its length, as 16 hex digits.
+// Equal contents give equal keys; the mask cache confirms a hit by
+// comparing the contents.
+napi_value IdsKey(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!args(env, info, 1, argv)) return throw_napi(env, "arguments");
+  bool is_ta = false;
+  napi_is_typedarray(env, argv[0], &is_ta);
+  napi_typedarray_type type = napi_int8_array;
+  size_t count = 0, off = 0;
+  void *data = nullptr;
+  napi_value ab;
+  if (is_ta) napi_get_typedarray_info(env, argv[0], &type, &count, &data, &ab, &off);
+  if (!is_ta || type != napi_uint32_array) {
+    napi_throw_type_error(env, nullptr, "sas_napi: expected a Uint32Array");
+    return nullptr;
+  }
+  const uint32_t *v = static_cast<const uint32_t *>(data);
+  // four independent chains (the multiplies overlap), folded at the end
+  uint64_t c[4] = {0xcbf29ce484222325ull, 0x84222325cbf29ce4ull, 0x9e3779b97f4a7c15ull, 0xbf58476d1ce4e5b9ull};
+  size_t i = 0;
+  for (; i + 4 <= count; i += 4)
+    for (int k = 0; k < 4; ++k) c[k] = (c[k] ^ v[i + k]) * 0x100000001b3ull;
+  for (; i < count; ++i) c[0] = (c[0] ^ v[i]) * 0x100000001b3ull;
+  uint64_t h = (uint64_t)count * 0x9e3779b97f4a7c15ull;
+  for (int k = 0; k < 4; ++k) {
+    h ^= c[k] ^ (c[k] >> 29);
+    h *= 0x100000001b3ull;
+  }
+  char buf[17];
+  static const char hex[] = "0123456789abcdef";
+  for (int i = 15; i >= 0; --i) {
+    buf[i] = hex[h & 0xF];
+    h >>= 4;
+  }
+  buf[16] = 0;
+  napi_value out;
+  napi_create_string_utf8(env, buf, 16, &out);
+  return out;
+}
+
+// Whether two Uint32Arrays hold the same values.
+napi_value U32Equal(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
+  const uint32_t *p[2] = {nullptr, nullptr};
+  size_t n[2] = {0, 0};
+  for (int k = 0; k < 2; ++k) {
+    bool is_ta = false;
+    napi_is_typedarray(env, argv[k], &is_ta);
+    napi_typedarray_type type = napi_int8_array;
+    size_t off = 0;
+    void *data = nullptr;
+    napi_value ab;
+    if (is_ta) napi_get_typedarray_info(env, argv[k], &type, &n[k], &data, &ab, &off);
+    if (!is_ta || type != napi_uint32_array) {
+      napi_throw_type_error(env, nullptr, "sas_napi: expected two Uint32Arrays");
+      return nullptr;
+    }
+    p[k] = static_cast<const uint32_t *>(data);
+  }
+  napi_value out;
+  napi_get_boolean(env, n[0] == n[1] && (n[0] == 0 || std::memcmp(p[0], p[1], n[0] * 4) == 0), &out);
+  return out;
+}
+
 napi_value MaskFromIds(napi_env env, napi_callback_info info) {
   napi_value argv[3];
   if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
@@ -714,6 +782,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"specExactAsync", nullptr, SpecExactAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"clampParams", nullptr, ClampParams, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"maskFromIds", nullptr, MaskFromIds, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"idsKey", nullptr, IdsKey, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"u32Equal", nullptr, U32Equal, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"pcgUniform", nullptr, PcgUniform, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof fns / sizeof fns[0], fns);

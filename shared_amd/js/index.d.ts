@@ -6,7 +6,35 @@
 export type TokenMask =
   | { kind: "all" }
   | { kind: "allow"; tokenIds: Uint32Array }
-  | { kind: "deny"; tokenIds: Uint32Array };
+  | { kind: "deny"; tokenIds: Uint32Array }
+  /** This build's extension: packed words (ceil(vocab / 32), bit id & 31 of word id >> 5 = allowed). */
+  | { kind: "words"; words: Uint32Array };
+
+/** Packed-bitmask producer for grammar code; results are immutable words arrays. */
+export declare class MaskBuilder {
+  constructor(vocab: number, cacheSize?: number);
+  readonly vocab: number;
+  readonly nwords: number;
+  hits: number;
+  misses: number;
+  all(): Uint32Array;
+  none(): Uint32Array;
+  allow(ids: Uint32Array | number[] | Set<number>): Uint32Array;
+  deny(ids: Uint32Array | number[] | Set<number>): Uint32Array;
+  fromTokenMask(mask: TokenMask): Uint32Array;
+  or(a: Uint32Array, b: Uint32Array): Uint32Array;
+  and(a: Uint32Array, b: Uint32Array): Uint32Array;
+  andNot(a: Uint32Array, b: Uint32Array): Uint32Array;
+  count(words: Uint32Array): number;
+}
+
+/** A ToolConstraint's TokenMask (tool-constraint.ts:653-661) as packed words. */
+export declare function packedToolMask(
+  constraint: { mask(raw: string, parseArguments: unknown): TokenMask },
+  raw: string,
+  parseArguments: unknown,
+  builder: MaskBuilder
+): { kind: "words"; words: Uint32Array };
 
 export interface SampleParams {
   temperature?: number;

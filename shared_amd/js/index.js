@@ -31,37 +31,170 @@ const KIND_CODE = { all: addon.MASK_ALL, allow: addon.MASK_ALLOW, deny: addon.MA
 
 function orDefault(v, d) { return v === undefined || v === null ? d : v; }
 
+function popcount32(x) {
+  x = x - ((x >>> 1) & 0x55555555);
+  x = (x & 0x33333333) + ((x >>> 2) & 0x33333333);
+  return (((x + (x >>> 4)) & 0x0F0F0F0F) * 0x01010101) >>> 24;
+}
+
+function sameWords(a, b) {
+  return !!a && !!b && (a === b || addon.u32Equal(a, b));
+}
+
 /**
  * Apply an immutable TokenMask to a mask state, as the reference does: the
  * same checks and messages (token-mask-state.js:9-20), and nothing is
  * re-uploaded for the same kind and the same Uint32Array object (:21).
  * A changed mask is packed into bitmask words on the host and handed to
- * state.upload(words).  Kind 'all' needs no words: rows sample unmasked.
+ * state.upload(words), unless the words equal the ones last uploaded (a
+ * grammar state rebuilt as a new but equal list).  Kind 'all' needs no
+ * words: rows sample unmasked.  Beyond the reference's kinds, a producer
+ * that already has packed words passes {kind: 'words', words} (ceil(vocab /
+ * 32) words, bit id & 31 of word id >> 5 = allowed): no id list is built
+ * or converted.
  */
 function updateTokenMaskState(state, mask) {
   const kind = orDefault(mask ? mask.kind : undefined, 'all');
-  if (kind !== 'all' && kind !== 'allow' && kind !== 'deny') {
+  if (kind !== 'all' && kind !== 'allow' && kind !== 'deny' && kind !== 'words') {
     throw new Error('Unknown token mask kind: ' + kind);
+  }
+  const vocab = state.cfg.text.vocab;
+  const nwords = Math.ceil(vocab / 32);
+  if (kind === 'words') {
+    const w = mask.words;
+    if (!(w instanceof Uint32Array) || w.length < nwords) {
+      throw new Error('A words token mask requires Uint32Array words of ceil(vocab / 32) entries.');
+    }
+    if (state.tokenMaskKind === 'words' && w === state.tokenMaskIds) return;
+    const words = w.length === nwords ? w : w.subarray(0, nwords);
+    let allowed = 0;
+    for (let i = 0; i < nwords; i++) allowed += popcount32(words[i]);
+    if (!sameWords(words, state.lastWords)) {
+      state.upload(words);
+      state.lastWords = Uint32Array.from(words);
+    }
+    state.allowedTokens = allowed;
+    state.allowedCount = allowed;
+    state.tokenMaskKind = kind;
+    state.tokenMaskIds = w;
+    return;
   }
   const ids = kind === 'all' ? null : (mask ? mask.tokenIds : undefined);
   if (kind !== 'all' && !(ids instanceof Uint32Array)) {
     throw new Error('A ' + kind + ' token mask requires Uint32Array tokenIds.');
   }
   const count = ids ? ids.length : 0;
-  if (count > state.cfg.text.vocab) {
+  if (count > vocab) {
     throw new Error('Tool constraint has too many token IDs.');
   }
   if (kind === state.tokenMaskKind && ids === state.tokenMaskIds) return;
   if (kind !== 'all') {
-    const packed = addon.maskFromIds(KIND_CODE[kind], ids, state.cfg.text.vocab);
-    state.upload(packed.words);
+    const packed = addon.maskFromIds(KIND_CODE[kind], ids, vocab);
+    if (!sameWords(packed.words, state.lastWords)) {
+      state.upload(packed.words);
+      state.lastWords = packed.words;
+    }
     state.allowedTokens = packed.allowed;
   } else {
-    state.allowedTokens = state.cfg.text.vocab;
+    state.allowedTokens = vocab;
+    state.lastWords = null;
   }
   state.allowedCount = count;
   state.tokenMaskKind = kind;
   state.tokenMaskIds = ids;
+}
+
+/**
+ * Packed-bitmask producer for grammar code (the host side of the mask's
+ * wire format): masks as words from the start, set algebra on words, and a
+ * content-keyed cache so that a grammar state rebuilt each step as a new but
+ * equal id list costs a hash and a compare, not a conversion.  Every result
+ * is a Uint32Array of ceil(vocab / 32) words, to be treated as immutable (a
+ * cache hit returns the same array, which updateTokenMaskState then skips
+ * by identity); wrap it as {kind: 'words', words} for updateTokenMaskState
+ * or pass it as a sampleRows mask.
+ */
+class MaskBuilder {
+  constructor(vocab, cacheSize) {
+    if (!(vocab >= 1 && vocab <= addon.MAX_VOCAB)) throw new RangeError('vocab must be in [1, MAX_VOCAB]');
+    this.vocab = vocab;
+    this.nwords = Math.ceil(vocab / 32);
+    this.cacheSize = cacheSize || 64;
+    this.cache = new Map();   // content key -> {ids copy, words}; insertion order = age
+    this.hits = 0;
+    this.misses = 0;
+    this._all = addon.maskFromIds(addon.MASK_ALL, null, vocab).words;
+  }
+  /** Every id allowed (a fresh copy). */
+  all() { return Uint32Array.from(this._all); }
+  /** No id allowed. */
+  none() { return new Uint32Array(this.nwords); }
+  /** Only `ids` (ids past the vocabulary are ignored). */
+  allow(ids) { return this._fromIds(addon.MASK_ALLOW, toU32(ids)); }
+  /** Every id but `ids`. */
+  deny(ids) { return this._fromIds(addon.MASK_DENY, toU32(ids)); }
+  /** The words of a TokenMask ({kind: 'all' | 'allow' | 'deny', tokenIds} or {kind: 'words', words}). */
+  fromTokenMask(mask) {
+    const kind = orDefault(mask ? mask.kind : undefined, 'all');
+    if (kind === 'all') return this.all();
+    if (kind === 'words') return Uint32Array.from(mask.words.subarray(0, this.nwords));
+    if (kind !== 'allow' && kind !== 'deny') throw new Error('Unknown token mask kind: ' + kind);
+    return kind === 'allow' ? this.allow(mask.tokenIds) : this.deny(mask.tokenIds);
+  }
+  or(a, b) { return this._zip(a, b, function (x, y) { return x | y; }); }
+  and(a, b) { return this._zip(a, b, function (x, y) { return x & y; }); }
+  andNot(a, b) { return this._zip(a, b, function (x, y) { return x & ~y; }); }
+  /** Number of allowed ids. */
+  count(w) {
+    let n = 0;
+    for (let i = 0; i < this.nwords; i++) n += popcount32(w[i]);
+    return n;
+  }
+  _zip(a, b, op) {
+    const out = new Uint32Array(this.nwords);
+    for (let i = 0; i < this.nwords; i++) out[i] = op(a[i], b[i]) >>> 0;
+    const tail = this.vocab & 31;
+    if (tail) out[this.nwords - 1] &= (1 << tail) - 1 >>> 0;
+    return out;
+  }
+  _fromIds(code, ids) {
+    // past a few thousand ids, hashing and comparing a list costs as much
+    // as packing it (about 1 ns per id each): pack it directly
+    if (ids.length > 4096) {
+      this.misses++;
+      return addon.maskFromIds(code, ids, this.vocab).words;
+    }
+    const key = code + ':' + addon.idsKey(ids);
+    const hit = this.cache.get(key);
+    if (hit && sameWords(hit.ids, ids)) {
+      this.cache.delete(key);
+      this.cache.set(key, hit);
+      this.hits++;
+      return hit.words;
+    }
+    this.misses++;
+    const words = addon.maskFromIds(code, ids, this.vocab).words;
+    this.cache.set(key, { ids: Uint32Array.from(ids), words: words });
+    if (this.cache.size > this.cacheSize) this.cache.delete(this.cache.keys().next().value);
+    return words;
+  }
+}
+
+/**
+ * The reference's ToolConstraint (tool-constraint.ts:653-661) as a packed
+ * mask producer: its TokenMask for `raw` as {kind: 'words', words} through
+ * `builder`; the same TokenMask object (its cached unrestricted masks) is
+ * packed once.
+ */
+function packedToolMask(constraint, raw, parseArguments, builder) {
+  const mask = constraint.mask(raw, parseArguments);
+  const memo = builder._byMask || (builder._byMask = new WeakMap());
+  let words = memo.get(mask);
+  if (!words) {
+    words = builder.fromTokenMask(mask);
+    memo.set(mask, words);
+  }
+  return { kind: 'words', words: words };
 }
 
 /**
@@ -351,6 +484,7 @@ class Sampler {
       allowedTokens: vocab,
       tokenMaskKind: 'all',
       tokenMaskIds: null,
+      lastWords: null,
       words: words,
       uploads: 0,
       upload: function (w) { words.upload(w); this.uploads++; },
@@ -915,6 +1049,8 @@ module.exports = {
   Sampler: Sampler,
   DeviceBuffer: DeviceBuffer,
   PenaltyWindow: PenaltyWindow,
+  MaskBuilder: MaskBuilder,
+  packedToolMask: packedToolMask,
   updateTokenMaskState: updateTokenMaskState,
   packSamplerParams: packSamplerParams,
   requestSamplingParams: requestSamplingParams,

@@ -36,7 +36,11 @@ check('mask uploads once per distinct immutable mask', function () {
   sas.updateTokenMaskState(state, mask);
   sas.updateTokenMaskState(state, { kind: 'deny', tokenIds: tokenIds });
   assert.strictEqual(state.uploads.length, 1);
+  // a new array with the same ids: the reference uploads it again; its words
+  // equal the ones on the device, so this build does not
   sas.updateTokenMaskState(state, { kind: 'deny', tokenIds: Uint32Array.of(1, 2, 3) });
+  assert.strictEqual(state.uploads.length, 1);
+  sas.updateTokenMaskState(state, { kind: 'deny', tokenIds: Uint32Array.of(1, 2, 4) });
   assert.strictEqual(state.uploads.length, 2);
   sas.updateTokenMaskState(state, undefined);
   assert.strictEqual(state.uploads.length, 2);      // 'all' needs no words
@@ -44,6 +48,52 @@ check('mask uploads once per distinct immutable mask', function () {
   assert.strictEqual(state.allowedCount, 0);
   // deny {1,2,3} over 32 ids: every bit but 1..3
   assert.strictEqual(state.uploads[0][0] >>> 0, (~0xE) >>> 0);
+});
+
+check('packed words masks: uploaded once per content, counted', function () {
+  const state = fakeMaskState(40);
+  const w = new Uint32Array(2);
+  w[0] = 0x0000000F; w[1] = 0x81;
+  sas.updateTokenMaskState(state, { kind: 'words', words: w });
+  assert.strictEqual(state.uploads.length, 1);
+  assert.strictEqual(state.allowedTokens, 6);
+  sas.updateTokenMaskState(state, { kind: 'words', words: w });
+  sas.updateTokenMaskState(state, { kind: 'words', words: Uint32Array.from(w) });
+  assert.strictEqual(state.uploads.length, 1);
+  sas.updateTokenMaskState(state, { kind: 'allow', tokenIds: Uint32Array.of(0, 1, 2, 3, 32, 39) });
+  assert.strictEqual(state.uploads.length, 1);      // the same words as ids
+  sas.updateTokenMaskState(state, { kind: 'allow', tokenIds: Uint32Array.of(5) });
+  assert.strictEqual(state.uploads.length, 2);
+  assert.throws(function () { sas.updateTokenMaskState(state, { kind: 'words', words: new Uint32Array(1) }); },
+    /^Error: A words token mask requires Uint32Array words of ceil\(vocab \/ 32\) entries\.$/);
+});
+
+check('MaskBuilder: words equal the brute-force masks; equal lists hit its cache', function () {
+  const V = 1000;
+  const b = new sas.MaskBuilder(V, 16);
+  const bits = function (w) { const o = []; for (let i = 0; i < V; i++) if ((w[i >> 5] >>> (i & 31)) & 1) o.push(i); return o; };
+  const ids = Uint32Array.of(3, 999, 64, 3, 1000, 500);
+  assert.deepStrictEqual(bits(b.allow(ids)), [3, 64, 500, 999]);
+  const d = bits(b.deny(ids));
+  assert.strictEqual(d.length, V - 4);
+  assert.ok(d.indexOf(3) < 0 && d.indexOf(998) >= 0);
+  assert.strictEqual(b.count(b.all()), V);
+  assert.strictEqual(b.count(b.none()), 0);
+  const u = b.or(b.allow(Uint32Array.of(1, 2)), b.allow(Uint32Array.of(2, 7)));
+  assert.deepStrictEqual(bits(u), [1, 2, 7]);
+  assert.deepStrictEqual(bits(b.and(u, b.deny(Uint32Array.of(2)))), [1, 7]);
+  assert.deepStrictEqual(bits(b.andNot(b.all(), b.deny(Uint32Array.of(9, 10)))), [9, 10]);
+  const hits = b.hits;
+  b.allow(Uint32Array.of(3, 999, 64, 3, 1000, 500));   // a new array, the same ids
+  assert.strictEqual(b.hits, hits + 1);
+  assert.deepStrictEqual(bits(b.fromTokenMask({ kind: 'deny', tokenIds: Uint32Array.of(0) })).length, V - 1);
+  // packedToolMask: a ToolConstraint-like producer's TokenMask, packed once per object
+  const cached = { kind: 'deny', tokenIds: Uint32Array.of(5, 6) };
+  const tc = { mask: function (raw) { return raw === 'x' ? cached : { kind: 'allow', tokenIds: Uint32Array.of(7) }; } };
+  const m1 = sas.packedToolMask(tc, 'x', null, b), m2 = sas.packedToolMask(tc, 'x', null, b);
+  assert.strictEqual(m1.kind, 'words');
+  assert.strictEqual(m1.words, m2.words);
+  assert.deepStrictEqual(bits(sas.packedToolMask(tc, 'y', null, b).words), [7]);
 });
 
 check('empty allow mask is kept as an empty constraint', function () {
