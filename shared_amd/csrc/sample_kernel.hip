@@ -211,6 +211,9 @@ struct MergeLds {
   double t_cum[SAS_MAX_TOP_K + 8];   // running top-p masses
   double t_r[SAS_MAX_TOP_K + 8];     // running draw residuals
   uint32_t m, clash;
+  double g_v[kWaves];                // greedy rows: each wave's best (value, id), has-any | slow bits
+  uint32_t g_id[kWaves];
+  uint32_t g_f[kWaves];
 };
 
 struct MergeOut {
@@ -532,6 +535,70 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   const uint32_t mkey = (uint32_t)sub < nm ? okey(__uint_as_float(mr.x)) : 0u;
   kmax = max(kmax, mkey);
   for_extra([&](uint32_t kx, uint64_t, double) { kmax = max(kmax, kx); });
+  if (greedy) {
+    // ---- a greedy row's token is its best record by (value desc, id asc)
+    // (the exact doubles: members by their penalized value), the first
+    // candidate sample() would rank (tokenizer.js:162); one barrier ----
+    bool have = false;
+    double bv = 0.0;
+    uint32_t bid = 0u;
+    auto offer = [&](double v, uint32_t id) __attribute__((always_inline)) {
+      if (!have || ranks_before(v, id, bv, bid)) {
+        have = true;
+        bv = v;
+        bid = id;
+      }
+    };
+#pragma unroll
+    for (int r = 0; r < kMR; ++r)
+      if (key[r] != 0u) offer((double)fkey(key[r]), rid[r]);
+    if (mkey != 0u) offer(member_value(mr), mr.y);
+    for_extra([&](uint32_t, uint64_t c, double v) { offer(v, comp_id(c)); });
+    wave_best(have, bv, bid);
+    const bool wslow = __ballot(pslow) != 0ull;
+    if (lane == 0) {
+      ml.g_v[wave] = bv;
+      ml.g_id[wave] = bid;
+      ml.g_f[wave] = (have ? 1u : 0u) | (wslow ? 2u : 0u);
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    bool h = false, sl = false;
+    double v = 0.0;
+    uint32_t id = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const uint32_t f = ml.g_f[w];
+      sl = sl || (f & 2u) != 0u;
+      if ((f & 1u) && (!h || ranks_before(ml.g_v[w], ml.g_id[w], v, id))) {
+        h = true;
+        v = ml.g_v[w];
+        id = ml.g_id[w];
+      }
+    }
+    const uint32_t tok = h ? id : SAS_NO_TOKEN;
+    // the outputs of sample()'s greedy return: no draw, so no candidates
+    if (lane == 0) {
+      a.out_ids[row] = tok;
+      if (a.out_counts) {
+        a.out_counts[2 * row] = 0;
+        a.out_counts[2 * row + 1] = 0;
+      }
+      if (a.out_flags) a.out_flags[row] = (sl ? SAS_FLAG_SLOW_SELECT : 0u) | (h ? 0u : SAS_FLAG_EMPTY_ROW);
+      if (a.st_state) step_feedback(a, row, tok, false);
+    }
+    if (a.out_probs) {
+      double *op = a.out_probs + (int64_t)row * SAS_MAX_TOP_K;
+      op[lane] = 0.0;
+      op[lane + 64] = 0.0;
+    }
+    if (a.out_cand_ids) {
+      uint32_t *oc = a.out_cand_ids + (int64_t)row * SAS_MAX_TOP_K;
+      oc[lane] = SAS_NO_TOKEN;
+      oc[lane + 64] = SAS_NO_TOKEN;
+    }
+    return;
+  }
   // ---- the bound: at least jw lanes of every wave hold a key at or above
   // the wave's result, so k keys reach the smallest; and every part's bound
   // certifies k values of its own ----
