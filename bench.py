@@ -40,6 +40,10 @@ WORKLOAD_DOC = {
           "batch 256",
     "C5": "speculative verify (rejection sampling): 32 sequences x (4 drafts + 1 bonus), vocab 151936, draft "
           "logits 0.8-correlated with the target, 5% mask on both",
+    "LMH1": "the LM head with the sampling step fused (sas_lm_head_sample): one decode row, hidden 2560 fp32 times "
+            "a 262144 x 2560 bf16 head (Gemma-4 E4B shape), softcap 30, then C3P's mask, penalties and "
+            "top-k 50 / top-p 0.9",
+    "LMH3": "as LMH1 with the three rows of a speculative verify round over the same head",
 }
 CPU_THREADS = 16  # the GPU box's CPU share for one GPU (its nproc may show more)
 
@@ -280,6 +284,66 @@ def bench_verify(args) -> int:
     return 0
 
 
+def bench_lm_head(args) -> int:
+    """LMH1 / LMH3: sas_lm_head_sample steps (three launches: the head with
+    the parts pass, the part groups, the merge).  The 1.34 GB head exceeds
+    the Infinity Cache, so one input set is read from HBM every step."""
+    import numpy as np
+    import torch
+
+    from shared_amd import Sampler
+    from shared_amd import workloads as W
+
+    rows = int(args.workload[3:])
+    b = W.lmh(rows=rows)
+    set_bytes = b.algorithmic_bytes()
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device is visible", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+
+    def dev(a, view=None):
+        if a is None:
+            return None
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        return (t.view(view) if view is not None else t).cuda()
+
+    hidden, weight = dev(b.hidden), dev(b.weight_bits.view(np.int16))
+    kw = dict(mask=dev(b.mask, torch.int32), hist_ids=dev(b.hist_ids, torch.int32),
+              hist_offsets=dev(b.hist_offsets), uniforms=dev(b.uniforms), params=b.params)
+    out_ids = torch.empty(rows, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    with Sampler(0) as s:
+        for _ in range(args.warmup):
+            s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, **kw)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, **kw)
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms_total = start.elapsed_time(end)
+    ms_step = ms_total / args.steps
+    achieved = set_bytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": rows * args.steps / (ms_total / 1e3), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32 (bf16 head widened to f32)", "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {WORKLOAD_DOC[args.workload]}", "rows": rows,
+                   "vocab": b.vocab, "dim": b.dim, "top_k": b.params.top_k, "top_p": b.params.top_p,
+                   "temperature": b.params.temperature, "softcap": b.params.softcap},
+        "gbps": achieved,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles(args.workload, "lm_head"),
+                     "kernel": "sas::lmh_parts_kernel + lmh_group_kernel + sample_merge_kernel (one step)",
+                     "algorithmic_bytes_per_launch": set_bytes},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -293,6 +357,8 @@ def main() -> int:
         return stream_probe(args)
     if args.workload == "C5":
         return bench_verify(args)
+    if args.workload.startswith("LMH"):
+        return bench_lm_head(args)
 
     import numpy as np
 

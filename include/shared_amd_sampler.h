@@ -284,6 +284,44 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
  * stream-ordered like sas_sample. */
 int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream);
 
+/* ---- the LM head with the sampling step fused into its epilogue ----
+ *
+ * Replaces the decode head's final projection and the topk pass that reads
+ * its logits: lib/webgpu-llm/model.js:466-471 (Qwen: rms -> lm per
+ * embedding shard -> topk) and gemma-model.js:786-799 (Gemma: finalNorm ->
+ * lmRuns -> topk with the softcap fused), over a BF16 head as
+ * ggml/kernels.js:31-33 reads it (f32 weight = bf16 bits << 16) and
+ * gemvGGML (ggml/kernels.js:84-110) computes it (f32 products of the
+ * widened weight and the f32 activation, summed in f32).
+ *
+ * logit[row][id] = sum over k of weight[id][k] * hidden[row][k] in f32, in
+ * this order exactly (the reference's WGSL order is its driver's): eight
+ * partial sums, partial g a fused multiply-add chain from 0 over
+ * k = 64 c + 8 g + j (c ascending, then j = 0 .. 7), added as
+ * ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).  The logits
+ * are consumed on chip: no [rows][vocab] array is written unless
+ * out_logits asks for it.  Then the sas_sample semantics over them
+ * (softcap, mask, penalties, top-k / top-p, draw). */
+#define SAS_LMH_MAX_ROWS 4        /* rows per call: decode (1) and verify rounds (3) */
+#define SAS_LMH_MAX_LDS_FLOATS 12288  /* rows * dim: the hidden states staged on chip */
+#define SAS_LMH_MAX_VOCAB 262144      /* vocabularies of the fused head */
+
+typedef struct sas_lm_head {
+  const float *hidden;        /* device [rows][hidden_stride] fp32: final-normed hidden states */
+  int64_t hidden_stride;      /* >= dim */
+  const uint16_t *weight;     /* device [vocab][weight_stride] bf16 bits, 16-byte aligned */
+  int64_t weight_stride;      /* >= dim, a multiple of 8 */
+  int32_t dim;                /* a multiple of 256; rows * dim <= SAS_LMH_MAX_LDS_FLOATS */
+  float *out_logits;          /* device [rows][vocab] or NULL: also write the logits */
+} sas_lm_head;
+
+/* Samples rows->rows rows (<= SAS_LMH_MAX_ROWS, vocab <= SAS_LMH_MAX_VOCAB)
+ * from the logits of `head`:
+ * rows->logits must be NULL and rows->logits_stride is ignored; every
+ * other field of `rows` means what it means for sas_sample.
+ * Stream-ordered; no host synchronisation. */
+int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *head, const sas_rows *rows, void *stream);
+
 /* Host: clamp parameters with the reference packer's rules
  * (model.js:418-423): non-finite or negative temperature -> 0 (greedy),
  * top_p -> [0, 1] (non-finite -> 1), presence -> [0, 10] (non-finite -> 0),

@@ -72,8 +72,23 @@ def lib() -> ctypes.CDLL:
         L.orc_spec_exact.argtypes = [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                      c_int64, c_void_p, c_void_p, POINTER(OrcParams), c_void_p, c_void_p, c_uint32,
                                      c_void_p, c_void_p, c_void_p, c_void_p]
+        L.orc_lm_head_logits.restype = None
+        L.orc_lm_head_logits.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p]
         _lib = L
     return _lib
+
+
+def lm_head_logits(hidden, weight_bits, dim: int | None = None) -> np.ndarray:
+    """The LM head's f32 logits in the order sas_lm_head_sample sums them
+    (hidden [rows][>= dim] f32, weight_bits [vocab][>= dim] uint16 bf16)."""
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+    weight_bits = np.ascontiguousarray(weight_bits, dtype=np.uint16)
+    rows, vocab = hidden.shape[0], weight_bits.shape[0]
+    dim = int(dim if dim is not None else hidden.shape[1])
+    out = np.empty((rows, vocab), dtype=np.float32)
+    lib().orc_lm_head_logits(hidden.ctypes.data, hidden.shape[1], weight_bits.ctypes.data, weight_bits.shape[1],
+                             dim, rows, vocab, out.ctypes.data)
+    return out
 
 
 def params(p) -> OrcParams:

@@ -543,3 +543,36 @@ void orc_spec_exact(const float *target, const float *draft, int64_t stride,
     if (out_next) out_next[s] = pk[a - 1];
   }
 }
+
+/* ---- the LM head (sas_lm_head_sample) ----------------------------------
+ * The reference's BF16 head (lib/webgpu-llm/ggml/kernels.js:31-33 widens
+ * the weight as bits << 16; gemvGGML, ggml/kernels.js:84-110, sums f32
+ * products) in the build's fixed order: eight partial fmaf chains over
+ * interleaved slices of k, then a fixed pairwise tree.  fmaf is the
+ * correctly rounded fused multiply-add, the GPU's v_fma_f32. */
+void orc_lm_head_logits(const float *hidden, int64_t hidden_stride, const uint16_t *weight,
+                        int64_t weight_stride, int32_t dim, int32_t rows, int32_t vocab,
+                        float *logits) {
+  for (int32_t r = 0; r < rows; ++r) {
+    const float *h = hidden + (int64_t)r * hidden_stride;
+    for (int32_t id = 0; id < vocab; ++id) {
+      const uint16_t *w = weight + (int64_t)id * weight_stride;
+      float p[8];
+      for (int g = 0; g < 8; ++g) {
+        float acc = 0.0f;
+        for (int32_t c = 0; 64 * c + 8 * g < dim; ++c) {
+          for (int j = 0; j < 8; ++j) {
+            const int32_t k = 64 * c + 8 * g + j;
+            if (k >= dim) break;
+            const uint32_t bits = (uint32_t)w[k] << 16;
+            float wf;
+            memcpy(&wf, &bits, sizeof wf);
+            acc = fmaf(wf, h[k], acc);
+          }
+        }
+        p[g] = acc;
+      }
+      logits[(int64_t)r * vocab + id] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+  }
+}

@@ -97,4 +97,14 @@ void orc_spec_exact(const float *target, const float *draft, int64_t stride,
                     uint32_t *out_picks, int32_t *out_accepted,
                     uint32_t *out_next);
 
+/* The LM head's logits (sas_lm_head_sample): the bf16 weight widened to
+ * f32 (bits << 16) times the f32 hidden value, summed as eight partials,
+ * partial g a fused multiply-add chain from 0 over k = 64 c + 8 g + j
+ * (c ascending, then j = 0 .. 7, k < dim), then
+ * ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).  weight:
+ * [vocab][weight_stride] bf16 bits; hidden: [rows][hidden_stride]. */
+void orc_lm_head_logits(const float *hidden, int64_t hidden_stride, const uint16_t *weight,
+                        int64_t weight_stride, int32_t dim, int32_t rows, int32_t vocab,
+                        float *logits);
+
 #endif

@@ -31,6 +31,9 @@ MAX_VOCAB = _header_define("SAS_MAX_VOCAB")
 MAX_HISTORY = _header_define("SAS_MAX_HISTORY")
 MAX_DRAFT = _header_define("SAS_MAX_DRAFT")
 NOALLOC_SCRATCH_BYTES = _header_define("SAS_NOALLOC_SCRATCH_BYTES")
+LMH_MAX_ROWS = _header_define("SAS_LMH_MAX_ROWS")
+LMH_MAX_LDS_FLOATS = _header_define("SAS_LMH_MAX_LDS_FLOATS")
+LMH_MAX_VOCAB = _header_define("SAS_LMH_MAX_VOCAB")
 NO_TOKEN = 0xFFFFFFFF
 STOP_PAD = 0xFFFFFFFF
 OK, ERR_INVALID, ERR_HIP, ERR_NOMEM = 0, 1, 2, 3
@@ -131,6 +134,17 @@ class SasSpecRows(ctypes.Structure):
     ]
 
 
+class SasLmHead(ctypes.Structure):
+    _fields_ = [
+        ("hidden", c_void_p),
+        ("hidden_stride", c_int64),
+        ("weight", c_void_p),
+        ("weight_stride", c_int64),
+        ("dim", c_int32),
+        ("out_logits", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); every function declared in the header.
 SIGNATURES = {
     "sas_version": (c_char_p, []),
@@ -143,6 +157,7 @@ SIGNATURES = {
     "sas_sample_step": (c_int, [c_void_p, POINTER(SasRows), POINTER(SasStep), c_void_p]),
     "sas_verify": (c_int, [c_void_p, POINTER(SasVerifyRows), c_void_p]),
     "sas_spec_exact": (c_int, [c_void_p, POINTER(SasSpecRows), c_void_p]),
+    "sas_lm_head_sample": (c_int, [c_void_p, POINTER(SasLmHead), POINTER(SasRows), c_void_p]),
     "sas_clamp_params": (c_int, [POINTER(SasParams), POINTER(SasParams)]),
     "sas_mask_from_ids": (c_int64, [c_int32, POINTER(c_uint32), c_size_t, c_int32, POINTER(c_uint32), c_int64]),
     "sas_pcg_uniform": (c_double, [c_uint32, c_uint32, c_uint32]),

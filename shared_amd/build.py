@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libshared_amd_sampler.so")
 NAPI = os.path.join(PKG, "js", "sas_napi.node")
-HIP_SOURCES = ["capi.hip", "sample_kernel.hip", "verify_kernel.hip"]
+HIP_SOURCES = ["capi.hip", "sample_kernel.hip", "verify_kernel.hip", "lmhead_kernel.hip"]
 
 # -ffp-contract=off: the double-precision tail must round like a JS engine.
 # -packed-fp32-ops: packed FP32 instructions are kept out of the code.

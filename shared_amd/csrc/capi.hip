@@ -354,6 +354,47 @@ int sas_sample_noalloc(int device, const sas_rows *r, void *stream) {
   return SAS_OK;
 }
 
+int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, void *stream) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_lm_head_sample: handle is NULL");
+  if (!h || !r) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: head and rows are required");
+  if (r->logits) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: rows->logits must be NULL (the head computes them)");
+  // the sampling fields are checked as for sas_sample
+  sas_rows chk = *r;
+  chk.logits = reinterpret_cast<const float *>(h->hidden ? static_cast<const void *>(h->hidden) : "");
+  chk.logits_stride = r->vocab;
+  if (const char *m = check_rows(&chk)) return fail(s, SAS_ERR_INVALID, std::string("sas_lm_head_sample: ") + m);
+  if (r->rows > SAS_LMH_MAX_ROWS) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: rows must be <= SAS_LMH_MAX_ROWS");
+  if (r->vocab > SAS_LMH_MAX_VOCAB) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: vocab must be <= SAS_LMH_MAX_VOCAB");
+  if (r->rows == 0) return SAS_OK;
+  if (!h->hidden || !h->weight) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden and weight are required");
+  if (h->dim < 256 || h->dim % 256 != 0) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: dim must be a positive multiple of 256");
+  if ((int64_t)r->rows * h->dim > SAS_LMH_MAX_LDS_FLOATS)
+    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: rows * dim must be <= SAS_LMH_MAX_LDS_FLOATS");
+  if (h->hidden_stride < h->dim) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden_stride < dim");
+  if (h->weight_stride < h->dim || h->weight_stride % 8 != 0)
+    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: weight_stride must be >= dim and a multiple of 8");
+  if (reinterpret_cast<uintptr_t>(h->weight) % 16 != 0)
+    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: weight must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(h->hidden) % 4 != 0)
+    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden must be 4-byte aligned");
+  if (int rc = set_device(s)) return rc;
+  if (int rc = grow(s, &s->recs, &s->recs_cap, sas::lmh_scratch_bytes(r->rows, r->vocab), false)) return rc;
+  sas::LmhArgs a{};
+  fill_args(r, nullptr, 0, 1, sas::kLmhSpan, s->recs, &a.s);
+  sas::lmh_layout(&a, s->recs);
+  a.hidden = h->hidden;
+  a.hidden_stride = h->hidden_stride;
+  a.weight = h->weight;
+  a.weight_stride = h->weight_stride;
+  a.dim = h->dim;
+  a.out_logits = h->out_logits;
+  hipError_t e = sas::launch_lm_head_sample(a, any_softcap(r), pick_stream(s, stream));
+  s->last_stream = pick_stream(s, stream);
+  s->launched = true;
+  if (e != hipSuccess) return hip_fail(s, e, "sas_lm_head_sample launch");
+  return SAS_OK;
+}
+
 int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream) {
   if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_spec_exact: handle is NULL");
   if (!r) return fail(s, SAS_ERR_INVALID, "sas_spec_exact: descriptor is NULL");

@@ -1,0 +1,566 @@
+// lmhead_kernel.hip - the LM head with the sampling step's parts pass fused
+// into its epilogue (gfx950).
+//
+// The decode head of the reference is a projection of the final-normed
+// hidden state onto every vocabulary row, then a topk pass that reads the
+// logits back (lib/webgpu-llm/model.js:466-471, gemma-model.js:786-799).
+// Here the logits never leave the chip: the block that computes a part's
+// logits also masks, penalizes and bounds them and writes only the part's
+// candidate records, in the records format of the sampling kernels.
+//
+// lmh_parts_kernel: grid = parts (kLmhSpan ids each), 256 threads, every
+// row of the call (<= SAS_LMH_MAX_ROWS).  The rows' hidden states are staged
+// once in LDS.  Eight lanes share one id: lane g of the group sums the
+// hidden indices 64 c + 8 g .. + 7 (c ascending) as one f32 fused
+// multiply-add chain, so each load of the group is a whole 128-byte line of
+// the weight row; the eight partial sums then add in one fixed tree.  That
+// order is the one the host oracle follows.  The bf16 weight widens exactly
+// to f32 (bits << 16, ggml/kernels.js:31-33), so each product is the
+// reference's f32 product.
+// The epilogue, per row: softcap, mask, history membership, the part's
+// bound (every wave's j-th largest lane maximum, the smallest of the four:
+// 4 j >= k values reach it), the values at or above it as records, the
+// members' penalized doubles as member records, the part's info word.
+//
+// lmh_group_kernel: one block per (row, kLmhGroup consecutive parts) keeps
+// the records at or above the largest of the parts' bounds (that part alone
+// holds k values above it) and writes them as one part of the merge kernel,
+// which then draws as for sas_sample.
+#include "sas_device.h"
+#include "sas_launch.h"
+
+namespace sas {
+
+constexpr int kLmhIds = kLmhSpan / kThreads;  // ids per lane
+static_assert(kLmhIds == 2, "a lane owns two ids of its part");
+constexpr int kLmhStep = 64;                   // hidden values per load step: 128 bytes of a weight row
+constexpr int kLmhHash = 512;                  // (id, count) hash slots of a part's history members
+constexpr uint32_t kLmhEmpty = 0xFFFFFFFFu;
+constexpr uint32_t kLmhMem = 0x80000000u;      // exact-selection entry flag: a history member
+
+struct LmhLds {
+  uint32_t hkey[kLmhHash];
+  uint32_t hcnt[kLmhHash];
+  uint32_t hbits[kLmhSpan / 32];  // history membership of the part's ids
+  double x_val[kLmhSpan];         // the part's allowed members: penalized value, id
+  uint32_t x_id[kLmhSpan];
+  uint32_t thr[kWaves];           // each wave's bound key
+  uint32_t nw[kWaves];            // each wave's plain records
+  uint32_t nx, nxk, nmw, hover, slow;
+  uint32_t hist[256];             // block_select96
+  uint32_t sel[4];
+};
+
+__device__ __forceinline__ uint32_t lmh_slot(uint32_t id) { return (id * 2654435761u) >> 23; }
+static_assert(kLmhHash == 512, "lmh_slot yields 9 bits");
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// One row's part: values v[0..1] of ids id0, id0 + 1 (raw logits), the
+// row's parameters and history; writes the part's records and info word.
+__device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int row, int part, const float v_in[2],
+                                               int id0) {
+  const SampleArgs &a = L.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int vocab = a.vocab;
+  const int base = part * kLmhSpan;
+  const int nids = min(kLmhSpan, vocab - base);
+  sas_params p = a.params;
+  if (a.row_params) p = load_row_params(a.row_params + row);
+  const bool greedy = !(p.temperature > 0.0);
+  const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
+  const int jw = (k + kWaves - 1) / kWaves;
+  // ---- history: the row's ids inside the part, in a bitmap and a hash ----
+  int h0 = 0, h1 = 0;
+  if (a.hist_ids) {
+    const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
+    const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
+    h0 = (int)o0;
+    h1 = (int)o1;
+  }
+  for (int s = tid; s < kLmhHash; s += kThreads) {
+    S.hkey[s] = kLmhEmpty;
+    S.hcnt[s] = 0u;
+  }
+  if (tid < kLmhSpan / 32) S.hbits[tid] = 0u;
+  if (tid == 0) {
+    S.nx = 0u;
+    S.nxk = 0u;
+    S.nmw = 0u;
+    S.hover = 0u;
+    S.slow = 0u;
+  }
+  __syncthreads();
+  for (int i = h0 + tid; i < h1; i += kThreads) {
+    const uint32_t id = a.hist_ids[i];
+    const uint32_t off = id - (uint32_t)base;
+    if (off >= (uint32_t)nids) continue;
+    atomicOr(&S.hbits[off >> 5], 1u << (off & 31u));
+    uint32_t sl = lmh_slot(id);
+    int probe = 0;
+    for (; probe < kLmhHash; ++probe) {
+      const uint32_t old = atomicCAS(&S.hkey[sl], kLmhEmpty, id);
+      if (old == kLmhEmpty || old == id) {
+        atomicAdd(&S.hcnt[sl], 1u);
+        break;
+      }
+      sl = (sl + 1u) & (uint32_t)(kLmhHash - 1);
+    }
+    if (probe == kLmhHash) S.hover = 1u;
+  }
+  __syncthreads();
+  auto hcount = [&](uint32_t id) -> uint32_t {
+    uint32_t sl = lmh_slot(id);
+    for (int probe = 0; probe < kLmhHash; ++probe) {
+      const uint32_t kk = S.hkey[sl];
+      if (kk == id) return S.hcnt[sl];
+      if (kk == kLmhEmpty) break;
+      sl = (sl + 1u) & (uint32_t)(kLmhHash - 1);
+    }
+    uint32_t c = 0u;
+    if (S.hover)
+      for (int i = h0; i < h1; ++i) c += a.hist_ids[i] == id ? 1u : 0u;
+    return c;
+  };
+  // ---- values: softcap, mask, membership ----
+  const uint32_t *mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
+  float pv[2];      // plain candidates (NaN: none)
+  bool mem[2];      // allowed history members
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int id = id0 + j;
+    float x = v_in[j];
+    if (p.softcap > 0.0f) x = softcap_f32(x, p.softcap);
+    bool ok = id < vocab && x == x;
+    if (ok && mrow) ok = ((mrow[id >> 5] >> (id & 31)) & 1u) != 0u;
+    const uint32_t off = (uint32_t)(id - base);
+    const bool hm = ok && off < (uint32_t)nids && ((S.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u;
+    mem[j] = hm;
+    pv[j] = ok && !hm ? x : qnan();
+    if (hm) {
+      const uint32_t d = atomicAdd(&S.nx, 1u);
+      S.x_val[d] = (double)x;  // d < kLmhSpan: one entry per id of the part
+      S.x_id[d] = (uint32_t)id;
+    }
+  }
+  // ---- the bound ----
+  const float m = fmaxf(pv[0], pv[1]);
+  const uint32_t tw = wave_jth_largest_key16(okey(m), jw);
+  if (lane == 0) S.thr[wave] = tw;
+  __syncthreads();
+  const uint32_t tkey = min(min(S.thr[0], S.thr[1]), min(S.thr[2], S.thr[3]));
+  const float tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
+  // ---- plain records: each wave's after the waves before it ----
+  const bool k0 = pv[0] >= tf, k1 = pv[1] >= tf;  // NaN never passes
+  const uint32_t c = (k0 ? 1u : 0u) + (k1 ? 1u : 0u);
+  const uint64_t b0 = __ballot(c & 1u), b1 = __ballot((c >> 1) & 1u);
+  const uint32_t pre = lanes_below(b0) + 2u * lanes_below(b1);
+  if (lane == 0) S.nw[wave] = (uint32_t)__popcll(b0) + 2u * (uint32_t)__popcll(b1);
+  // members: penalized doubles kept at or above the bound
+  const uint32_t nx = S.nx;  // complete: every member was listed before the bound barrier
+  bool xw = false;
+  double xv = 0.0;
+  uint32_t xid = 0u;
+  for (int i = tid; i < (int)nx; i += kThreads) {
+    // at most kLmhSpan entries: two per thread
+    const double pvv = penalize(S.x_val[i], hcount(S.x_id[i]), p);
+    if (pvv >= (double)tf) {
+      atomicAdd(&S.nxk, 1u);
+      if (i == tid) {
+        xw = true;
+        xv = pvv;
+        xid = S.x_id[i];
+      } else {
+        S.x_val[i] = pvv;  // the second entry of this thread keeps its value in LDS
+        S.x_id[i] |= kLmhMem;
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t off = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) off += w < wave ? S.nw[w] : 0u;
+  const uint32_t nplain = S.nw[0] + S.nw[1] + S.nw[2] + S.nw[3];
+  const uint32_t nmem = S.nxk;
+  const int64_t pq = (int64_t)row * a.parts + part;
+  uint64_t *rrow = a.rec + pq * kListCap;
+  uint4 *mrow4 = a.mrec + pq * kMemSlots;
+  uint32_t np_out = nplain, nm_out = nmem;
+  if (nmem <= (uint32_t)kMemSlots) {
+    uint32_t j = off + pre;
+    if (k0) rrow[j++] = (uint64_t)__float_as_uint(pv[0]) | ((uint64_t)(uint32_t)id0 << 32);
+    if (k1) rrow[j] = (uint64_t)__float_as_uint(pv[1]) | ((uint64_t)(uint32_t)(id0 + 1) << 32);
+    auto put_member = [&](double val, uint32_t id) {
+      const uint32_t d = atomicAdd(&S.nmw, 1u);
+      uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
+      w[0] = (uint64_t)__float_as_uint(rd_f32(val)) | ((uint64_t)id << 32);
+      w[1] = (uint64_t)__double_as_longlong(val);
+    };
+    if (xw) put_member(xv, xid);
+    const int i2 = tid + kThreads;
+    if (i2 < (int)nx && (S.x_id[i2] & kLmhMem)) put_member(S.x_val[i2], S.x_id[i2] & ~kLmhMem);
+  } else {
+    // more members above the bound than a part's member slots hold: the
+    // part's exact top k over (value, id), every value computed again
+    // from the registers and the history
+    const float xr[2] = {v_in[0], v_in[1]};
+    auto for_elems = [&](auto f) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int id = id0 + j;
+        float x = xr[j];
+        if (p.softcap > 0.0f) x = softcap_f32(x, p.softcap);
+        bool ok = id < vocab && x == x;
+        if (ok && mrow) ok = ((mrow[id >> 5] >> (id & 31)) & 1u) != 0u;
+        double val = (double)x;
+        if (ok && mem[j]) val = penalize(val, hcount((uint32_t)id), p);
+        ok = ok && val == val;
+        f(key96(val, (uint32_t)id), ok, val, (uint32_t)id, mem[j]);
+      }
+    };
+    uint32_t nval = 0u;
+    for_elems([&](const Key96 &, bool ok, double, uint32_t, bool) { nval += ok ? 1u : 0u; });
+    if (tid == 0) S.sel[3] = 0u;
+    __syncthreads();
+    atomicAdd(&S.sel[3], nval);
+    __syncthreads();
+    const uint32_t need = min(S.sel[3], (uint32_t)k);
+    __syncthreads();
+    if (tid == 0) {
+      S.nx = 0u;
+      S.nmw = 0u;
+      S.slow = 1u;
+    }
+    __syncthreads();
+    if (need > 0u) {
+      const Key96 kth = block_select96(
+          [&](auto f) { for_elems([&](const Key96 &kx, bool ok, double, uint32_t, bool) { f(kx, ok); }); }, need,
+          S.hist, S.sel);
+      for_elems([&](const Key96 &kx, bool ok, double val, uint32_t id, bool member) {
+        if (ok && key_ge(kx, kth)) {
+          if (member) {
+            const uint32_t d = atomicAdd(&S.nmw, 1u);
+            uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
+            w[0] = (uint64_t)__float_as_uint(rd_f32(val)) | ((uint64_t)id << 32);
+            w[1] = (uint64_t)__double_as_longlong(val);
+          } else {
+            rrow[atomicAdd(&S.nx, 1u)] = (uint64_t)__float_as_uint((float)val) | ((uint64_t)id << 32);
+          }
+        }
+      });
+    }
+    __syncthreads();
+    np_out = S.nx;
+    nm_out = S.nmw;
+  }
+  if (tid == 0)
+    a.pinfo[(int64_t)row * pinfo_stride(a.parts) + part] =
+        (uint64_t)(np_out | (nm_out << 16) | (S.slow ? kPinfoSlow : 0u)) | ((uint64_t)tkey << 32);
+  __syncthreads();  // the LDS tables are reused by the next row
+}
+
+template <int R>
+__global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [R][dim] hidden states
+  __shared__ LmhLds S;
+  __shared__ float s_logit[R][kLmhSpan];  // the part's logits, row by row
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int part = blockIdx.x;
+  const int base = part * kLmhSpan;
+  const int dim = L.dim;
+  const int vocab = L.s.vocab;
+  // ---- the rows' hidden states into LDS ----
+  for (int r = 0; r < R; ++r) {
+    const float *h = L.hidden + (int64_t)r * L.hidden_stride;
+    for (int i = tid; i < dim; i += kThreads) xs[r * dim + i] = h[i];
+  }
+  // ---- the dot products.  Lanes work in groups of 8 on one id: lane g of
+  // the group takes hidden indices 64 c + 8 g .. + 7 (c = 0, 1, ...), so a
+  // group reads whole 128-byte lines of the weight row and a wave eight of
+  // them per load.  Group grp (32 per block) takes ids base + grp + 32 m,
+  // m = 0 .. 15: at each m the block reads 32 consecutive rows. ----
+  const int g = lane & 7;
+  const int grp = (wave << 3) | (lane >> 3);
+  const int C = dim / kLmhStep;              // 128-byte steps per weight row
+  constexpr int kQ = 4;                       // steps per batch of loads
+  const int nb = C / kQ;                      // batches per id (dim is a multiple of 256)
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  auto wrow = [&](int m) __attribute__((always_inline)) {
+    const int id = min(base + grp + 32 * m, vocab - 1);  // loads stay inside the head
+    return L.weight + (int64_t)id * L.weight_stride + 8 * g;
+  };
+  u32x4 nxt[kQ];
+  auto load_batch = [&](int m, int cb) __attribute__((always_inline)) {
+    const uint16_t *w = wrow(m) + (int64_t)cb * kQ * kLmhStep;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) nxt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + q * kLmhStep));
+  };
+  load_batch(0, 0);
+  __syncthreads();  // the hidden states are in LDS
+  for (int m = 0; m < kLmhSpan / 32; ++m) {
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int cb = 0; cb < nb; ++cb) {
+      u32x4 cur[kQ];
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) cur[q] = nxt[q];
+      // the next batch in flight: this id's next, or the next id's first
+      if (cb + 1 < nb) load_batch(m, cb + 1);
+      else if (m + 1 < kLmhSpan / 32) load_batch(m + 1, 0);
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) {
+        const int k = (cb * kQ + q) * kLmhStep + 8 * g;  // hidden indices k .. k + 7
+        const uint32_t w4[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float4 *xp = reinterpret_cast<const float4 *>(xs + r * dim + k);
+          const float4 x0 = xp[0], x1 = xp[1];
+          const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            acc[r] = __builtin_fmaf(bf16_lo(w4[h]), xv[2 * h], acc[r]);
+            acc[r] = __builtin_fmaf(bf16_hi(w4[h]), xv[2 * h + 1], acc[r]);
+          }
+        }
+      }
+    }
+    // the group's eight partial sums, in one fixed tree: lane 0 of the
+    // group holds ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float v = acc[r];
+      v = v + __shfl_xor(v, 1, 64);
+      v = v + __shfl_xor(v, 2, 64);
+      v = v + __shfl_xor(v, 4, 64);
+      if (g == 0) s_logit[r][grp + 32 * m] = v;
+    }
+  }
+  __syncthreads();
+  // ---- the epilogue, row by row: lane t takes ids base + 2 t, + 1 ----
+  const int id0 = base + kLmhIds * tid;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v[2] = {s_logit[r][kLmhIds * tid], s_logit[r][kLmhIds * tid + 1]};
+    if (L.out_logits) {
+      float *o = L.out_logits + (int64_t)r * vocab;
+      if (id0 < vocab) o[id0] = v[0];
+      if (id0 + 1 < vocab) o[id0 + 1] = v[1];
+    }
+    lmh_select_row(L, S, r, part, v, id0);
+  }
+}
+
+// One block per (row, group of kLmhGroup parts).
+__global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
+  __shared__ uint32_t s_np[kLmhGroup], s_nm[kLmhGroup], s_nw[kWaves], s_nmw, s_slow, s_over;
+  __shared__ uint32_t s_hist[256], s_sel[4];
+  const SampleArgs &a = L.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row = blockIdx.x / L.gparts, g = blockIdx.x - row * L.gparts;
+  const int q0 = g * kLmhGroup;
+  const int nq = min(kLmhGroup, a.parts - q0);
+  sas_params p = a.params;
+  if (a.row_params) p = load_row_params(a.row_params + row);
+  const bool greedy = !(p.temperature > 0.0);
+  const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
+  // ---- the parts' info words: counts, bounds, slow flags ----
+  uint32_t bound = 0u, slow = 0u;
+#pragma unroll
+  for (int q = 0; q < kLmhGroup; ++q) {
+    if (q < nq) {
+      const uint64_t info = a.pinfo[(int64_t)row * pinfo_stride(a.parts) + q0 + q];
+      bound = max(bound, (uint32_t)(info >> 32));
+      slow |= (uint32_t)info & kPinfoSlow;
+      if (tid == 0) {
+        // within the part's slots whatever the word holds
+        s_np[q] = min((uint32_t)info & 0x7FFFu, (uint32_t)kLmhSpan);
+        s_nm[q] = min(((uint32_t)info >> 16) & 0x7FFFu, (uint32_t)kMemSlots);
+      }
+    }
+  }
+  if (tid == 0) {
+    s_nmw = 0u;
+    s_over = 0u;
+    s_slow = slow ? 1u : 0u;
+  }
+  __syncthreads();
+  // the largest part bound: that part alone holds k values above it, and
+  // every part recorded every value at or above its own (smaller) bound
+  const float bf = bound > 0x007FFFFFu ? fkey(bound) : -__builtin_inff();
+  const int64_t gq = (int64_t)row * L.gparts + g;
+  uint64_t *grec = L.g_rec + gq * kListCap;
+  uint4 *gmem = L.g_mrec + gq * kMemSlots;
+  // ---- plain records: thread (q, s) reads slots s, s + 32, ... of part q ----
+  const int q = tid >> 5, s0 = tid & 31;
+  const uint32_t npq = q < nq ? s_np[q] : 0u;
+  const uint64_t *src = a.rec + ((int64_t)row * a.parts + q0 + min(q, nq - 1)) * kListCap;
+  constexpr int kPer = kLmhSpan / 32;  // a part holds at most kLmhSpan plain records
+  uint64_t rc[kPer];
+  uint32_t keep = 0u;  // bit i: slot s0 + 32 i is kept
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t j = (uint32_t)(s0 + 32 * i);
+    rc[i] = j < npq ? src[j] : 0ull;
+    if (j < npq && __uint_as_float((uint32_t)rc[i]) >= bf) keep |= 1u << i;
+  }
+  const uint32_t mine = (uint32_t)__popc(keep);
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t bb = __ballot((mine >> bit) & 1u);
+    pre += lanes_below(bb) << bit;
+    tot += (uint32_t)__popcll(bb) << bit;
+  }
+  if (lane == 0) s_nw[wave] = tot;
+  // members: thread (q, s) reads member slots s, s + 32, ...
+  const uint32_t nmq = q < nq ? s_nm[q] : 0u;
+  const uint4 *msrc = a.mrec + ((int64_t)row * a.parts + q0 + min(q, nq - 1)) * kMemSlots;
+  __syncthreads();
+  uint32_t off = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) off += w < wave ? s_nw[w] : 0u;
+  const uint32_t nplain = s_nw[0] + s_nw[1] + s_nw[2] + s_nw[3];
+  if (nplain > (uint32_t)kListCap) {
+    if (tid == 0) s_over = 1u;
+  } else {
+    uint32_t j = off + pre;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if ((keep >> i) & 1u) grec[j++] = rc[i];
+  }
+  for (uint32_t j = (uint32_t)s0; j < nmq; j += 32u) {
+    const uint4 m = msrc[j];
+    const double v = __longlong_as_double((long long)(((uint64_t)m.w << 32) | m.z));
+    if (v >= (double)bf) {
+      const uint32_t d = atomicAdd(&s_nmw, 1u);
+      if (d < (uint32_t)kMemSlots) gmem[d] = m;
+      else s_over = 1u;
+    }
+  }
+  __syncthreads();
+  uint32_t np_out = nplain, nm_out = s_nmw;
+  if (s_over) {
+    // more records above the bound than a merge part holds (ties): the
+    // group's exact top k over (value, id) from the parts' records
+    auto for_recs = [&](auto f) {
+      for (int i = 0; i < kPer; ++i) {
+        const uint32_t j = (uint32_t)(s0 + 32 * i);
+        const bool ok = j < npq;
+        double v = 0.0;
+        uint32_t id = 0u;
+        if (ok) {
+          const uint64_t r = src[j];
+          v = (double)__uint_as_float((uint32_t)r);
+          id = (uint32_t)(r >> 32);
+        }
+        f(key96(v, id), ok, v, id, false, 0u);
+      }
+      for (int i = 0; i < (kMemSlots + 31) / 32; ++i) {
+        const uint32_t j = (uint32_t)(s0 + 32 * i);
+        const bool ok = j < nmq;
+        double v = 0.0;
+        uint32_t id = 0u, kb = 0u;
+        if (ok) {
+          const uint4 m = msrc[j];
+          v = __longlong_as_double((long long)(((uint64_t)m.w << 32) | m.z));
+          id = m.y;
+          kb = m.x;
+        }
+        f(key96(v, id), ok, v, id, true, kb);
+      }
+    };
+    uint32_t nval = 0u;
+    for_recs([&](const Key96 &, bool ok, double, uint32_t, bool, uint32_t) { nval += ok ? 1u : 0u; });
+    if (tid == 0) s_sel[3] = 0u;
+    __syncthreads();
+    atomicAdd(&s_sel[3], nval);
+    __syncthreads();
+    const uint32_t need = min(s_sel[3], (uint32_t)k);
+    __syncthreads();
+    if (tid == 0) {
+      s_nw[0] = 0u;
+      s_nmw = 0u;
+      s_slow = 1u;
+    }
+    __syncthreads();
+    if (need > 0u) {
+      const Key96 kth = block_select96(
+          [&](auto f) {
+            for_recs([&](const Key96 &kx, bool ok, double, uint32_t, bool, uint32_t) { f(kx, ok); });
+          },
+          need, s_hist, s_sel);
+      for_recs([&](const Key96 &kx, bool ok, double v, uint32_t id, bool member, uint32_t kb) {
+        if (ok && key_ge(kx, kth)) {
+          if (member) {
+            const uint64_t db = (uint64_t)__double_as_longlong(v);
+            gmem[atomicAdd(&s_nmw, 1u)] = make_uint4(kb, id, (uint32_t)db, (uint32_t)(db >> 32));
+          } else {
+            grec[atomicAdd(&s_nw[0], 1u)] = (uint64_t)__float_as_uint((float)v) | ((uint64_t)id << 32);
+          }
+        }
+      });
+    }
+    __syncthreads();
+    np_out = s_nw[0];
+    nm_out = s_nmw;
+  }
+  if (tid == 0)
+    L.g_pinfo[(int64_t)row * pinfo_stride(L.gparts) + g] =
+        (uint64_t)(np_out | (nm_out << 16) | (s_slow ? kPinfoSlow : 0u)) | ((uint64_t)bound << 32);
+}
+
+size_t lmh_scratch_bytes(int rows, int vocab) {
+  const int parts = (vocab + kLmhSpan - 1) / kLmhSpan;
+  const int gparts = (parts + kLmhGroup - 1) / kLmhGroup;
+  return sample_rec_bytes(rows, parts) + sample_rec_bytes(rows, gparts) + 256;
+}
+
+void lmh_layout(LmhArgs *a, void *scratch) {
+  const int rows = a->s.rows;
+  const int parts = (a->s.vocab + kLmhSpan - 1) / kLmhSpan;
+  const int gparts = (parts + kLmhGroup - 1) / kLmhGroup;
+  uint64_t *p = reinterpret_cast<uint64_t *>(scratch);
+  a->s.parts = parts;
+  a->s.span = kLmhSpan;
+  a->s.rec = p;
+  a->s.mrec = reinterpret_cast<uint4 *>(p + (size_t)rows * parts * kListCap);
+  a->s.pinfo = reinterpret_cast<uint64_t *>(a->s.mrec + (size_t)rows * parts * kMemSlots);
+  uint64_t *g = a->s.pinfo + (size_t)rows * pinfo_stride(parts);
+  g = reinterpret_cast<uint64_t *>((reinterpret_cast<uintptr_t>(g) + 255) & ~uintptr_t(255));
+  a->gparts = gparts;
+  a->g_rec = g;
+  a->g_mrec = reinterpret_cast<uint4 *>(g + (size_t)rows * gparts * kListCap);
+  a->g_pinfo = reinterpret_cast<uint64_t *>(a->g_mrec + (size_t)rows * gparts * kMemSlots);
+}
+
+template <int R>
+static hipError_t launch_parts(const LmhArgs &a, hipStream_t stream) {
+  const size_t lds = (size_t)R * a.dim * sizeof(float);
+  hipLaunchKernelGGL((lmh_parts_kernel<R>), dim3((unsigned)a.s.parts), dim3(kThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_head_sample(const LmhArgs &a, bool softcap, hipStream_t stream) {
+  (void)softcap;  // the epilogue reads each row's softcap itself
+  hipError_t e;
+  switch (a.s.rows) {
+    case 1: e = launch_parts<1>(a, stream); break;
+    case 2: e = launch_parts<2>(a, stream); break;
+    case 3: e = launch_parts<3>(a, stream); break;
+    default: e = launch_parts<4>(a, stream); break;
+  }
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(lmh_group_kernel, dim3((unsigned)(a.s.rows * a.gparts)), dim3(kThreads), 0, stream, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  SampleArgs m = a.s;
+  m.rec = a.g_rec;
+  m.mrec = a.g_mrec;
+  m.pinfo = a.g_pinfo;
+  m.parts = a.gparts;
+  m.span = kLmhSpan * kLmhGroup;
+  return launch_merge(m, stream);
+}
+
+}  // namespace sas

@@ -50,24 +50,7 @@ constexpr int kQuadCap = 64;                         // float4 entries of one wa
 static_assert(kQuadCap == 64, "a wave's list is one entry per lane at the end");
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 
-// The value of the wave's first active lane (wave-uniform values).
-__device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
-// One row's parameters from the per-row array: read as 32-bit words by
-// nontemporal loads, so that the compiler never forms a pointer that may
-// point into the kernel's by-value arguments (which would copy them to
-// scratch memory).
-__device__ __forceinline__ sas_params load_row_params(const sas_params *q) {
-  static_assert(sizeof(sas_params) % 4 == 0, "whole words");
-  union {
-    sas_params p;
-    uint32_t w[sizeof(sas_params) / 4];
-  } u;
-  const uint32_t *src = reinterpret_cast<const uint32_t *>(q);
-#pragma unroll
-  for (int i = 0; i < (int)(sizeof(sas_params) / 4); ++i) u.w[i] = __builtin_nontemporal_load(src + i);
-  return u.p;
-}
 
 // Lane i's double on every lane (i wave-uniform).
 __device__ __forceinline__ double bcast(double x, int i) {
@@ -77,111 +60,11 @@ __device__ __forceinline__ double bcast(double x, int i) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// Barrier over the block's LDS accesses alone: it waits for this wave's LDS
-// operations but not for its global loads, so loads stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // (va, ia) ranks before (vb, ib): value desc, then id asc (tokenizer.js:160
 // stable sort of an id-ascending list; kernels.js:1433, 1439 tie rule).
 __device__ __forceinline__ bool before(double va, uint32_t ia, double vb, uint32_t ib) {
   return va > vb || (va == vb && ia < ib);
-}
-
-// 96-bit key of (value, id), larger = ranks first: an order-preserving
-// image of the double (-0 and +0 one value), then the id reversed.
-struct Key96 {
-  uint32_t w[3];
-};
-__device__ __forceinline__ Key96 key96(double v, uint32_t id) {
-  v = v + 0.0;  // -0 -> +0
-  const uint64_t b = (uint64_t)__double_as_longlong(v);
-  const uint64_t d = (b >> 63) ? ~b : (b | 0x8000000000000000ull);
-  return Key96{{(uint32_t)(d >> 32), (uint32_t)d, ~id}};
-}
-__device__ __forceinline__ bool key_ge(const Key96 &a, const Key96 &b) {
-  if (a.w[0] != b.w[0]) return a.w[0] > b.w[0];
-  if (a.w[1] != b.w[1]) return a.w[1] > b.w[1];
-  return a.w[2] >= b.w[2];
-}
-
-// The need-th largest (1-based) of the block's 96-bit keys; need must not
-// exceed their number.  for_keys(f) calls f(key, valid) the same number of
-// times on every lane of a wave.  Radix passes of 8 bits from the top, each
-// an LDS histogram; ends early once the bin holding the need-th key is
-// taken whole (the bits below stay zero: exactly `need` keys reach the
-// result).  LDS: hist[256], sel[3].  Block-wide; every thread returns it.
-template <typename ForKeys>
-__device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need, uint32_t *hist, uint32_t *sel) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  Key96 res{{0u, 0u, 0u}};
-  for (int pass = 0; pass < 12; ++pass) {
-    const int w = pass >> 2;
-    const int sh = 24 - 8 * (pass & 3);
-    const uint32_t hm = sh == 24 ? 0u : ~0u << (sh + 8);
-    for (int i = tid; i < 256; i += (int)blockDim.x) hist[i] = 0u;
-    __syncthreads();
-    // word w of a key by selects (no indexed registers)
-    auto word = [&](const Key96 &x) { return w == 0 ? x.w[0] : w == 1 ? x.w[1] : x.w[2]; };
-    const uint32_t rw = word(res);
-    for_keys([&](const Key96 &key, bool valid) {
-      const uint32_t kw = word(key);
-      bool match = valid && (kw & hm) == (rw & hm);
-      if (w > 0) match = match && key.w[0] == res.w[0];
-      if (w > 1) match = match && key.w[1] == res.w[1];
-      const uint32_t d = (kw >> sh) & 0xFFu;
-      const uint64_t act = __ballot(match);
-      if (act) {
-        // one atomic per wave when every matching lane has the same digit
-        const int first = __builtin_ctzll(act);
-        const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)d, first);
-        if (__ballot(match && d != d0) == 0) {
-          if (lane == first) atomicAdd(&hist[d0], (uint32_t)__popcll(act));
-        } else if (match) {
-          atomicAdd(&hist[d], 1u);
-        }
-      }
-    });
-    __syncthreads();
-    if (wave == 0) {
-      const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
-      const uint32_t s4 = c0 + c1 + c2 + c3;
-      uint32_t suf = s4;  // keys in the bins of this lane and above
-#pragma unroll
-      for (int s = 1; s < 64; s <<= 1) {
-        const uint32_t y = (uint32_t)__shfl_down((int)suf, s, 64);
-        if (lane + s < 64) suf += y;
-      }
-      const uint32_t above = suf - s4;
-      if (above < need && need <= suf) {
-        uint32_t acc = above, d, cb;
-        if (acc + c3 >= need) {
-          d = 3; cb = c3;
-        } else if ((acc += c3) + c2 >= need) {
-          d = 2; cb = c2;
-        } else if ((acc += c2) + c1 >= need) {
-          d = 1; cb = c1;
-        } else {
-          acc += c1; d = 0; cb = c0;
-        }
-        sel[0] = 4u * (uint32_t)lane + d;
-        sel[1] = need - acc;
-        sel[2] = cb;
-      }
-    }
-    __syncthreads();
-    const uint32_t d = sel[0], cb = sel[2];
-    need = sel[1];
-    if (w == 0) res.w[0] |= d << sh;
-    else if (w == 1) res.w[1] |= d << sh;
-    else res.w[2] |= d << sh;
-    __syncthreads();
-    if (cb == need) break;
-  }
-  return res;
 }
 
 // ----------------------------------------------------------------- merge --
@@ -193,9 +76,7 @@ __device__ __forceinline__ Key96 block_select96(ForKeys for_keys, uint32_t need,
 
 constexpr int kMR = 16;           // plain record slots per thread loaded before the counts are known
 constexpr int kSurvCap = 512;     // survivors the merge ranks
-constexpr int kMemSlots = kListCap / 2;  // member records (16 bytes) of a part
 constexpr uint32_t kInexact = 0x80000000u;  // composite bit: the exact value lies above the key
-constexpr uint32_t kPinfoSlow = 0x80000000u;  // pinfo bit: the part took the exact slow selection
 
 struct MergeLds {
   uint32_t wred[kWaves][4];          // per-wave partial results
@@ -1518,6 +1399,10 @@ hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) 
     case 6: launch_kernel<true, true, false>(a, stream); break;
     default: launch_kernel<true, true, true>(a, stream); break;
   }
+  return launch_merge(a, stream);
+}
+
+hipError_t launch_merge(const SampleArgs &a, hipStream_t stream) {
   hipLaunchKernelGGL(sample_merge_kernel, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }

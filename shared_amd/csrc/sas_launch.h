@@ -19,6 +19,8 @@ constexpr int kSpanPass = 8192;   // ids of one pass of a block
 constexpr int kMaxSpan = 65536;   // ids one part may span (a multiple of kSpanPass above it)
 constexpr int kMaxParts = 64;     // blocks per row
 constexpr int kListCap = 640;     // records one part may write
+constexpr int kMemSlots = kListCap / 2;       // member records (16 bytes) of a part
+constexpr uint32_t kPinfoSlow = 0x80000000u;  // pinfo bit: the part took the exact slow selection
 
 // Part counts of a row (pinfo) per 128-byte line: rows never share a line.
 __host__ __device__ constexpr int pinfo_stride(int parts) { return (parts + 15) & ~15; }
@@ -84,6 +86,8 @@ struct SampleArgs {
 // (fewer, larger parts) unless the grid would hold fewer than
 // `min_blocks` blocks; at most kMaxParts parts per row.
 void choose_parts(int rows, int vocab, int min_blocks, int *parts, int *span);
+// The merge launch alone (one block per row) over `a`'s records.
+hipError_t launch_merge(const SampleArgs &a, hipStream_t stream);
 // Launches the sampling kernel on `stream`.  softcap: some row may have a
 // softcap (row_params, or params.softcap > 0).
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
@@ -104,6 +108,37 @@ hipError_t launch_probe_read(const void *src, int64_t n4, int blocks, float *sin
 size_t sample_rec_bytes(int rows, int parts);
 // Copies rows of vocab < 4 logits into dst[rows][4], NaN past vocab.
 hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows, float *dst, hipStream_t stream);
+
+// --------------------------------------------------------------- lm head --
+// sas_lm_head_sample: one block per part of kLmhSpan ids computes the
+// part's logits for every row (the hidden states staged in LDS, each lane
+// two ids' whole dot products) and writes the part's records as the parts
+// kernel does; a group launch folds kLmhGroup consecutive parts into one
+// part of the merge kernel's records, which then samples as for sas_sample.
+constexpr int kLmhSpan = 512;   // ids per part: two per thread
+constexpr int kLmhGroup = 8;    // parts per merge part (4,096 ids)
+
+struct LmhArgs {
+  SampleArgs s;          // the sampling descriptor; s.rec/mrec/pinfo: the parts' records, s.parts = parts
+  const float *hidden;
+  int64_t hidden_stride;
+  const uint16_t *weight;
+  int64_t weight_stride;
+  int32_t dim;
+  float *out_logits;     // [rows][vocab] or null
+  // the merge's records: kLmhGroup parts each (laid out as SampleArgs' records)
+  uint64_t *g_rec;
+  uint4 *g_mrec;
+  uint64_t *g_pinfo;
+  int32_t gparts;
+};
+
+// Scratch bytes of both record levels for a batch shape.
+size_t lmh_scratch_bytes(int rows, int vocab);
+// Fills the record pointers of `a` from `scratch` (lmh_scratch_bytes bytes).
+void lmh_layout(LmhArgs *a, void *scratch);
+// The three launches (parts with the head, groups, merge), in stream order.
+hipError_t launch_lm_head_sample(const LmhArgs &a, bool softcap, hipStream_t stream);
 
 // ---------------------------------------------------------------- verify --
 // Positions are the rows of target_logits: position p = seq * (L + 1) + j,

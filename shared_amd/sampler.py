@@ -13,7 +13,7 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import _capi
-from ._capi import SasParams, SasRows, SasSpecRows, SasVerifyRows, check, load
+from ._capi import SasLmHead, SasParams, SasRows, SasSpecRows, SasVerifyRows, check, load
 
 
 @dataclass
@@ -261,6 +261,49 @@ class Sampler:
         self.sample_into(logits, out["ids"], out_probs=out.get("probs"), out_cand_ids=out.get("cand_ids"),
                          out_counts=out.get("counts"), out_flags=out.get("flags"), **kw)
         return out if full else out["ids"]
+
+    def lm_head_sample_into(self, hidden, weight, out_ids, *, dim: Optional[int] = None, out_logits=None,
+                            vocab: Optional[int] = None, stream=None, **kw) -> None:
+        """sas_lm_head_sample: the LM head (hidden [rows][>= dim] fp32 times
+        weight [vocab][>= dim] bf16 bits, as int16/uint16 tensors) with the
+        sampling step fused into its epilogue; kw as for sample_into."""
+        rows = hidden.shape[0]
+        vocab = int(vocab if vocab is not None else weight.shape[0])
+        if hidden.dtype.itemsize != 4 or hidden.stride(1) != 1:
+            raise ValueError("hidden must be fp32 with unit element stride")
+        if weight.dtype.itemsize != 2 or weight.stride(1) != 1:
+            raise ValueError("weight must hold bf16 bits (2 bytes) with unit element stride")
+        h = SasLmHead()
+        h.hidden = hidden.data_ptr()
+        h.hidden_stride = hidden.stride(0)
+        h.weight = weight.data_ptr()
+        h.weight_stride = weight.stride(0)
+        h.dim = int(dim if dim is not None else hidden.shape[1])
+        h.out_logits = _ptr(out_logits)
+        d = rows_descriptor(hidden, out_ids, vocab=vocab, **kw)
+        d.logits = None
+        d.logits_stride = 0
+        check(self._lib.sas_lm_head_sample(self._h, ctypes.byref(h), ctypes.byref(d), _stream(stream)), self._h)
+
+    def lm_head_sample(self, hidden, weight, *, full: bool = False, logits: bool = False, **kw):
+        """Allocate outputs and run lm_head_sample_into; returns ids, or a
+        dict with the extras (and the head's logits when `logits`)."""
+        import torch
+        rows = hidden.shape[0]
+        vocab = int(kw.get("vocab") or weight.shape[0])
+        dev = hidden.device
+        out = {"ids": torch.empty(rows, dtype=torch.int32, device=dev)}
+        if full:
+            out["probs"] = torch.empty((rows, _capi.MAX_TOP_K), dtype=torch.float64, device=dev)
+            out["cand_ids"] = torch.empty((rows, _capi.MAX_TOP_K), dtype=torch.int32, device=dev)
+            out["counts"] = torch.empty((rows, 2), dtype=torch.int32, device=dev)
+            out["flags"] = torch.empty(rows, dtype=torch.int32, device=dev)
+        if logits:
+            out["logits"] = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
+        self.lm_head_sample_into(hidden, weight, out["ids"], out_logits=out.get("logits"),
+                                 out_probs=out.get("probs"), out_cand_ids=out.get("cand_ids"),
+                                 out_counts=out.get("counts"), out_flags=out.get("flags"), **kw)
+        return out if (full or logits) else out["ids"]
 
     def sample_step_into(self, logits, out_ids, state: DecodeState, *, stream=None, **kw) -> None:
         """One decode step with in-graph feedback (sas_sample_step): the

@@ -228,4 +228,75 @@ def spec_case(seqs: int = 32, vocab: int = QWEN_VOCAB, seed: int = 6, drafts: in
             "round": int(rng.integers(0, 1000)), "stop_ids": stop, "vocab": vocab, "seqs": seqs, "drafts": L}
 
 
+def bf16_bits(rng, shape, lo_exp: int = -6, hi_exp: int = -3) -> np.ndarray:
+    """Random bf16 bit patterns (uint16): random sign and 7-bit mantissa,
+    exponent uniform in [lo_exp, hi_exp] (magnitudes 2^lo_exp .. 2^(hi_exp+1)),
+    as one table lookup per uniform 16-bit draw."""
+    r = np.arange(1 << 16, dtype=np.uint32)
+    span = hi_exp - lo_exp + 1
+    e = ((r >> 7) & 0xFF) % span
+    table = ((r & 0x8000) | ((e + np.uint32(127 + lo_exp)) << 7) | (r & 0x7F)).astype(np.uint16)
+    return table[rng.integers(0, 1 << 16, size=shape, dtype=np.uint16)]
+
+
+@dataclass
+class LmhBatch:
+    """Inputs of sas_lm_head_sample: fp32 hidden states, a bf16 head (uint16
+    bits, [vocab][dim]) and the sampling descriptor's host arrays."""
+    name: str
+    hidden: np.ndarray            # float32 [rows, dim]
+    weight_bits: np.ndarray       # uint16 [vocab, dim]
+    params: Params
+    mask: Optional[np.ndarray] = None
+    hist_ids: Optional[np.ndarray] = None
+    hist_offsets: Optional[np.ndarray] = None
+    uniforms: Optional[np.ndarray] = None
+
+    @property
+    def rows(self) -> int:
+        return self.hidden.shape[0]
+
+    @property
+    def vocab(self) -> int:
+        return self.weight_bits.shape[0]
+
+    @property
+    def dim(self) -> int:
+        return self.hidden.shape[1]
+
+    def with_logits(self, logits: np.ndarray) -> Batch:
+        """The sampling step over given logits (the unfused path's input)."""
+        return Batch(self.name, logits, self.params, mask=self.mask, hist_ids=self.hist_ids,
+                     hist_offsets=self.hist_offsets, uniforms=self.uniforms)
+
+    def algorithmic_bytes(self) -> int:
+        """Compulsory HBM bytes of one call: the head read once, the hidden
+        states, mask words, history ids and offsets, uniforms, ids out."""
+        b = self.weight_bits.nbytes + self.hidden.nbytes + 4 * self.rows
+        if self.mask is not None:
+            b += self.rows * ((self.vocab + 31) // 32) * 4
+        if self.hist_ids is not None:
+            b += self.hist_ids.nbytes + self.hist_offsets.nbytes
+        if self.uniforms is not None and self.params.temperature > 0:
+            b += self.uniforms.nbytes
+        return b
+
+
+def lmh(rows: int = 1, vocab: int = GEMMA_VOCAB, dim: int = 2560, seed: int = 7, hist: int = 512,
+        softcap: float = 30.0, mask: bool = True) -> LmhBatch:
+    """LMH: the decode head with sampling fused (sas_lm_head_sample), Gemma-4
+    E4B-shaped: hidden 2560 fp32 rows times a [vocab][2560] bf16 head
+    (logits ~ N(0, 3) at dim 2560), softcap 30 (gemma-config.js:47), then
+    C3P's sampling: mask density U[0.5 %, 20 %], top-k 50 / top-p 0.9 /
+    T 1.0, repetition 1.1 / presence 0.5 / frequency 0.3 over `hist` ids."""
+    rng = _rng(seed)
+    hidden = rng.standard_normal((rows, dim), dtype=np.float32)
+    w = bf16_bits(rng, (vocab, dim), -7, -4)
+    m = random_mask(rng, rows, vocab, 0.005, 0.20) if mask else None
+    ids, offs = _csr([rng.integers(0, vocab, hist) for _ in range(rows)]) if hist else (None, None)
+    p = Params(temperature=1.0, top_k=50, top_p=0.9, repetition_penalty=1.1, presence_penalty=0.5,
+               frequency_penalty=0.3, softcap=softcap)
+    return LmhBatch("LMH", hidden, w, p, mask=m, hist_ids=ids, hist_offsets=offs, uniforms=rng.random(rows))
+
+
 CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C3P": c3p, "C4": c4}

@@ -89,6 +89,8 @@ static void null_handle_paths() {
   EXPECT(sas_sample_step(nullptr, &r, &st, nullptr) == SAS_ERR_INVALID);
   EXPECT(sas_spec_exact(nullptr, &sp, nullptr) == SAS_ERR_INVALID);
   EXPECT(sas_verify(nullptr, &v, nullptr) == SAS_ERR_INVALID);
+  sas_lm_head lh{};
+  EXPECT(sas_lm_head_sample(nullptr, &lh, &r, nullptr) == SAS_ERR_INVALID);
   EXPECT(sas_reserve(nullptr, 1, 1) == SAS_ERR_INVALID);
   EXPECT(sas_alloc(nullptr, 16, &p) == SAS_ERR_INVALID);
   EXPECT(sas_free(nullptr, p) == SAS_ERR_INVALID);
@@ -285,6 +287,48 @@ static void device_paths(sas_sampler *s) {
   for (int32_t a : download(s, (int32_t *)vacc, seqs)) EXPECT(a >= 0 && a <= L);
   v.temperature = 0.0;
   EXPECT(sas_verify(s, &v, nullptr) == SAS_ERR_INVALID);
+  // the LM head with the sampling step fused: the first 3 rows over a
+  // 64-wide head (bf16 bits of small values)
+  const int lrows = 3, dim = 256;
+  std::vector<float> hid((size_t)lrows * dim);
+  for (auto &e : hid) e = nd(g) * 0.1f;
+  std::vector<uint16_t> wt((size_t)vocab * dim);
+  for (auto &e : wt) {
+    const float f = nd(g) * 0.05f;
+    uint32_t b;
+    std::memcpy(&b, &f, 4);
+    e = (uint16_t)(b >> 16);
+  }
+  float *dhid = upload(s, hid);
+  uint16_t *dwt = upload(s, wt);
+  void *lgt = nullptr;
+  EXPECT(sas_alloc(s, (size_t)lrows * vocab * 4, &lgt) == SAS_OK);
+  sas_lm_head lh{};
+  lh.hidden = dhid;
+  lh.hidden_stride = dim;
+  lh.weight = dwt;
+  lh.weight_stride = dim;
+  lh.dim = dim;
+  lh.out_logits = (float *)lgt;
+  sas_rows lr = r;
+  lr.logits = nullptr;
+  lr.rows = lrows;
+  EXPECT(sas_lm_head_sample(s, &lh, &lr, nullptr) == SAS_OK);
+  EXPECT(sas_synchronize(s, nullptr) == SAS_OK);
+  for (uint32_t t : download(s, (uint32_t *)ids, lrows)) EXPECT(t < (uint32_t)vocab);
+  sas_rows blr = lr;
+  blr.logits = dx;
+  EXPECT(sas_lm_head_sample(s, &lh, &blr, nullptr) == SAS_ERR_INVALID && last_error_has(s, "NULL"));
+  blr = lr;
+  blr.rows = SAS_LMH_MAX_ROWS + 1;
+  EXPECT(sas_lm_head_sample(s, &lh, &blr, nullptr) == SAS_ERR_INVALID && last_error_has(s, "rows"));
+  sas_lm_head blh = lh;
+  blh.dim = 320;
+  EXPECT(sas_lm_head_sample(s, &blh, &lr, nullptr) == SAS_ERR_INVALID && last_error_has(s, "dim"));
+  blh = lh;
+  blh.weight_stride = 258;
+  EXPECT(sas_lm_head_sample(s, &blh, &lr, nullptr) == SAS_ERR_INVALID && last_error_has(s, "weight_stride"));
+  for (void *q : {(void *)dhid, (void *)dwt, lgt}) EXPECT(sas_free(s, q) == SAS_OK);
   for (void *q : {(void *)dx, (void *)dm, (void *)dh, (void *)doff, (void *)du, (void *)drp, ids, probs, cand, cnt,
                   flg, (void *)dst, (void *)dring, (void *)dseed, (void *)dstop, sampled, next, (void *)ddr, dids, picks,
                   acc, (void *)dvu, vtok, vacc})

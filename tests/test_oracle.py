@@ -454,3 +454,70 @@ def test_spec_history_is_the_rounds_start_for_every_row():
     o = O.spec_exact(_spec_inp(target, L, draft_ids=np.array([[4, 4]], np.uint32), params=p, hist=[[3, 3, 9]]))
     assert o["picks"].tolist() == [[4, 4, 4]]
     assert o["accepted"].tolist() == [3]
+
+
+# ---------------------------------------------------------------- lm head --
+
+def _bf16(x: float) -> int:
+    """bf16 bits of a float that bf16 holds exactly."""
+    b = struct.unpack("<I", struct.pack("<f", x))[0]
+    assert b & 0xFFFF == 0, x
+    return b >> 16
+
+
+def test_lm_head_one_hot_hidden_reads_a_weight_column():
+    """hidden = e_k gives logit[id] = weight[id][k] widened (bits << 16):
+    pins the widening and which index is the vocabulary."""
+    rng = np.random.default_rng(21)
+    w = W.bf16_bits(rng, (37, 64), -6, 2)
+    for k in (0, 5, 63):
+        h = np.zeros((1, 64), np.float32)
+        h[0, k] = 1.0
+        got = O.lm_head_logits(h, w)[0]
+        want = (w[:, k].astype(np.uint32) << 16).view(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_lm_head_lane_partial_is_one_fma_chain():
+    """w = [-1, 1 + 2^-7], x = [1, 1 + 2^-23] (both in partial 0): the fused
+    chain over k = 0, 1 keeps the product's 2^-30 bit (exact result
+    2^-7 + 2^-23 + 2^-30); a separately rounded product, or the chain run
+    k = 1, 0, loses it."""
+    w = np.array([[_bf16(-1.0), _bf16(1.0 + 2.0 ** -7)]], np.uint16)
+    h = np.array([[1.0, 1.0 + 2.0 ** -23]], np.float32)
+    got = float(O.lm_head_logits(h, w, dim=2)[0, 0])
+    assert got == 2.0 ** -7 + 2.0 ** -23 + 2.0 ** -30
+    reversed_order = float(np.float32(np.float32(1.0 + 2.0 ** -7) * np.float32(1.0 + 2.0 ** -23)) - np.float32(1.0))
+    assert reversed_order == 2.0 ** -7 + 2.0 ** -23 and got != reversed_order
+
+
+def test_lm_head_partials_add_in_a_pairwise_tree():
+    """Terms at k = 0, 8, 16, 24 fall in partials 0, 1, 2, 3 (lane g takes
+    k = 8 g .. 8 g + 7 of every 64): 1, 2^-24, 2^-24, 2^-24 add as
+    (1 + 2^-24) + (2^-24 + 2^-24) = 1 + 2^-23.  One chain over k, or the
+    four terms in one partial, rounds each 1 + 2^-24 back to 1."""
+    dim = 256
+    w = np.zeros((1, dim), np.uint16)
+    h = np.zeros((1, dim), np.float32)
+    for k, v in ((0, 1.0), (8, 2.0 ** -24), (16, 2.0 ** -24), (24, 2.0 ** -24)):
+        w[0, k] = _bf16(v)
+        h[0, k] = 1.0
+    assert float(O.lm_head_logits(h, w)[0, 0]) == 1.0 + 2.0 ** -23
+    seq = np.float32(0.0)
+    for v in (1.0, 2.0 ** -24, 2.0 ** -24, 2.0 ** -24):
+        seq = np.float32(seq + np.float32(v))
+    assert float(seq) == 1.0
+
+
+def test_lm_head_within_the_chain_bound_of_the_exact_dot():
+    """Against the float64 dot product: an f32 fma chain of n terms errs by
+    at most n * 2^-24 * sum |w x| (each step rounds once)."""
+    rng = np.random.default_rng(22)
+    h = rng.standard_normal((3, 512)).astype(np.float32)
+    w = W.bf16_bits(rng, (200, 512), -7, -4)
+    got = O.lm_head_logits(h, w).astype(np.float64)
+    wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    exact = h.astype(np.float64) @ wf.T
+    bound = 512 * 2.0 ** -24 * (np.abs(h.astype(np.float64)) @ np.abs(wf).T)
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.any(got != exact)  # the f32 chain does round
