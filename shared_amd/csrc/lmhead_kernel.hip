@@ -23,9 +23,10 @@
 // members' penalized doubles as member records, the part's info word.
 //
 // lmh_group_kernel: one block per (row, kLmhGroup consecutive parts) keeps
-// the records at or above the largest of the parts' bounds (that part alone
-// holds k values above it) and writes them as one part of the merge kernel,
-// which then draws as for sas_sample.
+// the records at or above the group's k-th largest key (at or above the
+// largest of the parts' bounds: that part alone holds k values above it)
+// and writes them as one part of the merge kernel, which then draws as for
+// sas_sample.
 #include "sas_device.h"
 #include "sas_launch.h"
 
@@ -290,13 +291,16 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
     const int id = min(base + grp + 32 * m, vocab - 1);  // loads stay inside the head
     return L.weight + (int64_t)id * L.weight_stride + 8 * g;
   };
-  u32x4 nxt[kQ];
-  auto load_batch = [&](int m, int cb) __attribute__((always_inline)) {
+  u32x4 nxt[kQ], nx2[kQ];
+  auto load_into = [&](u32x4 (&dst)[kQ], int m, int cb) __attribute__((always_inline)) {
     const uint16_t *w = wrow(m) + (int64_t)cb * kQ * kLmhStep;
 #pragma unroll
-    for (int q = 0; q < kQ; ++q) nxt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + q * kLmhStep));
+    for (int q = 0; q < kQ; ++q) dst[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + q * kLmhStep));
   };
-  load_batch(0, 0);
+  // batches in the flattened order (m, cb): two in flight ahead of the one computed
+  const int total = (kLmhSpan / 32) * nb;
+  load_into(nxt, 0, 0);
+  if (total > 1) load_into(nx2, nb > 1 ? 0 : 1, nb > 1 ? 1 : 0);
   __syncthreads();  // the hidden states are in LDS
   for (int m = 0; m < kLmhSpan / 32; ++m) {
     float acc[R];
@@ -305,10 +309,13 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
     for (int cb = 0; cb < nb; ++cb) {
       u32x4 cur[kQ];
 #pragma unroll
-      for (int q = 0; q < kQ; ++q) cur[q] = nxt[q];
-      // the next batch in flight: this id's next, or the next id's first
-      if (cb + 1 < nb) load_batch(m, cb + 1);
-      else if (m + 1 < kLmhSpan / 32) load_batch(m + 1, 0);
+      for (int q = 0; q < kQ; ++q) {
+        cur[q] = nxt[q];
+        nxt[q] = nx2[q];
+      }
+      // the batch two ahead in flight
+      const int t2 = m * nb + cb + 2;
+      if (t2 < total) load_into(nx2, t2 / nb, t2 - (t2 / nb) * nb);
 #pragma unroll
       for (int q = 0; q < kQ; ++q) {
         const int k = (cb * kQ + q) * kLmhStep + 8 * g;  // hidden indices k .. k + 7
@@ -352,9 +359,13 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
   }
 }
 
-// One block per (row, group of kLmhGroup parts).
+// One block per (row, group of kLmhGroup parts).  The records kept are
+// those at or above the group's k-th largest key (round-down keys for the
+// members: a member whose value reaches a key's value has a key that
+// reaches it), so a merge part holds about k records whatever the spread
+// of the parts' bounds.
 __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
-  __shared__ uint32_t s_np[kLmhGroup], s_nm[kLmhGroup], s_nw[kWaves], s_nmw, s_slow, s_over;
+  __shared__ uint32_t s_np[kLmhGroup], s_nm[kLmhGroup], s_nw[kWaves], s_nmw, s_slow, s_over, s_n;
   __shared__ uint32_t s_hist[256], s_sel[4];
   const SampleArgs &a = L.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -365,6 +376,23 @@ __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
   if (a.row_params) p = load_row_params(a.row_params + row);
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
+  // ---- every plain and member slot of the group's parts, loaded before
+  // the counts are known (all slots lie inside the parts' records) ----
+  const int q = tid >> 5, s0 = tid & 31;
+  const uint64_t *src = a.rec + ((int64_t)row * a.parts + q0 + min(q, nq - 1)) * kListCap;
+  const uint4 *msrc = a.mrec + ((int64_t)row * a.parts + q0 + min(q, nq - 1)) * kMemSlots;
+  constexpr int kPer = kLmhSpan / 32;                // plain slots per thread
+  constexpr int kMPer = (kMemSlots + 31) / 32;       // member slots per thread
+  static_assert(kPer * 32 <= kListCap, "plain slots inside a part's records");
+  uint64_t rc[kPer];
+  uint4 mr[kMPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) rc[i] = src[s0 + 32 * i];
+#pragma unroll
+  for (int i = 0; i < kMPer; ++i) {
+    const int j = s0 + 32 * i;
+    mr[i] = j < kMemSlots ? msrc[j] : make_uint4(0u, 0u, 0u, 0u);
+  }
   // ---- the parts' info words: counts, bounds, slow flags ----
   uint32_t bound = 0u, slow = 0u;
 #pragma unroll
@@ -383,28 +411,101 @@ __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
   if (tid == 0) {
     s_nmw = 0u;
     s_over = 0u;
+    s_n = 0u;
     s_slow = slow ? 1u : 0u;
   }
   __syncthreads();
   // the largest part bound: that part alone holds k values above it, and
   // every part recorded every value at or above its own (smaller) bound
-  const float bf = bound > 0x007FFFFFu ? fkey(bound) : -__builtin_inff();
+  const uint32_t bkey = bound > 0x007FFFFFu ? bound : 0u;
   const int64_t gq = (int64_t)row * L.gparts + g;
   uint64_t *grec = L.g_rec + gq * kListCap;
   uint4 *gmem = L.g_mrec + gq * kMemSlots;
-  // ---- plain records: thread (q, s) reads slots s, s + 32, ... of part q ----
-  const int q = tid >> 5, s0 = tid & 31;
+  // ---- the candidates: slots below the parts' counts, at or above bkey ----
   const uint32_t npq = q < nq ? s_np[q] : 0u;
-  const uint64_t *src = a.rec + ((int64_t)row * a.parts + q0 + min(q, nq - 1)) * kListCap;
-  constexpr int kPer = kLmhSpan / 32;  // a part holds at most kLmhSpan plain records
-  uint64_t rc[kPer];
-  uint32_t keep = 0u;  // bit i: slot s0 + 32 i is kept
+  const uint32_t nmq = q < nq ? s_nm[q] : 0u;
+  uint32_t rk[kPer];  // keys (0: not a candidate)
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const uint32_t j = (uint32_t)(s0 + 32 * i);
-    rc[i] = j < npq ? src[j] : 0ull;
-    if (j < npq && __uint_as_float((uint32_t)rc[i]) >= bf) keep |= 1u << i;
+    const uint32_t kk = j < npq ? okey(__uint_as_float((uint32_t)rc[i])) : 0u;
+    rk[i] = kk >= bkey ? kk : 0u;
   }
+  uint32_t mk[kMPer];
+#pragma unroll
+  for (int i = 0; i < kMPer; ++i) {
+    const uint32_t j = (uint32_t)(s0 + 32 * i);
+    const uint32_t kk = j < nmq ? okey(__uint_as_float(mr[i].x)) : 0u;
+    mk[i] = kk >= bkey ? kk : 0u;
+  }
+  // ---- the group's k-th largest key: a radix select, 8 bits a pass from
+  // the top, each pass an LDS histogram of the keys that match the bits
+  // found so far ----
+  {
+    uint32_t n = 0u;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) n += rk[i] != 0u ? 1u : 0u;
+#pragma unroll
+    for (int i = 0; i < kMPer; ++i) n += mk[i] != 0u ? 1u : 0u;
+    n = wave_sum_u32(n);
+    if (lane == 0) atomicAdd(&s_n, n);
+  }
+  __syncthreads();
+  uint32_t t = bkey;
+  if (s_n > (uint32_t)k) {
+    uint32_t res = 0u, need = (uint32_t)k;
+    for (int pass = 0; pass < 4; ++pass) {
+      const int sh = 24 - 8 * pass;
+      const uint32_t hm = sh == 24 ? 0u : ~0u << (sh + 8);  // the bits found so far
+      s_hist[tid] = 0u;
+      __syncthreads();
+      auto add = [&](uint32_t kk) __attribute__((always_inline)) {
+        if (kk != 0u && (kk & hm) == (res & hm)) atomicAdd(&s_hist[(kk >> sh) & 0xFFu], 1u);
+      };
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) add(rk[i]);
+#pragma unroll
+      for (int i = 0; i < kMPer; ++i) add(mk[i]);
+      __syncthreads();
+      if (wave == 0) {
+        // bins 4 lane .. 4 lane + 3; suf = keys in the bins of this lane and above
+        const uint32_t c0 = s_hist[4 * lane], c1 = s_hist[4 * lane + 1], c2 = s_hist[4 * lane + 2],
+                       c3 = s_hist[4 * lane + 3];
+        const uint32_t s4 = c0 + c1 + c2 + c3;
+        uint32_t suf = s4;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t y = (uint32_t)__shfl_down((int)suf, d, 64);
+          if (lane + d < 64) suf += y;
+        }
+        const uint32_t above = suf - s4;
+        if (above < need && need <= suf) {
+          uint32_t acc = above, d;
+          if (acc + c3 >= need) {
+            d = 3;
+          } else if ((acc += c3) + c2 >= need) {
+            d = 2;
+          } else if ((acc += c2) + c1 >= need) {
+            d = 1;
+          } else {
+            acc += c1;
+            d = 0;
+          }
+          s_sel[0] = 4u * (uint32_t)lane + d;
+          s_sel[1] = need - acc;
+        }
+      }
+      __syncthreads();
+      res |= s_sel[0] << sh;
+      need = s_sel[1];
+    }
+    t = res;
+  }
+  // ---- the records at or above t ----
+  uint32_t keep = 0u;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (rk[i] != 0u && rk[i] >= t) keep |= 1u << i;
   const uint32_t mine = (uint32_t)__popc(keep);
   uint32_t pre = 0u, tot = 0u;
 #pragma unroll
@@ -414,9 +515,6 @@ __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
     tot += (uint32_t)__popcll(bb) << bit;
   }
   if (lane == 0) s_nw[wave] = tot;
-  // members: thread (q, s) reads member slots s, s + 32, ...
-  const uint32_t nmq = q < nq ? s_nm[q] : 0u;
-  const uint4 *msrc = a.mrec + ((int64_t)row * a.parts + q0 + min(q, nq - 1)) * kMemSlots;
   __syncthreads();
   uint32_t off = 0u;
 #pragma unroll
@@ -430,20 +528,19 @@ __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
     for (int i = 0; i < kPer; ++i)
       if ((keep >> i) & 1u) grec[j++] = rc[i];
   }
-  for (uint32_t j = (uint32_t)s0; j < nmq; j += 32u) {
-    const uint4 m = msrc[j];
-    const double v = __longlong_as_double((long long)(((uint64_t)m.w << 32) | m.z));
-    if (v >= (double)bf) {
+#pragma unroll
+  for (int i = 0; i < kMPer; ++i) {
+    if (mk[i] != 0u && mk[i] >= t) {
       const uint32_t d = atomicAdd(&s_nmw, 1u);
-      if (d < (uint32_t)kMemSlots) gmem[d] = m;
+      if (d < (uint32_t)kMemSlots) gmem[d] = mr[i];
       else s_over = 1u;
     }
   }
   __syncthreads();
   uint32_t np_out = nplain, nm_out = s_nmw;
   if (s_over) {
-    // more records above the bound than a merge part holds (ties): the
-    // group's exact top k over (value, id) from the parts' records
+    // more records at the key than a merge part holds (ties): the group's
+    // exact top k over (value, id) from the parts' records
     auto for_recs = [&](auto f) {
       for (int i = 0; i < kPer; ++i) {
         const uint32_t j = (uint32_t)(s0 + 32 * i);
@@ -457,7 +554,7 @@ __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
         }
         f(key96(v, id), ok, v, id, false, 0u);
       }
-      for (int i = 0; i < (kMemSlots + 31) / 32; ++i) {
+      for (int i = 0; i < kMPer; ++i) {
         const uint32_t j = (uint32_t)(s0 + 32 * i);
         const bool ok = j < nmq;
         double v = 0.0;
@@ -508,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void lmh_group_kernel(const LmhArgs L) {
   }
   if (tid == 0)
     L.g_pinfo[(int64_t)row * pinfo_stride(L.gparts) + g] =
-        (uint64_t)(np_out | (nm_out << 16) | (s_slow ? kPinfoSlow : 0u)) | ((uint64_t)bound << 32);
+        (uint64_t)(np_out | (nm_out << 16) | (s_slow ? kPinfoSlow : 0u)) | ((uint64_t)max(t, bound) << 32);
 }
 
 size_t lmh_scratch_bytes(int rows, int vocab) {
