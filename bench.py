@@ -297,6 +297,28 @@ def bench_lm_head(args) -> int:
     rows = int(args.workload[3:])
     b = W.lmh(rows=rows)
     set_bytes = b.algorithmic_bytes()
+    base = None
+    if not args.no_cpu_baseline and args.cpu_seconds > 0:
+        import time
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+
+        def cpu_step():
+            O.sample_rows(b.with_logits(O.lm_head_logits(b.hidden, b.weight_bits)), threads=1)
+        t0 = time.perf_counter()
+        cpu_step()
+        one = time.perf_counter() - t0
+        reps = max(1, min(10, int(round(args.cpu_seconds / max(one, 1e-3)))))
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            cpu_step()
+            times.append(time.perf_counter() - t0)
+        med = sorted(times)[len(times) // 2]
+        base = {"value": rows / med, "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"the whole step ({rows} row(s), vocab {b.vocab}, dim {b.dim}), {reps} passes (median): "
+                          "the C restatement of the head's dot products (orc_lm_head_logits, eight FMA chains "
+                          "per id) then of the sampling step (oracle/sampler_oracle.c), single thread"}
     if not torch.cuda.is_available():
         print("bench.py: no HIP device is visible", file=sys.stderr)
         return 1
@@ -338,7 +360,7 @@ def bench_lm_head(args) -> int:
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles(args.workload, "lm_head"),
                      "kernel": "sas::lmh_parts_kernel + lmh_group_kernel + sample_merge_kernel (one step)",
                      "algorithmic_bytes_per_launch": set_bytes},
-        "cpu_baseline": None,
+        "cpu_baseline": base,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -446,6 +446,35 @@ napi_value SampleStep(napi_env env, napi_callback_info info) {
   return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
 }
 
+// A sas_lm_head descriptor: {hidden, hiddenStride, weight, weightStride,
+// dim, outLogits?} of device addresses (BigInt) and sizes.
+bool read_head(napi_env env, napi_value d, sas_lm_head *hd) {
+  std::memset(hd, 0, sizeof *hd);
+  int64_t dim = 0;
+  const bool ok = get_ptr(env, d, "hidden", (void **)&hd->hidden) &&
+                  get_i64(env, d, "hiddenStride", &hd->hidden_stride) &&
+                  get_ptr(env, d, "weight", (void **)&hd->weight) &&
+                  get_i64(env, d, "weightStride", &hd->weight_stride) && get_i64(env, d, "dim", &dim) &&
+                  get_ptr(env, d, "outLogits", (void **)&hd->out_logits);
+  if (!ok || dim < INT32_MIN || dim > INT32_MAX) return false;
+  hd->dim = (int32_t)dim;
+  return true;
+}
+
+napi_value LmHeadSample(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_rows r;
+  sas_lm_head hd;
+  if (!read_rows(env, argv[1], &r) || !read_head(env, argv[2], &hd)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad lm head descriptor");
+    return nullptr;
+  }
+  int rc = sas_lm_head_sample(s, &hd, &r, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
 napi_value Verify(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
@@ -482,6 +511,8 @@ struct AsyncCall {
   bool verify = false;
   bool step = false;
   bool spec = false;
+  bool head = false;
+  sas_lm_head hd;
   sas_spec_rows srows;
   sas_rows rows;
   sas_step srow;
@@ -502,6 +533,7 @@ void async_execute(napi_env, void *data) {
   c->rc = c->verify ? sas_verify(s, &c->vrows, sas_stream(s))
           : c->step ? sas_sample_step(s, &c->rows, &c->srow, sas_stream(s))
           : c->spec ? sas_spec_exact(s, &c->srows, sas_stream(s))
+          : c->head ? sas_lm_head_sample(s, &c->hd, &c->rows, sas_stream(s))
                     : sas_sample(s, &c->rows, sas_stream(s));
   if (c->rc == SAS_OK) c->rc = sas_synchronize(s, sas_stream(s));
   if (c->rc != SAS_OK) c->err = sas_last_error(s);
@@ -590,6 +622,22 @@ napi_value SampleStepAsync(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   return start_async(env, c, argv[0], "sas_sample_step");
+}
+
+napi_value LmHeadSampleAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
+  AsyncCall *c = new AsyncCall();
+  c->h = h;
+  c->head = true;
+  if (!read_rows(env, argv[1], &c->rows) || !read_head(env, argv[2], &c->hd)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad lm head descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, argv[0], "sas_lm_head_sample");
 }
 
 napi_value SpecExactAsync(napi_env env, napi_callback_info info) {
@@ -776,6 +824,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"sampleAsync", nullptr, SampleAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sampleStep", nullptr, SampleStep, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sampleStepAsync", nullptr, SampleStepAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHeadSample", nullptr, LmHeadSample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHeadSampleAsync", nullptr, LmHeadSampleAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verify", nullptr, Verify, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verifyAsync", nullptr, VerifyAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"specExact", nullptr, SpecExact, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
@@ -798,7 +848,9 @@ napi_value Init(napi_env env, napi_value exports) {
                 {"FLAG_EMPTY_ROW", SAS_FLAG_EMPTY_ROW}, {"FLAG_TOPP_EDGE", SAS_FLAG_TOPP_EDGE},
                 {"FLAG_DRAW_EDGE", SAS_FLAG_DRAW_EDGE}, {"FLAG_SLOW_SELECT", SAS_FLAG_SLOW_SELECT},
                 {"HINT_NO_SOFTCAP", SAS_HINT_NO_SOFTCAP}, {"STOP_PAD", (double)SAS_STOP_PAD},
-                {"PARAMS_BYTES", (double)sizeof(sas_params)}};
+                {"PARAMS_BYTES", (double)sizeof(sas_params)},
+                {"LMH_MAX_ROWS", SAS_LMH_MAX_ROWS}, {"LMH_MAX_LDS_FLOATS", SAS_LMH_MAX_LDS_FLOATS},
+                {"LMH_MAX_VOCAB", SAS_LMH_MAX_VOCAB}};
   for (const auto &k : consts) {
     napi_create_double(env, k.value, &c);
     napi_set_named_property(env, exports, k.name, c);

@@ -137,6 +137,25 @@ export interface SampleRowsOptions {
   full?: boolean;
 }
 
+/** The LM head of lmHeadSample: logits[row][id] = sum over k of
+ * weight[id][k] (bf16, widened to f32) * hidden[row][k] (f32). */
+export interface LmHead {
+  /** [rows][hiddenStride] f32 final-normed hidden states. */
+  hidden: DeviceBuffer | Float32Array;
+  /** [vocab][weightStride] bf16 bits, device-resident. */
+  weight: DeviceBuffer;
+  /** A multiple of 256; rows * dim <= LMH_MAX_LDS_FLOATS. */
+  dim: number;
+  hiddenStride?: number;
+  weightStride?: number;
+  /** Also write the logits [rows][vocab] f32 here. */
+  outLogits?: DeviceBuffer;
+}
+
+export interface LmHeadSampleOptions extends Omit<SampleRowsOptions, 'logits' | 'stride'> {
+  head: LmHead;
+}
+
 export interface DecodeStepsOptions {
   /** Step i's logits [rows][stride], computed from the tokens in nextTokens. */
   logits(i: number, nextTokens: DeviceBuffer): DeviceBuffer | Float32Array | Promise<DeviceBuffer | Float32Array>;
@@ -224,6 +243,9 @@ export declare class Sampler {
   createTokenMaskState(vocab: number): TokenMaskState;
   sampleRows(opts: SampleRowsOptions): SampleRowsResult;
   sampleRowsAsync(opts: SampleRowsOptions): Promise<SampleRowsResult>;
+  /** The LM head with the sampling step fused (rows <= LMH_MAX_ROWS). */
+  lmHeadSample(opts: LmHeadSampleOptions): SampleRowsResult;
+  lmHeadSampleAsync(opts: LmHeadSampleOptions): Promise<SampleRowsResult>;
   decodeRows(opts: SampleRowsOptions): DecodeBatchResult[];
   decodeRowsAsync(opts: SampleRowsOptions): Promise<DecodeBatchResult[]>;
   decodeSteps(opts: DecodeStepsOptions): DecodeBatchResult[];
@@ -271,3 +293,6 @@ export declare const FLAG_EMPTY_ROW: number;
 export declare const FLAG_TOPP_EDGE: number;
 export declare const FLAG_DRAW_EDGE: number;
 export declare const STOP_PAD: number;
+export declare const LMH_MAX_ROWS: number;
+export declare const LMH_MAX_LDS_FLOATS: number;
+export declare const LMH_MAX_VOCAB: number;

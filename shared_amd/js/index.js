@@ -9,6 +9,8 @@
 //   Sampler#sample(cands, opts)       <- sample(), lib/webgpu-llm/tokenizer.js:151-178
 //   Sampler#sampleRows                <- the topk + sampler WGSL pair,
 //                                        lib/webgpu-llm/kernels.js:65-201, 1389-1449
+//   Sampler#lmHeadSample              <- the decode head and the topk pass after it,
+//                                        lib/webgpu-llm/model.js:466-471, gemma-model.js:786-799
 //   Sampler#verify                    <- acceptSpec, lib/webgpu-llm/kernels.js:211-369
 //   Sampler#decodeRows                <- the sampling tail of decodeBatch, lib/webgpu-llm/model.js:656-742,
 //                                        lib/webgpu-llm/gemma-model.js:921-992 ({ids, fed, eos, stopped, stopId})
@@ -502,8 +504,9 @@ class Sampler {
     const d = { rows: rows, vocab: vocab, logitsStride: stride };
     // logits: device buffer (resident), or a host Float32Array staged up
     // (a step loop sets them per step)
-    if (step) {
+    if (step || opts.head) {
       d.logits = null;
+      if (opts.head) d.logitsStride = 0;
     } else if (opts.logits instanceof DeviceBuffer) {
       d.logits = opts.logits.ptr;
     } else if (opts.logits instanceof Float32Array) {
@@ -687,6 +690,58 @@ class Sampler {
     return this._enqueue(function () {
       const r = self._describe(opts);
       return self._worker(addon.sampleAsync(self._handle(), r.desc))
+        .then(function () { return self._collect(opts, r.packed); });
+    });
+  }
+
+  // The sas_lm_head descriptor of opts.head: {hidden, weight, dim,
+  // hiddenStride?, weightStride?, outLogits?}.  The head (bf16 bits
+  // [vocab][weightStride]) must be device-resident; the hidden states may be
+  // a host Float32Array [rows][hiddenStride], staged up per call.
+  _describeHead(opts) {
+    const h = opts.head;
+    if (!h || typeof h !== 'object') throw new TypeError('head must be {hidden, weight, dim}');
+    const dim = h.dim;
+    if (!Number.isInteger(dim) || dim <= 0) throw new RangeError('head.dim must be a positive integer');
+    const hd = { dim: dim, hiddenStride: orDefault(h.hiddenStride, dim), weightStride: orDefault(h.weightStride, dim) };
+    if (h.hidden instanceof DeviceBuffer) {
+      hd.hidden = h.hidden.ptr;
+    } else if (h.hidden instanceof Float32Array) {
+      if (h.hidden.length < opts.rows * hd.hiddenStride) throw new RangeError('head.hidden holds fewer than rows * hiddenStride values');
+      hd.hidden = this._buf('hidden', h.hidden.byteLength).upload(h.hidden).ptr;
+    } else {
+      throw new TypeError('head.hidden must be a DeviceBuffer or a Float32Array');
+    }
+    if (!(h.weight instanceof DeviceBuffer)) throw new TypeError('head.weight must be a DeviceBuffer (bf16 bits)');
+    hd.weight = h.weight.ptr;
+    if (h.outLogits !== undefined && h.outLogits !== null) {
+      if (!(h.outLogits instanceof DeviceBuffer)) throw new TypeError('head.outLogits must be a DeviceBuffer');
+      hd.outLogits = h.outLogits.ptr;
+    }
+    return hd;
+  }
+
+  /**
+   * The LM head with the sampling step fused: logits = head.weight (bf16)
+   * times head.hidden (f32) for each row, summed in the library's fixed
+   * order, then sampled as sampleRows samples them.  opts as sampleRows
+   * without logits, plus head: {hidden, weight, dim, hiddenStride?,
+   * weightStride?, outLogits?}.  rows <= LMH_MAX_ROWS.
+   */
+  lmHeadSample(opts) {
+    this._idle('lmHeadSample');
+    const hd = this._describeHead(opts);
+    const r = this._describe(opts);
+    addon.lmHeadSample(this._handle(), r.desc, hd);
+    return this._collect(opts, r.packed);
+  }
+
+  lmHeadSampleAsync(opts) {
+    const self = this;
+    return this._enqueue(function () {
+      const hd = self._describeHead(opts);
+      const r = self._describe(opts);
+      return self._worker(addon.lmHeadSampleAsync(self._handle(), r.desc, hd))
         .then(function () { return self._collect(opts, r.packed); });
     });
   }
@@ -1067,4 +1122,7 @@ module.exports = {
   FLAG_TOPP_EDGE: addon.FLAG_TOPP_EDGE,
   FLAG_DRAW_EDGE: addon.FLAG_DRAW_EDGE,
   STOP_PAD: STOP_PAD,
+  LMH_MAX_ROWS: addon.LMH_MAX_ROWS,
+  LMH_MAX_LDS_FLOATS: addon.LMH_MAX_LDS_FLOATS,
+  LMH_MAX_VOCAB: addon.LMH_MAX_VOCAB,
 };

@@ -236,6 +236,25 @@ check('a sampler needs a HIP device and says so', function () {
   assert.throws(function () { return new sas.Sampler(0); }, /no HIP device/);
 });
 
+check('lmHeadSample describes its head and rejects bad ones on the host', function () {
+  const self = Object.create(sas.Sampler.prototype);
+  const fake = function (ptr) { const b = Object.create(sas.DeviceBuffer.prototype); b.ptr = ptr; return b; };
+  const hd = self._describeHead({ rows: 2, head: { hidden: fake(16n), weight: fake(4096n), dim: 512, outLogits: fake(8192n) } });
+  assert.deepStrictEqual(hd, { dim: 512, hiddenStride: 512, weightStride: 512, hidden: 16n, weight: 4096n, outLogits: 8192n });
+  const hs = self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(32n), dim: 256, hiddenStride: 300, weightStride: 264 } });
+  assert.strictEqual(hs.hiddenStride, 300);
+  assert.strictEqual(hs.weightStride, 264);
+  assert.strictEqual(hs.outLogits, undefined);
+  assert.throws(function () { self._describeHead({ rows: 1 }); }, TypeError);
+  assert.throws(function () { self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(32n), dim: 1.5 } }); }, RangeError);
+  assert.throws(function () { self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: new Uint16Array(256), dim: 256 } }); },
+    /head.weight must be a DeviceBuffer/);
+  assert.throws(function () { self._describeHead({ rows: 2, head: { hidden: new Float32Array(256), weight: fake(32n), dim: 256 } }); },
+    /fewer than rows \* hiddenStride/);
+  assert.throws(function () { self._describeHead({ rows: 1, head: { hidden: [1, 2], weight: fake(32n), dim: 256 } }); }, TypeError);
+  assert.strictEqual(sas.LMH_MAX_ROWS, 4);
+});
+
 check('version names the target', function () {
   assert.ok(/^shared_amd_sampler \d+ gfx950$/.test(sas.version()));
 });

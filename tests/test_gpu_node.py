@@ -222,3 +222,39 @@ def test_node_spec_exact(tmp_path):
             for q in range(c["seqs"]):
                 kept = [t for t in o["picks"][q][:int(o["accepted"][q])].tolist() if t not in stops[q]]
                 assert got["windows"][q] == hist[q] + kept, q
+
+
+def test_node_lm_head_sample(tmp_path):
+    """Sampler#lmHeadSample / lmHeadSampleAsync: the fused head's ids,
+    candidates and probabilities bit-exact with the oracle over the oracle's
+    head logits, and the logits it writes bit-exact with orc_lm_head_logits."""
+    if shutil.which("node") is None:
+        pytest.skip("node is not installed")
+    d = str(tmp_path)
+    b = W.lmh(rows=3, vocab=W.QWEN_VOCAB, dim=1024, seed=44, softcap=0.0)
+    lo = O.lm_head_logits(b.hidden, b.weight_bits)
+    bl = b.with_logits(lo)
+    O.write_case(d, bl)
+    with open(os.path.join(d, "meta.json")) as f:
+        meta = json.load(f)
+    meta["dim"] = b.dim
+    with open(os.path.join(d, "meta.json"), "w") as f:
+        json.dump(meta, f)
+    np.ascontiguousarray(b.hidden, np.float32).tofile(os.path.join(d, "hidden.f32"))
+    np.ascontiguousarray(b.weight_bits, np.uint16).tofile(os.path.join(d, "weight.u16"))
+    want = O.sample_rows(bl)
+
+    print("[gpu] node lmhead_gpu.js", d, flush=True)
+    proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "lmhead_gpu.js"), d], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-3000:]
+
+    got = np.fromfile(os.path.join(d, "lmh_logits.f32"), np.float32).reshape(b.rows, b.vocab)
+    assert np.array_equal(got.view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(_u32(d, "lmh_sync_ids.u32"), want["ids"])
+    probs = np.fromfile(os.path.join(d, "lmh_sync_probs.f64")).reshape(b.rows, -1)
+    assert np.array_equal(probs, want["probs"])
+    assert np.array_equal(_u32(d, "lmh_sync_cand.u32").reshape(b.rows, -1), want["cand_ids"])
+    for name in ("lmh_async_ids.u32", "lmh_unfused_ids.u32"):
+        assert np.array_equal(_u32(d, name), want["ids"]), name
