@@ -794,8 +794,7 @@ static_assert(kXCap >= SAS_MAX_TOP_K, "an exact part selection fits the exact li
 constexpr uint32_t kXMem = 0x80000000u;
 
 struct PartLds {
-  uint32_t hkey[kHashSlots];    // (id, count) open-addressing hash of the part's history ids
-  uint32_t hcnt[kHashSlots];
+  uint2 hent[kHashSlots];       // (id, count) open-addressing hash of the part's history ids
   uint32_t hbits[kPassWords];   // history membership of the pass's ids
   uint32_t comb[kPassWords];    // the pass's ids to select from: allowed, not history, inside the part
   uint32_t hmem[kPassWords];    // the pass's allowed history members
@@ -931,8 +930,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   };
   if (has_hist) {
     for (int s = tid; s < kHashSlots; s += kThreads) {
-      L.hkey[s] = kEmpty;
-      L.hcnt[s] = 0u;
+      L.hent[s] = make_uint2(kEmpty, 0u);
     }
     L.hbits[tid] = 0u;
     if (tid == 0) L.hover = 0u;
@@ -944,9 +942,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       uint32_t sl = hash_slot(id);
       int probe = 0;
       for (; probe < kHashSlots; ++probe) {
-        const uint32_t old = atomicCAS(&L.hkey[sl], kEmpty, id);
+        const uint32_t old = atomicCAS(&L.hent[sl].x, kEmpty, id);
         if (old == kEmpty || old == id) {
-          atomicAdd(&L.hcnt[sl], 1u);
+          atomicAdd(&L.hent[sl].y, 1u);
           break;
         }
         sl = (sl + 1u) & (uint32_t)(kHashSlots - 1);
@@ -972,8 +970,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   auto hcount = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
     uint32_t sl = hash_slot(id);
     for (int probe = 0; probe < kHashSlots; ++probe) {
-      const uint32_t kk = L.hkey[sl];
-      if (kk == id) return L.hcnt[sl];
+      const uint2 e = L.hent[sl];
+      const uint32_t kk = e.x;
+      if (kk == id) return e.y;
       if (kk == kEmpty) break;
       sl = (sl + 1u) & (uint32_t)(kHashSlots - 1);
     }
@@ -1288,9 +1287,10 @@ hipError_t launch_pad_rows(const float *src, int64_t stride, int vocab, int rows
 // buckets take the row's own index range of hb_ids (its CSR range, or
 // ring_len slots of a ring row).  Each round holds kBucketPer ids per
 // thread, all loaded before any is counted.
-constexpr int kBucketPer = 16;
+constexpr int kBucketPer = 4;
+constexpr int kBucketThreads = 1024;
 
-__global__ __launch_bounds__(kThreads) void hist_bucket_kernel(const SampleArgs a) {
+__global__ __launch_bounds__(kBucketThreads) void hist_bucket_kernel(const SampleArgs a) {
   __shared__ uint32_t s_cnt[kMaxParts + 1];
   __shared__ uint32_t s_cur[kMaxParts + 1];
   const int h = blockIdx.x, tid = threadIdx.x;
@@ -1322,19 +1322,19 @@ __global__ __launch_bounds__(kThreads) void hist_bucket_kernel(const SampleArgs 
   auto load_round = [&](int64_t r0) {
 #pragma unroll
     for (int j = 0; j < kBucketPer; ++j) {
-      const int64_t i = r0 + (int64_t)j * kThreads + tid;
+      const int64_t i = r0 + (int64_t)j * kBucketThreads + tid;
       v[j] = i < o1 ? ids[i] : 0xFFFFFFFFu;
     }
   };
-  constexpr int64_t kRound = (int64_t)kBucketPer * kThreads;
-  for (int q = tid; q <= P; q += kThreads) s_cnt[q] = 0u;
+  constexpr int64_t kRound = (int64_t)kBucketPer * kBucketThreads;
+  for (int q = tid; q <= P; q += kBucketThreads) s_cnt[q] = 0u;
   load_round(o0);
   __syncthreads();
   for (int64_t r0 = o0; r0 < o1; r0 += kRound) {
     if (r0 != o0) load_round(r0);
 #pragma unroll
     for (int j = 0; j < kBucketPer; ++j)
-      if (r0 + (int64_t)j * kThreads + tid < o1) atomicAdd(&s_cnt[part_of(v[j])], 1u);
+      if (r0 + (int64_t)j * kBucketThreads + tid < o1) atomicAdd(&s_cnt[part_of(v[j])], 1u);
   }
   __syncthreads();
   // offsets: an exclusive scan of the counts by the first wave
@@ -1373,7 +1373,7 @@ __global__ __launch_bounds__(kThreads) void hist_bucket_kernel(const SampleArgs 
 #pragma unroll
     for (int j = 0; j < kBucketPer; ++j) {
       const uint32_t q = part_of(v[j]);
-      if (r0 + (int64_t)j * kThreads + tid < o1 && q < (uint32_t)P) a.hb_ids[base + atomicAdd(&s_cur[q], 1u)] = v[j];
+      if (r0 + (int64_t)j * kBucketThreads + tid < o1 && q < (uint32_t)P) a.hb_ids[base + atomicAdd(&s_cur[q], 1u)] = v[j];
     }
   }
 }
@@ -1387,7 +1387,7 @@ static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) {
   if (a.hb_offs) {
     const int hrows = a.group > 1 ? a.rows / a.group : a.rows;
-    hipLaunchKernelGGL(hist_bucket_kernel, dim3((unsigned)hrows), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(hist_bucket_kernel, dim3((unsigned)hrows), dim3(kBucketThreads), 0, stream, a);
   }
   switch ((a.mask ? 4 : 0) | (a.hist_ids || a.ring ? 2 : 0) | (softcap ? 1 : 0)) {
     case 0: launch_kernel<false, false, false>(a, stream); break;
