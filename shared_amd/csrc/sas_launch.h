@@ -162,6 +162,7 @@ struct VerifyArgs {
   double *stats;   // [positions][chunks][4]: target max, target sum, draft max, draft sum
   double *part;    // [seqs][chunks][2]: residual mass, target mass of the decided position
   double *seqrec;  // [seqs][8]: decided position, its target max / sum, draft max / sum
+  float *dtok;     // [positions][2]: target and draft logit of the position's draft token (NaN: masked)
   int32_t vocab;
   int32_t seqs;
   int32_t L;

@@ -183,6 +183,16 @@ __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
   load_strided(a.target + (int64_t)pos * a.stride, base, a.vocab, a.aligned, xt);
   if (has_draft) load_strided(a.draft + ((int64_t)s * a.L + j) * a.stride, base, a.vocab, a.aligned, xq);
   const uint32_t ok = allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr, base, a.vocab);
+  if (has_draft && tid == 0) {
+    // the block whose chunk holds the position's draft token records the
+    // token's two logits for the acceptance test (NaN when masked)
+    const uint32_t d = a.draft_ids[(int64_t)s * a.L + j];
+    if (d < (uint32_t)a.vocab && (int64_t)(d / kVChunk) == (int64_t)c) {
+      const bool allowed = !kMask || ((a.mask[(int64_t)pos * a.mask_stride + (d >> 5)] >> (d & 31)) & 1u);
+      a.dtok[2 * pos] = allowed ? a.target[(int64_t)pos * a.stride + d] : __builtin_nanf("");
+      a.dtok[2 * pos + 1] = allowed ? a.draft[((int64_t)s * a.L + j) * a.stride + d] : __builtin_nanf("");
+    }
+  }
   const uint32_t okt = nan_free(xt, ok), okq = has_draft ? nan_free(xq, ok) : 0u;
   // the chunk's masked maxima of both rows
   float mt = -__builtin_inff(), mq = -__builtin_inff();
@@ -248,6 +258,17 @@ __device__ Decided decide(const VerifyArgs &a, int s, DecideLds &l) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int L = a.L, P1 = L + 1;
   const double T = a.temperature;
+  // the acceptance inputs (loaded with the statistics: nothing depends on them)
+  uint32_t d = 0u;
+  float dxt = 0.0f, dxq = 0.0f;
+  double u1 = 0.0;
+  if (tid < L) {
+    const int pos = s * P1 + tid;
+    d = a.draft_ids[(int64_t)s * L + tid];
+    dxt = a.dtok[2 * pos];
+    dxq = a.dtok[2 * pos + 1];
+    u1 = a.uniforms[(int64_t)pos * 2];
+  }
   for (int j = wave; j < P1; j += kWaves) {
     const double *st = a.stats + (int64_t)(s * P1 + j) * a.chunks * 4;
     for (int side = 0; side < (j < L ? 2 : 1); ++side) {
@@ -269,20 +290,16 @@ __device__ Decided decide(const VerifyArgs &a, int s, DecideLds &l) {
   __syncthreads();
   if (tid < L) {
     const int j = tid;
-    const int pos = s * P1 + j;
-    const uint32_t d = a.draft_ids[(int64_t)s * L + j];
     double pd = 0.0, qd = 0.0;
     const bool in_vocab = d < (uint32_t)a.vocab;
     if (in_vocab) {
-      const bool allowed = !a.mask || ((a.mask[(int64_t)pos * a.mask_stride + (d >> 5)] >> (d & 31)) & 1u);
-      const float xt = a.target[(int64_t)pos * a.stride + d];
-      const float xq = a.draft[((int64_t)s * L + j) * a.stride + d];
-      const double wt = allowed && xt == xt ? fd_exp(((double)xt - l.m[j][0]) / T) : 0.0;
-      const double wq = allowed && xq == xq ? fd_exp(((double)xq - l.m[j][1]) / T) : 0.0;
+      // dtok: written by the statistics pass for every in-vocabulary draft
+      // token (NaN when masked)
+      const double wt = dxt == dxt ? fd_exp(((double)dxt - l.m[j][0]) / T) : 0.0;
+      const double wq = dxq == dxq ? fd_exp(((double)dxq - l.m[j][1]) / T) : 0.0;
       pd = wt / l.z[j][0];
       qd = wq / l.z[j][1];
     }
-    const double u1 = a.uniforms[(int64_t)pos * 2];
     l.acc[j] = in_vocab && pd > 0.0 && u1 * qd <= pd;
   }
   __syncthreads();
@@ -608,7 +625,8 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
 size_t verify_scratch_bytes(int seqs, int L, int vocab) {
   const size_t chunks = ((size_t)vocab + kVChunk - 1) / kVChunk;
   const size_t positions = (size_t)seqs * (L + 1);
-  return (positions * chunks * 4 + (size_t)seqs * chunks * 2 + (size_t)seqs * 8) * sizeof(double);
+  return (positions * chunks * 4 + (size_t)seqs * chunks * 2 + (size_t)seqs * 8) * sizeof(double) +
+         positions * 2 * sizeof(float);
 }
 
 hipError_t launch_verify(const VerifyArgs &a, hipStream_t stream) {
