@@ -120,3 +120,43 @@ def test_empty_rows(sampler):
     b.mask[1, :] = 0
     g, _ = check(sampler, b, "empty row")
     assert g["ids"][1] == NO_TOKEN and g["flags"][1] & FLAG_EMPTY_ROW
+
+
+def test_strided_head_and_broadcast_mask(sampler):
+    # hidden rows and head rows wider than dim (hidden_stride 544, weight
+    # stride 520), one mask row for every row (mask_stride 0)
+    import torch
+    b = W.lmh(rows=3, vocab=70000, dim=512, seed=15, hist=300)
+    rng = np.random.default_rng(15)
+    hid_w = np.zeros((3, 544), np.float32)
+    hid_w[:, :512] = b.hidden
+    hid_w[:, 512:] = rng.standard_normal((3, 32)).astype(np.float32)  # never read
+    w_w = np.zeros((b.vocab, 520), np.uint16)
+    w_w[:, :512] = b.weight_bits
+    w_w[:, 512:] = 0x7FC0  # NaN bits: a read past dim would show
+    b.mask[:] = b.mask[0]
+    b.params = Params(temperature=0.8, top_k=20, top_p=0.9, repetition_penalty=1.2, presence_penalty=0.3)
+    print(f"[gpu] lm head strided: rows={b.rows} vocab={b.vocab} dim={b.dim}", flush=True)
+    hid = to_dev(hid_w)[:, :512]
+    wt = to_dev(w_w.view(np.int16))[:, :512]
+    mask_row = to_dev(b.mask[:1], torch.int32)
+    out = sampler.lm_head_sample(hid, wt, full=True, logits=True, dim=512,
+                                 mask=mask_row.expand(b.rows, -1),
+                                 hist_ids=to_dev(b.hist_ids, torch.int32), hist_offsets=to_dev(b.hist_offsets),
+                                 uniforms=to_dev(b.uniforms), params=b.params)
+    torch.cuda.synchronize()
+    lo = O.lm_head_logits(b.hidden, b.weight_bits)
+    got = out["logits"].cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), lo.view(np.uint32))
+    g = {"ids": out["ids"].cpu().numpy().view(np.uint32), "probs": out["probs"].cpu().numpy(),
+         "cand_ids": out["cand_ids"].cpu().numpy().view(np.uint32), "counts": out["counts"].cpu().numpy(),
+         "flags": out["flags"].cpu().numpy().view(np.uint32)}
+    assert_parity(g, O.sample_rows(b.with_logits(lo)), "lm head strided")
+
+
+def test_greedy_rows(sampler):
+    # temperature 0: the best penalized (value, id) of every row
+    b = W.lmh(rows=4, vocab=W.QWEN_VOCAB, dim=256, seed=16, softcap=0.0)
+    b.params = Params(temperature=0.0, top_k=1, repetition_penalty=1.3, frequency_penalty=0.5)
+    g, o = check(sampler, b, "greedy rows")
+    assert np.array_equal(g["ids"], o["ids"])
