@@ -36,6 +36,8 @@ WORKLOAD_DOC = {
     "C2": "T0.7 top-k40 top-p0.95, vocab 151936, batch 64, Zipf-biased N(0,3) logits",
     "C3": "bitmask 0.5-20% + top-k50 top-p0.9 T1.0, vocab 262144, batch 128, N(0,4) logits",
     "C3P": "C3 + repetition 1.1 / presence 0.5 / frequency 0.3 over 512 history ids, vocab 262144, batch 128",
+    "C3P8": "one GPU's share of C3P sharded 8 ways over the vocabulary: vocab 32768, batch 128, 64 history ids "
+            "per row (the step before the records' all-gather)",
     "C4": "repetition 1.15 / presence 0.5 / frequency 0.3 over 4096 Zipf history ids, greedy, vocab 262144, "
           "batch 256",
     "C5": "speculative verify (rejection sampling): 32 sequences x (4 drafts + 1 bonus), vocab 151936, draft "

@@ -299,4 +299,11 @@ def lmh(rows: int = 1, vocab: int = GEMMA_VOCAB, dim: int = 2560, seed: int = 7,
     return LmhBatch("LMH", hidden, w, p, mask=m, hist_ids=ids, hist_offsets=offs, uniforms=rng.random(rows))
 
 
-CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C3P": c3p, "C4": c4}
+def c3p_shard8(rows: int = 128, seed: int = 38) -> Batch:
+    """One GPU's share of C3P split 8 ways over the vocabulary: 32,768 ids
+    (a multiple of 32, so the mask words split cleanly) and the history ids
+    that fall in the shard (512 / 8 on average)."""
+    return c3p(rows, GEMMA_VOCAB // 8, seed, hist=512 // 8)
+
+
+CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C3P": c3p, "C3P8": c3p_shard8, "C4": c4}
