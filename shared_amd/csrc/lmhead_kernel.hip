@@ -58,10 +58,43 @@ static_assert(kLmhHash == 512, "lmh_slot yields 9 bits");
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
+// What the epilogue of one row reads from memory, loaded when the block
+// starts so that no round trip waits after the dot products: the row's
+// history range, its first 2 x 256 history ids, the mask word of this
+// lane's two ids.
+struct LmhPre {
+  int h0, h1;
+  uint32_t hid[2];
+  uint32_t mword;
+};
+
+// The history range and the mask word (no load depends on another)...
+__device__ __forceinline__ void lmh_prefetch_range(const SampleArgs &a, int row, int id0, LmhPre &q) {
+  q.h0 = 0;
+  q.h1 = 0;
+  if (a.hist_ids) {
+    const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
+    const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
+    q.h0 = (int)o0;
+    q.h1 = (int)o1;
+  }
+  // id0 is even: both ids share one mask word
+  q.mword = a.mask && id0 < a.vocab ? a.mask[(int64_t)row * a.mask_stride + (id0 >> 5)] : ~0u;
+}
+
+// ... then the first history ids, once the range is known.
+__device__ __forceinline__ void lmh_prefetch_ids(const SampleArgs &a, LmhPre &q) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = q.h0 + j * kThreads + (int)threadIdx.x;
+    q.hid[j] = i < q.h1 ? a.hist_ids[i] : kLmhEmpty;
+  }
+}
+
 // One row's part: values v[0..1] of ids id0, id0 + 1 (raw logits), the
 // row's parameters and history; writes the part's records and info word.
 __device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int row, int part, const float v_in[2],
-                                               int id0) {
+                                               int id0, const LmhPre &pf) {
   const SampleArgs &a = L.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int vocab = a.vocab;
@@ -73,13 +106,7 @@ __device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int 
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
   const int jw = (k + kWaves - 1) / kWaves;
   // ---- history: the row's ids inside the part, in a bitmap and a hash ----
-  int h0 = 0, h1 = 0;
-  if (a.hist_ids) {
-    const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
-    const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
-    h0 = (int)o0;
-    h1 = (int)o1;
-  }
+  const int h0 = pf.h0, h1 = pf.h1;
   for (int s = tid; s < kLmhHash; s += kThreads) {
     S.hkey[s] = kLmhEmpty;
     S.hcnt[s] = 0u;
@@ -93,10 +120,9 @@ __device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int 
     S.slow = 0u;
   }
   __syncthreads();
-  for (int i = h0 + tid; i < h1; i += kThreads) {
-    const uint32_t id = a.hist_ids[i];
+  auto insert = [&](uint32_t id) __attribute__((always_inline)) {
     const uint32_t off = id - (uint32_t)base;
-    if (off >= (uint32_t)nids) continue;
+    if (off >= (uint32_t)nids) return;
     atomicOr(&S.hbits[off >> 5], 1u << (off & 31u));
     uint32_t sl = lmh_slot(id);
     int probe = 0;
@@ -109,7 +135,12 @@ __device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int 
       sl = (sl + 1u) & (uint32_t)(kLmhHash - 1);
     }
     if (probe == kLmhHash) S.hover = 1u;
-  }
+  };
+  // the first 2 x 256 ids came with the block's first loads (kLmhEmpty past
+  // the range: never inside the part)
+  insert(pf.hid[0]);
+  insert(pf.hid[1]);
+  for (int i = h0 + 2 * kThreads + tid; i < h1; i += kThreads) insert(a.hist_ids[i]);
   __syncthreads();
   auto hcount = [&](uint32_t id) -> uint32_t {
     uint32_t sl = lmh_slot(id);
@@ -134,7 +165,7 @@ __device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int 
     float x = v_in[j];
     if (p.softcap > 0.0f) x = softcap_f32(x, p.softcap);
     bool ok = id < vocab && x == x;
-    if (ok && mrow) ok = ((mrow[id >> 5] >> (id & 31)) & 1u) != 0u;
+    if (ok && mrow) ok = ((pf.mword >> (id & 31)) & 1u) != 0u;
     const uint32_t off = (uint32_t)(id - base);
     const bool hm = ok && off < (uint32_t)nids && ((S.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u;
     mem[j] = hm;
@@ -271,11 +302,6 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
   const int base = part * kLmhSpan;
   const int dim = L.dim;
   const int vocab = L.s.vocab;
-  // ---- the rows' hidden states into LDS ----
-  for (int r = 0; r < R; ++r) {
-    const float *h = L.hidden + (int64_t)r * L.hidden_stride;
-    for (int i = tid; i < dim; i += kThreads) xs[r * dim + i] = h[i];
-  }
   // ---- the dot products.  Lanes work in groups of 8 on one id: lane g of
   // the group takes hidden indices 64 c + 8 g .. + 7 (c = 0, 1, ...), so a
   // group reads whole 128-byte lines of the weight row and a wave eight of
@@ -301,6 +327,18 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
   const int total = (kLmhSpan / 32) * nb;
   load_into(nxt, 0, 0);
   if (total > 1) load_into(nx2, nb > 1 ? 0 : 1, nb > 1 ? 1 : 0);
+  // while the first batches are in flight: the epilogue's inputs (read at
+  // the end, loaded now so that no round trip waits after the dot
+  // products) and the rows' hidden states into LDS
+  LmhPre pre[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
+  for (int r = 0; r < R; ++r) {
+    const float *h = L.hidden + (int64_t)r * L.hidden_stride;
+    for (int i = tid; i < dim; i += kThreads) xs[r * dim + i] = h[i];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) lmh_prefetch_ids(L.s, pre[r]);
   __syncthreads();  // the hidden states are in LDS
   for (int m = 0; m < kLmhSpan / 32; ++m) {
     float acc[R];
@@ -355,7 +393,7 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
       if (id0 < vocab) o[id0] = v[0];
       if (id0 + 1 < vocab) o[id0 + 1] = v[1];
     }
-    lmh_select_row(L, S, r, part, v, id0);
+    lmh_select_row(L, S, r, part, v, id0, pre[r]);
   }
 }
 
