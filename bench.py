@@ -33,6 +33,8 @@ METRIC = "rows/s + % HBM peak: 262k-vocab penalties+mask+top-k/top-p, B=128"
 HBM_PEAK_GBPS = 8000.0
 KERNEL = "sampler_step"  # the profiles/ summaries of the two launches of one step
 WORKLOAD_DOC = {
+    "C1": "greedy + repetition 1.1 over 512 history ids, vocab 151936, one row (the case the reference runs on "
+          "the CPU)",
     "C2": "T0.7 top-k40 top-p0.95, vocab 151936, batch 64, Zipf-biased N(0,3) logits",
     "C3": "bitmask 0.5-20% + top-k50 top-p0.9 T1.0, vocab 262144, batch 128, N(0,4) logits",
     "C3P": "C3 + repetition 1.1 / presence 0.5 / frequency 0.3 over 512 history ids, vocab 262144, batch 128",
