@@ -812,7 +812,9 @@ static_assert(kHashSlots == 512, "hash_slot yields 9 bits");
 // the same XCD (rows stay on one XCD), so from L2.
 __device__ __forceinline__ void put_rec(uint64_t *p, uint64_t v) { *p = v; }
 
-template <bool kMask, bool kHist, bool kSoftcap>
+// kList: the history is bucketed (long histories, kHist only): members may
+// ride in the lists (see `lower`).
+template <bool kMask, bool kHist, bool kSoftcap, bool kList>
 __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6) void sample_parts_kernel(const SampleArgs a) {
   __shared__ PartLds L;
   __shared__ uint32_t s_nw[kWaves];   // records of each wave's list
@@ -983,6 +985,13 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   };
   // ---- passes: values, the bound, the lists ---------------------------------
   const int jw = (k + kWaves - 1) / kWaves;  // per-wave rank of the bound
+  // Long (bucketed) histories, whose members are many, with penalties that
+  // only lower values (repetition >= 1, frequency >= 0, presence >= 0;
+  // rounding keeps this): a member whose raw value is below the bound stays
+  // below it, so members ride in the lists with their raw values and only
+  // those that reach the bound are penalized.  Otherwise every allowed
+  // member goes to the exact list from the slot loop.
+  const bool lower = kList && p.repetition_penalty >= 1.0 && p.frequency_penalty >= 0.0 && p.presence_penalty >= 0.0;
   const uint32_t sh = 4u * (uint32_t)(tid & 7);
   uint32_t tkey = 0u;  // the part's bound (okey image; 0 = none)
   uint32_t n_q = 0u;   // float4 entries of this wave's list (may pass kQuadCap: overflow)
@@ -1019,12 +1028,13 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
         v[f].z = softcap_f32(v[f].z, softcap);
         v[f].w = softcap_f32(v[f].w, softcap);
       }
+      uint32_t hn = 0u;
       if (has_hist) {
         // allowed history members of this float4: their values (in the
         // registers now) and ids go to the exact list, penalized after the
-        // passes
-        const uint32_t hn = (L.hmem[32 * f + (tid >> 3)] >> sh) & 0xFu;
-        if (__ballot(hn != 0u)) {
+        // passes (unless penalties only lower values)
+        hn = (L.hmem[32 * f + (tid >> 3)] >> sh) & 0xFu;
+        if (!(kList && lower) && __ballot(hn != 0u)) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             if ((hn >> j) & 1u) {
@@ -1039,15 +1049,27 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       }
       // bit j of the nibble -> all ones or zero, then one bit-field insert
       // keeps the value or puts a quiet NaN in its place
-      auto keep = [&](float x, uint32_t bit) {
-        const uint32_t msk = (uint32_t)__builtin_amdgcn_sbfe((int)nib, bit, 1u);  // 0 or ~0
+      auto keep = [&](float x, uint32_t nb, uint32_t bit) {
+        const uint32_t msk = (uint32_t)__builtin_amdgcn_sbfe((int)nb, bit, 1u);  // 0 or ~0
         return __uint_as_float((msk & __float_as_uint(x)) | (~msk & 0x7FC00000u));
       };
-      v[f].x = keep(v[f].x, 0u);
-      v[f].y = keep(v[f].y, 1u);
-      v[f].z = keep(v[f].z, 2u);
-      v[f].w = keep(v[f].w, 3u);
-      m = fmaxf(m, fmaxf(fmaxf(v[f].x, v[f].y), fmaxf(v[f].z, v[f].w)));
+      // the bound from the plain values; the lists also take the members'
+      // raw values when penalties only lower them
+      if constexpr (kList) {
+        m = fmaxf(m, fmaxf(fmaxf(keep(v[f].x, nib, 0u), keep(v[f].y, nib, 1u)),
+                           fmaxf(keep(v[f].z, nib, 2u), keep(v[f].w, nib, 3u))));
+        const uint32_t an = lower ? nib | hn : nib;
+        v[f].x = keep(v[f].x, an, 0u);
+        v[f].y = keep(v[f].y, an, 1u);
+        v[f].z = keep(v[f].z, an, 2u);
+        v[f].w = keep(v[f].w, an, 3u);
+      } else {
+        v[f].x = keep(v[f].x, nib, 0u);
+        v[f].y = keep(v[f].y, nib, 1u);
+        v[f].z = keep(v[f].z, nib, 2u);
+        v[f].w = keep(v[f].w, nib, 3u);
+        m = fmaxf(m, fmaxf(fmaxf(v[f].x, v[f].y), fmaxf(v[f].z, v[f].w)));
+      }
     }
     // the bound: at least jw lane maxima of every wave reach its own
     // result, so at least 4 jw >= k values of the part reach the smallest
@@ -1098,6 +1120,28 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const float4 q = qin ? L.q_val[qat] : make_float4(qnan(), qnan(), qnan(), qnan());
   const uint32_t qid = L.q_base[qat];
   uint32_t pm = (q.x >= tff ? 1u : 0u) | (q.y >= tff ? 2u : 0u) | (q.z >= tff ? 4u : 0u) | (q.w >= tff ? 8u : 0u);
+  if (kList && has_hist && lower) {
+    // members that reached the bound with their raw values: to the exact
+    // list, penalized below like the others
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if ((pm >> c) & 1u) {
+        const uint32_t id = qid + (uint32_t)c;
+        // one pass: the part's history bitmap is still in LDS
+        const uint32_t off = id - (uint32_t)lo;
+        const bool member = npass == 1 ? ((L.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u : hcount(id) != 0u;
+        if (member) {
+          pm &= ~(1u << c);
+          const uint32_t d = atomicAdd(&s_nx, 1u);
+          if (d < (uint32_t)kXCap) {
+            L.x_val[d] = (double)(c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w);
+            L.x_id[d] = id;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the exact list is complete
+  }
   const uint32_t qcnt = (uint32_t)__popc(pm);
   uint32_t qpre = 0u, qtot = 0u;
 #pragma unroll
@@ -1380,8 +1424,12 @@ __global__ __launch_bounds__(kBucketThreads) void hist_bucket_kernel(const Sampl
 
 template <bool kMask, bool kHist, bool kSoftcap>
 static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
-  hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap>), dim3((unsigned)(a.rows * a.parts)),
-                     dim3(kThreads), 0, stream, a);
+  if (kHist && a.hb_offs)
+    hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap, kHist>), dim3((unsigned)(a.rows * a.parts)),
+                       dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap, false>), dim3((unsigned)(a.rows * a.parts)),
+                       dim3(kThreads), 0, stream, a);
 }
 
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) {
