@@ -1121,8 +1121,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const uint32_t qid = L.q_base[qat];
   uint32_t pm = (q.x >= tff ? 1u : 0u) | (q.y >= tff ? 2u : 0u) | (q.z >= tff ? 4u : 0u) | (q.w >= tff ? 8u : 0u);
   if (kList && has_hist && lower) {
-    // members that reached the bound with their raw values: to the exact
-    // list, penalized below like the others
+    // members that reached the bound with their raw values: penalized here,
+    // and written as member records when they still reach it
+    uint4 *mrow4 = a.mrec + ((int64_t)row * P + part) * kMemSlots;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if ((pm >> c) & 1u) {
@@ -1132,15 +1133,21 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
         const bool member = npass == 1 ? ((L.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u : hcount(id) != 0u;
         if (member) {
           pm &= ~(1u << c);
-          const uint32_t d = atomicAdd(&s_nx, 1u);
-          if (d < (uint32_t)kXCap) {
-            L.x_val[d] = (double)(c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w);
-            L.x_id[d] = id;
+          const double pen = penalize((double)(c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w), hcount(id), p);
+          if (pen >= (double)tff) {
+            atomicAdd(&s_nxk, 1u);
+            const uint32_t d = atomicAdd(&s_nmw, 1u);
+            if (d < (uint32_t)kMemSlots) {
+              uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
+              put_rec(w, (uint64_t)__float_as_uint(rd_f32(pen)) | ((uint64_t)id << 32));
+              put_rec(w + 1, (uint64_t)__double_as_longlong(pen));
+            } else {
+              s_qover = 1u;  // more than the part's member slots: the exact selection
+            }
           }
         }
       }
     }
-    __syncthreads();  // the exact list is complete
   }
   const uint32_t qcnt = (uint32_t)__popc(pm);
   uint32_t qpre = 0u, qtot = 0u;
@@ -1212,6 +1219,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     if (tid < kWaves) s_nw[tid] = 0u;
     if (tid == 0) {
       s_nx = 0u;
+      s_nmw = 0u;  // member records the cut may have written are rewritten
       s_flags = SAS_FLAG_SLOW_SELECT;
     }
     if (need > 0u) {
@@ -1424,6 +1432,8 @@ __global__ __launch_bounds__(kBucketThreads) void hist_bucket_kernel(const Sampl
 
 template <bool kMask, bool kHist, bool kSoftcap>
 static void launch_kernel(const SampleArgs &a, hipStream_t stream) {
+  // the list mode pays only with the many members of long (bucketed)
+  // histories; short ones keep collecting members in the slot loop
   if (kHist && a.hb_offs)
     hipLaunchKernelGGL((sample_parts_kernel<kMask, kHist, kSoftcap, kHist>), dim3((unsigned)(a.rows * a.parts)),
                        dim3(kThreads), 0, stream, a);
