@@ -248,6 +248,34 @@ def test_dense_and_long_histories(sampler):
         check(sampler, b, label="dense_hist")
 
 
+def test_long_history_members_in_the_lists(sampler):
+    # bucketed (long) histories with penalties that only lower values: the
+    # members ride in the lists with their raw values.  Row 0's 1,024 members
+    # lead its first part (more than a part's member slots: the exact
+    # selection restarts its member records); row 1 mixes members and plain
+    # values near the top; the third case's repetition < 1 raises values
+    # (members collected in the slot loop instead)
+    rng = np.random.default_rng(23)
+    vocab, rows = 40000, 3
+    x = rng.standard_normal((rows, vocab)).astype(np.float32)
+    x[0, :1024] += np.float32(10.0)
+    x[1, 5000:5100] += np.float32(3.0)
+    hist = [np.concatenate([np.arange(0, 1024), rng.integers(0, vocab, 176)]),
+            np.concatenate([np.arange(5000, 5100, 2), rng.integers(0, vocab, 1150)]),
+            rng.integers(0, vocab, 1200)]
+    hi, ho = W._csr(hist)
+    for p in (Params(temperature=1.0, top_k=128, top_p=1.0, repetition_penalty=1.0001),
+              Params(temperature=0.9, top_k=40, top_p=0.9, repetition_penalty=1.3, frequency_penalty=0.4,
+                     presence_penalty=0.2),
+              Params(temperature=1.0, top_k=64, top_p=0.95, repetition_penalty=0.9),
+              Params(temperature=0.0, repetition_penalty=1.2, presence_penalty=0.5)):
+        b = W.Batch("members_in_lists", x, p, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+        print(f"[gpu] members in the lists {p}", flush=True)
+        g, _ = check(sampler, b, label="members_in_lists")
+        if p.repetition_penalty == 1.0001:
+            assert g["flags"][0] & FLAG_SLOW_SELECT
+
+
 def test_repeated_launches_reset_state(sampler):
     b = W.c3p(rows=32, vocab=50000)
     first = run_gpu(sampler, b)
