@@ -17,7 +17,9 @@
 //      the part reach it, so no value below it is in the row's top k;
 //   4. values at or above the bound go to per-wave LDS lists (one ballot per
 //      value slot); the part's history ids are handled one by one with their
-//      exact penalized double values;
+//      exact penalized double values (with long, bucketed histories and
+//      penalties that only lower values, members ride in the lists with
+//      their raw values and only those reaching the bound are penalized);
 //   5. the lists are written as records to the part's own slots: plain
 //      values as {fp32 value, id}, history members as {round-down key, id,
 //      exact double}.
