@@ -356,3 +356,46 @@ def test_one_mask_for_every_row(sampler):
     got = sampler.sample(lg, vocab=b.vocab, mask=shared, uniforms=u, params=b.params).cpu().numpy().view(np.uint32)
     want = O.sample_rows(b)["ids"]
     assert np.array_equal(got, want)
+
+
+def test_random_sweep(sampler):
+    # 200 seeded random cases, each bit-exact with the oracle: shapes from 7
+    # to 600,001 ids (multi-pass parts), ties, masks of 0.2-90 % density,
+    # short and long (bucketed) uniform or Zipf histories with members near
+    # the top, penalties that lower or raise values, softcap, greedy rows,
+    # top-k 1-128, top-p, and per-row params
+    for case in range(200):
+        rng = np.random.default_rng(70000 + case)
+        rows = int(rng.choice([1, 2, 3, 5, 8, 16]))
+        vocab = int(rng.choice([7, 300, 1024, 4097, 20000, 65536, 151936, 262144, 600001]))
+        sigma = float(rng.choice([0.5, 2.0, 4.0]))
+        x = (rng.standard_normal((rows, vocab)) * sigma).astype(np.float32)
+        if rng.random() < 0.3:
+            x = np.round(x * 2) / 2
+        mask = None
+        if rng.random() < 0.6:
+            d = float(rng.choice([0.002, 0.05, 0.3, 0.9]))
+            mask = W.random_mask(rng, rows, vocab, d, d)
+        hi = ho = None
+        hlen = int(rng.choice([0, 16, 512, 1500, 4096]))
+        if hlen:
+            hs = [rng.integers(0, vocab, hlen) if rng.random() < 0.5 else W.zipf_ranks(rng, hlen, vocab, 1.2) % vocab
+                  for _ in range(rows)]
+            hi, ho = W._csr(hs)
+            if rng.random() < 0.5:
+                for r in range(rows):
+                    x[r, hs[r][:64]] += np.float32(3 * sigma)
+
+        def params():
+            return Params(temperature=float(rng.choice([0.0, 0.7, 1.0, 1.5])), top_k=int(rng.integers(1, 129)),
+                          top_p=float(rng.choice([1.0, 0.9, 0.5])),
+                          repetition_penalty=float(rng.choice([1.0, 1.1, 1.5, 0.8])),
+                          presence_penalty=float(rng.choice([0.0, 0.5, -0.3])),
+                          frequency_penalty=float(rng.choice([0.0, 0.3, -0.2])),
+                          softcap=float(rng.choice([0.0, 0.0, 30.0])))
+        b = W.Batch("sweep", x, params(), mask=mask, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+        rp = [params() for _ in range(rows)] if rng.random() < 0.3 else None
+        if case % 50 == 0:
+            print(f"[gpu] random sweep case {case}", flush=True)
+        check(sampler, b, row_params=rp,
+              label=f"sweep {case}: rows={rows} vocab={vocab} hist={hlen} mask={mask is not None} rp={rp is not None}")
