@@ -160,3 +160,26 @@ def test_greedy_rows(sampler):
     b.params = Params(temperature=0.0, top_k=1, repetition_penalty=1.3, frequency_penalty=0.5)
     g, o = check(sampler, b, "greedy rows")
     assert np.array_equal(g["ids"], o["ids"])
+
+
+def test_random_sweep(sampler):
+    # 40 seeded random cases: 1-4 rows, dim 256-3072 within the LDS limit,
+    # vocabularies from 1 to 50,000, masks, histories, softcap, greedy rows,
+    # penalties that lower or raise values, per-row params
+    for case in range(40):
+        rng = np.random.default_rng(90000 + case)
+        rows = int(rng.integers(1, 5))
+        dim = int(rng.choice([d for d in range(256, 3073, 256) if rows * d <= 12288]))
+        vocab = int(rng.choice([1, 5, 300, 513, 4097, 20000, 50000]))
+        b = W.lmh(rows=rows, vocab=vocab, dim=dim, seed=90000 + case,
+                  hist=int(rng.choice([0, 16, 600])) if vocab > 16 else 0, softcap=float(rng.choice([0.0, 30.0])),
+                  mask=bool(rng.random() < 0.6))
+
+        def params():
+            return Params(temperature=float(rng.choice([0.0, 0.7, 1.0])), top_k=int(rng.integers(1, 129)),
+                          top_p=float(rng.choice([1.0, 0.9])), repetition_penalty=float(rng.choice([1.0, 1.2, 0.8])),
+                          presence_penalty=float(rng.choice([0.0, 0.5])),
+                          frequency_penalty=float(rng.choice([0.0, 0.3])), softcap=float(rng.choice([0.0, 30.0])))
+        b.params = params()
+        rp = [params() for _ in range(rows)] if rng.random() < 0.3 else None
+        check(sampler, b, f"sweep {case}: rows={rows} dim={dim} vocab={vocab}", row_params=rp)
