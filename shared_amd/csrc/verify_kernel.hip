@@ -170,6 +170,42 @@ __device__ __forceinline__ double side_sum(const float x[kPerThread], uint32_t o
   return wave_sum_d(z);
 }
 
+// Both sides' sums when they allow the same ids (the usual case: a NaN
+// logit in one row and not the other is rare): one packing of the allowed
+// ids' two values into the wave's LDS slots serves both, when at most
+// kCompact are allowed.  Returns false (nothing summed) otherwise.
+__device__ __forceinline__ bool joint_sums(const float xt[kPerThread], const float xq[kPerThread], uint32_t ok,
+                                           double Mt, double Mq, double inv_t, float *cvt, float *cvq, double &zt,
+                                           double &zq) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t n = (uint32_t)__popc(ok);
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t bb = __ballot((n >> bit) & 1u);
+    pre += lanes_below(bb) << bit;
+    tot += (uint32_t)__popcll(bb) << bit;
+  }
+  if (tot > (uint32_t)kCompact) return false;
+  uint32_t j = pre;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i)
+    if ((ok >> i) & 1u) {
+      cvt[j] = xt[i];
+      cvq[j] = xq[i];
+      ++j;
+    }
+  wave_lds_sync();
+  double st = 0.0, sq = 0.0;
+  for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
+    st += exp_sum(((double)cvt[e] - Mt) * inv_t);
+    sq += exp_sum(((double)cvq[e] - Mq) * inv_t);
+  }
+  zt = wave_sum_d(st);
+  zq = wave_sum_d(sq);
+  return true;
+}
+
 template <bool kMask>
 __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
   __shared__ StatsLds l;
@@ -216,8 +252,12 @@ __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
   }
   // sums of exp((x - max) / T)
   const double Mt = (double)bt, Mq = (double)bq;
-  const double zt = side_sum(xt, okt, Mt, a.inv_t, l.cv[wave][0]);
-  const double zq = has_draft ? side_sum(xq, okq, Mq, a.inv_t, l.cv[wave][1]) : 0.0;
+  double zt = 0.0, zq = 0.0;
+  const bool same = has_draft && __ballot(okt != okq) == 0ull;  // uniform over the wave
+  if (!(same && joint_sums(xt, xq, okt, Mt, Mq, a.inv_t, l.cv[wave][0], l.cv[wave][1], zt, zq))) {
+    zt = side_sum(xt, okt, Mt, a.inv_t, l.cv[wave][0]);
+    zq = has_draft ? side_sum(xq, okq, Mq, a.inv_t, l.cv[wave][1]) : 0.0;
+  }
   if (lane == 0) {
     l.z[wave][0] = zt;
     l.z[wave][1] = zq;
