@@ -37,18 +37,21 @@ static_assert(kLmhIds == 2, "a lane owns two ids of its part");
 constexpr int kLmhStep = 64;                   // hidden values per load step: 128 bytes of a weight row
 constexpr int kLmhHash = 512;                  // (id, count) hash slots of a part's history members
 constexpr uint32_t kLmhEmpty = 0xFFFFFFFFu;
-constexpr uint32_t kLmhMem = 0x80000000u;      // exact-selection entry flag: a history member
 
+// The epilogue's tables, one set per row of the call: the rows are
+// selected together, so each barrier serves all of them.
+template <int R>
 struct LmhLds {
-  uint32_t hkey[kLmhHash];
-  uint32_t hcnt[kLmhHash];
-  uint32_t hbits[kLmhSpan / 32];  // history membership of the part's ids
-  double x_val[kLmhSpan];         // the part's allowed members: penalized value, id
-  uint32_t x_id[kLmhSpan];
-  uint32_t thr[kWaves];           // each wave's bound key
-  uint32_t nw[kWaves];            // each wave's plain records
-  uint32_t nx, nxk, nmw, hover, slow;
-  uint32_t hist[256];             // block_select96
+  uint32_t hkey[R][kLmhHash];
+  uint32_t hcnt[R][kLmhHash];
+  uint32_t hbits[R][kLmhSpan / 32];  // history membership of the part's ids
+  uint32_t thr[R][kWaves];           // each wave's bound key
+  uint32_t nw[R][kWaves];            // each wave's plain records
+  uint32_t nmem[R];                  // members kept at or above the bound
+  uint32_t nmw[R];                   // member records written
+  uint32_t hover[R];                 // some history id did not fit in the hash
+  uint32_t nx, slow;                 // an exact selection's plain records, and whether one ran
+  uint32_t hist[256];                // block_select96
   uint32_t sel[4];
 };
 
@@ -91,211 +94,203 @@ __device__ __forceinline__ void lmh_prefetch_ids(const SampleArgs &a, LmhPre &q)
   }
 }
 
-// One row's part: values v[0..1] of ids id0, id0 + 1 (raw logits), the
-// row's parameters and history; writes the part's records and info word.
-__device__ __forceinline__ void lmh_select_row(const LmhArgs &L, LmhLds &S, int row, int part, const float v_in[2],
-                                               int id0, const LmhPre &pf) {
+// The part's selection for every row of the call: values v[r][0..1] of ids
+// id0, id0 + 1 (raw logits), each row's parameters and history; writes each
+// row's records and info word.  A member is penalized by the lane that holds
+// it (its count from the row's hash) and kept when it reaches the bound,
+// which comes from the plain values only.
+template <int R>
+__device__ __forceinline__ void lmh_select_rows(const LmhArgs &L, LmhLds<R> &S, int part, const float (&v_in)[R][2],
+                                                int id0, const LmhPre (&pf)[R]) {
   const SampleArgs &a = L.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int vocab = a.vocab;
   const int base = part * kLmhSpan;
   const int nids = min(kLmhSpan, vocab - base);
-  sas_params p = a.params;
-  if (a.row_params) p = load_row_params(a.row_params + row);
-  const bool greedy = !(p.temperature > 0.0);
-  const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
-  const int jw = (k + kWaves - 1) / kWaves;
-  // ---- history: the row's ids inside the part, in a bitmap and a hash ----
-  const int h0 = pf.h0, h1 = pf.h1;
-  for (int s = tid; s < kLmhHash; s += kThreads) {
-    S.hkey[s] = kLmhEmpty;
-    S.hcnt[s] = 0u;
-  }
-  if (tid < kLmhSpan / 32) S.hbits[tid] = 0u;
-  if (tid == 0) {
-    S.nx = 0u;
-    S.nxk = 0u;
-    S.nmw = 0u;
-    S.hover = 0u;
-    S.slow = 0u;
+  // ---- history: each row's ids inside the part, in a bitmap and a hash ----
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    for (int s2 = tid; s2 < kLmhHash; s2 += kThreads) {
+      S.hkey[r][s2] = kLmhEmpty;
+      S.hcnt[r][s2] = 0u;
+    }
+    if (tid < kLmhSpan / 32) S.hbits[r][tid] = 0u;
+    if (tid == 0) {
+      S.nmem[r] = 0u;
+      S.nmw[r] = 0u;
+      S.hover[r] = 0u;
+    }
   }
   __syncthreads();
-  auto insert = [&](uint32_t id) __attribute__((always_inline)) {
+  auto insert = [&](int r, uint32_t id) __attribute__((always_inline)) {
     const uint32_t off = id - (uint32_t)base;
     if (off >= (uint32_t)nids) return;
-    atomicOr(&S.hbits[off >> 5], 1u << (off & 31u));
+    atomicOr(&S.hbits[r][off >> 5], 1u << (off & 31u));
     uint32_t sl = lmh_slot(id);
     int probe = 0;
     for (; probe < kLmhHash; ++probe) {
-      const uint32_t old = atomicCAS(&S.hkey[sl], kLmhEmpty, id);
+      const uint32_t old = atomicCAS(&S.hkey[r][sl], kLmhEmpty, id);
       if (old == kLmhEmpty || old == id) {
-        atomicAdd(&S.hcnt[sl], 1u);
+        atomicAdd(&S.hcnt[r][sl], 1u);
         break;
       }
       sl = (sl + 1u) & (uint32_t)(kLmhHash - 1);
     }
-    if (probe == kLmhHash) S.hover = 1u;
+    if (probe == kLmhHash) S.hover[r] = 1u;
   };
-  // the first 2 x 256 ids came with the block's first loads (kLmhEmpty past
-  // the range: never inside the part)
-  insert(pf.hid[0]);
-  insert(pf.hid[1]);
-  for (int i = h0 + 2 * kThreads + tid; i < h1; i += kThreads) insert(a.hist_ids[i]);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // the first 2 x 256 ids came with the block's first loads (kLmhEmpty past
+    // the range: never inside the part)
+    insert(r, pf[r].hid[0]);
+    insert(r, pf[r].hid[1]);
+    for (int i = pf[r].h0 + 2 * kThreads + tid; i < pf[r].h1; i += kThreads) insert(r, a.hist_ids[i]);
+  }
   __syncthreads();
-  auto hcount = [&](uint32_t id) -> uint32_t {
+  auto hcount = [&](int r, uint32_t id) -> uint32_t {
     uint32_t sl = lmh_slot(id);
     for (int probe = 0; probe < kLmhHash; ++probe) {
-      const uint32_t kk = S.hkey[sl];
-      if (kk == id) return S.hcnt[sl];
+      const uint32_t kk = S.hkey[r][sl];
+      if (kk == id) return S.hcnt[r][sl];
       if (kk == kLmhEmpty) break;
       sl = (sl + 1u) & (uint32_t)(kLmhHash - 1);
     }
     uint32_t c = 0u;
-    if (S.hover)
-      for (int i = h0; i < h1; ++i) c += a.hist_ids[i] == id ? 1u : 0u;
+    if (S.hover[r])
+      for (int i = pf[r].h0; i < pf[r].h1; ++i) c += a.hist_ids[i] == id ? 1u : 0u;
     return c;
   };
-  // ---- values: softcap, mask, membership ----
-  const uint32_t *mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
-  float pv[2];      // plain candidates (NaN: none)
-  bool mem[2];      // allowed history members
+  // ---- values: softcap, mask, membership; members penalized here; the bound ----
+  sas_params p[R];
+  int kr[R];
+  float pv[R][2];   // plain candidates (NaN: none)
+  bool mem[R][2];   // allowed history members
+  double mv[R][2];  // their penalized values
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int id = id0 + j;
-    float x = v_in[j];
-    if (p.softcap > 0.0f) x = softcap_f32(x, p.softcap);
-    bool ok = id < vocab && x == x;
-    if (ok && mrow) ok = ((pf.mword >> (id & 31)) & 1u) != 0u;
-    const uint32_t off = (uint32_t)(id - base);
-    const bool hm = ok && off < (uint32_t)nids && ((S.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u;
-    mem[j] = hm;
-    pv[j] = ok && !hm ? x : qnan();
-    if (hm) {
-      const uint32_t d = atomicAdd(&S.nx, 1u);
-      S.x_val[d] = (double)x;  // d < kLmhSpan: one entry per id of the part
-      S.x_id[d] = (uint32_t)id;
+  for (int r = 0; r < R; ++r) {
+    p[r] = a.params;
+    if (a.row_params) p[r] = load_row_params(a.row_params + r);
+    kr[r] = !(p[r].temperature > 0.0) ? 1 : min(max(p[r].top_k, 1), SAS_MAX_TOP_K);
+    const uint32_t *mrow = a.mask ? a.mask + (int64_t)r * a.mask_stride : nullptr;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int id = id0 + j;
+      float x = v_in[r][j];
+      if (p[r].softcap > 0.0f) x = softcap_f32(x, p[r].softcap);
+      bool ok = id < vocab && x == x;
+      if (ok && mrow) ok = ((pf[r].mword >> (id & 31)) & 1u) != 0u;
+      const uint32_t off = (uint32_t)(id - base);
+      const bool hm = ok && off < (uint32_t)nids && ((S.hbits[r][off >> 5] >> (off & 31u)) & 1u) != 0u;
+      mem[r][j] = hm;
+      pv[r][j] = ok && !hm ? x : qnan();
+      mv[r][j] = hm ? penalize((double)x, hcount(r, (uint32_t)id), p[r]) : 0.0;
     }
-  }
-  // ---- the bound ----
-  const float m = fmaxf(pv[0], pv[1]);
-  const uint32_t tw = wave_jth_largest_key16(okey(m), jw);
-  if (lane == 0) S.thr[wave] = tw;
-  __syncthreads();
-  const uint32_t tkey = min(min(S.thr[0], S.thr[1]), min(S.thr[2], S.thr[3]));
-  const float tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
-  // ---- plain records: each wave's after the waves before it ----
-  const bool k0 = pv[0] >= tf, k1 = pv[1] >= tf;  // NaN never passes
-  const uint32_t c = (k0 ? 1u : 0u) + (k1 ? 1u : 0u);
-  const uint64_t b0 = __ballot(c & 1u), b1 = __ballot((c >> 1) & 1u);
-  const uint32_t pre = lanes_below(b0) + 2u * lanes_below(b1);
-  if (lane == 0) S.nw[wave] = (uint32_t)__popcll(b0) + 2u * (uint32_t)__popcll(b1);
-  // members: penalized doubles kept at or above the bound
-  const uint32_t nx = S.nx;  // complete: every member was listed before the bound barrier
-  bool xw = false;
-  double xv = 0.0;
-  uint32_t xid = 0u;
-  for (int i = tid; i < (int)nx; i += kThreads) {
-    // at most kLmhSpan entries: two per thread
-    const double pvv = penalize(S.x_val[i], hcount(S.x_id[i]), p);
-    if (pvv >= (double)tf) {
-      atomicAdd(&S.nxk, 1u);
-      if (i == tid) {
-        xw = true;
-        xv = pvv;
-        xid = S.x_id[i];
-      } else {
-        S.x_val[i] = pvv;  // the second entry of this thread keeps its value in LDS
-        S.x_id[i] |= kLmhMem;
-      }
-    }
+    const float m = fmaxf(pv[r][0], pv[r][1]);
+    const uint32_t tw = wave_jth_largest_key16(okey(m), (kr[r] + kWaves - 1) / kWaves);
+    if (lane == 0) S.thr[r][wave] = tw;
   }
   __syncthreads();
-  uint32_t off = 0u;
+  // ---- plain records: each wave's after the waves before it; members kept ----
+  uint32_t tkey[R], pre[R];
+  float tf[R];
+  bool k0[R], k1[R], m0[R], m1[R];
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) off += w < wave ? S.nw[w] : 0u;
-  const uint32_t nplain = S.nw[0] + S.nw[1] + S.nw[2] + S.nw[3];
-  const uint32_t nmem = S.nxk;
-  const int64_t pq = (int64_t)row * a.parts + part;
-  uint64_t *rrow = a.rec + pq * kListCap;
-  uint4 *mrow4 = a.mrec + pq * kMemSlots;
-  uint32_t np_out = nplain, nm_out = nmem;
-  if (nmem <= (uint32_t)kMemSlots) {
-    uint32_t j = off + pre;
-    if (k0) rrow[j++] = (uint64_t)__float_as_uint(pv[0]) | ((uint64_t)(uint32_t)id0 << 32);
-    if (k1) rrow[j] = (uint64_t)__float_as_uint(pv[1]) | ((uint64_t)(uint32_t)(id0 + 1) << 32);
-    auto put_member = [&](double val, uint32_t id) {
-      const uint32_t d = atomicAdd(&S.nmw, 1u);
+  for (int r = 0; r < R; ++r) {
+    tkey[r] = min(min(S.thr[r][0], S.thr[r][1]), min(S.thr[r][2], S.thr[r][3]));
+    tf[r] = tkey[r] > 0x007FFFFFu ? fkey(tkey[r]) : -__builtin_inff();
+    k0[r] = pv[r][0] >= tf[r];  // NaN never passes
+    k1[r] = pv[r][1] >= tf[r];
+    const uint32_t c = (k0[r] ? 1u : 0u) + (k1[r] ? 1u : 0u);
+    const uint64_t b0 = __ballot(c & 1u), b1 = __ballot((c >> 1) & 1u);
+    pre[r] = lanes_below(b0) + 2u * lanes_below(b1);
+    if (lane == 0) S.nw[r][wave] = (uint32_t)__popcll(b0) + 2u * (uint32_t)__popcll(b1);
+    m0[r] = mem[r][0] && mv[r][0] >= (double)tf[r];  // NaN never passes
+    m1[r] = mem[r][1] && mv[r][1] >= (double)tf[r];
+    const uint32_t nm = (m0[r] ? 1u : 0u) + (m1[r] ? 1u : 0u);
+    if (nm) atomicAdd(&S.nmem[r], nm);
+  }
+  __syncthreads();
+  // ---- records, row by row (a row past its member slots selects exactly) ----
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t off = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) off += w < wave ? S.nw[r][w] : 0u;
+    const uint32_t nplain = S.nw[r][0] + S.nw[r][1] + S.nw[r][2] + S.nw[r][3];
+    const uint32_t nmem = S.nmem[r];
+    const int64_t pq = (int64_t)r * a.parts + part;
+    uint64_t *rrow = a.rec + pq * kListCap;
+    uint4 *mrow4 = a.mrec + pq * kMemSlots;
+    uint32_t np_out = nplain, nm_out = nmem, slow = 0u;
+    auto put_member = [&](uint32_t d, double val, uint32_t id) __attribute__((always_inline)) {
       uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
       w[0] = (uint64_t)__float_as_uint(rd_f32(val)) | ((uint64_t)id << 32);
       w[1] = (uint64_t)__double_as_longlong(val);
     };
-    if (xw) put_member(xv, xid);
-    const int i2 = tid + kThreads;
-    if (i2 < (int)nx && (S.x_id[i2] & kLmhMem)) put_member(S.x_val[i2], S.x_id[i2] & ~kLmhMem);
-  } else {
-    // more members above the bound than a part's member slots hold: the
-    // part's exact top k over (value, id), every value computed again
-    // from the registers and the history
-    const float xr[2] = {v_in[0], v_in[1]};
-    auto for_elems = [&](auto f) {
+    if (nmem <= (uint32_t)kMemSlots) {
+      uint32_t j = off + pre[r];
+      if (k0[r]) rrow[j++] = (uint64_t)__float_as_uint(pv[r][0]) | ((uint64_t)(uint32_t)id0 << 32);
+      if (k1[r]) rrow[j] = (uint64_t)__float_as_uint(pv[r][1]) | ((uint64_t)(uint32_t)(id0 + 1) << 32);
+      if (m0[r]) put_member(atomicAdd(&S.nmw[r], 1u), mv[r][0], (uint32_t)id0);
+      if (m1[r]) put_member(atomicAdd(&S.nmw[r], 1u), mv[r][1], (uint32_t)(id0 + 1));
+    } else {
+      // more members above the bound than a part's member slots hold: the
+      // part's exact top k over (value, id), every value computed again
+      const uint32_t *mrow = a.mask ? a.mask + (int64_t)r * a.mask_stride : nullptr;
+      auto for_elems = [&](auto f) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int id = id0 + j;
-        float x = xr[j];
-        if (p.softcap > 0.0f) x = softcap_f32(x, p.softcap);
-        bool ok = id < vocab && x == x;
-        if (ok && mrow) ok = ((mrow[id >> 5] >> (id & 31)) & 1u) != 0u;
-        double val = (double)x;
-        if (ok && mem[j]) val = penalize(val, hcount((uint32_t)id), p);
-        ok = ok && val == val;
-        f(key96(val, (uint32_t)id), ok, val, (uint32_t)id, mem[j]);
-      }
-    };
-    uint32_t nval = 0u;
-    for_elems([&](const Key96 &, bool ok, double, uint32_t, bool) { nval += ok ? 1u : 0u; });
-    if (tid == 0) S.sel[3] = 0u;
-    __syncthreads();
-    atomicAdd(&S.sel[3], nval);
-    __syncthreads();
-    const uint32_t need = min(S.sel[3], (uint32_t)k);
-    __syncthreads();
-    if (tid == 0) {
-      S.nx = 0u;
-      S.nmw = 0u;
-      S.slow = 1u;
-    }
-    __syncthreads();
-    if (need > 0u) {
-      const Key96 kth = block_select96(
-          [&](auto f) { for_elems([&](const Key96 &kx, bool ok, double, uint32_t, bool) { f(kx, ok); }); }, need,
-          S.hist, S.sel);
-      for_elems([&](const Key96 &kx, bool ok, double val, uint32_t id, bool member) {
-        if (ok && key_ge(kx, kth)) {
-          if (member) {
-            const uint32_t d = atomicAdd(&S.nmw, 1u);
-            uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
-            w[0] = (uint64_t)__float_as_uint(rd_f32(val)) | ((uint64_t)id << 32);
-            w[1] = (uint64_t)__double_as_longlong(val);
-          } else {
-            rrow[atomicAdd(&S.nx, 1u)] = (uint64_t)__float_as_uint((float)val) | ((uint64_t)id << 32);
-          }
+        for (int j = 0; j < 2; ++j) {
+          const int id = id0 + j;
+          float x = v_in[r][j];
+          if (p[r].softcap > 0.0f) x = softcap_f32(x, p[r].softcap);
+          bool ok = id < vocab && x == x;
+          if (ok && mrow) ok = ((mrow[id >> 5] >> (id & 31)) & 1u) != 0u;
+          double val = (double)x;
+          if (ok && mem[r][j]) val = mv[r][j];
+          ok = ok && val == val;
+          f(key96(val, (uint32_t)id), ok, val, (uint32_t)id, mem[r][j]);
         }
-      });
+      };
+      uint32_t nval = 0u;
+      for_elems([&](const Key96 &, bool ok, double, uint32_t, bool) { nval += ok ? 1u : 0u; });
+      if (tid == 0) S.sel[3] = 0u;
+      __syncthreads();
+      atomicAdd(&S.sel[3], nval);
+      __syncthreads();
+      const uint32_t need = min(S.sel[3], (uint32_t)kr[r]);
+      __syncthreads();
+      if (tid == 0) {
+        S.nx = 0u;
+        S.nmw[r] = 0u;
+      }
+      __syncthreads();
+      if (need > 0u) {
+        const Key96 kth = block_select96(
+            [&](auto f) { for_elems([&](const Key96 &kx, bool ok, double, uint32_t, bool) { f(kx, ok); }); }, need,
+            S.hist, S.sel);
+        for_elems([&](const Key96 &kx, bool ok, double val, uint32_t id, bool member) {
+          if (ok && key_ge(kx, kth)) {
+            if (member) put_member(atomicAdd(&S.nmw[r], 1u), val, id);
+            else rrow[atomicAdd(&S.nx, 1u)] = (uint64_t)__float_as_uint((float)val) | ((uint64_t)id << 32);
+          }
+        });
+      }
+      __syncthreads();
+      np_out = S.nx;
+      nm_out = S.nmw[r];
+      slow = 1u;
+      __syncthreads();  // S.nx and S.sel are reused by the next row
     }
-    __syncthreads();
-    np_out = S.nx;
-    nm_out = S.nmw;
+    if (tid == 0)
+      a.pinfo[(int64_t)r * pinfo_stride(a.parts) + part] =
+          (uint64_t)(np_out | (nm_out << 16) | (slow ? kPinfoSlow : 0u)) | ((uint64_t)tkey[r] << 32);
   }
-  if (tid == 0)
-    a.pinfo[(int64_t)row * pinfo_stride(a.parts) + part] =
-        (uint64_t)(np_out | (nm_out << 16) | (S.slow ? kPinfoSlow : 0u)) | ((uint64_t)tkey << 32);
-  __syncthreads();  // the LDS tables are reused by the next row
 }
 
 template <int R>
 __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L) {
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [R][dim] hidden states
-  __shared__ LmhLds S;
+  __shared__ LmhLds<R> S;
   __shared__ float s_logit[R][kLmhSpan];  // the part's logits, row by row
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int part = blockIdx.x;
@@ -383,18 +378,20 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
     }
   }
   __syncthreads();
-  // ---- the epilogue, row by row: lane t takes ids base + 2 t, + 1 ----
+  // ---- the epilogue, all rows together: lane t takes ids base + 2 t, + 1 ----
   const int id0 = base + kLmhIds * tid;
+  float v[R][2];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float v[2] = {s_logit[r][kLmhIds * tid], s_logit[r][kLmhIds * tid + 1]};
+    v[r][0] = s_logit[r][kLmhIds * tid];
+    v[r][1] = s_logit[r][kLmhIds * tid + 1];
     if (L.out_logits) {
       float *o = L.out_logits + (int64_t)r * vocab;
-      if (id0 < vocab) o[id0] = v[0];
-      if (id0 + 1 < vocab) o[id0 + 1] = v[1];
+      if (id0 < vocab) o[id0] = v[r][0];
+      if (id0 + 1 < vocab) o[id0 + 1] = v[r][1];
     }
-    lmh_select_row(L, S, r, part, v, id0, pre[r]);
   }
+  lmh_select_rows<R>(L, S, part, v, id0, pre);
 }
 
 // One block per (row, group of kLmhGroup parts).  The records kept are
