@@ -7,7 +7,11 @@
  * temperature, top-k, top-p and the categorical draw with a host-supplied
  * uniform (or greedy argmax).  A second call runs speculative verification
  * (accept/resample of draft tokens).  Everything is stream-ordered on the
- * caller's HIP stream; no call blocks unless its name says so.
+ * caller's HIP stream; no call blocks unless its name says so.  A call
+ * whose scratch is already sized (by sas_reserve, or by an earlier call of
+ * the same shape on the handle) issues kernel launches on `stream` and
+ * nothing else: no allocation, memset or synchronisation, so it can be
+ * recorded into a hipGraph by stream capture and replayed.
  *
  * Reference interfaces replaced (paths relative to the reference repo):
  *   sas_sample        <- sample()            lib/webgpu-llm/tokenizer.js:151-178
