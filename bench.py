@@ -63,6 +63,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work of the baseline sample (0 disables it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph-steps", type=int, default=0,
+                    help="sampling workloads: record this many steps (input sets in turn) into one HIP graph by "
+                         "stream capture and time its replays (the k-step submit of a decode loop)")
     ap.add_argument("--row-params", action="store_true",
                     help="pass the workload's parameters per row (row_params, with the no-softcap hint) "
                          "instead of one sas_params for every row")
@@ -447,11 +450,29 @@ def main() -> int:
             j = i % nsets
             s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
         torch.cuda.synchronize()
+        per = args.graph_steps
+        if per > 0:
+            # the handle's scratch is sized by reserve() and the calls above,
+            # so a captured call records kernel launches only
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cs = torch.cuda.current_stream()
+                for i in range(per):
+                    j = i % nsets
+                    s.sample_into(out_ids=out_ids[j], stream=cs, **sets[j])
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            args.steps = max(1, args.steps // per) * per
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for i in range(args.steps):
-            j = i % nsets
-            s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
+        if per > 0:
+            for _ in range(args.steps // per):
+                g.replay()
+        else:
+            for i in range(args.steps):
+                j = i % nsets
+                s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
         end.record(stream)
         torch.cuda.synchronize()
         ms_total = start.elapsed_time(end)
@@ -478,7 +499,9 @@ def main() -> int:
                    "top_k": first.params.top_k, "top_p": first.params.top_p,
                    "temperature": first.params.temperature, "input_sets": nsets,
                    "rotating_set_mb": round(nsets * set_bytes / 1e6, 1),
-                   "params": "per row (row_params)" if args.row_params else "one sas_params for every row"},
+                   "params": "per row (row_params)" if args.row_params else "one sas_params for every row",
+                   "launch": f"HIP graph of {args.graph_steps} steps, replayed" if args.graph_steps > 0
+                   else "stream launches"},
         "topp_edge_rows": {"rows": edge_rows, "of": nsets * rows,
                            "rule": "top-p running mass within 1e-6 of top_p (SAS_FLAG_TOPP_EDGE)"},
         "gbps": achieved,
