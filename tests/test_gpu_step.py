@@ -189,3 +189,46 @@ def test_step_rejects_bad_descriptors(sampler):
     call(rows_descriptor(x[:0], ids, params=Params(temperature=1.0)), st.descriptor())
     torch.cuda.synchronize()
     assert st.state.cpu().numpy().tolist() == [[0, 0]] * rows
+
+
+def test_random_sweep(sampler):
+    # 40 seeded random cases: 1-12 rows, vocabularies 300 to 262,144, 2-6
+    # steps, rings of 1 to 4,096 ids (bucketed from 2,048), seeded or host
+    # uniforms, masks, stop ids among the tall ids, histories longer than the
+    # ring, per-row params that lower or raise values, softcap
+    from shared_amd import workloads as W
+    for case in range(40):
+        rng = np.random.default_rng(70000 + case)
+        rows, vocab = int(rng.integers(1, 13)), int(rng.choice([300, 5000, 50_000, 151_936, 262_144]))
+        steps, ring_len = int(rng.integers(2, 7)), int(rng.choice([1, 3, 64, 512, 2048, 4096]))
+        seeded = bool(rng.random() < 0.6)
+        spikes = [int(v) for v in rng.integers(0, vocab, 5)]
+        xs = spiky_logits(rng, steps, rows, vocab, spikes, height=float(rng.choice([2.0, 6.0])))
+        prm = [Params(temperature=float(rng.choice([0.0, 0.7, 1.0])), top_k=int(rng.integers(1, 129)),
+                      top_p=float(rng.choice([1.0, 0.9])), repetition_penalty=float(rng.choice([1.0, 1.3, 0.8])),
+                      presence_penalty=float(rng.choice([0.0, 0.7, -0.5])),
+                      frequency_penalty=float(rng.choice([0.0, 0.4])), softcap=float(rng.choice([0.0, 0.0, 30.0])))
+               for _ in range(rows)]
+        mask = None
+        if rng.random() < 0.4:
+            d = float(rng.choice([0.01, 0.3, 0.9]))
+            mask = W.random_mask(rng, rows, vocab, d, d)
+            for r in range(rows):
+                if rng.random() < 0.5:
+                    for sid in spikes:
+                        mask[r, sid >> 5] |= np.uint32(1 << (sid & 31))
+        stop_ids = [[int(v) for v in rng.choice(spikes, int(rng.integers(0, 3)), replace=False)]
+                    if rng.random() < 0.5 else [] for _ in range(rows)]
+        pool = spikes + [int(u) for u in rng.integers(0, vocab, 8)]
+        history = [[int(v) for v in rng.choice(pool, int(rng.integers(0, 3000)))] for _ in range(rows)]
+        seeds = rng.integers(0, 2**32, rows, dtype=np.uint64).astype(np.uint32) if seeded else None
+        uniforms = None if seeded else rng.random((steps, rows))
+        label = f"sweep {case}: rows={rows} vocab={vocab} steps={steps} ring={ring_len} seeded={seeded}"
+        print(f"[gpu] {label}", flush=True)
+        state = DecodeState(rows, max_steps=int(rng.integers(1, steps + 1)), ring_len=ring_len, stop_ids=stop_ids,
+                            seeds=seeds, history=history)
+        got = run_steps(sampler, xs, prm, state, mask=mask, uniforms=uniforms)
+        want, stopped, it, window = oracle_steps(xs, prm, mask=mask, stop_ids=stop_ids, seeds=seeds,
+                                                 uniforms=uniforms, history=history, ring_len=ring_len)
+        assert_steps(got, want, label)
+        assert_state(state, stopped, it, window, got, ring_len, label)
