@@ -97,3 +97,28 @@ def test_spec_rejects_bad_descriptors(sampler):
     with pytest.raises(SasError, match="draft_len"):
         sampler.spec_exact_into(torch.zeros((42, 1000), device="cuda"), big, dev(c["seeds"], torch.int32),
                                 torch.empty((2, 21), dtype=torch.int32, device="cuda"), acc)
+
+
+def test_random_sweep(sampler):
+    # 30 seeded random rounds: 1-16 sequences, 1-16 drafts, vocabularies 300
+    # to 151,936, masks, histories up to 1,500 ids, greedy and sampled
+    # sequences, drafts from the draft head or handed in, stop ids among the
+    # target's own picks
+    for case in range(30):
+        rng = np.random.default_rng(80000 + case)
+        seqs, L = int(rng.integers(1, 17)), int(rng.choice([1, 2, 3, 4, 8, 16]))
+        vocab = int(rng.choice([300, 5000, 40_000, W.QWEN_VOCAB]))
+        c = W.spec_case(seqs=seqs, vocab=vocab, drafts=L, hist=int(rng.choice([0, 64, 1500])),
+                        mask=bool(rng.random() < 0.4), greedy_every=int(rng.integers(0, 4)), seed=80000 + case)
+        given = bool(rng.random() < 0.3)
+        if given:
+            o0 = O.spec_exact(c)
+            c["draft_ids"] = o0["draft_ids"].copy()
+            miss = rng.random(c["draft_ids"].shape) < 0.3
+            c["draft_ids"][miss] = rng.integers(0, vocab, int(miss.sum()))
+            c["draft"] = None
+            if rng.random() < 0.5:
+                c["stop_ids"][:, 1] = o0["picks"][:, 0]
+        label = f"sweep {case}: seqs={seqs} L={L} vocab={vocab} given={given}"
+        print(f"[gpu] spec {label}", flush=True)
+        check(run_spec(sampler, c, drafts_given=given), O.spec_exact(c), label)
