@@ -181,6 +181,18 @@ def test_masked_out_rows_and_nans(sampler):
             assert (w >> (tok & 31)) & 1, (s, j, tok)
 
 
+@pytest.mark.parametrize("density", [0.05, None])  # packed sums (sparse mask) and every id summed (no mask)
+def test_nans_in_both_rows_of_a_position(sampler, density):
+    # a position whose target and draft rows hold NaNs at different ids, and
+    # one whose draft row is all NaN: each side leaves out its own NaNs
+    inp = _random_inp(18, 5, 3, 9000, density)
+    for s in range(5):
+        inp["target"][s * 4 + 1, s::11] = np.nan
+        inp["draft"][s * 3 + 1, (s + 3)::13] = np.nan
+    inp["draft"][2 * 3 + 0, :] = np.nan
+    check(sampler, inp, f"nans density {density}")
+
+
 def test_tokens_respect_the_mask_at_c5(sampler):
     inp = W.c5(seqs=8)
     g = run_verify(sampler, inp)
