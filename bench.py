@@ -64,8 +64,8 @@ def parse_args():
                     help="approximate CPU work of the baseline sample (0 disables it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph-steps", type=int, default=0,
-                    help="sampling workloads: record this many steps (input sets in turn) into one HIP graph by "
-                         "stream capture and time its replays (the k-step submit of a decode loop)")
+                    help="record this many steps (input sets in turn) into one HIP graph by stream capture and "
+                         "time its replays (the k-step submit of a decode loop)")
     ap.add_argument("--row-params", action="store_true",
                     help="pass the workload's parameters per row (row_params, with the no-softcap hint) "
                          "instead of one sas_params for every row")
@@ -194,6 +194,41 @@ def cpu_baseline(batch, target_s: float) -> dict:
             "ids": np.asarray(o["ids"])}
 
 
+def timed_steps(args, stream, issue) -> float:
+    """Milliseconds for args.steps calls of issue(i, stream), HIP events on
+    `stream`.  With --graph-steps N, N calls (i = 0 .. N-1) are recorded into
+    one HIP graph by stream capture and the graph is replayed; args.steps is
+    rounded down to a multiple of N."""
+    import torch
+    per = args.graph_steps
+    g = None
+    if per > 0:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cs = torch.cuda.current_stream()
+            for i in range(per):
+                issue(i, cs)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        args.steps = max(1, args.steps // per) * per
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    if g is not None:
+        for _ in range(args.steps // per):
+            g.replay()
+    else:
+        for i in range(args.steps):
+            issue(i, stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
+def launch_doc(args) -> str:
+    return f"HIP graph of {args.graph_steps} steps, replayed" if args.graph_steps > 0 else "stream launches"
+
+
 def verify_bytes(inp) -> int:
     """Compulsory HBM bytes of one verify step as the C ABI takes it: every
     target and draft logit row once, one mask row per position (read once,
@@ -258,20 +293,15 @@ def bench_verify(args) -> int:
     acc = [torch.empty(seqs, dtype=torch.int32, device="cuda") for _ in sets]
     stream = torch.cuda.current_stream()
     with Sampler(0) as s:
-        def step(j):
+        def step(i, st_stream=stream):
+            j = i % nsets
             st = sets[j]
             s.verify_into(st["target"], st["draft"], st["draft_ids"], st["uniforms"], toks[j], acc[j],
-                          temperature=first["temperature"], mask=st["mask"], vocab=vocab, stream=stream)
+                          temperature=first["temperature"], mask=st["mask"], vocab=vocab, stream=st_stream)
         for i in range(args.warmup):
-            step(i % nsets)
+            step(i)
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(args.steps):
-            step(i % nsets)
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms_total = start.elapsed_time(end)
+        ms_total = timed_steps(args, stream, step)
     ms_step = ms_total / args.steps
     achieved = set_bytes / (ms_step * 1e-3) / 1e9
     line = {
@@ -279,7 +309,8 @@ def bench_verify(args) -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"C5: {WORKLOAD_DOC['C5']}", "sequences": seqs, "drafts": L, "vocab": vocab,
-                   "input_sets": nsets, "rotating_set_mb": round(nsets * set_bytes / 1e6, 1)},
+                   "input_sets": nsets, "rotating_set_mb": round(nsets * set_bytes / 1e6, 1),
+                   "launch": launch_doc(args)},
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles("C5", "verify_step"),
@@ -346,13 +377,8 @@ def bench_lm_head(args) -> int:
         for _ in range(args.warmup):
             s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, **kw)
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(args.steps):
-            s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, **kw)
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms_total = start.elapsed_time(end)
+        ms_total = timed_steps(args, stream, lambda i, st: s.lm_head_sample_into(hidden, weight, out_ids, stream=st,
+                                                                                  **kw))
     ms_step = ms_total / args.steps
     achieved = set_bytes / (ms_step * 1e-3) / 1e9
     line = {
@@ -361,7 +387,7 @@ def bench_lm_head(args) -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "f32 (bf16 head widened to f32)", "data": "synthetic",
         "config": {"workload": f"{args.workload}: {WORKLOAD_DOC[args.workload]}", "rows": rows,
                    "vocab": b.vocab, "dim": b.dim, "top_k": b.params.top_k, "top_p": b.params.top_p,
-                   "temperature": b.params.temperature, "softcap": b.params.softcap},
+                   "temperature": b.params.temperature, "softcap": b.params.softcap, "launch": launch_doc(args)},
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles(args.workload, "lm_head"),
@@ -450,32 +476,10 @@ def main() -> int:
             j = i % nsets
             s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
         torch.cuda.synchronize()
-        per = args.graph_steps
-        if per > 0:
-            # the handle's scratch is sized by reserve() and the calls above,
-            # so a captured call records kernel launches only
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                cs = torch.cuda.current_stream()
-                for i in range(per):
-                    j = i % nsets
-                    s.sample_into(out_ids=out_ids[j], stream=cs, **sets[j])
-            for _ in range(3):
-                g.replay()
-            torch.cuda.synchronize()
-            args.steps = max(1, args.steps // per) * per
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        if per > 0:
-            for _ in range(args.steps // per):
-                g.replay()
-        else:
-            for i in range(args.steps):
-                j = i % nsets
-                s.sample_into(out_ids=out_ids[j], stream=stream, **sets[j])
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms_total = start.elapsed_time(end)
+        # the handle's scratch is sized by reserve() and the calls above, so
+        # a captured call records kernel launches only
+        ms_total = timed_steps(args, stream,
+                               lambda i, st: s.sample_into(out_ids=out_ids[i % nsets], stream=st, **sets[i % nsets]))
         gpu_ids0 = out_ids[0].cpu().numpy().view(np.uint32)
 
     ms_step = ms_total / args.steps
@@ -500,8 +504,7 @@ def main() -> int:
                    "temperature": first.params.temperature, "input_sets": nsets,
                    "rotating_set_mb": round(nsets * set_bytes / 1e6, 1),
                    "params": "per row (row_params)" if args.row_params else "one sas_params for every row",
-                   "launch": f"HIP graph of {args.graph_steps} steps, replayed" if args.graph_steps > 0
-                   else "stream launches"},
+                   "launch": launch_doc(args)},
         "topp_edge_rows": {"rows": edge_rows, "of": nsets * rows,
                            "rule": "top-p running mass within 1e-6 of top_p (SAS_FLAG_TOPP_EDGE)"},
         "gbps": achieved,
