@@ -12,7 +12,8 @@ than 512 MB so the 256 MB Infinity Cache cannot serve them.
 
 Prints ONE JSON line (rank 0): rows/s, the roofline of the sampling step
 (its two launches, sas::sample_parts_kernel then sas::sample_merge_kernel:
-algorithmic bytes / average step time, HIP events on the launch stream)
+algorithmic bytes / median step time, a HIP event pair around each step on
+the launch stream)
 and the CPU baseline: the Node restatement of the reference's JS sampling
 path timed on this host's cores on a bounded sample of the same workload.
 """
@@ -70,7 +71,12 @@ def parse_args():
                     help="pass the workload's parameters per row (row_params, with the no-softcap hint) "
                          "instead of one sas_params for every row")
     ap.add_argument("--stream-probe", action="store_true",
-                    help="time sas_probe_read: the parts kernel's loads alone over one C3P step's bytes")
+                    help="time sasp_read (libsas_probe.so): the parts kernel's loads alone over one C3P step's "
+                         "bytes")
+    ap.add_argument("--mask-probe", action="store_true",
+                    help="time sasp_masked_read (libsas_probe.so): C3's logits read whole or only where the "
+                         "grammar mask allows an id")
+    ap.add_argument("--mask-probe-mode", type=int, default=-1, help="with --mask-probe: one mode only")
     ap.add_argument("--calibrate-copy-mb", type=float, default=0.0,
                     help="instead of the benchmark, run device-to-device copies of this many MB (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -94,44 +100,121 @@ def calibrate_copy(mb: float, steps: int) -> int:
     return 0
 
 
+def _probe_lib():
+    """libsas_probe.so: the measurement probes (never part of the sampling
+    library)."""
+    import ctypes
+    from ctypes import c_int, c_int32, c_size_t, c_void_p
+
+    path = os.path.join(ROOT, "shared_amd", "libsas_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with python -m shared_amd.build")
+    lib = ctypes.CDLL(path)
+    lib.sasp_read.restype = c_int
+    lib.sasp_read.argtypes = [c_void_p, c_size_t, c_int32, c_void_p, c_void_p]
+    lib.sasp_masked_read.restype = c_int
+    lib.sasp_masked_read.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]
+    return lib
+
+
+def _probe_time(args, stream, launch) -> float:
+    """Microseconds per launch of launch(i): warm-up, then args.steps launches
+    between two HIP events on `stream`."""
+    import torch
+
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / args.steps
+
+
 def stream_probe(args) -> int:
-    """The streaming bound of the sampling kernels: sas_probe_read reads the
-    C3P step's algorithmic bytes with the parts kernel's access pattern and
+    """The streaming bound of the sampling kernels: sasp_read reads the C3P
+    step's algorithmic bytes with the parts kernel's access pattern and
     nothing else, over rotating buffers (more bytes than the caches hold),
     for several grid sizes.  Prints one JSON line."""
     import ctypes
 
     import torch
 
-    from shared_amd import Sampler
     from shared_amd import workloads as W
-    from shared_amd._capi import check
 
+    lib = _probe_lib()
     set_bytes = W.c3p().algorithmic_bytes() // 16 * 16  # one C3P step
     nsets = max(2, int(-(-args.min_set_mb * 1e6 // set_bytes)))
     bufs = [torch.empty(set_bytes // 4, dtype=torch.float32, device="cuda").uniform_() for _ in range(nsets)]
+    sink = torch.zeros(256, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
     res = {}
-    with Sampler(0) as s:
-        stream = torch.cuda.current_stream()
-        for blocks in (1024, 2048, 4096, 8192):
-            def launch(i):
-                check(s._lib.sas_probe_read(s._h, ctypes.c_void_p(bufs[i % nsets].data_ptr()), set_bytes, blocks,
-                                            ctypes.c_void_p(stream.cuda_stream)), s._h)
-            for i in range(args.warmup):
-                launch(i)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for i in range(args.steps):
-                launch(i)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / args.steps
-            res[blocks] = {"us_per_launch": us, "gbps": set_bytes / us / 1e3}
+    for blocks in (1024, 2048, 4096, 8192):
+        def launch(i):
+            rc = lib.sasp_read(ctypes.c_void_p(bufs[i % nsets].data_ptr()), set_bytes, blocks,
+                               ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"sasp_read failed ({rc})")
+        us = _probe_time(args, stream, launch)
+        res[blocks] = {"us_per_launch": us, "gbps": set_bytes / us / 1e3}
     best = max(res.values(), key=lambda r: r["gbps"])
-    print(json.dumps({"probe": "streaming read (sas_probe_read)", "bytes_per_launch": set_bytes, "sets": nsets,
+    print(json.dumps({"probe": "streaming read (sasp_read)", "bytes_per_launch": set_bytes, "sets": nsets,
                       "by_blocks": res, "best_us": best["us_per_launch"], "best_gbps": best["gbps"],
                       "frac": best["gbps"] / HBM_PEAK_GBPS}), flush=True)
+    return 0
+
+
+MASK_PROBE_MODES = {0: "every float4, loads issued with the mask's", 5: "every float4, after the mask words",
+                    1: "float4s whose 16 B hold an allowed id", 4: "float4s whose 32 B span holds an allowed id",
+                    3: "float4s whose 64 B span holds an allowed id", 2: "float4s whose 128 B line holds an allowed id"}
+
+
+def mask_probe(args) -> int:
+    """Whether a grammar mask can cut the logits' HBM bytes: sasp_masked_read
+    over C3's logits and masks (128 rows x 262,144 ids, densities 0.5-20 %),
+    reading every float4 or only those whose 16/32/64/128-byte span holds an
+    allowed id.  With --mask-probe-mode M only that mode runs (one kernel
+    per process, for rocprofv3 --pmc).  Prints one JSON line."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from shared_amd import workloads as W
+
+    lib = _probe_lib()
+    first = W.c3()
+    set_bytes = first.rows * first.vocab * 4 + first.mask.nbytes
+    nsets = max(2, int(np.ceil(args.min_set_mb * 1e6 / set_bytes)))
+    batches = [first] + [W.c3(seed=1000 + i) for i in range(1, nsets)]
+    logits = [torch.from_numpy(np.ascontiguousarray(b.logits)).cuda() for b in batches]
+    masks = [torch.from_numpy(np.ascontiguousarray(b.mask).view(np.int32)).cuda() for b in batches]
+    # the fraction of each span size that holds an allowed id (what a skipping read must still fetch)
+    words = first.mask.astype(np.uint64)
+    touched = {}
+    for ids in (4, 8, 16, 32):
+        per = 32 // ids
+        spans = (words[..., None] >> (np.arange(per, dtype=np.uint64) * ids)) & np.uint64((1 << ids) - 1)
+        touched[f"{ids * 4}B"] = float((spans != 0).mean())
+    sink = torch.zeros(256, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    modes = [args.mask_probe_mode] if args.mask_probe_mode >= 0 else [0, 5, 1, 4, 3, 2]
+    res = {}
+    for mode in modes:
+        def launch(i):
+            j = i % nsets
+            rc = lib.sasp_masked_read(ctypes.c_void_p(logits[j].data_ptr()), ctypes.c_void_p(masks[j].data_ptr()),
+                                      first.rows, first.vocab, mode, ctypes.c_void_p(sink.data_ptr()),
+                                      ctypes.c_void_p(stream.cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"sasp_masked_read failed ({rc})")
+        us = _probe_time(args, stream, launch)
+        res[mode] = {"reads": MASK_PROBE_MODES[mode], "us_per_launch": us, "gbps": set_bytes / us / 1e3}
+    print(json.dumps({"probe": "mask-predicated read (sasp_masked_read)", "bytes_per_launch": set_bytes,
+                      "sets": nsets, "spans_touched": touched, "by_mode": res}), flush=True)
     return 0
 
 
@@ -194,11 +277,17 @@ def cpu_baseline(batch, target_s: float) -> dict:
             "ids": np.asarray(o["ids"])}
 
 
-def timed_steps(args, stream, issue) -> float:
-    """Milliseconds for args.steps calls of issue(i, stream), HIP events on
-    `stream`.  With --graph-steps N, N calls (i = 0 .. N-1) are recorded into
-    one HIP graph by stream capture and the graph is replayed; args.steps is
-    rounded down to a multiple of N."""
+def timed_steps(args, stream, issue) -> dict:
+    """Times args.steps calls of issue(i, stream) with a HIP event on `stream`
+    before the first step and after every step, so each step has its own
+    event pair.  With --graph-steps N, N calls (i = 0 .. N-1) are recorded
+    into one HIP graph by stream capture and the graph is replayed, one event
+    pair per replay (a replay's time / N is each of its steps); args.steps is
+    rounded down to a multiple of N.  Returns {"median_ms", "mean_ms",
+    "total_ms", "samples"}: the median and mean per step, the whole timed
+    region, and the number of event pairs."""
+    import statistics
+
     import torch
     per = args.graph_steps
     g = None
@@ -212,17 +301,26 @@ def timed_steps(args, stream, issue) -> float:
             g.replay()
         torch.cuda.synchronize()
         args.steps = max(1, args.steps // per) * per
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    if g is not None:
-        for _ in range(args.steps // per):
+    n = args.steps // per if g is not None else args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record(stream)
+    for k in range(n):
+        if g is not None:
             g.replay()
-    else:
-        for i in range(args.steps):
-            issue(i, stream)
-    end.record(stream)
+        else:
+            issue(k, stream)
+        ev[k + 1].record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end)
+    div = per if g is not None else 1
+    each = [ev[k].elapsed_time(ev[k + 1]) / div for k in range(n)]
+    total = ev[0].elapsed_time(ev[n])
+    return {"median_ms": statistics.median(each), "mean_ms": total / args.steps, "total_ms": total, "samples": n}
+
+
+def timing_doc(t: dict, args) -> dict:
+    return {"ms_per_step_median": t["median_ms"], "ms_per_step_mean": t["mean_ms"], "event_pairs": t["samples"],
+            "rule": "ms_per_step is the median over event pairs around each step (each graph replay / its "
+                    "steps with --graph-steps); value = rows per step / that median"}
 
 
 def launch_doc(args) -> str:
@@ -301,16 +399,17 @@ def bench_verify(args) -> int:
         for i in range(args.warmup):
             step(i)
         torch.cuda.synchronize()
-        ms_total = timed_steps(args, stream, step)
-    ms_step = ms_total / args.steps
+        t = timed_steps(args, stream, step)
+    ms_step = t["median_ms"]
     achieved = set_bytes / (ms_step * 1e-3) / 1e9
     line = {
-        "metric": METRIC, "value": seqs * args.steps / (ms_total / 1e3), "unit": "sequences/s", "n_gpus": 1,
+        "metric": METRIC, "value": seqs / (ms_step / 1e3), "unit": "sequences/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"C5: {WORKLOAD_DOC['C5']}", "sequences": seqs, "drafts": L, "vocab": vocab,
                    "input_sets": nsets, "rotating_set_mb": round(nsets * set_bytes / 1e6, 1),
                    "launch": launch_doc(args)},
+        "timing": timing_doc(t, args),
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles("C5", "verify_step"),
@@ -377,17 +476,17 @@ def bench_lm_head(args) -> int:
         for _ in range(args.warmup):
             s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, **kw)
         torch.cuda.synchronize()
-        ms_total = timed_steps(args, stream, lambda i, st: s.lm_head_sample_into(hidden, weight, out_ids, stream=st,
-                                                                                  **kw))
-    ms_step = ms_total / args.steps
+        t = timed_steps(args, stream, lambda i, st: s.lm_head_sample_into(hidden, weight, out_ids, stream=st, **kw))
+    ms_step = t["median_ms"]
     achieved = set_bytes / (ms_step * 1e-3) / 1e9
     line = {
-        "metric": METRIC, "value": rows * args.steps / (ms_total / 1e3), "unit": "rows/s", "n_gpus": 1,
+        "metric": METRIC, "value": rows / (ms_step / 1e3), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32 (bf16 head widened to f32)", "data": "synthetic",
         "config": {"workload": f"{args.workload}: {WORKLOAD_DOC[args.workload]}", "rows": rows,
                    "vocab": b.vocab, "dim": b.dim, "top_k": b.params.top_k, "top_p": b.params.top_p,
                    "temperature": b.params.temperature, "softcap": b.params.softcap, "launch": launch_doc(args)},
+        "timing": timing_doc(t, args),
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles(args.workload, "lm_head"),
@@ -410,6 +509,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy_mb, min(args.steps, 50))
     if args.stream_probe:
         return stream_probe(args)
+    if args.mask_probe:
+        return mask_probe(args)
     if args.workload == "C5":
         return bench_verify(args)
     if args.workload.startswith("LMH"):
@@ -478,12 +579,12 @@ def main() -> int:
         torch.cuda.synchronize()
         # the handle's scratch is sized by reserve() and the calls above, so
         # a captured call records kernel launches only
-        ms_total = timed_steps(args, stream,
-                               lambda i, st: s.sample_into(out_ids=out_ids[i % nsets], stream=st, **sets[i % nsets]))
+        t = timed_steps(args, stream,
+                        lambda i, st: s.sample_into(out_ids=out_ids[i % nsets], stream=st, **sets[i % nsets]))
         gpu_ids0 = out_ids[0].cpu().numpy().view(np.uint32)
 
-    ms_step = ms_total / args.steps
-    value = rows * args.steps / (ms_total / 1e3)
+    ms_step = t["median_ms"]
+    value = rows / (ms_step / 1e3)
     achieved = set_bytes / (ms_step * 1e-3) / 1e9
     traffic = traffic_from_profiles(args.workload)
     line = {
@@ -505,6 +606,7 @@ def main() -> int:
                    "rotating_set_mb": round(nsets * set_bytes / 1e6, 1),
                    "params": "per row (row_params)" if args.row_params else "one sas_params for every row",
                    "launch": launch_doc(args)},
+        "timing": timing_doc(t, args),
         "topp_edge_rows": {"rows": edge_rows, "of": nsets * rows,
                            "rule": "top-p running mass within 1e-6 of top_p (SAS_FLAG_TOPP_EDGE)"},
         "gbps": achieved,

@@ -219,8 +219,42 @@ void sas_destroy(sas_sampler *s);
  * sas_create / handle-free call on this thread when s is NULL). */
 const char *sas_last_error(const sas_sampler *s);
 
-/* Pre-size scratch so later calls of at most this shape allocate nothing. */
+/*
+ * Scratch.  A handle owns device scratch and grows it when a call needs
+ * more; a call whose scratch is already big enough allocates nothing (see
+ * the top of this file).  A growth never frees the buffer it replaces:
+ * launches already queued on any stream, and HIP graphs that recorded
+ * them, keep valid addresses until sas_destroy, which synchronises the
+ * device and frees every buffer.  (A graph replayed after sas_destroy of
+ * its handle reads freed memory.)  A call that would grow scratch while
+ * its stream is being captured fails with SAS_ERR_INVALID instead.
+ */
+
+/* Pre-size scratch for sas_sample / sas_sample_step calls of at most
+ * `rows` rows at `vocab` with histories shorter than 1,024 ids per row:
+ * sas_reserve_for with only rows and vocab set. */
 int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab);
+
+/* The largest calls a handle must run without allocating.  Zero fields
+ * reserve nothing for that entry point. */
+typedef struct sas_reserve_desc {
+  int32_t rows;              /* sampling rows of one call: sas_sample, sas_sample_step,
+                                sas_spec_exact's seqs * (draft_len + 1) verify rows */
+  int32_t vocab;             /* 1..SAS_MAX_VOCAB, the vocabulary of every call below */
+  int64_t hist_ids;          /* the most history ids of one call (hist_count, or
+                                rows * ring_len for sas_sample_step): long histories
+                                (>= 1,024 ids per row) are bucketed in scratch */
+  int32_t lm_head_rows;      /* 0, or the rows of sas_lm_head_sample (<= SAS_LMH_MAX_ROWS;
+                                vocab <= SAS_LMH_MAX_VOCAB) */
+  int32_t verify_seqs;       /* 0, or the sequences of sas_verify ... */
+  int32_t verify_draft_len;  /* ... with this many drafts (1..SAS_MAX_DRAFT) */
+} sas_reserve_desc;
+
+/* Pre-size every scratch buffer for calls of at most the shapes of `d`,
+ * so that those calls allocate nothing (and can be captured into a HIP
+ * graph with no eager call first).  No reference counterpart: the
+ * reference allocates its buffers once per model (gemma-model.js:123-178). */
+int sas_reserve_for(sas_sampler *s, const sas_reserve_desc *d);
 
 /* Sample one token per row, stream-ordered on `stream` (a hipStream_t; NULL
  * is HIP's null stream, as everywhere in HIP).  A handle must not run two
@@ -356,13 +390,6 @@ int sas_synchronize(sas_sampler *s, void *stream);
 /* The handle's own non-blocking hipStream_t, for hosts that have no HIP
  * binding of their own (the N-API addon passes it to every call). */
 void *sas_stream(sas_sampler *s);
-
-/* Measurement helper, no reference counterpart: one launch that reads
- * `bytes` (a multiple of 16, at `src`, 16-byte aligned) with the sampling
- * kernel's access pattern and nothing else: `blocks` blocks of 256 threads,
- * each a contiguous share, 16-byte nontemporal loads, eight per thread in
- * flight.  Its time is the streaming bound of the sampling kernels. */
-int sas_probe_read(sas_sampler *s, const void *src, size_t bytes, int32_t blocks, void *stream);
 
 #ifdef __cplusplus
 }

@@ -134,6 +134,17 @@ class SasSpecRows(ctypes.Structure):
     ]
 
 
+class SasReserveDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("vocab", c_int32),
+        ("hist_ids", c_int64),
+        ("lm_head_rows", c_int32),
+        ("verify_seqs", c_int32),
+        ("verify_draft_len", c_int32),
+    ]
+
+
 class SasLmHead(ctypes.Structure):
     _fields_ = [
         ("hidden", c_void_p),
@@ -152,6 +163,7 @@ SIGNATURES = {
     "sas_destroy": (None, [c_void_p]),
     "sas_last_error": (c_char_p, [c_void_p]),
     "sas_reserve": (c_int, [c_void_p, c_int32, c_int32]),
+    "sas_reserve_for": (c_int, [c_void_p, POINTER(SasReserveDesc)]),
     "sas_sample": (c_int, [c_void_p, POINTER(SasRows), c_void_p]),
     "sas_sample_noalloc": (c_int, [c_int, POINTER(SasRows), c_void_p]),
     "sas_sample_step": (c_int, [c_void_p, POINTER(SasRows), POINTER(SasStep), c_void_p]),
@@ -166,7 +178,6 @@ SIGNATURES = {
     "sas_memcpy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_void_p]),
     "sas_synchronize": (c_int, [c_void_p, c_void_p]),
     "sas_stream": (c_void_p, [c_void_p]),
-    "sas_probe_read": (c_int, [c_void_p, c_void_p, c_size_t, c_int32, c_void_p]),
 }
 
 _lib = None

@@ -2,6 +2,8 @@
 
 * ``libshared_amd_sampler.so``: the HIP kernels and the C ABI, for gfx950.
 * ``js/sas_napi.node``: the N-API addon that exposes the C ABI to Node.
+* ``libsas_probe.so``: measurement probes for bench.py (the streaming
+  bound of the sampling kernels); the sampling library never loads it.
 
 Run ``python -m shared_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -18,7 +20,9 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libshared_amd_sampler.so")
 NAPI = os.path.join(PKG, "js", "sas_napi.node")
+PROBE = os.path.join(PKG, "libsas_probe.so")
 HIP_SOURCES = ["capi.hip", "sample_kernel.hip", "verify_kernel.hip", "lmhead_kernel.hip"]
+PROBE_SOURCES = ["probe_kernel.hip"]
 
 # -ffp-contract=off: the double-precision tail must round like a JS engine.
 # -packed-fp32-ops: packed FP32 instructions are kept out of the code.
@@ -44,8 +48,8 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
 
 
-def build_hip(out: str = LIB) -> str:
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+def build_hip(out: str = LIB, sources: list[str] = HIP_SOURCES) -> str:
+    srcs = [os.path.join(CSRC, s) for s in sources]
     tmp = out + ".tmp"
     _run([_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, *srcs, "-o", tmp])
     os.replace(tmp, out)
@@ -65,8 +69,13 @@ def build_napi(out: str = NAPI) -> str | None:
     return out
 
 
+def build_probe(out: str = PROBE) -> str:
+    return build_hip(out, PROBE_SOURCES)
+
+
 def build_all() -> None:
     build_hip()
+    build_probe()
     build_napi()
 
 

@@ -4,11 +4,13 @@
 // host; a missing device is an error, never a fallback.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "sas_device.h"
 #include "sas_launch.h"
@@ -27,10 +29,9 @@ struct sas_sampler {
   void *hb = nullptr;         // long histories bucketed by part
   size_t hb_cap = 0;
   int cus = 0;                 // compute units of the device
-  // The stream of the handle's last launch: a handle's calls are ordered by
-  // the caller, so its scratch is idle once that stream has drained.
-  hipStream_t last_stream = nullptr;
-  bool launched = false;
+  // Buffers a growth replaced.  Work already queued (or recorded into a
+  // HIP graph) may still use them, so they are freed by sas_destroy only.
+  std::vector<void *> retired;
 };
 
 namespace {
@@ -49,35 +50,39 @@ int hip_fail(sas_sampler *s, hipError_t e, const char *what) {
 
 hipStream_t pick_stream(sas_sampler *, void *stream) { return reinterpret_cast<hipStream_t>(stream); }
 
-// Wait for the handle's last launch (its scratch may still be in use).
-hipError_t drain(sas_sampler *s) {
-  if (!s->launched) return hipSuccess;
-  return hipStreamSynchronize(s->last_stream);
-}
-
-// Grow a scratch buffer; waits for the handle's queued work before freeing
-// the old one (that stream only: other streams of the process run on).
-int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, bool zero) {
+// Grow a scratch buffer to at least `need` bytes.  The buffer it replaces
+// is retired, not freed: launches queued on any stream, and graphs that
+// recorded them, keep a valid address; sas_destroy frees it.  Capacities
+// at least double, so retired buffers hold less than the live one.  Under
+// stream capture nothing is allocated: the call fails and names the fix.
+int grow(sas_sampler *s, void **buf, size_t *cap, size_t need, void *stream, const char *who) {
   if (need <= *cap) return SAS_OK;
-  hipError_t e;
-  if (*buf) {
-    if ((e = drain(s)) != hipSuccess) return hip_fail(s, e, "hipStreamSynchronize");
-    if ((e = hipFree(*buf)) != hipSuccess) return hip_fail(s, e, "hipFree");
-    *buf = nullptr;
-    *cap = 0;
-  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cs) == hipSuccess &&
+      cs != hipStreamCaptureStatusNone)
+    return fail(s, SAS_ERR_INVALID,
+                std::string(who) + ": the handle's scratch is too small for this call and the stream is being "
+                                   "captured: size it before the capture (sas_reserve_for, or one eager call "
+                                   "of this shape)");
   size_t bytes = (need + 255) & ~size_t(255);
-  if ((e = hipMalloc(buf, bytes)) != hipSuccess) {
-    *buf = nullptr;
-    return fail(s, SAS_ERR_NOMEM, std::string("hipMalloc scratch: ") + hipGetErrorString(e));
-  }
-  if (zero && (e = hipMemset(*buf, 0, bytes)) != hipSuccess) return hip_fail(s, e, "hipMemset");
+  if (*cap && bytes < 2 * *cap) bytes = 2 * *cap;
+  void *fresh = nullptr;
+  hipError_t e = hipMalloc(&fresh, bytes);
+  if (e != hipSuccess) return fail(s, SAS_ERR_NOMEM, std::string(who) + ": hipMalloc scratch: " + hipGetErrorString(e));
+  if (*buf) s->retired.push_back(*buf);
+  *buf = fresh;
   *cap = bytes;
   return SAS_OK;
 }
 
-int ensure_sample_scratch(sas_sampler *s, int rows, int parts) {
-  return grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, parts), false);
+// Scratch bytes of each buffer for a call shape (the same sizes the calls
+// ask for).
+size_t hb_bytes(int64_t hist_ids, int hrows, int parts) {
+  return (((size_t)hist_ids * 4 + 255) & ~size_t(255)) + (size_t)hrows * (parts + 1) * 4;
+}
+
+int ensure_sample_scratch(sas_sampler *s, int rows, int parts, void *stream, const char *who) {
+  return grow(s, &s->recs, &s->recs_cap, sas::sample_rec_bytes(rows, parts), stream, who);
 }
 
 int set_device(sas_sampler *s) {
@@ -194,13 +199,13 @@ int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char 
   // at least two blocks per CU: small batches take shorter parts
   int parts = 0, span = 0;
   sas::choose_parts(r->rows, r->vocab, 2 * s->cus, &parts, &span);
-  if (int rc = ensure_sample_scratch(s, r->rows, parts)) return rc;
+  if (int rc = ensure_sample_scratch(s, r->rows, parts, stream, who)) return rc;
   const float *logits = r->logits;
   int64_t stride = r->logits_stride;
   if (r->vocab < 4) {
     // the kernel loads 16 bytes at a time from inside a row: copy rows of
     // fewer than 4 logits into rows of 4, NaN (never selected) past vocab
-    if (int rc = grow(s, &s->pad, &s->pad_cap, (size_t)r->rows * 16, false)) return rc;
+    if (int rc = grow(s, &s->pad, &s->pad_cap, (size_t)r->rows * 16, stream, who)) return rc;
     hipError_t e = sas::launch_pad_rows(r->logits, r->logits_stride, r->vocab, r->rows,
                                         reinterpret_cast<float *>(s->pad), pick_stream(s, stream));
     if (e != hipSuccess) return hip_fail(s, e, "sas_sample pad launch");
@@ -230,13 +235,11 @@ int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char 
   const int64_t hist_ids = ring ? (int64_t)hrows * a.ring_len : (r->hist_ids ? r->hist_count : 0);
   if (hist_ids >= sas::kBucketMinIds * hrows && hist_ids > 0) {
     const size_t ids_bytes = ((size_t)hist_ids * 4 + 255) & ~size_t(255);
-    if (int rc = grow(s, &s->hb, &s->hb_cap, ids_bytes + (size_t)hrows * (parts + 1) * 4, false)) return rc;
+    if (int rc = grow(s, &s->hb, &s->hb_cap, hb_bytes(hist_ids, hrows, parts), stream, who)) return rc;
     a.hb_ids = reinterpret_cast<uint32_t *>(s->hb);
     a.hb_offs = reinterpret_cast<int32_t *>(static_cast<char *>(s->hb) + ids_bytes);
   }
   hipError_t e = sas::launch_sample(a, any_softcap(r), pick_stream(s, stream));
-  s->last_stream = pick_stream(s, stream);
-  s->launched = true;
   if (e != hipSuccess) return hip_fail(s, e, (std::string(who) + " launch").c_str());
   return SAS_OK;
 }
@@ -279,7 +282,9 @@ int sas_create(int device, sas_sampler **out) {
 void sas_destroy(sas_sampler *s) {
   if (!s) return;
   (void)hipSetDevice(s->device);
-  (void)drain(s);
+  // the scratch may still be in use by queued work on any stream
+  (void)hipDeviceSynchronize();
+  for (void *p : s->retired) (void)hipFree(p);
   if (s->recs) (void)hipFree(s->recs);
   if (s->hb) (void)hipFree(s->hb);
   if (s->vscratch) (void)hipFree(s->vscratch);
@@ -292,13 +297,40 @@ const char *sas_last_error(const sas_sampler *s) { return s ? s->err.c_str() : g
 
 int sas_reserve(sas_sampler *s, int32_t rows, int32_t vocab) {
   if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_reserve: handle is NULL");
-  if (rows < 0 || vocab < 1 || vocab > SAS_MAX_VOCAB)
-    return fail(s, SAS_ERR_INVALID, "sas_reserve: rows must be >= 0 and vocab in [1, SAS_MAX_VOCAB]");
+  sas_reserve_desc d{};
+  d.rows = rows;
+  d.vocab = vocab;
+  return sas_reserve_for(s, &d);
+}
+
+int sas_reserve_for(sas_sampler *s, const sas_reserve_desc *d) {
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_reserve_for: handle is NULL");
+  if (!d) return fail(s, SAS_ERR_INVALID, "sas_reserve_for: descriptor is NULL");
+  if (d->rows < 0 || d->vocab < 1 || d->vocab > SAS_MAX_VOCAB || d->hist_ids < 0 || d->lm_head_rows < 0 ||
+      d->lm_head_rows > SAS_LMH_MAX_ROWS || d->verify_seqs < 0 || d->verify_draft_len < 0 ||
+      d->verify_draft_len > SAS_MAX_DRAFT || (d->verify_seqs > 0 && d->verify_draft_len < 1) ||
+      (d->lm_head_rows > 0 && d->vocab > SAS_LMH_MAX_VOCAB))
+    return fail(s, SAS_ERR_INVALID,
+                "sas_reserve_for: rows, hist_ids, lm_head_rows (<= SAS_LMH_MAX_ROWS, vocab <= SAS_LMH_MAX_VOCAB) "
+                "and verify_seqs must be >= 0, vocab in [1, SAS_MAX_VOCAB], verify_draft_len in "
+                "[1, SAS_MAX_DRAFT] with verify_seqs");
   if (int rc = set_device(s)) return rc;
+  const char *who = "sas_reserve_for";
   // the most parts any batch of <= rows rows may pick (a single row)
   int parts = 0, span = 0;
-  sas::choose_parts(1, vocab, 2 * s->cus, &parts, &span);
-  return ensure_sample_scratch(s, rows, parts);
+  sas::choose_parts(1, d->vocab, 2 * s->cus, &parts, &span);
+  size_t recs = sas::sample_rec_bytes(d->rows, parts);
+  if (d->lm_head_rows > 0) recs = std::max(recs, sas::lmh_scratch_bytes(d->lm_head_rows, d->vocab));
+  if (int rc = grow(s, &s->recs, &s->recs_cap, recs, nullptr, who)) return rc;
+  if (d->vocab < 4 && d->rows > 0)
+    if (int rc = grow(s, &s->pad, &s->pad_cap, (size_t)d->rows * 16, nullptr, who)) return rc;
+  if (d->hist_ids >= sas::kBucketMinIds && d->rows > 0)
+    if (int rc = grow(s, &s->hb, &s->hb_cap, hb_bytes(d->hist_ids, d->rows, parts), nullptr, who)) return rc;
+  if (d->verify_seqs > 0)
+    if (int rc = grow(s, &s->vscratch, &s->vscratch_cap,
+                      sas::verify_scratch_bytes(d->verify_seqs, d->verify_draft_len, d->vocab), nullptr, who))
+      return rc;
+  return SAS_OK;
 }
 
 int sas_sample(sas_sampler *s, const sas_rows *r, void *stream) {
@@ -378,7 +410,9 @@ int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, 
   if (reinterpret_cast<uintptr_t>(h->hidden) % 4 != 0)
     return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden must be 4-byte aligned");
   if (int rc = set_device(s)) return rc;
-  if (int rc = grow(s, &s->recs, &s->recs_cap, sas::lmh_scratch_bytes(r->rows, r->vocab), false)) return rc;
+  if (int rc = grow(s, &s->recs, &s->recs_cap, sas::lmh_scratch_bytes(r->rows, r->vocab), stream,
+                    "sas_lm_head_sample"))
+    return rc;
   sas::LmhArgs a{};
   fill_args(r, nullptr, 0, 1, sas::kLmhSpan, s->recs, &a.s);
   sas::lmh_layout(&a, s->recs);
@@ -389,8 +423,6 @@ int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, 
   a.dim = h->dim;
   a.out_logits = h->out_logits;
   hipError_t e = sas::launch_lm_head_sample(a, any_softcap(r), pick_stream(s, stream));
-  s->last_stream = pick_stream(s, stream);
-  s->launched = true;
   if (e != hipSuccess) return hip_fail(s, e, "sas_lm_head_sample launch");
   return SAS_OK;
 }
@@ -471,7 +503,7 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
     return fail(s, SAS_ERR_INVALID, "sas_verify: seqs * (draft_len + 1) must be <= 65535");
   if (int rc = set_device(s)) return rc;
   if (int rc = grow(s, &s->vscratch, &s->vscratch_cap, sas::verify_scratch_bytes(v->seqs, v->draft_len, v->vocab),
-                    false))
+                    stream, "sas_verify"))
     return rc;
   sas::VerifyArgs a;
   a.target = v->target_logits;
@@ -497,8 +529,6 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
   a.aligned = (reinterpret_cast<uintptr_t>(v->target_logits) & 15u) == 0 &&
               (reinterpret_cast<uintptr_t>(v->draft_logits) & 15u) == 0 && (v->logits_stride & 3) == 0;
   hipError_t e = sas::launch_verify(a, pick_stream(s, stream));
-  s->last_stream = pick_stream(s, stream);
-  s->launched = true;
   if (e != hipSuccess) return hip_fail(s, e, "sas_verify launch");
   return SAS_OK;
 }
@@ -600,19 +630,5 @@ int sas_synchronize(sas_sampler *s, void *stream) {
 }
 
 void *sas_stream(sas_sampler *s) { return s ? reinterpret_cast<void *>(s->stream) : nullptr; }
-
-int sas_probe_read(sas_sampler *s, const void *src, size_t bytes, int32_t blocks, void *stream) {
-  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_probe_read: handle is NULL");
-  if (!src || bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16 || blocks < 1)
-    return fail(s, SAS_ERR_INVALID, "sas_probe_read: src must be 16-byte aligned, bytes a multiple of 16, blocks >= 1");
-  if (int rc = set_device(s)) return rc;
-  // the sink: the pad scratch (never read)
-  if (int rc = grow(s, &s->pad, &s->pad_cap, 1024, false)) return rc;
-  hipError_t e = sas::launch_probe_read(src, (int64_t)(bytes / 16), blocks, reinterpret_cast<float *>(s->pad),
-                                        pick_stream(s, stream));
-  s->last_stream = pick_stream(s, stream);
-  s->launched = true;
-  return e == hipSuccess ? SAS_OK : hip_fail(s, e, "sas_probe_read launch");
-}
 
 }  // extern "C"

@@ -319,14 +319,23 @@ napi_value Destroy(napi_env env, napi_callback_info info) {
   }                                                                             \
   sas_sampler *s = s##_w->s;
 
+// reserve(handle, rows, vocab[, histIds, lmHeadRows, verifySeqs, verifyDraftLen])
 napi_value Reserve(napi_env env, napi_callback_info info) {
-  napi_value argv[3];
-  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  napi_value argv[7];
+  size_t argc = 7;
+  NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
+  if (argc != 3 && argc != 7) return throw_napi(env, "arguments");
   HANDLE_OR_THROW(argv[0], s);
-  int32_t rows = 0, vocab = 0;
-  NAPI_OK(napi_get_value_int32(env, argv[1], &rows));
-  NAPI_OK(napi_get_value_int32(env, argv[2], &vocab));
-  int rc = sas_reserve(s, rows, vocab);
+  sas_reserve_desc d{};
+  NAPI_OK(napi_get_value_int32(env, argv[1], &d.rows));
+  NAPI_OK(napi_get_value_int32(env, argv[2], &d.vocab));
+  if (argc == 7) {
+    NAPI_OK(napi_get_value_int64(env, argv[3], &d.hist_ids));
+    NAPI_OK(napi_get_value_int32(env, argv[4], &d.lm_head_rows));
+    NAPI_OK(napi_get_value_int32(env, argv[5], &d.verify_seqs));
+    NAPI_OK(napi_get_value_int32(env, argv[6], &d.verify_draft_len));
+  }
+  int rc = sas_reserve_for(s, &d);
   return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
 }
 

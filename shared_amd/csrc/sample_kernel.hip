@@ -749,33 +749,6 @@ __global__ __launch_bounds__(kThreads) void spec_cascade_kernel(const uint32_t *
   if (next) next[s] = pk[n - 1];
 }
 
-// sas_probe_read: a block reads its contiguous share of n4 float4s, eight
-// 16-byte loads per thread in flight per round, and folds them into one
-// value that is stored only if it equals an impossible bit pattern.
-__global__ __launch_bounds__(kThreads) void probe_read_kernel(const float4 *src, int64_t n4, float *sink) {
-  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
-  const int64_t b0 = (int64_t)blockIdx.x * per, b1 = min(b0 + per, n4);
-  float m = 0.0f;
-  for (int64_t r = b0 + threadIdx.x; r < b1; r += 8 * kThreads) {
-    f32x4u v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int64_t i = r + (int64_t)u * kThreads;
-      v[u] = i < b1 ? __builtin_nontemporal_load(reinterpret_cast<const f32x4u *>(src + i)) : f32x4u{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) m = fmaxf(m, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
-  }
-  if (__float_as_uint(m) == 0x7FBADBADu) sink[blockIdx.x & 255] = m;
-}
-
-hipError_t launch_probe_read(const void *src, int64_t n4, int blocks, float *sink, hipStream_t stream) {
-  if (n4 <= 0 || blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(probe_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream,
-                     reinterpret_cast<const float4 *>(src), n4, sink);
-  return hipGetLastError();
-}
-
 hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, const uint32_t *stop_ids, int seqs,
                                int L, int32_t *accepted, uint32_t *next, hipStream_t stream) {
   if (seqs <= 0) return hipSuccess;

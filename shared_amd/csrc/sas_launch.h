@@ -101,8 +101,6 @@ hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, co
 // part first (one more launch): each part then reads its own ids only.
 constexpr int64_t kBucketMinIds = 1024;
 
-// The streaming-read probe (sas_probe_read); sink: 256 floats of scratch.
-hipError_t launch_probe_read(const void *src, int64_t n4, int blocks, float *sink, hipStream_t stream);
 
 // Scratch bytes of the records and part counts for a batch shape.
 size_t sample_rec_bytes(int rows, int parts);

@@ -34,6 +34,13 @@ time('MaskBuilder.allow: the same 4,000 ids in a new array (cache hit)', 500, fu
 time('  of which copying the 4,000 ids', 500, function () { mid.slice(); });
 time('MaskBuilder.allow: a 6-id list (cache hit)', 2000, function () { b.allow(Uint32Array.of(1, 2, 3, 42, 9000, 100000 % vocab)); });
 time('maskFromIds: a 6-id list', 2000, function () { sas.maskFromIds(1, small, vocab); });
+// Qwen's ToolConstraint.mask(): its cached unrestricted() array in a new
+// {kind: 'allow'} object every step (tool-constraint.ts:286-293, 653-661)
+const constraint = { mask: function () { return { kind: 'allow', tokenIds: unrestricted }; } };
+const b2 = new sas.MaskBuilder(vocab, 64);
+time('packedToolMask: repeated unrestricted Qwen state (new object)', 2000, function () {
+  sas.packedToolMask(constraint, '', null, b2);
+});
 const w = b.allow(unrestricted);
 time('updateTokenMaskState, words equal to the uploaded ones', 2000, function () {
   sas.updateTokenMaskState(state, { kind: 'words', words: Uint32Array.from(w) });

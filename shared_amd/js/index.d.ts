@@ -237,7 +237,9 @@ export interface VerifyResult {
 export declare class Sampler {
   constructor(device?: number);
   close(): Promise<void>;
-  reserve(rows: number, vocab: number): void;
+  /** Pre-sizes device scratch so calls of at most these shapes allocate nothing (sas_reserve_for). */
+  reserve(rows: number, vocab: number, opts?: { histIds?: number; lmHeadRows?: number; verifySeqs?: number;
+    verifyDraftLen?: number }): void;
   alloc(bytes: number): DeviceBuffer;
   synchronize(): void;
   createTokenMaskState(vocab: number): TokenMaskState;

@@ -126,15 +126,19 @@ class MaskBuilder {
     this.hits = 0;
     this.misses = 0;
     this._all = addon.maskFromIds(addon.MASK_ALL, null, vocab).words;
+    // words by id-list object: a TokenMask's tokenIds are immutable and
+    // compared by identity (token-mask-state.js:21), so the same array
+    // packs once, whatever its length
+    this._byIds = new WeakMap();
   }
   /** Every id allowed (a fresh copy). */
   all() { return Uint32Array.from(this._all); }
   /** No id allowed. */
   none() { return new Uint32Array(this.nwords); }
   /** Only `ids` (ids past the vocabulary are ignored). */
-  allow(ids) { return this._fromIds(addon.MASK_ALLOW, toU32(ids)); }
+  allow(ids) { return this._fromIds(addon.MASK_ALLOW, toU32(ids), ids); }
   /** Every id but `ids`. */
-  deny(ids) { return this._fromIds(addon.MASK_DENY, toU32(ids)); }
+  deny(ids) { return this._fromIds(addon.MASK_DENY, toU32(ids), ids); }
   /** The words of a TokenMask ({kind: 'all' | 'allow' | 'deny', tokenIds} or {kind: 'words', words}). */
   fromTokenMask(mask) {
     const kind = orDefault(mask ? mask.kind : undefined, 'all');
@@ -159,25 +163,43 @@ class MaskBuilder {
     if (tail) out[this.nwords - 1] &= (1 << tail) - 1 >>> 0;
     return out;
   }
-  _fromIds(code, ids) {
-    // past a few thousand ids, hashing and comparing a list costs as much
-    // as packing it (about 1 ns per id each): pack it directly
-    if (ids.length > 4096) {
-      this.misses++;
-      return addon.maskFromIds(code, ids, this.vocab).words;
-    }
-    const key = code + ':' + addon.idsKey(ids);
-    const hit = this.cache.get(key);
-    if (hit && sameWords(hit.ids, ids)) {
-      this.cache.delete(key);
-      this.cache.set(key, hit);
+  _fromIds(code, ids, original) {
+    // the same Uint32Array again (a TokenMask's tokenIds): its words, with
+    // no work per id.  Other lists (arrays, sets) are converted per call.
+    const owner = original instanceof Uint32Array ? original : null;
+    let byCode = owner ? this._byIds.get(owner) : undefined;
+    if (byCode && byCode[code]) {
       this.hits++;
-      return hit.words;
+      return byCode[code];
     }
-    this.misses++;
-    const words = addon.maskFromIds(code, ids, this.vocab).words;
-    this.cache.set(key, { ids: Uint32Array.from(ids), words: words });
-    if (this.cache.size > this.cacheSize) this.cache.delete(this.cache.keys().next().value);
+    let words;
+    if (ids.length > 4096) {
+      // past a few thousand ids, hashing and comparing a list costs as much
+      // as packing it (about 1 ns per id each): pack it directly
+      this.misses++;
+      words = addon.maskFromIds(code, ids, this.vocab).words;
+    } else {
+      const key = code + ':' + addon.idsKey(ids);
+      const hit = this.cache.get(key);
+      if (hit && sameWords(hit.ids, ids)) {
+        this.cache.delete(key);
+        this.cache.set(key, hit);
+        this.hits++;
+        words = hit.words;
+      } else {
+        this.misses++;
+        words = addon.maskFromIds(code, ids, this.vocab).words;
+        this.cache.set(key, { ids: Uint32Array.from(ids), words: words });
+        if (this.cache.size > this.cacheSize) this.cache.delete(this.cache.keys().next().value);
+      }
+    }
+    if (owner) {
+      if (!byCode) {
+        byCode = {};
+        this._byIds.set(owner, byCode);
+      }
+      byCode[code] = words;
+    }
     return words;
   }
 }
@@ -190,11 +212,23 @@ class MaskBuilder {
  */
 function packedToolMask(constraint, raw, parseArguments, builder) {
   const mask = constraint.mask(raw, parseArguments);
-  const memo = builder._byMask || (builder._byMask = new WeakMap());
-  let words = memo.get(mask);
-  if (!words) {
+  const kind = orDefault(mask ? mask.kind : undefined, 'all');
+  let words;
+  if (kind === 'all') {
+    // one immutable all-allowed array for every 'all' mask
+    words = builder._allShared || (builder._allShared = builder.all());
+  } else if (kind === 'allow' || kind === 'deny') {
+    // keyed by the tokenIds array: Qwen's mask() wraps its cached
+    // unrestricted() list in a new {kind: 'allow'} object every step
+    // (tool-constraint.ts:286-293, 653-661), and the same array is packed once
     words = builder.fromTokenMask(mask);
-    memo.set(mask, words);
+  } else {
+    const memo = builder._byMask || (builder._byMask = new WeakMap());
+    words = memo.get(mask);
+    if (!words) {
+      words = builder.fromTokenMask(mask);
+      memo.set(mask, words);
+    }
   }
   return { kind: 'words', words: words };
 }
@@ -456,7 +490,14 @@ class Sampler {
     return Promise.resolve();
   }
 
-  reserve(rows, vocab) { addon.reserve(this._idle('reserve'), rows, vocab); }
+  // Pre-sizes the handle's device scratch (sas_reserve_for): calls of at
+  // most these shapes then allocate nothing.  opts: {histIds, lmHeadRows,
+  // verifySeqs, verifyDraftLen} (all 0 by default).
+  reserve(rows, vocab, opts) {
+    const o = opts || {};
+    addon.reserve(this._idle('reserve'), rows, vocab, o.histIds || 0, o.lmHeadRows || 0, o.verifySeqs || 0,
+      o.verifyDraftLen || 0);
+  }
 
   /** Device memory owned by the caller (e.g. the LM head's logits). */
   alloc(bytes) { return new DeviceBuffer(this, bytes); }

@@ -231,9 +231,14 @@ class Sampler:
     def __exit__(self, *exc):
         self.close()
 
-    def reserve(self, rows: int, vocab: int) -> None:
-        check(self._lib.sas_reserve(self._h, int(rows), int(vocab)), self._h)
-
+    def reserve(self, rows: int, vocab: int, *, hist_ids: int = 0, lm_head_rows: int = 0, verify_seqs: int = 0,
+                verify_draft_len: int = 0) -> None:
+        """Pre-size the handle's scratch (sas_reserve_for): calls of at most
+        these shapes then allocate nothing and can be captured directly."""
+        from ._capi import SasReserveDesc
+        d = SasReserveDesc(int(rows), int(vocab), int(hist_ids), int(lm_head_rows), int(verify_seqs),
+                           int(verify_draft_len))
+        check(self._lib.sas_reserve_for(self._h, ctypes.byref(d)), self._h)
 
     def sample_into(self, logits, out_ids, *, stream=None, **kw) -> None:
         """Launch sas_sample on caller-provided device buffers (no allocation,

@@ -94,6 +94,27 @@ check('MaskBuilder: words equal the brute-force masks; equal lists hit its cache
   assert.strictEqual(m1.kind, 'words');
   assert.strictEqual(m1.words, m2.words);
   assert.deepStrictEqual(bits(sas.packedToolMask(tc, 'y', null, b).words), [7]);
+  // Qwen's mask(): the same cached array in a new {kind: 'allow'} object per
+  // call (tool-constraint.ts:286-293, 653-661) packs once, a long list too
+  const big = Uint32Array.from({ length: 900 }, function (_, i) { return i; });
+  const long = new sas.MaskBuilder(V, 16);
+  const qwen = { mask: function () { return { kind: 'allow', tokenIds: big }; } };
+  const q1 = sas.packedToolMask(qwen, 'a', null, long);
+  const misses = long.misses;
+  const q2 = sas.packedToolMask(qwen, 'b', null, long);
+  assert.strictEqual(q1.words, q2.words);
+  assert.strictEqual(long.misses, misses);
+  assert.strictEqual(long.count(q1.words), 900);
+  // 'all' masks share one array; arrays that are not Uint32Arrays are not memoized
+  const all1 = sas.packedToolMask({ mask: function () { return { kind: 'all' }; } }, '', null, long).words;
+  const all2 = sas.packedToolMask({ mask: function () { return { kind: 'all' }; } }, '', null, long).words;
+  assert.strictEqual(all1, all2);
+  assert.strictEqual(long.count(all1), V);
+  const plain = [1, 2, 3];
+  const p1 = long.allow(plain);
+  plain.push(4);
+  assert.deepStrictEqual(bits(long.allow(plain)), [1, 2, 3, 4]);
+  assert.deepStrictEqual(bits(p1), [1, 2, 3]);
 });
 
 check('empty allow mask is kept as an empty constraint', function () {

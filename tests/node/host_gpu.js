@@ -85,6 +85,30 @@ async function main() {
     }
 
     if (allow) {
+      // the packed producer: MaskBuilder words (set algebra on words) through
+      // updateTokenMaskState, then packedToolMask over a ToolConstraint-shaped
+      // object whose mask() wraps one cached array in a new object per call
+      // (tool-constraint.ts:286-293, 653-661): packed once, uploaded once
+      const mb = new sas.MaskBuilder(vocab, 8);
+      const wstate = s.createTokenMaskState(vocab);
+      const words = mb.andNot(mb.allow(allow), mb.allow(allow.subarray(0, 100)));
+      sas.updateTokenMaskState(wstate, { kind: 'words', words: words });
+      const g1 = s.sampleRows(Object.assign({}, base, { logits: logits, mask: wstate }));
+      write('js_words_ids.u32', g1.ids);
+      const constraint = { mask: function () { return { kind: 'allow', tokenIds: allow }; } };
+      const pm1 = sas.packedToolMask(constraint, '', null, mb);
+      sas.updateTokenMaskState(wstate, pm1);
+      const up = wstate.uploads;
+      const pm2 = sas.packedToolMask(constraint, '', null, mb);
+      if (pm2.words !== pm1.words) throw new Error('packedToolMask packed the same tokenIds again');
+      sas.updateTokenMaskState(wstate, pm2);
+      if (wstate.uploads !== up) throw new Error('the same words were uploaded again');
+      const g2 = s.sampleRows(Object.assign({}, base, { logits: logits, mask: wstate }));
+      write('js_tool_ids.u32', g2.ids);
+      step('sampleRows (MaskBuilder words, packedToolMask) done');
+    }
+
+    if (allow) {
       // Qwen's SampleParams.allowedTokenIds (model.js:661-666): one list for
       // every row, then rows with and without one
       const qp = Object.assign({}, params, { allowedTokenIds: allow });

@@ -92,6 +92,10 @@ static void null_handle_paths() {
   sas_lm_head lh{};
   EXPECT(sas_lm_head_sample(nullptr, &lh, &r, nullptr) == SAS_ERR_INVALID);
   EXPECT(sas_reserve(nullptr, 1, 1) == SAS_ERR_INVALID);
+  sas_reserve_desc rd{};
+  rd.rows = 1;
+  rd.vocab = 1;
+  EXPECT(sas_reserve_for(nullptr, &rd) == SAS_ERR_INVALID);
   EXPECT(sas_alloc(nullptr, 16, &p) == SAS_ERR_INVALID);
   EXPECT(sas_free(nullptr, p) == SAS_ERR_INVALID);
   EXPECT(sas_memcpy(nullptr, &p, &p, 8, 0, nullptr) == SAS_ERR_INVALID);
@@ -183,6 +187,27 @@ static void device_paths(sas_sampler *s) {
   r.out_counts = (int32_t *)cnt;
   r.out_flags = (uint32_t *)flg;
   EXPECT(sas_reserve(s, rows, vocab) == SAS_OK);
+  {
+    // every shape field of the reserve descriptor, then its range checks
+    sas_reserve_desc d{};
+    d.rows = rows;
+    d.vocab = vocab;
+    d.hist_ids = 2048 * (int64_t)rows;
+    d.lm_head_rows = 2;
+    d.verify_seqs = 3;
+    d.verify_draft_len = 4;
+    EXPECT(sas_reserve_for(s, &d) == SAS_OK);
+    EXPECT(sas_reserve_for(s, nullptr) == SAS_ERR_INVALID);
+    sas_reserve_desc b = d;
+    b.lm_head_rows = SAS_LMH_MAX_ROWS + 1;
+    EXPECT(sas_reserve_for(s, &b) == SAS_ERR_INVALID);
+    b = d;
+    b.verify_draft_len = 0;
+    EXPECT(sas_reserve_for(s, &b) == SAS_ERR_INVALID);
+    b = d;
+    b.hist_ids = -1;
+    EXPECT(sas_reserve_for(s, &b) == SAS_ERR_INVALID);
+  }
   EXPECT(sas_sample(s, &r, sas_stream(s)) == SAS_OK);
   EXPECT(sas_synchronize(s, sas_stream(s)) == SAS_OK);
   std::vector<uint32_t> out = download(s, (uint32_t *)ids, rows);

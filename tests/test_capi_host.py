@@ -22,6 +22,31 @@ def test_library_exports_every_header_function():
     assert set(names) == set(_capi.SIGNATURES), "ctypes signatures and header differ"
 
 
+def test_probe_library_exports_its_header():
+    """libsas_probe.so (bench.py's measurement probes, outside the sampling
+    ABI) exports what include/sas_probe.h declares."""
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    path = os.path.join(root, "shared_amd", "libsas_probe.so")
+    if not os.path.exists(path):
+        pytest.skip("libsas_probe.so is not built")
+    text = open(os.path.join(root, "include", "sas_probe.h")).read()
+    names = sorted(set(re.findall(r"^int\s+(sasp_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+    assert names == ["sasp_masked_read", "sasp_read"]
+    lib = ctypes.CDLL(path)
+    for name in names:
+        assert hasattr(lib, name), name
+    # the sampling library does not carry the probes
+    assert not hasattr(_capi.load(), "sas_probe_read")
+
+
+def test_reserve_for_rejects_bad_shapes_without_a_handle():
+    lib = _capi.load()
+    d = _capi.SasReserveDesc(1, 1000, 0, 0, 0, 0)
+    assert lib.sas_reserve_for(None, ctypes.byref(d)) == _capi.ERR_INVALID
+    assert b"handle is NULL" in lib.sas_last_error(None)
+
+
 def test_version_names_the_target():
     v = _capi.load().sas_version().decode()
     assert v.startswith("shared_amd_sampler ") and v.endswith("gfx950")
@@ -38,7 +63,9 @@ def test_ctypes_layout_matches_the_c_compiler(tmp_path):
     import subprocess
     if shutil.which("gcc") is None:
         pytest.skip("gcc is not installed")
-    structs = {"sas_params": _capi.SasParams, "sas_rows": _capi.SasRows, "sas_verify_rows": _capi.SasVerifyRows}
+    structs = {"sas_params": _capi.SasParams, "sas_rows": _capi.SasRows, "sas_verify_rows": _capi.SasVerifyRows,
+               "sas_spec_rows": _capi.SasSpecRows, "sas_step": _capi.SasStep, "sas_lm_head": _capi.SasLmHead,
+               "sas_reserve_desc": _capi.SasReserveDesc}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "shared_amd_sampler.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')

@@ -180,3 +180,94 @@ def test_verify_in_a_graph():
             g.replay()
             torch.cuda.synchronize()
             _equal(_host(o), ww, f"verify replay {rep}")
+
+
+def test_reserved_handle_captures_with_no_eager_call():
+    """sas_reserve_for sizes every buffer, so a fresh handle's first calls can
+    be captured: a decode step whose ring (2,048 ids) is bucketed, the LM
+    head and a verify round, in one graph, each replay equal to the same
+    calls run eagerly on another handle."""
+    import torch
+    from shared_amd._capi import SasError
+    rows, vocab, ring_len = 4, 20_000, 2048
+    print(f"[gpu] graph: reserved handle, step rows={rows} ring={ring_len}, lm head, verify; vocab={vocab}", flush=True)
+    rng = np.random.default_rng(41)
+    x = to_dev((rng.standard_normal((rows, vocab)) * 2.0).astype(np.float32))
+    seeds = rng.integers(0, 2**32, rows, dtype=np.uint64).astype(np.uint32)
+    history = [[int(i) for i in rng.integers(0, vocab, 3000)] for _ in range(rows)]
+    prm = Params(temperature=0.9, top_k=40, top_p=0.9, repetition_penalty=1.2, frequency_penalty=0.2)
+    b = W.lmh(rows=2, vocab=vocab, dim=512, seed=42, hist=300)
+    inp = W.c5(seqs=4, vocab=vocab, seed=43, drafts=3, density=0.3)
+    seqs, L = inp["seqs"], inp["drafts"]
+
+    def make(s):
+        st = DecodeState(rows, max_steps=2, ring_len=ring_len, seeds=seeds, history=history)
+        bufs = {"st": st, "init": {k: getattr(st, k).clone() for k in ("state", "sampled", "next_tokens", "ring")},
+                "step": _outs(rows), "lmh": _outs(b.rows),
+                "hid": to_dev(b.hidden), "wt": to_dev(b.weight_bits.view(np.int16)),
+                "mask": to_dev(b.mask, torch.int32), "hist": to_dev(b.hist_ids, torch.int32),
+                "offs": to_dev(b.hist_offsets), "uni": to_dev(b.uniforms),
+                "t": to_dev(inp["target"]), "d": to_dev(inp["draft"]), "m": to_dev(inp["mask"].view(np.int32)),
+                "ids": to_dev(np.ascontiguousarray(inp["draft_ids"], np.uint32).view(np.int32)),
+                "u": to_dev(np.ascontiguousarray(inp["uniforms"], np.float64)),
+                "tok": torch.empty((seqs, L + 1), dtype=torch.int32, device="cuda"),
+                "acc": torch.empty(seqs, dtype=torch.int32, device="cuda")}
+
+        def run():
+            o = bufs["step"]
+            s.sample_step_into(x, o["ids"], bufs["st"], params=prm, out_probs=o["probs"], out_cand_ids=o["cand_ids"],
+                               out_counts=o["counts"])
+            o = bufs["lmh"]
+            s.lm_head_sample_into(bufs["hid"], bufs["wt"], o["ids"], mask=bufs["mask"], hist_ids=bufs["hist"],
+                                  hist_offsets=bufs["offs"], uniforms=bufs["uni"], params=b.params,
+                                  out_probs=o["probs"], out_cand_ids=o["cand_ids"], out_counts=o["counts"])
+            s.verify_into(bufs["t"], bufs["d"], bufs["ids"], bufs["u"], bufs["tok"], bufs["acc"],
+                          temperature=inp["temperature"], mask=bufs["m"], vocab=vocab)
+
+        def reset():
+            for k, v in bufs["init"].items():
+                getattr(bufs["st"], k).copy_(v)
+
+        def host():
+            st = bufs["st"]
+            return {**{"step_" + k: v for k, v in _host(bufs["step"]).items()},
+                    **{"lmh_" + k: v for k, v in _host(bufs["lmh"]).items()},
+                    "tok": bufs["tok"].cpu().numpy().copy(), "acc": bufs["acc"].cpu().numpy().copy(),
+                    **_host({k: getattr(st, k) for k in ("state", "sampled", "next_tokens", "ring")})}
+
+        def scrub():
+            for d in (bufs["step"], bufs["lmh"]):
+                _scrub(d)
+            bufs["tok"].fill_(-7)
+            bufs["acc"].fill_(-7)
+        return run, reset, host, scrub
+
+    with Sampler(0) as e:
+        run, reset, host, _ = make(e)
+        run()
+        torch.cuda.synchronize()
+        want = host()
+    with Sampler(0) as s:
+        s.reserve(rows, vocab, hist_ids=rows * ring_len, lm_head_rows=b.rows, verify_seqs=seqs, verify_draft_len=L)
+        run, reset, host, scrub = make(s)
+        g = _capture(run)
+        for rep in range(REPLAYS):
+            scrub()
+            reset()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            _equal(host(), want, f"reserved handle replay {rep}")
+        # a shape past the reservation cannot grow scratch under capture: the
+        # call fails with the reason and records nothing
+        big = to_dev(np.zeros((64, vocab), np.float32))
+        big_ids = torch.empty(64, dtype=torch.int32, device="cuda")
+        g2 = torch.cuda.CUDAGraph()
+        err = None
+        with torch.cuda.graph(g2):
+            try:
+                s.sample_into(big, big_ids, vocab=vocab, params=Params())
+            except SasError as ex:
+                err = str(ex)
+        torch.cuda.synchronize()
+        assert err is not None and "being captured" in err, err

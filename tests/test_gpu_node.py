@@ -76,6 +76,13 @@ def test_node_api_end_to_end(tmp_path):
     wt = O.sample_rows(bt)["ids"]
     assert np.array_equal(_u32(d, "js_tokmask_ids.u32"), wt)
     assert np.array_equal(_u32(d, "js_tokmask2_ids.u32"), wt)
+    # MaskBuilder words: the allow list minus its first 100 ids; packedToolMask
+    # over the allow list itself
+    mw = O.mask_from_ids(MASK_ALLOW, allow[100:], b.vocab)
+    bw = W.Batch("words", b.logits, b.params, mask=np.repeat(mw[None, :], b.rows, axis=0),
+                 hist_ids=b.hist_ids, hist_offsets=b.hist_offsets, uniforms=b.uniforms)
+    assert np.array_equal(_u32(d, "js_words_ids.u32"), O.sample_rows(bw)["ids"])
+    assert np.array_equal(_u32(d, "js_tool_ids.u32"), wt)
 
     # allowedTokenIds: every row, then the even rows only
     ba = W.Batch("allowed", b.logits, b.params, mask=np.repeat(m1[None, :], b.rows, axis=0),

@@ -1,7 +1,9 @@
 """sas_sample_noalloc, the entry point that allocates nothing (its scratch is
 a static device array), against sas_sample on the same inputs: bit-exact ids,
 ranked candidates, probabilities, counts and flags, on two calls in a row
-(the second with a smaller batch), and its size limit."""
+(the second with a smaller batch), for C3P-shaped batches and for C4's long
+histories (which sas_sample buckets by part and the no-allocation path does
+not), and its size limit."""
 import numpy as np
 import pytest
 
@@ -35,9 +37,26 @@ def _host(out):
     return {k: v.cpu().numpy() for k, v in out.items()}
 
 
-def test_noalloc_matches_sample_on_two_calls(request):
+def _c4_sampled(rows, seed):
+    """C4's long Zipf histories (4,096 ids per row: sas_sample buckets them,
+    sas_sample_noalloc does not) under sampling parameters, so the ranked
+    candidates and probabilities are compared too."""
+    from shared_amd import Params
+    b = W.c4(rows=rows, seed=seed)
+    b.params = Params(temperature=0.9, top_k=50, top_p=0.9, repetition_penalty=1.15, presence_penalty=0.5,
+                      frequency_penalty=0.3)
+    b.uniforms = np.random.default_rng(seed).random(rows)
+    return b
+
+
+@pytest.mark.parametrize("case", ["c3p", "c4"])
+def test_noalloc_matches_sample_on_two_calls(request, case):
     import torch
-    batches = [W.c3p(seed=71), W.c3(rows=24, vocab=W.QWEN_VOCAB, seed=72)]
+    if case == "c3p":
+        batches = [W.c3p(seed=71), W.c3(rows=24, vocab=W.QWEN_VOCAB, seed=72)]
+    else:
+        # 64 rows x 32 parts x 10 KiB fit the static scratch
+        batches = [_c4_sampled(64, 73), _c4_sampled(16, 74)]
     got = []
     # the static path first: in a fresh process its first call resolves the
     # scratch address itself
