@@ -322,6 +322,42 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream);
  * stream-ordered like sas_sample. */
 int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream);
 
+/*
+ * acceptSpec's on-device commit (kernels.js:340-367), so that rounds chain
+ * with no host work between them (specChain runs R rounds per submit,
+ * model.js:867-1008).  Each sas_spec_step call is one round of every
+ * sequence, as sas_spec_exact runs it, except:
+ *   - a sequence's history is its ring as of the round's start, and its
+ *     round number is its state's (rows->round and rows->hist_* are unused);
+ *   - a frozen sequence (one that committed a stop id) reads no logits: its
+ *     picks are SAS_STOP_PAD, its accepted count 0, its next token its first
+ *     stop id, and its log entry {0, first stop id, 0, ...} (kernels.js:358-362);
+ *   - any other sequence, after the cascade (a tokens accepted, next =
+ *     pick[a - 1]): its log entry {a, next, draft_0 .. draft_{L-1}}, pos += a,
+ *     accepted = a, pick[0 .. a) minus stop ids appended to its ring, and it
+ *     freezes when next is a stop id (kernels.js:341-357);
+ *   - every sequence's round advances by one and next_tokens receives next
+ *     (tokens[0] = next, kernels.js:364-365).
+ * The state persists across calls in caller-owned device memory; a chain
+ * starts from state {0, first round, pos, 0} and a ring seeded by the caller.
+ * previous pos = pos - accepted and "partial accept" = accepted < L + 1 are
+ * the reference's posBuf[2] and posBuf[3].
+ */
+typedef struct sas_spec_state {
+  uint32_t *state;          /* device [seqs][4] = {frozen, round, pos, accepted}
+                               (the reference's ctl[0], posBuf[4], posBuf[0], posBuf[1]) */
+  uint32_t *ring;           /* device [seqs][1 + ring_len] = {count, ids} or NULL (no history) */
+  int32_t ring_len;         /* 1..SAS_MAX_HISTORY with ring (the reference uses 512) */
+  uint32_t *log;            /* device [seqs][max_rounds][2 + draft_len] or NULL: per round
+                               {a, next, drafts}; rounds >= max_rounds are not logged */
+  int32_t max_rounds;
+  uint32_t *next_tokens;    /* device [seqs] or NULL */
+} sas_spec_state;
+
+/* One chained round: `r` as for sas_spec_exact (hist_ids must be NULL,
+ * round is ignored), `st` the sequences' persistent state. */
+int sas_spec_step(sas_sampler *s, const sas_spec_rows *r, const sas_spec_state *st, void *stream);
+
 /* ---- the LM head with the sampling step fused into its epilogue ----
  *
  * Replaces the decode head's final projection and the topk pass that reads

@@ -72,6 +72,9 @@ def lib() -> ctypes.CDLL:
         L.orc_spec_exact.argtypes = [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                      c_int64, c_void_p, c_void_p, POINTER(OrcParams), c_void_p, c_void_p, c_uint32,
                                      c_void_p, c_void_p, c_void_p, c_void_p]
+        L.orc_spec_commit.restype = None
+        L.orc_spec_commit.argtypes = [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_int32, c_void_p, c_int32, c_void_p, c_void_p]
         L.orc_lm_head_logits.restype = None
         L.orc_lm_head_logits.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p]
         _lib = L
@@ -183,6 +186,32 @@ def spec_exact(inp: dict) -> dict:
                          None if sp is None else ctypes.cast(sp, c_void_p), _p(seeds), int(inp.get("round", 0)),
                          _p(st), _p(picks), _p(acc), _p(nxt))
     return {"draft_ids": ids, "picks": picks, "accepted": acc, "next": nxt}
+
+
+def spec_commit(picks, draft_ids, accepted, stop_ids, state, ring=None, log=None):
+    """acceptSpec's commit (orc_spec_commit) in place on `state` ([seqs][4]
+    uint32), `ring` ([seqs][1 + ring_len] uint32 or None) and `log`
+    ([seqs][max_rounds][2 + L] uint32 or None); returns (next tokens,
+    accepted counts) of the round."""
+    picks = np.ascontiguousarray(picks, np.uint32)
+    seqs, L1 = picks.shape
+    ids = np.ascontiguousarray(draft_ids, np.uint32)
+    acc = np.ascontiguousarray(accepted, np.int32)
+    st = None if stop_ids is None else np.ascontiguousarray(stop_ids, np.uint32)
+    assert state.dtype == np.uint32 and state.flags.c_contiguous
+    ring_len = 0
+    if ring is not None:
+        assert ring.dtype == np.uint32 and ring.flags.c_contiguous
+        ring_len = ring.shape[1] - 1
+    max_rounds = 0
+    if log is not None:
+        assert log.dtype == np.uint32 and log.flags.c_contiguous and log.shape[2] == L1 + 1
+        max_rounds = log.shape[1]
+    nxt = np.zeros(seqs, np.uint32)
+    out_acc = np.zeros(seqs, np.int32)
+    lib().orc_spec_commit(seqs, L1 - 1, _p(picks), _p(ids), _p(acc), _p(st), state.ctypes.data, _p(ring), ring_len,
+                          _p(log), max_rounds, nxt.ctypes.data, out_acc.ctypes.data)
+    return nxt, out_acc
 
 
 # ------------------------------------------------------------ Node driver --

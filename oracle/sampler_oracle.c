@@ -48,6 +48,13 @@
  *                      maxima).  Pinned by closed forms: drafts = first
  *                      np.argmax over the non-NaN values, planted picks with
  *                      hand-derived accept counts, and a stop-id draft.
+ *   orc_spec_commit    acceptSpec's commit kernels.js:340-367 (log entry,
+ *                      position, ring appends without stop ids, stop freeze,
+ *                      frozen rounds, round counter).  Pinned by hand-derived
+ *                      chains (tests/test_oracle.py): planted picks whose
+ *                      logs, positions, rings and freezes are worked out by
+ *                      hand, a ring that wraps, a stop among the accepted
+ *                      picks.
  */
 #include "sampler_oracle.h"
 
@@ -574,5 +581,54 @@ void orc_lm_head_logits(const float *hidden, int64_t hidden_stride, const uint16
       }
       logits[(int64_t)r * vocab + id] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
     }
+  }
+}
+
+/* ------------------------------------------------- chained round commit -- */
+
+void orc_spec_commit(int32_t seqs, int32_t draft_len, const uint32_t *picks, const uint32_t *draft_ids,
+                     const int32_t *accepted, const uint32_t *stop_ids, uint32_t *state, uint32_t *ring,
+                     int32_t ring_len, uint32_t *log, int32_t max_rounds, uint32_t *next_tokens,
+                     int32_t *accepted_out) {
+  const int32_t L = draft_len;
+  for (int32_t s = 0; s < seqs; s++) {
+    const uint32_t *sp = stop_ids ? stop_ids + 4 * (int64_t)s : NULL;
+    const uint32_t stop0 = sp ? sp[0] : 0xFFFFFFFFu;
+    uint32_t *st = state + 4 * (int64_t)s;
+    const uint32_t frozen = st[0], rnd = st[1];
+    const uint32_t *pk = picks + (int64_t)s * (L + 1);
+    int32_t a = 0;
+    uint32_t next = stop0;
+    if (!frozen) {
+      a = accepted[s];
+      next = pk[a - 1];
+    }
+    if (log && rnd < (uint32_t)max_rounds) {
+      uint32_t *lg = log + ((int64_t)s * max_rounds + rnd) * (L + 2);
+      lg[0] = (uint32_t)a;
+      lg[1] = next;
+      for (int32_t j = 0; j < L; j++) lg[2 + j] = frozen ? 0u : draft_ids[(int64_t)s * L + j];
+    }
+    if (!frozen) {
+      st[2] += (uint32_t)a;   /* posBuf[0] += a */
+      st[3] = (uint32_t)a;    /* posBuf[1] = a */
+      for (int32_t i = 0; i < a; i++) {
+        const uint32_t t = pk[i];
+        int stop = 0;
+        for (int q = 0; q < 4 && sp; q++) stop |= t == sp[q];
+        if (!stop && ring) {
+          uint32_t *rg = ring + (int64_t)s * (ring_len + 1);
+          const uint32_t c = rg[0];
+          rg[1 + c % (uint32_t)ring_len] = t;
+          rg[0] = c + 1u;
+        }
+      }
+      int stop = 0;
+      for (int q = 0; q < 4 && sp; q++) stop |= next == sp[q];
+      if (stop) st[0] = 1u;
+    }
+    if (next_tokens) next_tokens[s] = next;
+    if (accepted_out) accepted_out[s] = a;
+    st[1] = rnd + 1u;
   }
 }

@@ -97,6 +97,20 @@ void orc_spec_exact(const float *target, const float *draft, int64_t stride,
                     uint32_t *out_picks, int32_t *out_accepted,
                     uint32_t *out_next);
 
+/* acceptSpec's commit (kernels.js:340-367) after one round of
+ * orc_spec_exact, for chained rounds (layout as sas_spec_state):
+ * state [seqs][4] = {frozen, round, pos, accepted}, ring [seqs][1 +
+ * ring_len] or NULL, log [seqs][max_rounds][2 + draft_len] or NULL,
+ * next_tokens [seqs] or NULL.  A frozen sequence logs {0, first stop id,
+ * 0, ...} and its next token is its first stop id; any other logs {a, next,
+ * drafts}, advances pos by a, appends picks[0 .. a) that are not stop ids
+ * to its ring and freezes when next is a stop id.  accepted_out (may be
+ * NULL) receives a (0 when frozen).  Every round advances. */
+void orc_spec_commit(int32_t seqs, int32_t draft_len, const uint32_t *picks, const uint32_t *draft_ids,
+                     const int32_t *accepted, const uint32_t *stop_ids, uint32_t *state, uint32_t *ring,
+                     int32_t ring_len, uint32_t *log, int32_t max_rounds, uint32_t *next_tokens,
+                     int32_t *accepted_out);
+
 /* The LM head's logits (sas_lm_head_sample): the bf16 weight widened to
  * f32 (bits << 16) times the f32 hidden value, summed as eight partials,
  * partial g a fused multiply-add chain from 0 over k = 64 c + 8 g + j

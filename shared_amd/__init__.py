@@ -6,7 +6,7 @@ Node by js/ over an N-API addon.  This Python package is the build and test
 harness' handle on the same library.
 """
 from ._capi import MAX_TOP_K, NO_TOKEN, SasError  # noqa: F401
-from .sampler import DecodeState, Params, Sampler, clamp_params, mask_from_ids, pack_params  # noqa: F401
+from .sampler import DecodeState, Params, Sampler, SpecState, clamp_params, mask_from_ids, pack_params  # noqa: F401
 
-__all__ = ["DecodeState", "Params", "Sampler", "SasError", "clamp_params", "mask_from_ids", "pack_params", "MAX_TOP_K",
+__all__ = ["DecodeState", "Params", "Sampler", "SasError", "SpecState", "clamp_params", "mask_from_ids", "pack_params", "MAX_TOP_K",
            "NO_TOKEN"]

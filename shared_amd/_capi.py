@@ -134,6 +134,17 @@ class SasSpecRows(ctypes.Structure):
     ]
 
 
+class SasSpecState(ctypes.Structure):
+    _fields_ = [
+        ("state", c_void_p),
+        ("ring", c_void_p),
+        ("ring_len", c_int32),
+        ("log", c_void_p),
+        ("max_rounds", c_int32),
+        ("next_tokens", c_void_p),
+    ]
+
+
 class SasReserveDesc(ctypes.Structure):
     _fields_ = [
         ("rows", c_int32),
@@ -169,6 +180,7 @@ SIGNATURES = {
     "sas_sample_step": (c_int, [c_void_p, POINTER(SasRows), POINTER(SasStep), c_void_p]),
     "sas_verify": (c_int, [c_void_p, POINTER(SasVerifyRows), c_void_p]),
     "sas_spec_exact": (c_int, [c_void_p, POINTER(SasSpecRows), c_void_p]),
+    "sas_spec_step": (c_int, [c_void_p, POINTER(SasSpecRows), POINTER(SasSpecState), c_void_p]),
     "sas_lm_head_sample": (c_int, [c_void_p, POINTER(SasLmHead), POINTER(SasRows), c_void_p]),
     "sas_clamp_params": (c_int, [POINTER(SasParams), POINTER(SasParams)]),
     "sas_mask_from_ids": (c_int64, [c_int32, POINTER(c_uint32), c_size_t, c_int32, POINTER(c_uint32), c_int64]),

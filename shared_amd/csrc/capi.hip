@@ -189,6 +189,7 @@ struct SpecDraw {
   const uint32_t *seeds;
   uint32_t round;
   int group;
+  const sas_spec_state *state;  // chained rounds (sas_spec_step), or null
 };
 
 // sas_sample, sas_sample_step (st) and the sampling of sas_spec_exact (sp):
@@ -228,6 +229,13 @@ int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char 
     a.spec_seeds = sp->seeds;
     a.spec_round = sp->round;
     a.group = sp->group;
+    if (sp->state) {
+      // a chained round: each sequence's ring is its history, its state
+      // holds its round and whether it is frozen
+      a.sp_state = sp->state->state;
+      a.ring = sp->state->ring;
+      a.ring_len = sp->state->ring ? sp->state->ring_len : 0;
+    }
   }
   // long histories: bucket them by part first, so a part reads its own ids
   const int hrows = sp && sp->group > 1 ? r->rows / sp->group : r->rows;
@@ -427,17 +435,30 @@ int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, 
   return SAS_OK;
 }
 
-int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream) {
-  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_spec_exact: handle is NULL");
-  if (!r) return fail(s, SAS_ERR_INVALID, "sas_spec_exact: descriptor is NULL");
-  if (r->seqs < 0) return fail(s, SAS_ERR_INVALID, "sas_spec_exact: seqs must be >= 0");
+}  // extern "C"
+
+namespace {
+
+// sas_spec_exact (st null) and sas_spec_step: one speculative round.
+int spec_on(sas_sampler *s, const sas_spec_rows *r, const sas_spec_state *st, const char *who, void *stream) {
+  const std::string w(who);
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, w + ": handle is NULL");
+  if (!r) return fail(s, SAS_ERR_INVALID, w + ": descriptor is NULL");
+  if (r->seqs < 0) return fail(s, SAS_ERR_INVALID, w + ": seqs must be >= 0");
   if (r->draft_len < 1 || r->draft_len > SAS_MAX_DRAFT)
-    return fail(s, SAS_ERR_INVALID, "sas_spec_exact: draft_len must be in [1, SAS_MAX_DRAFT]");
+    return fail(s, SAS_ERR_INVALID, w + ": draft_len must be in [1, SAS_MAX_DRAFT]");
+  if (st) {
+    if (!st->state) return fail(s, SAS_ERR_INVALID, w + ": state is required");
+    if (r->hist_ids) return fail(s, SAS_ERR_INVALID, w + ": hist_ids must be NULL: the ring is the history");
+    if (st->ring && (st->ring_len < 1 || st->ring_len > SAS_MAX_HISTORY))
+      return fail(s, SAS_ERR_INVALID, w + ": ring_len must be in [1, SAS_MAX_HISTORY]");
+    if (st->log && st->max_rounds < 1) return fail(s, SAS_ERR_INVALID, w + ": max_rounds must be >= 1 with log");
+  }
   if (r->seqs == 0) return SAS_OK;
   if ((int64_t)r->seqs * (r->draft_len + 1) > INT32_MAX)
-    return fail(s, SAS_ERR_INVALID, "sas_spec_exact: too many verify rows");
+    return fail(s, SAS_ERR_INVALID, w + ": too many verify rows");
   if (!r->draft_ids || !r->seeds || !r->out_picks || !r->out_accepted)
-    return fail(s, SAS_ERR_INVALID, "sas_spec_exact: draft_ids, seeds, out_picks and out_accepted are required");
+    return fail(s, SAS_ERR_INVALID, w + ": draft_ids, seeds, out_picks and out_accepted are required");
   hipStream_t stream_h = pick_stream(s, stream);
   const int L = r->draft_len;
   // the drafts: the argmax of every draft row (argmaxMerge, kernels.js:373-401)
@@ -452,8 +473,8 @@ int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream) {
     d.params.repetition_penalty = 1.0;
     d.params.top_k = 1;
     d.out_ids = r->draft_ids;
-    if (const char *m = check_rows(&d)) return fail(s, SAS_ERR_INVALID, std::string("sas_spec_exact: drafts: ") + m);
-    if (int rc = sample_on(s, &d, nullptr, "sas_spec_exact drafts", stream)) return rc;
+    if (const char *m = check_rows(&d)) return fail(s, SAS_ERR_INVALID, w + ": drafts: " + m);
+    if (int rc = sample_on(s, &d, nullptr, (w + " drafts").c_str(), stream)) return rc;
   }
   // every verify row, sampled on its own (kernels.js:255-327)
   sas_rows v{};
@@ -463,21 +484,46 @@ int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream) {
   v.rows = r->seqs * (L + 1);
   v.mask = r->mask;
   v.mask_stride = r->mask_stride;
-  v.hist_ids = r->hist_ids;
-  v.hist_offsets = r->hist_offsets;
-  v.hist_count = r->hist_count;
+  if (!st) {
+    v.hist_ids = r->hist_ids;
+    v.hist_offsets = r->hist_offsets;
+    v.hist_count = r->hist_count;
+  }
   v.params = r->params;
   v.row_params = r->seq_params;
   v.row_hints = r->row_hints;
   v.out_ids = r->out_picks;
-  if (const char *m = check_rows(&v, true)) return fail(s, SAS_ERR_INVALID, std::string("sas_spec_exact: ") + m);
-  const SpecDraw sp{r->seeds, r->round, L + 1};
-  if (int rc = sample_on(s, &v, nullptr, "sas_spec_exact", stream, &sp)) return rc;
-  // the cascade (kernels.js:328-339)
+  if (const char *m = check_rows(&v, true)) return fail(s, SAS_ERR_INVALID, w + ": " + m);
+  const SpecDraw sp{r->seeds, r->round, L + 1, st};
+  if (int rc = sample_on(s, &v, nullptr, who, stream, &sp)) return rc;
+  // the cascade (kernels.js:328-339), and a chained round's commit
+  // (kernels.js:340-367)
+  sas::SpecCommit c{};
+  if (st) {
+    c.state = st->state;
+    c.ring = st->ring;
+    c.ring_len = st->ring ? st->ring_len : 0;
+    c.log = st->log;
+    c.max_rounds = st->log ? st->max_rounds : 0;
+    c.next_tokens = st->next_tokens;
+  }
   hipError_t e = sas::launch_spec_cascade(r->out_picks, r->draft_ids, r->stop_ids, r->seqs, L, r->out_accepted,
-                                          r->out_next, stream_h);
-  if (e != hipSuccess) return hip_fail(s, e, "sas_spec_exact cascade launch");
+                                          r->out_next, c, stream_h);
+  if (e != hipSuccess) return hip_fail(s, e, (w + " cascade launch").c_str());
   return SAS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sas_spec_exact(sas_sampler *s, const sas_spec_rows *r, void *stream) {
+  return spec_on(s, r, nullptr, "sas_spec_exact", stream);
+}
+
+int sas_spec_step(sas_sampler *s, const sas_spec_rows *r, const sas_spec_state *st, void *stream) {
+  if (s && !st) return fail(s, SAS_ERR_INVALID, "sas_spec_step: state descriptor is NULL");
+  return spec_on(s, r, st, "sas_spec_step", stream);
 }
 
 int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {

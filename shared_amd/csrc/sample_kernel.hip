@@ -375,7 +375,8 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   const uint64_t info = qok ? load_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + q) : 0ull;
   const int srow = a.group > 1 ? row / a.group : row;
   const double u_row = greedy        ? 0.0
-                       : a.spec_seeds ? pcg_uniform(a.spec_seeds[srow], a.spec_round, (uint32_t)(row - srow * a.group))
+                       : a.spec_seeds ? pcg_uniform(a.spec_seeds[srow], a.sp_state ? a.sp_state[4 * srow + 1] : a.spec_round,
+                                                    (uint32_t)(row - srow * a.group))
                        : a.seeds      ? pcg_uniform(a.seeds[row], a.st_state[2 * row + 1], 0u)
                                       : a.uniforms[row];
   for (int i = tid; i < kSurvCap + 8; i += kThreads) ml.s_c[i] = 0ull;  // padding: ranks after everything
@@ -701,10 +702,13 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   __shared__ uint32_t s_sel[4];
   int row = blockIdx.x;
   if ((a.rows & 7) == 0 && ((a.rows * a.parts) & 7) == 0) row = (row & 7) * (a.rows >> 3) + (row >> 3);
-  if (a.st_state && a.st_state[2 * row] != 0u) {
-    // a frozen row emits its first stop id (kernels.js:184-185) and no candidates
+  const bool stopped = a.st_state && a.st_state[2 * row] != 0u;
+  const bool frozen = a.sp_state && a.sp_state[4 * (a.group > 1 ? row / a.group : row)] != 0u;
+  if (stopped || frozen) {
+    // a stopped row emits its first stop id (kernels.js:184-185), a frozen
+    // sequence's verify row no pick; neither has candidates
     const int tid = threadIdx.x;
-    const uint32_t tok = a.stop_ids ? a.stop_ids[4 * row] : SAS_STOP_PAD;
+    const uint32_t tok = stopped && a.stop_ids ? a.stop_ids[4 * row] : SAS_STOP_PAD;
     if (tid == 0) {
       a.out_ids[row] = tok;
       if (a.out_counts) {
@@ -712,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
         a.out_counts[2 * row + 1] = 0;
       }
       if (a.out_flags) a.out_flags[row] = 0u;
-      step_feedback(a, row, tok, true);
+      if (stopped) step_feedback(a, row, tok, true);
     }
     if (tid < SAS_MAX_TOP_K) {
       if (a.out_probs) a.out_probs[(int64_t)row * SAS_MAX_TOP_K + tid] = 0.0;
@@ -727,10 +731,12 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
 
 // The exact-match cascade (kernels.js:328-339): a = 1, next = pick[0];
 // each draft equal to the pick before it that is not a stop id accepts one
-// more pick.
+// more pick.  With a chained round's state, the commit of acceptSpec
+// (kernels.js:340-367) follows, by the same thread.
 __global__ __launch_bounds__(kThreads) void spec_cascade_kernel(const uint32_t *picks, const uint32_t *drafts,
                                                                 const uint32_t *stop_ids, int seqs, int L,
-                                                                int32_t *accepted, uint32_t *next) {
+                                                                int32_t *accepted, uint32_t *next,
+                                                                const SpecCommit c) {
   const int s = (int)(blockIdx.x * kThreads + threadIdx.x);
   if (s >= seqs) return;
   const uint32_t *pk = picks + (int64_t)s * (L + 1);
@@ -738,22 +744,57 @@ __global__ __launch_bounds__(kThreads) void spec_cascade_kernel(const uint32_t *
   uint32_t st[4] = {SAS_STOP_PAD, SAS_STOP_PAD, SAS_STOP_PAD, SAS_STOP_PAD};
   if (stop_ids)
     for (int i = 0; i < 4; ++i) st[i] = stop_ids[4 * s + i];
-  int n = 1;
-  while (n <= L) {
-    const uint32_t t = pk[n - 1];
-    const bool stop = t == st[0] || t == st[1] || t == st[2] || t == st[3];
-    if (t != dr[n - 1] || stop) break;
-    ++n;
+  auto is_stop = [&](uint32_t t) { return t == st[0] || t == st[1] || t == st[2] || t == st[3]; };
+  uint32_t *sq = c.state ? c.state + 4 * (int64_t)s : nullptr;
+  const uint32_t frozen = sq ? sq[0] : 0u;
+  int n = 0;
+  uint32_t tok = st[0];
+  if (!frozen) {
+    n = 1;
+    while (n <= L) {
+      const uint32_t t = pk[n - 1];
+      if (t != dr[n - 1] || is_stop(t)) break;
+      ++n;
+    }
+    tok = pk[n - 1];
   }
   accepted[s] = n;
-  if (next) next[s] = pk[n - 1];
+  if (next) next[s] = tok;
+  if (!sq) return;
+  // ---- the commit: log, position, ring, stop freeze, round ----
+  const uint32_t rnd = sq[1];
+  if (c.log && rnd < (uint32_t)c.max_rounds) {
+    uint32_t *lg = c.log + ((int64_t)s * c.max_rounds + rnd) * (L + 2);
+    lg[0] = (uint32_t)n;
+    lg[1] = tok;
+    for (int j = 0; j < L; ++j) lg[2 + j] = frozen ? 0u : dr[j];
+  }
+  if (!frozen) {
+    sq[2] += (uint32_t)n;
+    sq[3] = (uint32_t)n;
+    if (c.ring) {
+      uint32_t *rg = c.ring + (int64_t)s * (c.ring_len + 1);
+      uint32_t cnt = rg[0];
+      for (int i = 0; i < n; ++i) {
+        const uint32_t t = pk[i];
+        if (!is_stop(t)) {
+          rg[1 + cnt % (uint32_t)c.ring_len] = t;
+          ++cnt;
+        }
+      }
+      rg[0] = cnt;
+    }
+    if (is_stop(tok)) sq[0] = 1u;
+  }
+  if (c.next_tokens) c.next_tokens[s] = tok;
+  sq[1] = rnd + 1u;
 }
 
 hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, const uint32_t *stop_ids, int seqs,
-                               int L, int32_t *accepted, uint32_t *next, hipStream_t stream) {
+                               int L, int32_t *accepted, uint32_t *next, const SpecCommit &c, hipStream_t stream) {
   if (seqs <= 0) return hipSuccess;
   hipLaunchKernelGGL(spec_cascade_kernel, dim3((unsigned)((seqs + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                     stream, picks, drafts, stop_ids, seqs, L, accepted, next);
+                     stream, picks, drafts, stop_ids, seqs, L, accepted, next, c);
   return hipGetLastError();
 }
 
@@ -818,9 +859,11 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const int lo = part * a.span;
   const int nids = min(a.span, vocab - lo);  // > 0
 
-  // a row that already sampled a stop id (sas_sample_step) reads nothing
-  if (a.st_state && a.st_state[2 * row] != 0u) return;
   const int srow = a.group > 1 ? row / a.group : row;  // the row's sequence
+  // a row that already sampled a stop id (sas_sample_step), or a row of a
+  // frozen sequence (sas_spec_step), reads nothing
+  if (a.st_state && a.st_state[2 * row] != 0u) return;
+  if (a.sp_state && a.sp_state[4 * srow] != 0u) return;
   sas_params p = a.params;
   if (a.row_params) p = load_row_params(a.row_params + srow);
   const bool greedy = !(p.temperature > 0.0);
@@ -840,8 +883,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       h0 = bo[0];
       h1 = bo[1];
     } else if (a.ring) {
-      // the row's penalty ring: its first min(count, ring_len) slots
-      const uint32_t *rg = a.ring + (int64_t)row * (a.ring_len + 1);
+      // the row's (or its sequence's) penalty ring: its first
+      // min(count, ring_len) slots
+      const uint32_t *rg = a.ring + (int64_t)srow * (a.ring_len + 1);
       hid = rg + 1;
       h1 = (int)min(rg[0], (uint32_t)a.ring_len);
     } else {

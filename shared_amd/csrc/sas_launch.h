@@ -70,6 +70,10 @@ struct SampleArgs {
   const uint32_t *spec_seeds;
   uint32_t spec_round;
   int32_t group;
+  // Chained rounds (sas_spec_step): per sequence {frozen, round, pos,
+  // accepted}.  A frozen sequence's rows read nothing; the others draw with
+  // their own round; the ring above is then indexed by sequence.
+  const uint32_t *sp_state;
   // Long histories bucketed by part before the parts kernel: the ids of
   // history row h (a row, or a group's sequence) that fall in part q are
   // hb_ids[hb_offs[h * (parts + 1) + q] .. hb_offs[h * (parts + 1) + q + 1]).
@@ -92,10 +96,23 @@ hipError_t launch_merge(const SampleArgs &a, hipStream_t stream);
 // softcap (row_params, or params.softcap > 0).
 hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream);
 
+// The commit of a chained round (sas_spec_step), all null for
+// sas_spec_exact: per sequence {frozen, round, pos, accepted}, the ring,
+// the round log [seqs][max_rounds][2 + L] and the next input tokens.
+struct SpecCommit {
+  uint32_t *state;
+  uint32_t *ring;
+  int32_t ring_len;
+  uint32_t *log;
+  int32_t max_rounds;
+  uint32_t *next_tokens;
+};
+
 // The exact-match cascade of sas_spec_exact, one thread per sequence:
-// picks [seqs][L + 1], drafts [seqs][L], stop ids [seqs][4] or null.
+// picks [seqs][L + 1], drafts [seqs][L], stop ids [seqs][4] or null; with
+// c.state, the round's commit too.
 hipError_t launch_spec_cascade(const uint32_t *picks, const uint32_t *drafts, const uint32_t *stop_ids, int seqs,
-                               int L, int32_t *accepted, uint32_t *next, hipStream_t stream);
+                               int L, int32_t *accepted, uint32_t *next, const SpecCommit &c, hipStream_t stream);
 
 // Histories of at least this many ids per row on average are bucketed by
 // part first (one more launch): each part then reads its own ids only.

@@ -154,6 +154,53 @@ def sample_noalloc_into(device: int, logits, out_ids, *, stream=None, **kw) -> N
     check(load().sas_sample_noalloc(int(device), ctypes.byref(d), _stream(stream)), None)
 
 
+class SpecState:
+    """The caller-owned device state of sas_spec_step for `seqs` sequences
+    with `draft_len` drafts: {frozen, round, pos, accepted} per sequence (the
+    reference's ctl[0], posBuf[4], posBuf[0], posBuf[1]), the penalty ring,
+    the per-round log {a, next, drafts} and the next input tokens
+    (kernels.js:340-367 keeps the same state for one sequence)."""
+
+    def __init__(self, seqs: int, draft_len: int, *, max_rounds: int, ring_len: int = 512, first_round: int = 0,
+                 pos=None, history=None, device=0):
+        import torch
+        if not 1 <= ring_len <= _capi.MAX_HISTORY:
+            raise ValueError("ring_len must be in [1, SAS_MAX_HISTORY]")
+        dev = torch.device("cuda", device) if isinstance(device, int) else device
+        self.seqs, self.draft_len, self.max_rounds, self.ring_len = seqs, draft_len, max_rounds, ring_len
+        st = np.zeros((seqs, 4), dtype=np.uint32)
+        st[:, 1] = first_round
+        if pos is not None:
+            st[:, 2] = np.asarray(pos, dtype=np.uint32)
+        self.state = torch.from_numpy(st.view(np.int32)).to(dev)
+        self.ring = torch.from_numpy(ring_rows(seqs, ring_len, history).view(np.int32)).to(dev)
+        self.log = torch.zeros((seqs, max_rounds, draft_len + 2), dtype=torch.int32, device=dev)
+        self.next_tokens = torch.full((seqs,), -1, dtype=torch.int32, device=dev)
+
+    def descriptor(self):
+        from ._capi import SasSpecState
+        d = SasSpecState()
+        d.state = self.state.data_ptr()
+        d.ring = self.ring.data_ptr()
+        d.ring_len = self.ring_len
+        d.log = self.log.data_ptr()
+        d.max_rounds = self.max_rounds
+        d.next_tokens = self.next_tokens.data_ptr()
+        return d
+
+
+def ring_rows(rows: int, ring_len: int, history=None) -> np.ndarray:
+    """uint32 [rows][1 + ring_len] rings {count, ids}: the last ring_len ids
+    of each row's window, id i of the window at slot i % ring_len."""
+    ring = np.zeros((rows, 1 + ring_len), dtype=np.uint32)
+    for r, h in enumerate(history or []):
+        h = [int(x) for x in h]
+        for i in range(max(0, len(h) - ring_len), len(h)):
+            ring[r, 1 + i % ring_len] = h[i]
+        ring[r, 0] = len(h)
+    return ring
+
+
 class DecodeState:
     """The caller-owned device state of sas_sample_step for `rows` sequences:
     {stopped, iteration} per row, the sampled tokens, the next input token,
@@ -170,14 +217,7 @@ class DecodeState:
         self.state = torch.zeros((rows, 2), dtype=torch.int32, device=dev)
         self.sampled = torch.full((rows, max_steps), -1, dtype=torch.int32, device=dev)
         self.next_tokens = torch.full((rows,), -1, dtype=torch.int32, device=dev)
-        ring = np.zeros((rows, 1 + ring_len), dtype=np.uint32)
-        for r, h in enumerate(history or []):
-            # the last ring_len ids of the row's window, id i at slot i % ring_len
-            h = [int(x) for x in h]
-            for i in range(max(0, len(h) - ring_len), len(h)):
-                ring[r, 1 + i % ring_len] = h[i]
-            ring[r, 0] = len(h)
-        self.ring = torch.from_numpy(ring.view(np.int32)).to(dev)
+        self.ring = torch.from_numpy(ring_rows(rows, ring_len, history).view(np.int32)).to(dev)
         self.stop_ids = None
         if stop_ids is not None:
             st = np.full((rows, 4), _capi.STOP_PAD, dtype=np.uint32)
@@ -320,13 +360,10 @@ class Sampler:
         st = state.descriptor()
         check(self._lib.sas_sample_step(self._h, ctypes.byref(d), ctypes.byref(st), _stream(stream)), self._h)
 
-    def spec_exact_into(self, target, draft_ids, seeds, out_picks, out_accepted, *, draft_logits=None,
-                        out_next=None, round: int = 0, vocab: Optional[int] = None, mask=None, hist_ids=None,
-                        hist_offsets=None, params: Optional[Params] = None, seq_params=None, row_hints: int = 0,
-                        stop_ids=None, stream=None) -> None:
-        """sas_spec_exact: the reference's exact-match speculative round
-        (argmax drafts when draft_logits is given, every verify row sampled
-        on its own, the cascade) on caller-provided device buffers."""
+    @staticmethod
+    def _spec_rows(target, draft_ids, seeds, out_picks, out_accepted, *, draft_logits=None, out_next=None,
+                   round: int = 0, vocab: Optional[int] = None, mask=None, hist_ids=None, hist_offsets=None,
+                   params: Optional[Params] = None, seq_params=None, row_hints: int = 0, stop_ids=None):
         seqs, L = draft_ids.shape
         if target.shape[0] != seqs * (L + 1):
             raise ValueError("target must hold seqs * (draft_len + 1) rows")
@@ -358,7 +395,27 @@ class Sampler:
         d.out_picks = _ptr(out_picks)
         d.out_accepted = _ptr(out_accepted)
         d.out_next = _ptr(out_next)
+        return d
+
+    def spec_exact_into(self, target, draft_ids, seeds, out_picks, out_accepted, *, stream=None, **kw) -> None:
+        """sas_spec_exact: the reference's exact-match speculative round
+        (argmax drafts when draft_logits is given, every verify row sampled
+        on its own, the cascade) on caller-provided device buffers."""
+        d = self._spec_rows(target, draft_ids, seeds, out_picks, out_accepted, **kw)
         check(self._lib.sas_spec_exact(self._h, ctypes.byref(d), _stream(stream)), self._h)
+
+    def spec_step_into(self, target, draft_ids, seeds, out_picks, out_accepted, state: "SpecState", *, stream=None,
+                       **kw) -> None:
+        """sas_spec_step: one chained round; the history is `state`'s ring,
+        the round number its own, and the commit (log, pos, ring, stop
+        freeze, next token) is written back into `state`."""
+        if kw.get("hist_ids") is not None:
+            raise ValueError("a chained round's history is its ring")
+        if draft_ids.shape != (state.seqs, state.draft_len):
+            raise ValueError("draft_ids must be [seqs][draft_len] of the state's shape")
+        d = self._spec_rows(target, draft_ids, seeds, out_picks, out_accepted, **kw)
+        st = state.descriptor()
+        check(self._lib.sas_spec_step(self._h, ctypes.byref(d), ctypes.byref(st), _stream(stream)), self._h)
 
     def verify_into(self, target, draft, draft_ids, uniforms, out_tokens, out_accepted, *, temperature=1.0,
                     mask=None, vocab: Optional[int] = None, stream=None) -> None:

@@ -88,6 +88,8 @@ static void null_handle_paths() {
   EXPECT(last_error_has(nullptr, "handle is NULL"));
   EXPECT(sas_sample_step(nullptr, &r, &st, nullptr) == SAS_ERR_INVALID);
   EXPECT(sas_spec_exact(nullptr, &sp, nullptr) == SAS_ERR_INVALID);
+  sas_spec_state sst{};
+  EXPECT(sas_spec_step(nullptr, &sp, &sst, nullptr) == SAS_ERR_INVALID);
   EXPECT(sas_verify(nullptr, &v, nullptr) == SAS_ERR_INVALID);
   sas_lm_head lh{};
   EXPECT(sas_lm_head_sample(nullptr, &lh, &r, nullptr) == SAS_ERR_INVALID);
@@ -289,6 +291,43 @@ static void device_paths(sas_sampler *s) {
   bsp = sp;
   bsp.seeds = nullptr;
   EXPECT(sas_spec_exact(s, &bsp, nullptr) == SAS_ERR_INVALID && last_error_has(s, "required"));
+  {
+    // a chained round over the same rows: state, ring, log and next tokens
+    // in device memory, then its argument checks
+    std::vector<uint32_t> st0((size_t)seqs * 4, 0u), ring0((size_t)seqs * 9, 0u);
+    uint32_t *cst = upload(s, st0), *dring = upload(s, ring0);
+    void *dlog = nullptr, *dnext = nullptr;
+    EXPECT(sas_alloc(s, (size_t)seqs * 2 * (L + 2) * 4, &dlog) == SAS_OK && sas_alloc(s, seqs * 4, &dnext) == SAS_OK);
+    sas_spec_state cs{};
+    cs.state = cst;
+    cs.ring = dring;
+    cs.ring_len = 8;
+    cs.log = (uint32_t *)dlog;
+    cs.max_rounds = 2;
+    cs.next_tokens = (uint32_t *)dnext;
+    sas_spec_rows csp = sp;
+    csp.hist_ids = nullptr;
+    csp.hist_offsets = nullptr;
+    csp.hist_count = 0;
+    EXPECT(sas_spec_step(s, &csp, &cs, nullptr) == SAS_OK);
+    EXPECT(sas_spec_step(s, &csp, &cs, nullptr) == SAS_OK);
+    EXPECT(sas_synchronize(s, nullptr) == SAS_OK);
+    std::vector<uint32_t> st1 = download(s, cst, (size_t)seqs * 4);
+    for (int32_t q = 0; q < seqs; ++q) EXPECT(st1[4 * q + 1] == 2u);  // two rounds
+    EXPECT(sas_spec_step(s, &csp, nullptr, nullptr) == SAS_ERR_INVALID && last_error_has(s, "state"));
+    EXPECT(sas_spec_step(s, &sp, &cs, nullptr) == SAS_ERR_INVALID && last_error_has(s, "ring is the history"));
+    sas_spec_state bad = cs;
+    bad.ring_len = 0;
+    EXPECT(sas_spec_step(s, &csp, &bad, nullptr) == SAS_ERR_INVALID && last_error_has(s, "ring_len"));
+    bad = cs;
+    bad.max_rounds = 0;
+    EXPECT(sas_spec_step(s, &csp, &bad, nullptr) == SAS_ERR_INVALID && last_error_has(s, "max_rounds"));
+    bad = cs;
+    bad.state = nullptr;
+    EXPECT(sas_spec_step(s, &csp, &bad, nullptr) == SAS_ERR_INVALID && last_error_has(s, "state is required"));
+    EXPECT(sas_free(s, cst) == SAS_OK && sas_free(s, dring) == SAS_OK && sas_free(s, dlog) == SAS_OK &&
+           sas_free(s, dnext) == SAS_OK);
+  }
   // rejection-sampling verify over the same rows
   std::vector<double> vu((size_t)seqs * (L + 1) * 2);
   for (size_t i = 0; i < vu.size(); ++i) vu[i] = (i + 0.25) / vu.size();

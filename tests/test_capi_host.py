@@ -65,7 +65,7 @@ def test_ctypes_layout_matches_the_c_compiler(tmp_path):
         pytest.skip("gcc is not installed")
     structs = {"sas_params": _capi.SasParams, "sas_rows": _capi.SasRows, "sas_verify_rows": _capi.SasVerifyRows,
                "sas_spec_rows": _capi.SasSpecRows, "sas_step": _capi.SasStep, "sas_lm_head": _capi.SasLmHead,
-               "sas_reserve_desc": _capi.SasReserveDesc}
+               "sas_reserve_desc": _capi.SasReserveDesc, "sas_spec_state": _capi.SasSpecState}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "shared_amd_sampler.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')

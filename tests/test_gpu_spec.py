@@ -122,3 +122,124 @@ def test_random_sweep(sampler):
         label = f"sweep {case}: seqs={seqs} L={L} vocab={vocab} given={given}"
         print(f"[gpu] spec {label}", flush=True)
         check(run_spec(sampler, c, drafts_given=given), O.spec_exact(c), label)
+
+
+def _oracle_chain(cases, seeds, stop_ids, rounds, ring0, first_round):
+    """orc_spec_exact then orc_spec_commit, round by round, every sequence's
+    history being its ring as of the round's start."""
+    seqs, L = cases[0]["seqs"], cases[0]["drafts"]
+    ring = ring0.copy()
+    ring_len = ring.shape[1] - 1
+    state = np.zeros((seqs, 4), np.uint32)
+    state[:, 1] = first_round
+    log = np.zeros((seqs, rounds, L + 2), np.uint32)
+    per = []
+    for r in range(rounds):
+        c = dict(cases[r])
+        hist = [ring[s, 1:1 + min(int(ring[s, 0]), ring_len)] for s in range(seqs)]
+        c["hist_ids"], c["hist_offsets"] = W._csr(hist)
+        c["seeds"], c["stop_ids"], c["round"] = seeds, stop_ids, int(state[0, 1])
+        frozen = state[:, 0].copy()
+        o = O.spec_exact(c)
+        nxt, acc = O.spec_commit(o["picks"], o["draft_ids"], o["accepted"], stop_ids, state, ring, log)
+        per.append({"frozen": frozen, "draft_ids": o["draft_ids"], "picks": o["picks"], "accepted": acc,
+                    "next": nxt})
+    return per, state, ring, log
+
+
+def test_spec_chain_of_rounds_in_a_graph(sampler):
+    """sas_spec_step: four chained rounds recorded into one HIP graph (the
+    reference's specChain submits R rounds at once, model.js:867-1008), every
+    replay bit-exact with the oracle stepped round by round: drafts, picks and
+    accepted counts of the live sequences, the round log, the state {frozen,
+    round, pos, accepted}, the rings and the next tokens; one sequence draws
+    its stop id mid-chain and freezes, one ring wraps."""
+    import torch
+    from shared_amd import SpecState
+    from shared_amd.sampler import ring_rows
+    seqs, L, vocab, rounds, ring_len, first = 8, 2, 32_000, 4, 48, 3
+    cases = [W.spec_case(seqs=seqs, vocab=vocab, drafts=L, hist=0, seed=300 + r) for r in range(rounds)]
+    for c in cases[1:]:
+        c["seq_params"] = cases[0]["seq_params"]
+    rng = np.random.default_rng(9)
+    seeds = rng.integers(0, 2**32, seqs, dtype=np.uint64).astype(np.uint32)
+    hist = [[int(i) for i in rng.integers(0, vocab, 10 + 9 * s)] for s in range(seqs)]  # seq 5 on wrap past 48
+    ring0 = ring_rows(seqs, ring_len, hist)
+    pad = 0xFFFFFFFF
+    stops = np.full((seqs, 4), pad, np.uint32)
+    stops[:, 0] = 151645
+    # plant: sequence 2's round-1 next token becomes one of its stop ids
+    per0, _, _, _ = _oracle_chain(cases, seeds, stops, rounds, ring0, first)
+    stops[2, 1] = per0[1]["next"][2]
+    per, want_state, want_ring, want_log = _oracle_chain(cases, seeds, stops, rounds, ring0, first)
+    assert want_state[2, 0] == 1 and (want_log[2, 2:, 0] == 0).all(), "the plant must freeze seq 2 mid-chain"
+    print(f"[gpu] spec chain: {rounds} rounds x {seqs} seqs, L={L}, vocab={vocab}, ring {ring_len}", flush=True)
+    sp = dev(pack_params(cases[0]["seq_params"]).view(np.uint8))
+    hints = row_hints(cases[0]["seq_params"])
+    tg = [dev(c["target"]) for c in cases]
+    dr = [dev(c["draft"]) for c in cases]
+    ids = [torch.zeros((seqs, L), dtype=torch.int32, device="cuda") for _ in range(rounds)]
+    picks = [torch.empty((seqs, L + 1), dtype=torch.int32, device="cuda") for _ in range(rounds)]
+    acc = [torch.empty(seqs, dtype=torch.int32, device="cuda") for _ in range(rounds)]
+    sd, st_d = dev(seeds, torch.int32), dev(stops, torch.int32)
+    state = SpecState(seqs, L, max_rounds=rounds, ring_len=ring_len, first_round=first, history=hist)
+    init = {k: getattr(state, k).clone() for k in ("state", "ring", "log", "next_tokens")}
+
+    def run(stream=None):
+        for r in range(rounds):
+            sampler.spec_step_into(tg[r], ids[r], sd, picks[r], acc[r], state, draft_logits=dr[r], seq_params=sp,
+                                   row_hints=hints, stop_ids=st_d, stream=stream)
+
+    def reset():
+        for k, v in init.items():
+            getattr(state, k).copy_(v)
+
+    def check(label):
+        u32 = lambda t: t.cpu().numpy().view(np.uint32)  # noqa: E731
+        for r in range(rounds):
+            live = per[r]["frozen"] == 0
+            assert np.array_equal(u32(ids[r]), per[r]["draft_ids"]), f"{label} round {r}: drafts"
+            assert np.array_equal(u32(picks[r])[live], per[r]["picks"][live]), f"{label} round {r}: picks"
+            assert (u32(picks[r])[~live] == pad).all(), f"{label} round {r}: frozen picks"
+            assert np.array_equal(acc[r].cpu().numpy(), per[r]["accepted"]), f"{label} round {r}: accepted"
+        assert np.array_equal(u32(state.state), want_state), f"{label}: state"
+        assert np.array_equal(u32(state.ring), want_ring), f"{label}: rings"
+        assert np.array_equal(u32(state.log), want_log), f"{label}: log"
+        assert np.array_equal(u32(state.next_tokens), per[-1]["next"]), f"{label}: next tokens"
+
+    run()
+    torch.cuda.synchronize()
+    check("eager")
+    reset()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for t in picks + acc + ids:
+            t.fill_(-7)
+        reset()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        check(f"replay {rep}")
+
+
+def test_spec_step_argument_errors(sampler):
+    import torch
+    from shared_amd import SpecState
+    seqs, L, vocab = 2, 2, 1000
+    state = SpecState(seqs, L, max_rounds=1, ring_len=8)
+    t = torch.zeros((seqs * (L + 1), vocab), dtype=torch.float32, device="cuda")
+    ids = torch.zeros((seqs, L), dtype=torch.int32, device="cuda")
+    seeds = torch.zeros(seqs, dtype=torch.int32, device="cuda")
+    picks = torch.empty((seqs, L + 1), dtype=torch.int32, device="cuda")
+    acc = torch.empty(seqs, dtype=torch.int32, device="cuda")
+    h = torch.zeros(4, dtype=torch.int32, device="cuda")
+    ho = torch.tensor([0, 2, 4], dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="ring"):
+        sampler.spec_step_into(t, ids, seeds, picks, acc, state, hist_ids=h, hist_offsets=ho)
+    state.ring_len = 0
+    with pytest.raises(SasError, match="ring_len"):
+        sampler.spec_step_into(t, ids, seeds, picks, acc, state)

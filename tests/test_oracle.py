@@ -456,6 +456,65 @@ def test_spec_history_is_the_rounds_start_for_every_row():
     assert o["accepted"].tolist() == [3]
 
 
+def test_spec_commit_hand_derived_chain():
+    """acceptSpec's commit (kernels.js:340-367) over planted rounds whose
+    results are worked out by hand: the log entry {a, next, d0, d1}, pos += a,
+    accepted = a, pick[0 .. a) appended to a ring of 3 that wraps, a stop id
+    that ends the cascade is not appended and freezes the sequence, a frozen
+    round logs {0, first stop id, 0, 0} and changes nothing else, and a round
+    past max_rounds is not logged."""
+    pad = 0xFFFFFFFF
+    stops = np.array([[99, pad, pad, pad], [pad] * 4, [77, pad, pad, pad]], np.uint32)
+    state = np.array([[0, 0, 10, 0], [0, 0, 0, 0], [1, 5, 20, 2]], np.uint32)
+    ring = np.array([[2, 1, 2, 0], [0, 0, 0, 0], [1, 55, 0, 0]], np.uint32)
+    log = np.full((3, 4, 4), 7, np.uint32)
+    # round 0: seq 0 accepts both drafts (a = 3), seq 1 misses its first (a = 1)
+    nxt, acc = O.spec_commit([[5, 6, 7], [4, 9, 9], [1, 2, 3]], [[5, 6], [3, 9], [1, 2]], [3, 1, 3], stops, state,
+                             ring, log)
+    assert nxt.tolist() == [7, 4, 77] and acc.tolist() == [3, 1, 0]
+    assert log[0, 0].tolist() == [3, 7, 5, 6] and log[1, 0].tolist() == [1, 4, 3, 9]
+    assert (log[2] == 7).all()                       # round 5 of seq 2: past max_rounds, not logged
+    # ring of seq 0: count 2 -> slots 2, 0, 1 take 5, 6, 7
+    assert ring[0].tolist() == [5, 6, 7, 5] and ring[1].tolist() == [1, 4, 0, 0]
+    assert ring[2].tolist() == [1, 55, 0, 0]
+    assert state.tolist() == [[0, 1, 13, 3], [0, 1, 1, 1], [1, 6, 20, 2]]
+    # round 1: seq 0's first pick is its stop id 99 (the cascade stopped at a = 1)
+    nxt, acc = O.spec_commit([[99, 8, 8], [4, 4, 4], [0, 0, 0]], [[99, 8], [4, 4], [0, 0]], [1, 3, 3], stops,
+                             state, ring, log)
+    assert nxt.tolist() == [99, 4, 77] and acc.tolist() == [1, 3, 0]
+    assert log[0, 1].tolist() == [1, 99, 99, 8] and log[1, 1].tolist() == [3, 4, 4, 4]
+    assert ring[0].tolist() == [5, 6, 7, 5]          # the stop id is not appended
+    assert ring[1].tolist() == [4, 4, 4, 4]          # count 1 -> 4: slots 1, 2, 0
+    assert state.tolist() == [[1, 2, 14, 1], [0, 2, 4, 3], [1, 7, 20, 2]]
+    # round 2: seq 0 is frozen now
+    nxt, acc = O.spec_commit([[1, 1, 1], [5, 6, 6], [0, 0, 0]], [[1, 1], [5, 7], [0, 0]], [3, 2, 3], stops, state,
+                             ring, log)
+    assert nxt.tolist() == [99, 6, 77] and acc.tolist() == [0, 2, 0]
+    assert log[0, 2].tolist() == [0, 99, 0, 0] and log[1, 2].tolist() == [2, 6, 5, 7]
+    assert state.tolist() == [[1, 3, 14, 1], [0, 3, 6, 2], [1, 8, 20, 2]]
+    assert ring[0].tolist() == [5, 6, 7, 5] and ring[1].tolist() == [6, 4, 5, 6]  # count 4: slots 1, 2 take 5, 6
+
+
+def test_spec_commit_stop_among_the_accepted_picks():
+    """A stop id drawn as the second pick when it equals the second draft
+    ends the cascade there (a = 2, next = the stop id): the first pick is
+    appended, the stop is not, and the sequence freezes."""
+    pad = 0xFFFFFFFF
+    state = np.zeros((1, 4), np.uint32)
+    ring = np.zeros((1, 9), np.uint32)
+    target = np.zeros((3, 64), np.float32)
+    for j, t in enumerate([3, 4, 5]):
+        target[j, t] = 5.0                            # greedy picks 3, 4, 5
+    o = O.spec_exact(_spec_inp(target, 2, draft_ids=np.array([[3, 4]], np.uint32), params=Params(temperature=0.0),
+                               stop=[[4]]))
+    assert o["picks"].tolist() == [[3, 4, 5]] and o["accepted"].tolist() == [2] and o["next"].tolist() == [4]
+    nxt, acc = O.spec_commit(o["picks"], [[3, 4]], o["accepted"], np.array([[4, pad, pad, pad]], np.uint32), state,
+                             ring)
+    assert nxt.tolist() == [4] and acc.tolist() == [2]
+    assert ring[0, :3].tolist() == [1, 3, 0]
+    assert state.tolist() == [[1, 1, 2, 2]]
+
+
 # ---------------------------------------------------------------- lm head --
 
 def _bf16(x: float) -> int:
