@@ -157,7 +157,7 @@ def test_spec_chain_of_rounds_in_a_graph(sampler):
     import torch
     from shared_amd import SpecState
     from shared_amd.sampler import ring_rows
-    seqs, L, vocab, rounds, ring_len, first = 8, 2, 32_000, 4, 48, 3
+    seqs, L, vocab, rounds, ring_len, first = 8, 2, 32_000, 4, 48, 0  # a chain starts at round 0 (posBuf[4])
     cases = [W.spec_case(seqs=seqs, vocab=vocab, drafts=L, hist=0, seed=300 + r) for r in range(rounds)]
     for c in cases[1:]:
         c["seq_params"] = cases[0]["seq_params"]
