@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SAS_ABI_VERSION 2
+#define SAS_ABI_VERSION 3
 
 /* Largest top_k honoured; the request API accepts 1..128
  * (lib/completions.ts:271).  The reference GPU path caps at 20
@@ -380,13 +380,46 @@ int sas_spec_step(sas_sampler *s, const sas_spec_rows *r, const sas_spec_state *
 #define SAS_LMH_MAX_LDS_FLOATS 12288  /* rows * dim: the hidden states staged on chip */
 #define SAS_LMH_MAX_VOCAB 262144      /* vocabularies of the fused head */
 
+/*
+ * Head formats.  SAS_HEAD_BF16: the order above.  The GGUF formats are
+ * ggml's block layouts (the reference loads them, gguf/parser.js:29-36, and
+ * its GEMVs read them, ggml/kernels.js:64-80, 291-315, ggml/q8.js:202-240):
+ *   SAS_HEAD_Q8_0: 34-byte blocks of 32 values: f16 d, int8 q[32]; w = d q
+ *   SAS_HEAD_Q4_0: 18-byte blocks of 32: f16 d, 16 bytes; value i < 16 is the
+ *                  low nibble of byte i, i >= 16 the high nibble of byte i - 16;
+ *                  w = d (nibble - 8)
+ *   SAS_HEAD_Q6_K: 210-byte super-blocks of 256: ql[128], qh[64], int8
+ *                  scales[16], f16 d; w = d scale (q - 32), q six bits
+ *                  (the Qwen head's format, gguf/sources.js:122)
+ * For them the hidden states are quantized on chip as the reference's
+ * Q8_1 operand (ggml/q8.js:27-42): per 32 values, amax = max |x|,
+ * d8 = amax / 127, q8 = round-half-even(x / d8) (x times the f32 reciprocal),
+ * and the f16 fields d8 and d8 * sum(q8).  Each block's integer dot product
+ * is exact; its term is, in f32 left to right (the reference's Q8_1 GEMV
+ * terms, q8.js:202-240):
+ *   Q8_0: (dot * d) * d8      Q4_0: (dot * d) * d8 - (8 d) * s8 (nibble dot)
+ *   Q6_K: ((d * scale) * d8) * dot, per 16 values (dot over q - 32)
+ * and the logit is eight partial sums: partial g adds the terms of blocks
+ * g, g + 8, ... (Q6_K: of 64-value units g, g + 8, ..., unit u being
+ * super-block u / 4, half (u / 2) % 2 and 16-value half u % 2, its four
+ * terms in ascending order), then ((p0 + p1) + (p2 + p3)) + ((p4 + p5) +
+ * (p6 + p7)).
+ */
+#define SAS_HEAD_BF16 0
+#define SAS_HEAD_Q8_0 1
+#define SAS_HEAD_Q4_0 2
+#define SAS_HEAD_Q6_K 3
+
 typedef struct sas_lm_head {
   const float *hidden;        /* device [rows][hidden_stride] fp32: final-normed hidden states */
   int64_t hidden_stride;      /* >= dim */
-  const uint16_t *weight;     /* device [vocab][weight_stride] bf16 bits, 16-byte aligned */
-  int64_t weight_stride;      /* >= dim, a multiple of 8 */
+  const void *weight;         /* device [vocab] rows, 16-byte aligned: bf16 bits, or GGUF blocks */
+  int64_t weight_stride;      /* between rows: elements (bf16: >= dim, a multiple of 8) or bytes
+                                 (GGUF: >= the row's bytes; Q8_0 / Q4_0 a multiple of 4,
+                                 Q6_K of 2) */
   int32_t dim;                /* a multiple of 256; rows * dim <= SAS_LMH_MAX_LDS_FLOATS */
   float *out_logits;          /* device [rows][vocab] or NULL: also write the logits */
+  int32_t format;             /* SAS_HEAD_* (0: bf16) */
 } sas_lm_head;
 
 /* Samples rows->rows rows (<= SAS_LMH_MAX_ROWS, vocab <= SAS_LMH_MAX_VOCAB)
@@ -395,6 +428,14 @@ typedef struct sas_lm_head {
  * other field of `rows` means what it means for sas_sample.
  * Stream-ordered; no host synchronisation. */
 int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *head, const sas_rows *rows, void *stream);
+
+/* The fused head as one step of the in-graph decode loop: the LM head,
+ * then the step of sas_sample_step (ring history, seeded draws, stop
+ * freeze, feedback) over its logits; the reference's per-iteration
+ * lm -> topk -> sampler with tokens[0] fed back (model.js:711-717,
+ * kernels.js:189-199).  rows->hist_ids must be NULL. */
+int sas_lm_head_sample_step(sas_sampler *s, const sas_lm_head *head, const sas_rows *rows, const sas_step *step,
+                            void *stream);
 
 /* Host: clamp parameters with the reference packer's rules
  * (model.js:418-423): non-finite or negative temperature -> 0 (greedy),

@@ -75,10 +75,50 @@ def lib() -> ctypes.CDLL:
         L.orc_spec_commit.restype = None
         L.orc_spec_commit.argtypes = [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_int32, c_void_p, c_int32, c_void_p, c_void_p]
+        L.orc_f16_round.restype = ctypes.c_float
+        L.orc_f16_round.argtypes = [ctypes.c_float]
+        L.orc_q81_quantize.restype = None
+        L.orc_q81_quantize.argtypes = [c_void_p, c_int32, c_void_p, c_void_p, c_void_p]
+        L.orc_lm_head_q_logits.restype = None
+        L.orc_lm_head_q_logits.argtypes = [c_int32, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_int32,
+                                           c_void_p]
         L.orc_lm_head_logits.restype = None
         L.orc_lm_head_logits.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p]
         _lib = L
     return _lib
+
+
+HEAD_BF16, HEAD_Q8_0, HEAD_Q4_0, HEAD_Q6_K = 0, 1, 2, 3
+HEAD_BLOCK = {HEAD_Q8_0: (32, 34), HEAD_Q4_0: (32, 18), HEAD_Q6_K: (256, 210)}  # values, bytes per block
+
+
+def f16_round(x: float) -> float:
+    return float(lib().orc_f16_round(float(x)))
+
+
+def q81_quantize(x) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """orc_q81_quantize of one row: (int8 q [dim], f32 d8 [dim/32], f32 s8)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dim = x.shape[0]
+    q = np.empty(dim, np.int8)
+    d8 = np.empty(dim // 32, np.float32)
+    s8 = np.empty(dim // 32, np.float32)
+    lib().orc_q81_quantize(x.ctypes.data, dim, q.ctypes.data, d8.ctypes.data, s8.ctypes.data)
+    return q, d8, s8
+
+
+def lm_head_q_logits(fmt: int, hidden, weight, dim: int | None = None) -> np.ndarray:
+    """The quantized head's f32 logits in the order sas_lm_head_sample sums
+    them (hidden [rows][>= dim] f32, weight [vocab][row_bytes] uint8 GGUF
+    blocks)."""
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+    weight = np.ascontiguousarray(weight, dtype=np.uint8)
+    rows, vocab = hidden.shape[0], weight.shape[0]
+    dim = int(dim if dim is not None else hidden.shape[1])
+    out = np.empty((rows, vocab), dtype=np.float32)
+    lib().orc_lm_head_q_logits(fmt, hidden.ctypes.data, hidden.shape[1], weight.ctypes.data, weight.shape[1], dim,
+                               rows, vocab, out.ctypes.data)
+    return out
 
 
 def lm_head_logits(hidden, weight_bits, dim: int | None = None) -> np.ndarray:

@@ -48,6 +48,18 @@
  *                      maxima).  Pinned by closed forms: drafts = first
  *                      np.argmax over the non-NaN values, planted picks with
  *                      hand-derived accept counts, and a stop-id draft.
+ *   orc_q81_quantize   quantizeQ81 ggml/q8.js:27-42 (amax / 127 scale,
+ *                      round-half-even, f16 d and d * sum).  Pinned by hand
+ *                      blocks (tests/test_oracle.py): scale and rounding of
+ *                      a planted block, ties to even, numpy's float16.
+ *   orc_lm_head_q_logits  the GGUF heads (ggml/kernels.js:64-80 dequant
+ *                      formulas; the Q8_1 GEMV terms of ggml/q8.js:202-240)
+ *                      in this build's order.  Pinned by closed forms: a
+ *                      block's weights recovered through one-hot hiddens
+ *                      (scale 127 exactness), every block term against the
+ *                      reference's per-element dequantization formula in
+ *                      double, a planted order that separates the tree.
+ *                      Against the reference's WGSL order: parity unpinned.
  *   orc_spec_commit    acceptSpec's commit kernels.js:340-367 (log entry,
  *                      position, ring appends without stop ids, stop freeze,
  *                      frozen rounds, round counter).  Pinned by hand-derived
@@ -631,4 +643,135 @@ void orc_spec_commit(int32_t seqs, int32_t draft_len, const uint32_t *picks, con
     if (accepted_out) accepted_out[s] = a;
     st[1] = rnd + 1u;
   }
+}
+
+/* ------------------------------------------------ quantized LM head ---- */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+static uint16_t f32_to_f16_bits(float f) {
+  const uint32_t x = f2u(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t e = (x >> 23) & 0xFFu;
+  uint32_t m = x & 0x7FFFFFu;
+  if (e == 0xFFu) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u | (m >> 13) : 0u));
+  const int32_t ee = (int32_t)e - 127 + 15;
+  if (ee >= 31) return (uint16_t)(sign | 0x7C00u);
+  if (ee <= 0) {
+    if (ee < -10) return (uint16_t)sign;
+    m |= 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - ee);
+    const uint32_t half = 1u << (shift - 1), rest = m & ((1u << shift) - 1u);
+    uint32_t r = m >> shift;
+    if (rest > half || (rest == half && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+  }
+  uint32_t r = ((uint32_t)ee << 10) | (m >> 13);
+  const uint32_t rest = m & 0x1FFFu;
+  if (rest > 0x1000u || (rest == 0x1000u && (r & 1u))) r++;
+  return (uint16_t)(sign | r);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  if (e == 0x1Fu) return u2f(sign | 0x7F800000u | (m << 13));
+  if (e == 0) {
+    /* subnormal: m * 2^-24, exact in f32 */
+    const float v = (float)m * 5.9604644775390625e-08f;
+    return sign ? -v : v;
+  }
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+float orc_f16_round(float x) { return orc_f16_to_f32(f32_to_f16_bits(x)); }
+
+void orc_q81_quantize(const float *x, int32_t dim, int8_t *q, float *d8, float *s8) {
+  for (int32_t b = 0; b < dim / 32; b++) {
+    const float *v = x + 32 * b;
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+      const float a = fabsf(v[i]);
+      if (a > amax) amax = a;
+    }
+    const float d = amax / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    int32_t sum = 0;
+    for (int i = 0; i < 32; i++) {
+      const float t = v[i] * inv;
+      float r = t != t ? 0.0f : rintf(t);
+      if (r > 127.0f) r = 127.0f;
+      if (r < -128.0f) r = -128.0f;
+      q[32 * b + i] = (int8_t)r;
+      sum += (int32_t)r;
+    }
+    d8[b] = orc_f16_round(d);
+    s8[b] = orc_f16_round(d * (float)sum);
+  }
+}
+
+static inline float head_f16(const uint8_t *p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* The term of weight block / piece `it` of one row (see the header). */
+static float q_term(int32_t format, const uint8_t *w, int32_t it, int32_t piece, const int8_t *q, const float *d8,
+                    const float *s8) {
+  if (format == ORC_HEAD_Q8_0) {
+    const uint8_t *blk = w + 34 * (int64_t)it;
+    int32_t dot = 0;
+    for (int i = 0; i < 32; i++) dot += (int32_t)(int8_t)blk[2 + i] * q[32 * it + i];
+    const float d = head_f16(blk);
+    return ((float)dot * d) * d8[it];
+  }
+  if (format == ORC_HEAD_Q4_0) {
+    const uint8_t *blk = w + 18 * (int64_t)it;
+    int32_t dot = 0;
+    for (int i = 0; i < 32; i++) {
+      const int32_t nib = i < 16 ? (blk[2 + i] & 15) : (blk[2 + i - 16] >> 4);
+      dot += nib * q[32 * it + i];
+    }
+    const float d = head_f16(blk);
+    return ((float)dot * d) * d8[it] - (8.0f * d) * s8[it];
+  }
+  /* Q6_K: unit it, piece (quarter) 0..3 */
+  const int32_t sb = it / 4, un = it % 4, h = un >> 1, lh = un & 1, quarter = piece;
+  const uint8_t *blk = w + 210 * (int64_t)sb;
+  int32_t dot = 0;
+  const int32_t qblk = sb * 8 + h * 4 + quarter;  /* the Q8_1 block of the 16 values */
+  for (int e = 0; e < 16; e++) {
+    const int32_t l = lh * 16 + e;
+    const uint8_t packed = blk[h * 64 + ((quarter & 1) ? 32 : 0) + l];
+    const int32_t nib = quarter >= 2 ? packed >> 4 : packed & 15;
+    const int32_t hi = (blk[128 + h * 32 + l] >> (quarter * 2)) & 3;
+    dot += ((nib | (hi << 4)) - 32) * q[32 * qblk + lh * 16 + e];
+  }
+  const float d = head_f16(blk + 208);
+  const float sc = (float)(int8_t)blk[192 + h * 8 + lh + quarter * 2];
+  return ((d * sc) * d8[qblk]) * (float)dot;
+}
+
+void orc_lm_head_q_logits(int32_t format, const float *hidden, int64_t hidden_stride, const uint8_t *weight,
+                          int64_t row_bytes, int32_t dim, int32_t rows, int32_t vocab, float *logits) {
+  int8_t *q = (int8_t *)malloc((size_t)dim);
+  float *d8 = (float *)malloc(sizeof(float) * (size_t)(dim / 32));
+  float *s8 = (float *)malloc(sizeof(float) * (size_t)(dim / 32));
+  const int32_t items = format == ORC_HEAD_Q6_K ? dim / 64 : dim / 32;
+  const int32_t pieces = format == ORC_HEAD_Q6_K ? 4 : 1;
+  for (int32_t r = 0; r < rows; r++) {
+    orc_q81_quantize(hidden + (int64_t)r * hidden_stride, dim, q, d8, s8);
+    for (int32_t id = 0; id < vocab; id++) {
+      const uint8_t *w = weight + (int64_t)id * row_bytes;
+      float p[8];
+      for (int g = 0; g < 8; g++) {
+        float acc = 0.0f;
+        for (int32_t it = g; it < items; it += 8)
+          for (int32_t pc = 0; pc < pieces; pc++) acc = acc + q_term(format, w, it, pc, q, d8, s8);
+        p[g] = acc;
+      }
+      logits[(int64_t)r * vocab + id] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+  }
+  free(q);
+  free(d8);
+  free(s8);
 }

@@ -121,4 +121,42 @@ void orc_lm_head_logits(const float *hidden, int64_t hidden_stride, const uint16
                         int64_t weight_stride, int32_t dim, int32_t rows, int32_t vocab,
                         float *logits);
 
+/* ---- the quantized LM head (sas_lm_head_sample with a GGUF head) ----
+ *
+ * Weight formats (ggml's published block layouts, as gguf/parser.js:29-36
+ * sizes them): ORC_HEAD_Q8_0 (34-byte blocks of 32: f16 d, 32 int8),
+ * ORC_HEAD_Q4_0 (18-byte blocks of 32: f16 d, 16 bytes, element i < 16 the
+ * low nibble of byte i, i >= 16 the high nibble of byte i - 16), ORC_HEAD_Q6_K
+ * (210-byte super-blocks of 256: ql[128], qh[64], int8 scales[16], f16 d). */
+#define ORC_HEAD_BF16 0
+#define ORC_HEAD_Q8_0 1
+#define ORC_HEAD_Q4_0 2
+#define ORC_HEAD_Q6_K 3
+
+/* f32 -> nearest f16 (ties to even) -> f32; and f16 bits -> f32. */
+float orc_f16_round(float x);
+float orc_f16_to_f32(uint16_t h);
+
+/* The Q8_1 quantization of one activation row (q8.js:27-42): per block of
+ * 32 values, amax = max |x|, d = amax / 127, inv = d > 0 ? 1 / d : 0,
+ * q = round-half-even(x * inv) (0 when not a number), sum = sum of q;
+ * d8 = f16(d), s8 = f16(d * sum), each read back as f32.  dim % 32 == 0. */
+void orc_q81_quantize(const float *x, int32_t dim, int8_t *q, float *d8, float *s8);
+
+/* The quantized head's logits in the order sas_lm_head_sample sums them:
+ * the hidden row quantized by orc_q81_quantize, exact integer dot products
+ * per weight block, then per block (f32, left to right, no fused ops):
+ *   Q8_0: (dot * d) * d8
+ *   Q4_0: (dot * d) * d8 - (8 * d) * s8                 (dot over the nibbles)
+ *   Q6_K: ((d * scale) * d8) * dot, per 16 values        (dot over q6 - 32)
+ * (the reference's Q8_1 GEMV terms, q8.js:202-240).  Eight partial sums:
+ * partial g adds, in ascending order, the terms of blocks b = g, g + 8, ...
+ * (Q8_0, Q4_0) or of 64-value units u = g, g + 8, ... (Q6_K; unit u is
+ * super-block u / 4, half (u / 2) % 2, 16-value half u % 2, its four
+ * 16-value pieces in ascending order); then
+ * ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).
+ * weight: [vocab] rows of row_bytes bytes; dim % 256 == 0. */
+void orc_lm_head_q_logits(int32_t format, const float *hidden, int64_t hidden_stride, const uint8_t *weight,
+                          int64_t row_bytes, int32_t dim, int32_t rows, int32_t vocab, float *logits);
+
 #endif

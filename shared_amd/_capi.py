@@ -39,6 +39,7 @@ STOP_PAD = 0xFFFFFFFF
 OK, ERR_INVALID, ERR_HIP, ERR_NOMEM = 0, 1, 2, 3
 FLAG_EMPTY_ROW, FLAG_TOPP_EDGE, FLAG_DRAW_EDGE, FLAG_SLOW_SELECT = 1, 2, 4, 8
 HINT_NO_SOFTCAP = 1
+HEAD_BF16, HEAD_Q8_0, HEAD_Q4_0, HEAD_Q6_K = 0, 1, 2, 3
 MASK_ALL, MASK_ALLOW, MASK_DENY = 0, 1, 2
 
 
@@ -164,6 +165,7 @@ class SasLmHead(ctypes.Structure):
         ("weight_stride", c_int64),
         ("dim", c_int32),
         ("out_logits", c_void_p),
+        ("format", c_int32),
     ]
 
 
@@ -182,6 +184,7 @@ SIGNATURES = {
     "sas_spec_exact": (c_int, [c_void_p, POINTER(SasSpecRows), c_void_p]),
     "sas_spec_step": (c_int, [c_void_p, POINTER(SasSpecRows), POINTER(SasSpecState), c_void_p]),
     "sas_lm_head_sample": (c_int, [c_void_p, POINTER(SasLmHead), POINTER(SasRows), c_void_p]),
+    "sas_lm_head_sample_step": (c_int, [c_void_p, POINTER(SasLmHead), POINTER(SasRows), POINTER(SasStep), c_void_p]),
     "sas_clamp_params": (c_int, [POINTER(SasParams), POINTER(SasParams)]),
     "sas_mask_from_ids": (c_int64, [c_int32, POINTER(c_uint32), c_size_t, c_int32, POINTER(c_uint32), c_int64]),
     "sas_pcg_uniform": (c_double, [c_uint32, c_uint32, c_uint32]),

@@ -252,11 +252,86 @@ int sample_on(sas_sampler *s, const sas_rows *r, const sas_step *st, const char 
   return SAS_OK;
 }
 
+// Bytes of one row of a GGUF head of `dim` values (0 for bf16).
+int64_t head_row_bytes(int32_t format, int32_t dim) {
+  switch (format) {
+    case SAS_HEAD_Q8_0: return (int64_t)dim / 32 * 34;
+    case SAS_HEAD_Q4_0: return (int64_t)dim / 32 * 18;
+    case SAS_HEAD_Q6_K: return (int64_t)dim / 256 * 210;
+    default: return 0;
+  }
+}
+
+// sas_lm_head_sample and sas_lm_head_sample_step (st).
+int lm_head_on(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, const sas_step *st, const char *who,
+               void *stream) {
+  const std::string w(who);
+  if (!s) return fail(nullptr, SAS_ERR_INVALID, w + ": handle is NULL");
+  if (!h || !r) return fail(s, SAS_ERR_INVALID, w + ": head and rows are required");
+  if (r->logits) return fail(s, SAS_ERR_INVALID, w + ": rows->logits must be NULL (the head computes them)");
+  // the sampling fields are checked as for sas_sample (sas_sample_step)
+  sas_rows chk = *r;
+  chk.logits = reinterpret_cast<const float *>(h->hidden ? static_cast<const void *>(h->hidden) : "");
+  chk.logits_stride = r->vocab;
+  if (const char *m = check_rows(&chk, st && st->seeds)) return fail(s, SAS_ERR_INVALID, w + ": " + m);
+  if (st)
+    if (const char *m = check_step(r, st)) return fail(s, SAS_ERR_INVALID, w + ": " + m);
+  if (r->rows > SAS_LMH_MAX_ROWS) return fail(s, SAS_ERR_INVALID, w + ": rows must be <= SAS_LMH_MAX_ROWS");
+  if (r->vocab > SAS_LMH_MAX_VOCAB) return fail(s, SAS_ERR_INVALID, w + ": vocab must be <= SAS_LMH_MAX_VOCAB");
+  if (h->format < SAS_HEAD_BF16 || h->format > SAS_HEAD_Q6_K)
+    return fail(s, SAS_ERR_INVALID, w + ": format must be one of SAS_HEAD_*");
+  if (r->rows == 0) return SAS_OK;
+  if (!h->hidden || !h->weight) return fail(s, SAS_ERR_INVALID, w + ": hidden and weight are required");
+  if (h->dim < 256 || h->dim % 256 != 0) return fail(s, SAS_ERR_INVALID, w + ": dim must be a positive multiple of 256");
+  if ((int64_t)r->rows * h->dim > SAS_LMH_MAX_LDS_FLOATS)
+    return fail(s, SAS_ERR_INVALID, w + ": rows * dim must be <= SAS_LMH_MAX_LDS_FLOATS");
+  if (h->hidden_stride < h->dim) return fail(s, SAS_ERR_INVALID, w + ": hidden_stride < dim");
+  if (h->format == SAS_HEAD_BF16) {
+    if (h->weight_stride < h->dim || h->weight_stride % 8 != 0)
+      return fail(s, SAS_ERR_INVALID, w + ": weight_stride must be >= dim and a multiple of 8");
+  } else {
+    const int64_t rb = head_row_bytes(h->format, h->dim);
+    if (h->weight_stride < rb || h->weight_stride % (h->format == SAS_HEAD_Q6_K ? 2 : 4) != 0)
+      return fail(s, SAS_ERR_INVALID,
+                  w + ": weight_stride must be >= the row's " + std::to_string(rb) +
+                      " bytes and a multiple of 4 (Q8_0, Q4_0) or 2 (Q6_K)");
+  }
+  if (reinterpret_cast<uintptr_t>(h->weight) % 16 != 0)
+    return fail(s, SAS_ERR_INVALID, w + ": weight must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(h->hidden) % 4 != 0)
+    return fail(s, SAS_ERR_INVALID, w + ": hidden must be 4-byte aligned");
+  if (int rc = set_device(s)) return rc;
+  if (int rc = grow(s, &s->recs, &s->recs_cap, sas::lmh_scratch_bytes(r->rows, r->vocab), stream, who)) return rc;
+  sas::LmhArgs a{};
+  fill_args(r, nullptr, 0, 1, sas::kLmhSpan, s->recs, &a.s);
+  sas::lmh_layout(&a, s->recs);
+  if (st) {
+    a.s.st_state = st->state;
+    a.s.st_sampled = st->sampled;
+    a.s.st_max_steps = st->sampled ? st->max_steps : 0;
+    a.s.st_next = st->next_tokens;
+    a.s.ring = st->ring;
+    a.s.ring_len = st->ring ? st->ring_len : 0;
+    a.s.stop_ids = st->stop_ids;
+    a.s.seeds = st->seeds;
+  }
+  a.hidden = h->hidden;
+  a.hidden_stride = h->hidden_stride;
+  a.weight = h->weight;
+  a.weight_stride = h->weight_stride;
+  a.format = h->format;
+  a.dim = h->dim;
+  a.out_logits = h->out_logits;
+  hipError_t e = sas::launch_lm_head_sample(a, any_softcap(r), pick_stream(s, stream));
+  if (e != hipSuccess) return hip_fail(s, e, (w + " launch").c_str());
+  return SAS_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-const char *sas_version(void) { return "shared_amd_sampler 2 gfx950"; }
+const char *sas_version(void) { return "shared_amd_sampler 3 gfx950"; }
 
 int sas_create(int device, sas_sampler **out) {
   if (!out) return fail(nullptr, SAS_ERR_INVALID, "sas_create: out is NULL");
@@ -395,44 +470,13 @@ int sas_sample_noalloc(int device, const sas_rows *r, void *stream) {
 }
 
 int sas_lm_head_sample(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, void *stream) {
-  if (!s) return fail(nullptr, SAS_ERR_INVALID, "sas_lm_head_sample: handle is NULL");
-  if (!h || !r) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: head and rows are required");
-  if (r->logits) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: rows->logits must be NULL (the head computes them)");
-  // the sampling fields are checked as for sas_sample
-  sas_rows chk = *r;
-  chk.logits = reinterpret_cast<const float *>(h->hidden ? static_cast<const void *>(h->hidden) : "");
-  chk.logits_stride = r->vocab;
-  if (const char *m = check_rows(&chk)) return fail(s, SAS_ERR_INVALID, std::string("sas_lm_head_sample: ") + m);
-  if (r->rows > SAS_LMH_MAX_ROWS) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: rows must be <= SAS_LMH_MAX_ROWS");
-  if (r->vocab > SAS_LMH_MAX_VOCAB) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: vocab must be <= SAS_LMH_MAX_VOCAB");
-  if (r->rows == 0) return SAS_OK;
-  if (!h->hidden || !h->weight) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden and weight are required");
-  if (h->dim < 256 || h->dim % 256 != 0) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: dim must be a positive multiple of 256");
-  if ((int64_t)r->rows * h->dim > SAS_LMH_MAX_LDS_FLOATS)
-    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: rows * dim must be <= SAS_LMH_MAX_LDS_FLOATS");
-  if (h->hidden_stride < h->dim) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden_stride < dim");
-  if (h->weight_stride < h->dim || h->weight_stride % 8 != 0)
-    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: weight_stride must be >= dim and a multiple of 8");
-  if (reinterpret_cast<uintptr_t>(h->weight) % 16 != 0)
-    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: weight must be 16-byte aligned");
-  if (reinterpret_cast<uintptr_t>(h->hidden) % 4 != 0)
-    return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample: hidden must be 4-byte aligned");
-  if (int rc = set_device(s)) return rc;
-  if (int rc = grow(s, &s->recs, &s->recs_cap, sas::lmh_scratch_bytes(r->rows, r->vocab), stream,
-                    "sas_lm_head_sample"))
-    return rc;
-  sas::LmhArgs a{};
-  fill_args(r, nullptr, 0, 1, sas::kLmhSpan, s->recs, &a.s);
-  sas::lmh_layout(&a, s->recs);
-  a.hidden = h->hidden;
-  a.hidden_stride = h->hidden_stride;
-  a.weight = h->weight;
-  a.weight_stride = h->weight_stride;
-  a.dim = h->dim;
-  a.out_logits = h->out_logits;
-  hipError_t e = sas::launch_lm_head_sample(a, any_softcap(r), pick_stream(s, stream));
-  if (e != hipSuccess) return hip_fail(s, e, "sas_lm_head_sample launch");
-  return SAS_OK;
+  return lm_head_on(s, h, r, nullptr, "sas_lm_head_sample", stream);
+}
+
+int sas_lm_head_sample_step(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, const sas_step *st,
+                            void *stream) {
+  if (s && !st) return fail(s, SAS_ERR_INVALID, "sas_lm_head_sample_step: step descriptor is NULL");
+  return lm_head_on(s, h, r, st, "sas_lm_head_sample_step", stream);
 }
 
 }  // extern "C"

@@ -67,6 +67,7 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 // lane's two ids.
 struct LmhPre {
   int h0, h1;
+  const uint32_t *ids;  // the history: hist_ids, or the row's ring slots
   uint32_t hid[2];
   uint32_t mword;
 };
@@ -75,7 +76,13 @@ struct LmhPre {
 __device__ __forceinline__ void lmh_prefetch_range(const SampleArgs &a, int row, int id0, LmhPre &q) {
   q.h0 = 0;
   q.h1 = 0;
-  if (a.hist_ids) {
+  q.ids = a.hist_ids;
+  if (a.ring) {
+    // a decode step's penalty ring: its first min(count, ring_len) slots
+    const uint32_t *rg = a.ring + (int64_t)row * (a.ring_len + 1);
+    q.ids = rg + 1;
+    q.h1 = (int)min(rg[0], (uint32_t)a.ring_len);
+  } else if (a.hist_ids) {
     const int64_t o0 = min(max((int64_t)a.hist_offsets[row], (int64_t)0), a.hist_count);
     const int64_t o1 = min(max((int64_t)a.hist_offsets[row + 1], o0), min(a.hist_count, o0 + SAS_MAX_HISTORY));
     q.h0 = (int)o0;
@@ -86,11 +93,11 @@ __device__ __forceinline__ void lmh_prefetch_range(const SampleArgs &a, int row,
 }
 
 // ... then the first history ids, once the range is known.
-__device__ __forceinline__ void lmh_prefetch_ids(const SampleArgs &a, LmhPre &q) {
+__device__ __forceinline__ void lmh_prefetch_ids(LmhPre &q) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = q.h0 + j * kThreads + (int)threadIdx.x;
-    q.hid[j] = i < q.h1 ? a.hist_ids[i] : kLmhEmpty;
+    q.hid[j] = i < q.h1 ? q.ids[i] : kLmhEmpty;
   }
 }
 
@@ -144,7 +151,7 @@ __device__ __forceinline__ void lmh_select_rows(const LmhArgs &L, LmhLds<R> &S, 
     // the range: never inside the part)
     insert(r, pf[r].hid[0]);
     insert(r, pf[r].hid[1]);
-    for (int i = pf[r].h0 + 2 * kThreads + tid; i < pf[r].h1; i += kThreads) insert(r, a.hist_ids[i]);
+    for (int i = pf[r].h0 + 2 * kThreads + tid; i < pf[r].h1; i += kThreads) insert(r, pf[r].ids[i]);
   }
   __syncthreads();
   auto hcount = [&](int r, uint32_t id) -> uint32_t {
@@ -157,7 +164,7 @@ __device__ __forceinline__ void lmh_select_rows(const LmhArgs &L, LmhLds<R> &S, 
     }
     uint32_t c = 0u;
     if (S.hover[r])
-      for (int i = pf[r].h0; i < pf[r].h1; ++i) c += a.hist_ids[i] == id ? 1u : 0u;
+      for (int i = pf[r].h0; i < pf[r].h1; ++i) c += pf[r].ids[i] == id ? 1u : 0u;
     return c;
   };
   // ---- values: softcap, mask, membership; members penalized here; the bound ----
@@ -287,9 +294,184 @@ __device__ __forceinline__ void lmh_select_rows(const LmhArgs &L, LmhLds<R> &S, 
   }
 }
 
+// ---- GGUF heads: the Q8_1 operand on chip, exact integer block dots ----
+
+// Dwords 0..N-1 of the bytes at p (p even): aligned loads of the dwords that
+// cover them, shifted by two bytes when p is not a multiple of four.  Reads
+// nothing outside [p, p + 4 N) when p is aligned, else at most the two bytes
+// on each side (inside the neighbouring fields of the same head).
+template <int N>
+__device__ __forceinline__ void load_span(const uint8_t *p, uint32_t (&out)[N]) {
+  static_assert(N % 4 == 0, "whole 16-byte loads");
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+  const bool mis = (a & 2u) != 0u;
+  typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));  // 16 bytes, 4-byte aligned
+  uint32_t u[N + 1];
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    const u32x4a4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4a4 *>(q + i));
+    u[i] = v.x;
+    u[i + 1] = v.y;
+    u[i + 2] = v.z;
+    u[i + 3] = v.w;
+  }
+  u[N] = 0u;
+  if (mis) u[N] = __builtin_nontemporal_load(q + N);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = mis ? __builtin_amdgcn_alignbyte(u[i + 1], u[i], 2u) : u[i];
+}
+
+__device__ __forceinline__ float f16_at(const uint8_t *p) {
+  return (float)__builtin_bit_cast(_Float16, __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p)));
+}
+
+// Four six-bit values q (bytes of `raw`, 0..63) as the bytes of q - 32.
+__device__ __forceinline__ uint32_t center32(uint32_t raw) {
+  return ((raw | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+// The Q8_1 operand of R hidden rows, in LDS: q8[r][dim / 4] (four int8 per
+// word), d8[r][dim / 32], s8[r][dim / 32].  One 32-value block per thread per
+// round (q8.js:27-42): amax, d = amax / 127, q = round-half-even(x * (1 / d)),
+// the f16 d and d * sum(q).
 template <int R>
+__device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *d8, float *s8) {
+  const int dim = L.dim, nq = dim / 32;
+  for (int t = threadIdx.x; t < R * nq; t += kThreads) {
+    const int r = t / nq, b = t - r * nq;
+    const float *h = L.hidden + (int64_t)r * L.hidden_stride + 32 * b;
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = h[i];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    const float d = amax / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t w = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = v[4 * j + i] * inv;
+        const float rq = x != x ? 0.0f : fminf(fmaxf(rintf(x), -128.0f), 127.0f);
+        const int qi = (int)rq;
+        sum += qi;
+        w |= ((uint32_t)qi & 0xFFu) << (8 * i);
+      }
+      q8[r * (dim / 4) + 8 * b + j] = (int32_t)w;
+    }
+    d8[r * nq + b] = (float)(_Float16)d;
+    s8[r * nq + b] = (float)(_Float16)(d * (float)sum);
+  }
+}
+
+template <int kFmt>
+struct QItem;  // the raw words of one work item of a lane
+
+// Q8_0 / Q4_0: one 32-value block
+template <>
+struct QItem<SAS_HEAD_Q8_0> {
+  uint32_t w[8];
+  float d;
+};
+template <>
+struct QItem<SAS_HEAD_Q4_0> {
+  uint32_t w[4];
+  float d;
+};
+// Q6_K: one 64-value unit of a super-block: its two ql spans, its qh span,
+// the super-block's scales and d
+template <>
+struct QItem<SAS_HEAD_Q6_K> {
+  uint32_t la[4], lb[4], qh[4], sc[4];
+  float d;
+};
+
+template <int kFmt>
+__device__ __forceinline__ void q_load(const uint8_t *row, int it, QItem<kFmt> &x) {
+  if constexpr (kFmt == SAS_HEAD_Q8_0) {
+    const uint8_t *blk = row + 34 * it;
+    load_span<8>(blk + 2, x.w);
+    x.d = f16_at(blk);
+  } else if constexpr (kFmt == SAS_HEAD_Q4_0) {
+    const uint8_t *blk = row + 18 * it;
+    load_span<4>(blk + 2, x.w);
+    x.d = f16_at(blk);
+  } else {
+    const int sb = it >> 2, un = it & 3, h = un >> 1, lh = un & 1;
+    const uint8_t *blk = row + 210 * sb;
+    load_span<4>(blk + h * 64 + lh * 16, x.la);
+    load_span<4>(blk + h * 64 + 32 + lh * 16, x.lb);
+    load_span<4>(blk + 128 + h * 32 + lh * 16, x.qh);
+    load_span<4>(blk + 192, x.sc);
+    x.d = f16_at(blk + 208);
+  }
+}
+
+// Adds item `it`'s terms to acc[r] for every row (the order of the header).
+template <int R, int kFmt>
+__device__ __forceinline__ void q_terms(const QItem<kFmt> &x, int it, const int32_t *q8, const float *d8,
+                                        const float *s8, int dim, float (&acc)[R]) {
+  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+  const int nq = dim / 32;
+  if constexpr (kFmt == SAS_HEAD_Q8_0 || kFmt == SAS_HEAD_Q4_0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const i32x4 *qa = reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * it);
+      const i32x4 a0 = qa[0], a1 = qa[1];
+      const int32_t qv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      int dot = 0;
+      if constexpr (kFmt == SAS_HEAD_Q8_0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)x.w[j], qv[j], dot, false);
+        acc[r] = acc[r] + ((float)dot * x.d) * d8[r * nq + it];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dot = __builtin_amdgcn_sdot4((int)(x.w[j] & 0x0F0F0F0Fu), qv[j], dot, false);
+          dot = __builtin_amdgcn_sdot4((int)((x.w[j] >> 4) & 0x0F0F0F0Fu), qv[4 + j], dot, false);
+        }
+        acc[r] = acc[r] + (((float)dot * x.d) * d8[r * nq + it] - (8.0f * x.d) * s8[r * nq + it]);
+      }
+    }
+  } else {
+    const int sb = it >> 2, un = it & 3, h = un >> 1, lh = un & 1;
+    const uint32_t s0 = h ? x.sc[2] : x.sc[0], s1 = h ? x.sc[3] : x.sc[1];  // scales h*8 .. h*8 + 7
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      const uint32_t *src = (qt & 1) ? x.lb : x.la;
+      uint32_t cen[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t nib = (qt >= 2 ? src[j] >> 4 : src[j]) & 0x0F0F0F0Fu;
+        const uint32_t hi = ((x.qh[j] >> (2 * qt)) & 0x03030303u) << 4;
+        cen[j] = center32(nib | hi);
+      }
+      // scale byte h*8 + lh + 2 qt: word qt >> 1 of the pair, byte lh + 2 (qt & 1)
+      const uint32_t sw = (qt >> 1) ? s1 : s0;
+      const float sc = (float)__builtin_amdgcn_sbfe((int)sw, 8u * (uint32_t)(lh + 2 * (qt & 1)), 8u);
+      const float ds = x.d * sc;
+      const int qb = sb * 8 + h * 4 + qt;  // the Q8_1 block of these 16 values
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const i32x4 qa = *reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * qb + 4 * lh);
+        int dot = __builtin_amdgcn_sdot4((int)cen[0], qa.x, 0, false);
+        dot = __builtin_amdgcn_sdot4((int)cen[1], qa.y, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)cen[2], qa.z, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)cen[3], qa.w, dot, false);
+        acc[r] = acc[r] + (ds * d8[r * nq + qb]) * (float)dot;
+      }
+    }
+  }
+}
+
+template <int R, int kFmt>
 __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L) {
-  extern __shared__ __attribute__((aligned(16))) float xs[];  // [R][dim] hidden states
+  // bf16: [R][dim] hidden states; GGUF: their Q8_1 operand
+  extern __shared__ __attribute__((aligned(16))) float xs[];
   __shared__ LmhLds<R> S;
   __shared__ float s_logit[R][kLmhSpan];  // the part's logits, row by row
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -301,80 +483,132 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
   // the group takes hidden indices 64 c + 8 g .. + 7 (c = 0, 1, ...), so a
   // group reads whole 128-byte lines of the weight row and a wave eight of
   // them per load.  Group grp (32 per block) takes ids base + grp + 32 m,
-  // m = 0 .. 15: at each m the block reads 32 consecutive rows. ----
+  // m = 0 .. 15: at each m the block reads 32 consecutive rows.  (GGUF
+  // heads: lane g takes blocks or units g, g + 8, ... of the row.) ----
   const int g = lane & 7;
   const int grp = (wave << 3) | (lane >> 3);
-  const int C = dim / kLmhStep;              // 128-byte steps per weight row
-  constexpr int kQ = 4;                       // steps per batch of loads
-  const int nb = C / kQ;                      // batches per id (dim is a multiple of 256)
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  auto wrow = [&](int m) __attribute__((always_inline)) {
-    const int id = min(base + grp + 32 * m, vocab - 1);  // loads stay inside the head
-    return L.weight + (int64_t)id * L.weight_stride + 8 * g;
-  };
-  u32x4 nxt[kQ], nx2[kQ];
-  auto load_into = [&](u32x4 (&dst)[kQ], int m, int cb) __attribute__((always_inline)) {
-    const uint16_t *w = wrow(m) + (int64_t)cb * kQ * kLmhStep;
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) dst[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + q * kLmhStep));
-  };
-  // batches in the flattened order (m, cb): two in flight ahead of the one computed
-  const int total = (kLmhSpan / 32) * nb;
-  load_into(nxt, 0, 0);
-  if (total > 1) load_into(nx2, nb > 1 ? 0 : 1, nb > 1 ? 1 : 0);
-  // while the first batches are in flight: the epilogue's inputs (read at
-  // the end, loaded now so that no round trip waits after the dot
-  // products) and the rows' hidden states into LDS
   LmhPre pre[R];
+  if constexpr (kFmt == SAS_HEAD_BF16) {
+    const int C = dim / kLmhStep;              // 128-byte steps per weight row
+    constexpr int kQ = 4;                       // steps per batch of loads
+    const int nb = C / kQ;                      // batches per id (dim is a multiple of 256)
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const uint16_t *W = static_cast<const uint16_t *>(L.weight);
+    auto wrow = [&](int m) __attribute__((always_inline)) {
+      const int id = min(base + grp + 32 * m, vocab - 1);  // loads stay inside the head
+      return W + (int64_t)id * L.weight_stride + 8 * g;
+    };
+    u32x4 nxt[kQ], nx2[kQ];
+    auto load_into = [&](u32x4 (&dst)[kQ], int m, int cb) __attribute__((always_inline)) {
+      const uint16_t *w = wrow(m) + (int64_t)cb * kQ * kLmhStep;
 #pragma unroll
-  for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
-  for (int r = 0; r < R; ++r) {
-    const float *h = L.hidden + (int64_t)r * L.hidden_stride;
-    for (int i = tid; i < dim; i += kThreads) xs[r * dim + i] = h[i];
-  }
+      for (int q = 0; q < kQ; ++q) dst[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + q * kLmhStep));
+    };
+    // batches in the flattened order (m, cb): two in flight ahead of the one computed
+    const int total = (kLmhSpan / 32) * nb;
+    load_into(nxt, 0, 0);
+    if (total > 1) load_into(nx2, nb > 1 ? 0 : 1, nb > 1 ? 1 : 0);
+    // while the first batches are in flight: the epilogue's inputs (read at
+    // the end, loaded now so that no round trip waits after the dot
+    // products) and the rows' hidden states into LDS
 #pragma unroll
-  for (int r = 0; r < R; ++r) lmh_prefetch_ids(L.s, pre[r]);
-  __syncthreads();  // the hidden states are in LDS
-  for (int m = 0; m < kLmhSpan / 32; ++m) {
-    float acc[R];
+    for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
+    for (int r = 0; r < R; ++r) {
+      const float *h = L.hidden + (int64_t)r * L.hidden_stride;
+      for (int i = tid; i < dim; i += kThreads) xs[r * dim + i] = h[i];
+    }
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int cb = 0; cb < nb; ++cb) {
-      u32x4 cur[kQ];
+    for (int r = 0; r < R; ++r) lmh_prefetch_ids(pre[r]);
+    __syncthreads();  // the hidden states are in LDS
+    for (int m = 0; m < kLmhSpan / 32; ++m) {
+      float acc[R];
 #pragma unroll
-      for (int q = 0; q < kQ; ++q) {
-        cur[q] = nxt[q];
-        nxt[q] = nx2[q];
-      }
-      // the batch two ahead in flight
-      const int t2 = m * nb + cb + 2;
-      if (t2 < total) load_into(nx2, t2 / nb, t2 - (t2 / nb) * nb);
+      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+      for (int cb = 0; cb < nb; ++cb) {
+        u32x4 cur[kQ];
 #pragma unroll
-      for (int q = 0; q < kQ; ++q) {
-        const int k = (cb * kQ + q) * kLmhStep + 8 * g;  // hidden indices k .. k + 7
-        const uint32_t w4[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+        for (int q = 0; q < kQ; ++q) {
+          cur[q] = nxt[q];
+          nxt[q] = nx2[q];
+        }
+        // the batch two ahead in flight
+        const int t2 = m * nb + cb + 2;
+        if (t2 < total) load_into(nx2, t2 / nb, t2 - (t2 / nb) * nb);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const float4 *xp = reinterpret_cast<const float4 *>(xs + r * dim + k);
-          const float4 x0 = xp[0], x1 = xp[1];
-          const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        for (int q = 0; q < kQ; ++q) {
+          const int k = (cb * kQ + q) * kLmhStep + 8 * g;  // hidden indices k .. k + 7
+          const uint32_t w4[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
 #pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            acc[r] = __builtin_fmaf(bf16_lo(w4[h]), xv[2 * h], acc[r]);
-            acc[r] = __builtin_fmaf(bf16_hi(w4[h]), xv[2 * h + 1], acc[r]);
+          for (int r = 0; r < R; ++r) {
+            const float4 *xp = reinterpret_cast<const float4 *>(xs + r * dim + k);
+            const float4 x0 = xp[0], x1 = xp[1];
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              acc[r] = __builtin_fmaf(bf16_lo(w4[h]), xv[2 * h], acc[r]);
+              acc[r] = __builtin_fmaf(bf16_hi(w4[h]), xv[2 * h + 1], acc[r]);
+            }
           }
         }
       }
-    }
-    // the group's eight partial sums, in one fixed tree: lane 0 of the
-    // group holds ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
+      // the group's eight partial sums, in one fixed tree: lane 0 of the
+      // group holds ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float v = acc[r];
-      v = v + __shfl_xor(v, 1, 64);
-      v = v + __shfl_xor(v, 2, 64);
-      v = v + __shfl_xor(v, 4, 64);
-      if (g == 0) s_logit[r][grp + 32 * m] = v;
+      for (int r = 0; r < R; ++r) {
+        float v = acc[r];
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        if (g == 0) s_logit[r][grp + 32 * m] = v;
+      }
+    }
+  } else {
+    const uint8_t *W = static_cast<const uint8_t *>(L.weight);
+    // items per id: blocks (Q8_0, Q4_0) or 64-value units (Q6_K); lane g
+    // takes g, g + 8, ... (a lane past the last item loads the last one and
+    // adds nothing)
+    const int items = kFmt == SAS_HEAD_Q6_K ? dim / 64 : dim / 32;
+    const int per = (items + 7) / 8;
+    const int total = (kLmhSpan / 32) * per;
+    auto row_of = [&](int m) __attribute__((always_inline)) {
+      const int id = min(base + grp + 32 * m, vocab - 1);  // loads stay inside the head
+      return W + (int64_t)id * L.weight_stride;
+    };
+    auto load_at = [&](int t, QItem<kFmt> &dst) __attribute__((always_inline)) {
+      const int m2 = t / per;
+      q_load<kFmt>(row_of(m2), min(g + 8 * (t - m2 * per), items - 1), dst);
+    };
+    QItem<kFmt> nxt, nx2;
+    load_at(0, nxt);
+    if (total > 1) load_at(1, nx2);
+#pragma unroll
+    for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
+    int32_t *q8 = reinterpret_cast<int32_t *>(xs);
+    float *d8 = reinterpret_cast<float *>(q8 + R * (dim / 4));
+    float *s8 = d8 + R * (dim / 32);
+    q81_stage<R>(L, q8, d8, s8);
+#pragma unroll
+    for (int r = 0; r < R; ++r) lmh_prefetch_ids(pre[r]);
+    __syncthreads();  // the Q8_1 operand is in LDS
+    for (int m = 0; m < kLmhSpan / 32; ++m) {
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+      for (int c = 0; c < per; ++c) {
+        const QItem<kFmt> cur = nxt;
+        nxt = nx2;
+        const int t2 = m * per + c + 2;
+        if (t2 < total) load_at(t2, nx2);
+        if (g + 8 * c < items) q_terms<R, kFmt>(cur, g + 8 * c, q8, d8, s8, dim, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float v = acc[r];
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        if (g == 0) s_logit[r][grp + 32 * m] = v;
+      }
     }
   }
   __syncthreads();
@@ -667,21 +901,33 @@ void lmh_layout(LmhArgs *a, void *scratch) {
   a->g_pinfo = reinterpret_cast<uint64_t *>(a->g_mrec + (size_t)rows * gparts * kMemSlots);
 }
 
-template <int R>
+template <int R, int kFmt>
 static hipError_t launch_parts(const LmhArgs &a, hipStream_t stream) {
-  const size_t lds = (size_t)R * a.dim * sizeof(float);
-  hipLaunchKernelGGL((lmh_parts_kernel<R>), dim3((unsigned)a.s.parts), dim3(kThreads), lds, stream, a);
+  // bf16: the f32 hidden rows; GGUF: q8 (dim bytes) + d8 + s8 per row
+  const size_t lds = kFmt == SAS_HEAD_BF16 ? (size_t)R * a.dim * sizeof(float)
+                                           : (size_t)R * ((size_t)a.dim + 2 * sizeof(float) * (a.dim / 32));
+  hipLaunchKernelGGL((lmh_parts_kernel<R, kFmt>), dim3((unsigned)a.s.parts), dim3(kThreads), lds, stream, a);
   return hipGetLastError();
+}
+
+template <int kFmt>
+static hipError_t launch_parts_rows(const LmhArgs &a, hipStream_t stream) {
+  switch (a.s.rows) {
+    case 1: return launch_parts<1, kFmt>(a, stream);
+    case 2: return launch_parts<2, kFmt>(a, stream);
+    case 3: return launch_parts<3, kFmt>(a, stream);
+    default: return launch_parts<4, kFmt>(a, stream);
+  }
 }
 
 hipError_t launch_lm_head_sample(const LmhArgs &a, bool softcap, hipStream_t stream) {
   (void)softcap;  // the epilogue reads each row's softcap itself
   hipError_t e;
-  switch (a.s.rows) {
-    case 1: e = launch_parts<1>(a, stream); break;
-    case 2: e = launch_parts<2>(a, stream); break;
-    case 3: e = launch_parts<3>(a, stream); break;
-    default: e = launch_parts<4>(a, stream); break;
+  switch (a.format) {
+    case SAS_HEAD_Q8_0: e = launch_parts_rows<SAS_HEAD_Q8_0>(a, stream); break;
+    case SAS_HEAD_Q4_0: e = launch_parts_rows<SAS_HEAD_Q4_0>(a, stream); break;
+    case SAS_HEAD_Q6_K: e = launch_parts_rows<SAS_HEAD_Q6_K>(a, stream); break;
+    default: e = launch_parts_rows<SAS_HEAD_BF16>(a, stream); break;
   }
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(lmh_group_kernel, dim3((unsigned)(a.s.rows * a.gparts)), dim3(kThreads), 0, stream, a);

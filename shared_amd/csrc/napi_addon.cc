@@ -456,17 +456,19 @@ napi_value SampleStep(napi_env env, napi_callback_info info) {
 }
 
 // A sas_lm_head descriptor: {hidden, hiddenStride, weight, weightStride,
-// dim, outLogits?} of device addresses (BigInt) and sizes.
+// dim, outLogits?, format?} of device addresses (BigInt) and sizes.
 bool read_head(napi_env env, napi_value d, sas_lm_head *hd) {
   std::memset(hd, 0, sizeof *hd);
   int64_t dim = 0;
+  int64_t format = SAS_HEAD_BF16;
   const bool ok = get_ptr(env, d, "hidden", (void **)&hd->hidden) &&
                   get_i64(env, d, "hiddenStride", &hd->hidden_stride) &&
                   get_ptr(env, d, "weight", (void **)&hd->weight) &&
                   get_i64(env, d, "weightStride", &hd->weight_stride) && get_i64(env, d, "dim", &dim) &&
-                  get_ptr(env, d, "outLogits", (void **)&hd->out_logits);
-  if (!ok || dim < INT32_MIN || dim > INT32_MAX) return false;
+                  get_ptr(env, d, "outLogits", (void **)&hd->out_logits) && get_i64(env, d, "format", &format);
+  if (!ok || dim < INT32_MIN || dim > INT32_MAX || format < INT32_MIN || format > INT32_MAX) return false;
   hd->dim = (int32_t)dim;
+  hd->format = (int32_t)format;
   return true;
 }
 

@@ -137,8 +137,9 @@ struct LmhArgs {
   SampleArgs s;          // the sampling descriptor; s.rec/mrec/pinfo: the parts' records, s.parts = parts
   const float *hidden;
   int64_t hidden_stride;
-  const uint16_t *weight;
-  int64_t weight_stride;
+  const void *weight;    // bf16 bits, or GGUF blocks (format)
+  int64_t weight_stride; // elements (bf16) or bytes (GGUF) between rows
+  int32_t format;        // SAS_HEAD_*
   int32_t dim;
   float *out_logits;     // [rows][vocab] or null
   // the merge's records: kLmhGroup parts each (laid out as SampleArgs' records)

@@ -138,15 +138,22 @@ export interface SampleRowsOptions {
 }
 
 /** The LM head of lmHeadSample: logits[row][id] = sum over k of
- * weight[id][k] (bf16, widened to f32) * hidden[row][k] (f32). */
+ * weight[id][k] * hidden[row][k]: a bf16 head widened to f32, or a GGUF
+ * head (Q8_0 / Q4_0 / Q6_K blocks) against the Q8_1-quantized hidden
+ * state, summed in the library's fixed order. */
+export type LmHeadFormat = 'bf16' | 'q8_0' | 'q4_0' | 'q6_k';
+
 export interface LmHead {
   /** [rows][hiddenStride] f32 final-normed hidden states. */
   hidden: DeviceBuffer | Float32Array;
-  /** [vocab][weightStride] bf16 bits, device-resident. */
+  /** [vocab] rows, device-resident: bf16 bits, or GGUF blocks. */
   weight: DeviceBuffer;
+  /** Default 'bf16'. */
+  format?: LmHeadFormat;
   /** A multiple of 256; rows * dim <= LMH_MAX_LDS_FLOATS. */
   dim: number;
   hiddenStride?: number;
+  /** Between rows: elements (bf16, default dim) or bytes (GGUF, default the row's bytes). */
   weightStride?: number;
   /** Also write the logits [rows][vocab] f32 here. */
   outLogits?: DeviceBuffer;

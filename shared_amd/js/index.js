@@ -239,6 +239,15 @@ function packedToolMask(constraint, raw, parseArguments, builder) {
  * end-of-sequence id.  Gemma (gemma-model.js:900-919): temperature 0.6,
  * top-p 0.95, a random seed, and eos only when eosId is given.
  */
+// LM head formats (sas_lm_head.format): bf16, and the GGUF block types the
+// reference loads (gguf/parser.js:29-36) with their values and bytes per block.
+const HEAD_FORMATS = {
+  bf16: { id: 0, values: 1, bytesPer: 0 },
+  q8_0: { id: 1, values: 32, bytesPer: 34 },
+  q4_0: { id: 2, values: 32, bytesPer: 18 },
+  q6_k: { id: 3, values: 256, bytesPer: 210 },
+};
+
 const PACKER_DEFAULTS = {
   qwen: { temperature: 0, topP: 1, topK: 20, seed: 1, eosFromStops: true },
   gemma: { temperature: 0.6, topP: 0.95, topK: 20, seed: null, eosFromStops: false },
@@ -735,16 +744,25 @@ class Sampler {
     });
   }
 
-  // The sas_lm_head descriptor of opts.head: {hidden, weight, dim,
-  // hiddenStride?, weightStride?, outLogits?}.  The head (bf16 bits
-  // [vocab][weightStride]) must be device-resident; the hidden states may be
-  // a host Float32Array [rows][hiddenStride], staged up per call.
+  // The sas_lm_head descriptor of opts.head: {hidden, weight, dim, format?,
+  // hiddenStride?, weightStride?, outLogits?}.  format: 'bf16' (default:
+  // bits [vocab][weightStride elements]) or a GGUF type, 'q8_0', 'q4_0',
+  // 'q6_k' (blocks [vocab][weightStride bytes], the row's bytes by
+  // default).  The head must be device-resident; the hidden states may be a
+  // host Float32Array [rows][hiddenStride], staged up per call.
   _describeHead(opts) {
     const h = opts.head;
     if (!h || typeof h !== 'object') throw new TypeError('head must be {hidden, weight, dim}');
     const dim = h.dim;
     if (!Number.isInteger(dim) || dim <= 0) throw new RangeError('head.dim must be a positive integer');
-    const hd = { dim: dim, hiddenStride: orDefault(h.hiddenStride, dim), weightStride: orDefault(h.weightStride, dim) };
+    const fmt = orDefault(h.format, 'bf16');
+    if (!Object.prototype.hasOwnProperty.call(HEAD_FORMATS, fmt)) {
+      throw new RangeError('head.format must be one of ' + Object.keys(HEAD_FORMATS).join(', '));
+    }
+    const code = HEAD_FORMATS[fmt];
+    const rowDefault = code.bytesPer ? dim / code.values * code.bytesPer : dim;
+    const hd = { dim: dim, hiddenStride: orDefault(h.hiddenStride, dim), weightStride: orDefault(h.weightStride, rowDefault),
+      format: code.id };
     if (h.hidden instanceof DeviceBuffer) {
       hd.hidden = h.hidden.ptr;
     } else if (h.hidden instanceof Float32Array) {
@@ -753,7 +771,7 @@ class Sampler {
     } else {
       throw new TypeError('head.hidden must be a DeviceBuffer or a Float32Array');
     }
-    if (!(h.weight instanceof DeviceBuffer)) throw new TypeError('head.weight must be a DeviceBuffer (bf16 bits)');
+    if (!(h.weight instanceof DeviceBuffer)) throw new TypeError('head.weight must be a DeviceBuffer');
     hd.weight = h.weight.ptr;
     if (h.outLogits !== undefined && h.outLogits !== null) {
       if (!(h.outLogits instanceof DeviceBuffer)) throw new TypeError('head.outLogits must be a DeviceBuffer');

@@ -307,17 +307,15 @@ class Sampler:
                          out_counts=out.get("counts"), out_flags=out.get("flags"), **kw)
         return out if full else out["ids"]
 
-    def lm_head_sample_into(self, hidden, weight, out_ids, *, dim: Optional[int] = None, out_logits=None,
-                            vocab: Optional[int] = None, stream=None, **kw) -> None:
-        """sas_lm_head_sample: the LM head (hidden [rows][>= dim] fp32 times
-        weight [vocab][>= dim] bf16 bits, as int16/uint16 tensors) with the
-        sampling step fused into its epilogue; kw as for sample_into."""
-        rows = hidden.shape[0]
-        vocab = int(vocab if vocab is not None else weight.shape[0])
+    @staticmethod
+    def _head(hidden, weight, dim, out_logits, fmt):
         if hidden.dtype.itemsize != 4 or hidden.stride(1) != 1:
             raise ValueError("hidden must be fp32 with unit element stride")
-        if weight.dtype.itemsize != 2 or weight.stride(1) != 1:
-            raise ValueError("weight must hold bf16 bits (2 bytes) with unit element stride")
+        if fmt == _capi.HEAD_BF16:
+            if weight.dtype.itemsize != 2 or weight.stride(1) != 1:
+                raise ValueError("a bf16 head holds bf16 bits (2 bytes) with unit element stride")
+        elif weight.dtype.itemsize != 1 or weight.stride(1) != 1:
+            raise ValueError("a GGUF head holds its blocks as bytes (uint8 / int8), one row per id")
         h = SasLmHead()
         h.hidden = hidden.data_ptr()
         h.hidden_stride = hidden.stride(0)
@@ -325,10 +323,39 @@ class Sampler:
         h.weight_stride = weight.stride(0)
         h.dim = int(dim if dim is not None else hidden.shape[1])
         h.out_logits = _ptr(out_logits)
+        h.format = int(fmt)
+        return h
+
+    def lm_head_sample_into(self, hidden, weight, out_ids, *, dim: Optional[int] = None, out_logits=None,
+                            vocab: Optional[int] = None, fmt: int = _capi.HEAD_BF16, stream=None, **kw) -> None:
+        """sas_lm_head_sample: the LM head (hidden [rows][>= dim] fp32 times
+        weight: [vocab][>= dim] bf16 bits as an int16/uint16 tensor, or with
+        fmt = HEAD_Q8_0 / HEAD_Q4_0 / HEAD_Q6_K the GGUF blocks as a
+        [vocab][row bytes] uint8 tensor) with the sampling step fused into its
+        epilogue; kw as for sample_into."""
+        vocab = int(vocab if vocab is not None else weight.shape[0])
+        h = self._head(hidden, weight, dim, out_logits, fmt)
         d = rows_descriptor(hidden, out_ids, vocab=vocab, **kw)
         d.logits = None
         d.logits_stride = 0
         check(self._lib.sas_lm_head_sample(self._h, ctypes.byref(h), ctypes.byref(d), _stream(stream)), self._h)
+
+    def lm_head_step_into(self, hidden, weight, out_ids, state: "DecodeState", *, dim: Optional[int] = None,
+                          out_logits=None, vocab: Optional[int] = None, fmt: int = _capi.HEAD_BF16, stream=None,
+                          **kw) -> None:
+        """sas_lm_head_sample_step: the fused head as one step of the in-graph
+        decode loop (the rows' history is `state`'s ring, their draws its
+        seeds, and the token is written back into `state`)."""
+        if kw.get("hist_ids") is not None:
+            raise ValueError("a decode step's history is its ring")
+        vocab = int(vocab if vocab is not None else weight.shape[0])
+        h = self._head(hidden, weight, dim, out_logits, fmt)
+        d = rows_descriptor(hidden, out_ids, vocab=vocab, **kw)
+        d.logits = None
+        d.logits_stride = 0
+        st = state.descriptor()
+        check(self._lib.sas_lm_head_sample_step(self._h, ctypes.byref(h), ctypes.byref(d), ctypes.byref(st),
+                                                _stream(stream)), self._h)
 
     def lm_head_sample(self, hidden, weight, *, full: bool = False, logits: bool = False, **kw):
         """Allocate outputs and run lm_head_sample_into; returns ids, or a

@@ -239,18 +239,25 @@ def bf16_bits(rng, shape, lo_exp: int = -6, hi_exp: int = -3) -> np.ndarray:
     return table[rng.integers(0, 1 << 16, size=shape, dtype=np.uint16)]
 
 
+HEAD_BF16, HEAD_Q8_0, HEAD_Q4_0, HEAD_Q6_K = 0, 1, 2, 3
+HEAD_NAMES = {HEAD_BF16: "bf16", HEAD_Q8_0: "Q8_0", HEAD_Q4_0: "Q4_0", HEAD_Q6_K: "Q6_K"}
+
+
 @dataclass
 class LmhBatch:
-    """Inputs of sas_lm_head_sample: fp32 hidden states, a bf16 head (uint16
-    bits, [vocab][dim]) and the sampling descriptor's host arrays."""
+    """Inputs of sas_lm_head_sample: fp32 hidden states, the head (bf16 bits
+    [vocab][dim] as uint16, or GGUF blocks [vocab][row bytes] as uint8 with
+    fmt set) and the sampling descriptor's host arrays."""
     name: str
     hidden: np.ndarray            # float32 [rows, dim]
-    weight_bits: np.ndarray       # uint16 [vocab, dim]
+    weight_bits: Optional[np.ndarray]  # uint16 [vocab, dim] (bf16) or None
     params: Params
     mask: Optional[np.ndarray] = None
     hist_ids: Optional[np.ndarray] = None
     hist_offsets: Optional[np.ndarray] = None
     uniforms: Optional[np.ndarray] = None
+    fmt: int = HEAD_BF16
+    weight_q: Optional[np.ndarray] = None  # uint8 [vocab, row bytes] (GGUF formats)
 
     @property
     def rows(self) -> int:
@@ -258,7 +265,12 @@ class LmhBatch:
 
     @property
     def vocab(self) -> int:
-        return self.weight_bits.shape[0]
+        return (self.weight_bits if self.fmt == HEAD_BF16 else self.weight_q).shape[0]
+
+    @property
+    def weight(self) -> np.ndarray:
+        """The head as the C ABI takes it (bf16 bits or GGUF bytes)."""
+        return self.weight_bits if self.fmt == HEAD_BF16 else self.weight_q
 
     @property
     def dim(self) -> int:
@@ -272,7 +284,7 @@ class LmhBatch:
     def algorithmic_bytes(self) -> int:
         """Compulsory HBM bytes of one call: the head read once, the hidden
         states, mask words, history ids and offsets, uniforms, ids out."""
-        b = self.weight_bits.nbytes + self.hidden.nbytes + 4 * self.rows
+        b = self.weight.nbytes + self.hidden.nbytes + 4 * self.rows
         if self.mask is not None:
             b += self.rows * ((self.vocab + 31) // 32) * 4
         if self.hist_ids is not None:
@@ -297,6 +309,51 @@ def lmh(rows: int = 1, vocab: int = GEMMA_VOCAB, dim: int = 2560, seed: int = 7,
     p = Params(temperature=1.0, top_k=50, top_p=0.9, repetition_penalty=1.1, presence_penalty=0.5,
                frequency_penalty=0.3, softcap=softcap)
     return LmhBatch("LMH", hidden, w, p, mask=m, hist_ids=ids, hist_offsets=offs, uniforms=rng.random(rows))
+
+
+def gguf_head(rng, fmt: int, vocab: int, dim: int) -> np.ndarray:
+    """A random GGUF head [vocab][row bytes] (uint8) of ggml's block layout,
+    scaled so that an N(0, 1) hidden row gives logits of about N(0, 3):
+    f16 block scales, random quants; Q6_K scales signed."""
+    if fmt == HEAD_Q8_0:
+        nb, bs = dim // 32, 34
+    elif fmt == HEAD_Q4_0:
+        nb, bs = dim // 32, 18
+    elif fmt == HEAD_Q6_K:
+        nb, bs = dim // 256, 210
+    else:
+        raise ValueError("not a GGUF format")
+    w = rng.integers(0, 256, size=(vocab * nb, bs), dtype=np.uint8)
+    if fmt == HEAD_Q8_0:
+        d = (rng.uniform(0.5, 1.5, vocab * nb) * 8.1e-4).astype(np.float16)
+        w[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    elif fmt == HEAD_Q4_0:
+        d = (rng.uniform(0.5, 1.5, vocab * nb) * 1.28e-2).astype(np.float16)
+        w[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    else:
+        sc = rng.integers(-63, 64, size=(vocab * nb, 16)).astype(np.int8)
+        w[:, 192:208] = sc.view(np.uint8)
+        d = (rng.uniform(0.5, 1.5, vocab * nb) * 1.0e-4).astype(np.float16)
+        w[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return np.ascontiguousarray(w.reshape(vocab, nb * bs))
+
+
+def lmhq(fmt: int = HEAD_Q6_K, rows: int = 1, vocab: int = 248320, dim: int = 2560, seed: int = 8, hist: int = 512,
+         softcap: float = 0.0, mask: bool = True) -> LmhBatch:
+    """LMQ: the decode head with sampling fused over a GGUF head, by default
+    Qwen3.5-4B's tied Q6_K head (hidden 2560, vocabulary 248,320,
+    config.js:6-9, gguf/sources.js:122), then C3P's sampling (mask density
+    U[0.5 %, 20 %], top-k 50 / top-p 0.9 / T 1.0, repetition 1.1 / presence
+    0.5 / frequency 0.3 over `hist` ids)."""
+    rng = _rng(seed)
+    hidden = rng.standard_normal((rows, dim), dtype=np.float32)
+    w = gguf_head(rng, fmt, vocab, dim)
+    m = random_mask(rng, rows, vocab, 0.005, 0.20) if mask else None
+    ids, offs = _csr([rng.integers(0, vocab, hist) for _ in range(rows)]) if hist else (None, None)
+    p = Params(temperature=1.0, top_k=50, top_p=0.9, repetition_penalty=1.1, presence_penalty=0.5,
+               frequency_penalty=0.3, softcap=softcap)
+    return LmhBatch("LMQ", hidden, None, p, mask=m, hist_ids=ids, hist_offsets=offs, uniforms=rng.random(rows),
+                    fmt=fmt, weight_q=w)
 
 
 def c3p_shard8(rows: int = 128, seed: int = 38) -> Batch:

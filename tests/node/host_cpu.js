@@ -261,7 +261,18 @@ check('lmHeadSample describes its head and rejects bad ones on the host', functi
   const self = Object.create(sas.Sampler.prototype);
   const fake = function (ptr) { const b = Object.create(sas.DeviceBuffer.prototype); b.ptr = ptr; return b; };
   const hd = self._describeHead({ rows: 2, head: { hidden: fake(16n), weight: fake(4096n), dim: 512, outLogits: fake(8192n) } });
-  assert.deepStrictEqual(hd, { dim: 512, hiddenStride: 512, weightStride: 512, hidden: 16n, weight: 4096n, outLogits: 8192n });
+  assert.deepStrictEqual(hd, { dim: 512, hiddenStride: 512, weightStride: 512, format: 0, hidden: 16n, weight: 4096n,
+    outLogits: 8192n });
+  // GGUF heads: the format code and the row's bytes as the default stride
+  const q6 = self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(64n), dim: 2560, format: 'q6_k' } });
+  assert.strictEqual(q6.format, 3);
+  assert.strictEqual(q6.weightStride, 2100);
+  assert.strictEqual(self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(64n), dim: 512, format: 'q8_0' } })
+    .weightStride, 544);
+  assert.strictEqual(self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(64n), dim: 512, format: 'q4_0' } })
+    .weightStride, 288);
+  assert.throws(function () { self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(64n), dim: 256, format: 'q5_k' } }); },
+    /head.format must be one of bf16, q8_0, q4_0, q6_k/);
   const hs = self._describeHead({ rows: 1, head: { hidden: fake(16n), weight: fake(32n), dim: 256, hiddenStride: 300, weightStride: 264 } });
   assert.strictEqual(hs.hiddenStride, 300);
   assert.strictEqual(hs.weightStride, 264);

@@ -64,6 +64,26 @@ async function main() {
     write('lmh_unfused_ids.u32', c.ids);
     step('sampleRows over the written logits done');
 
+    // a GGUF Q6_K head (the Qwen head's format) with the same rows and inputs
+    const q6k = read('q6k.u8', Uint8Array);
+    if (q6k) {
+      const wq = s.alloc(q6k.byteLength).upload(q6k);
+      const qlog = s.alloc(rows * vocab * 4);
+      const qd = await s.lmHeadSampleAsync(Object.assign({ full: true,
+        head: { hidden: hidden, weight: wq, dim: dim, format: 'q6_k', outLogits: qlog } }, base));
+      write('lmh_q6k_ids.u32', qd.ids);
+      write('lmh_q6k_probs.f64', qd.probs);
+      write('lmh_q6k_logits.f32', qlog.download(new Float32Array(rows * vocab)));
+      let bad = '';
+      try {
+        s.lmHeadSample(Object.assign({ head: { hidden: hidden, weight: wq, dim: dim, format: 'q5_k' } }, base));
+      } catch (e) { bad = String(e.message); }
+      if (!/format/.test(bad)) throw new Error('an unknown head format did not throw: ' + bad);
+      wq.free();
+      qlog.free();
+      step('lmHeadSampleAsync (Q6_K head) done');
+    }
+
     let threw = '';
     try {
       s.lmHeadSample(Object.assign({ head: { hidden: hdev, weight: w, dim: dim + 64 } }, base));

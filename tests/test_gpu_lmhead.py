@@ -25,7 +25,8 @@ def run_lmh(s, b: W.LmhBatch, *, logits=True, row_params=None):
     if row_params is not None:
         kw["row_params"] = to_dev(pack_params(row_params).view(np.uint8))
         kw["row_hints"] = row_hints(row_params)
-    out = s.lm_head_sample(to_dev(b.hidden), to_dev(b.weight_bits.view(np.int16)), full=True, logits=logits,
+    wt = to_dev(b.weight_bits.view(np.int16)) if b.fmt == W.HEAD_BF16 else to_dev(b.weight_q)
+    out = s.lm_head_sample(to_dev(b.hidden), wt, full=True, logits=logits, fmt=b.fmt,
                            mask=to_dev(b.mask, torch.int32) if b.mask is not None else None,
                            hist_ids=to_dev(b.hist_ids, torch.int32) if b.hist_ids is not None else None,
                            hist_offsets=to_dev(b.hist_offsets) if b.hist_offsets is not None else None,
@@ -43,7 +44,8 @@ def run_lmh(s, b: W.LmhBatch, *, logits=True, row_params=None):
 def check(s, b: W.LmhBatch, label: str, row_params=None):
     print(f"[gpu] lm head {label}: rows={b.rows} vocab={b.vocab} dim={b.dim}", flush=True)
     g = run_lmh(s, b, row_params=row_params)
-    lo = O.lm_head_logits(b.hidden, b.weight_bits)
+    lo = O.lm_head_logits(b.hidden, b.weight_bits) if b.fmt == W.HEAD_BF16 else \
+        O.lm_head_q_logits(b.fmt, b.hidden, b.weight_q)
     bad = np.nonzero(g["logits"].view(np.uint32) != lo.view(np.uint32))
     assert bad[0].size == 0, f"{label}: logits differ at {list(zip(*bad))[:4]}"
     o = O.sample_rows(b.with_logits(lo), row_params=row_params)
@@ -183,3 +185,121 @@ def test_random_sweep(sampler):
         b.params = params()
         rp = [params() for _ in range(rows)] if rng.random() < 0.3 else None
         check(sampler, b, f"sweep {case}: rows={rows} dim={dim} vocab={vocab}", row_params=rp)
+
+
+# ---------------------------------------------------------------- GGUF heads --
+
+def test_qwen_q6k_head_full_size(sampler):
+    """Qwen3.5-4B's tied Q6_K head (gguf/sources.js:122): vocabulary 248,320,
+    hidden 2,560, one decode row."""
+    check(sampler, W.lmhq(W.HEAD_Q6_K, rows=1), "qwen q6_k decode")
+
+
+def test_qwen_q6k_verify_rows(sampler):
+    check(sampler, W.lmhq(W.HEAD_Q6_K, rows=3, seed=12), "qwen q6_k verify rows")
+
+
+@pytest.mark.parametrize("fmt", [W.HEAD_Q8_0, W.HEAD_Q4_0])
+def test_gemma_shape_q8_0_q4_0(sampler, fmt):
+    check(sampler, W.lmhq(fmt, rows=1, vocab=W.GEMMA_VOCAB, dim=2560, seed=13 + fmt, softcap=30.0),
+          f"gemma-shaped {W.HEAD_NAMES[fmt]}")
+
+
+@pytest.mark.parametrize("fmt,vocab,dim,rows", [(W.HEAD_Q6_K, 300, 256, 2), (W.HEAD_Q6_K, 4097, 768, 4),
+                                                (W.HEAD_Q6_K, 20000, 1280, 3), (W.HEAD_Q8_0, 777, 256, 4),
+                                                (W.HEAD_Q4_0, 5000, 512, 2), (W.HEAD_Q8_0, 1, 256, 1)])
+def test_gguf_shapes(sampler, fmt, vocab, dim, rows):
+    # dims of 256 and 768 leave lanes with fewer Q6_K units than others
+    check(sampler, W.lmhq(fmt, rows=rows, vocab=vocab, dim=dim, seed=vocab + dim + fmt, hist=min(300, vocab)),
+          f"{W.HEAD_NAMES[fmt]} {rows}x{vocab}x{dim}")
+
+
+def test_gguf_head_with_a_row_stride(sampler):
+    """Rows further apart than their blocks (a stride of the row's bytes plus
+    padding), one Q6_K row length odd in super-blocks (2-byte aligned rows)."""
+    import torch
+    b = W.lmhq(W.HEAD_Q6_K, rows=2, vocab=3000, dim=768, seed=21)
+    rb = b.weight_q.shape[1]
+    padded = np.zeros((b.vocab, rb + 6), np.uint8)
+    padded[:, :rb] = b.weight_q
+    dev_w = to_dev(padded)[:, :rb]
+    print(f"[gpu] lm head q6_k strided rows: stride {rb + 6} bytes, row {rb}", flush=True)
+    out = sampler.lm_head_sample(to_dev(b.hidden), dev_w, full=True, logits=True, fmt=W.HEAD_Q6_K,
+                                 mask=to_dev(b.mask, torch.int32), hist_ids=to_dev(b.hist_ids, torch.int32),
+                                 hist_offsets=to_dev(b.hist_offsets), uniforms=to_dev(b.uniforms), params=b.params)
+    torch.cuda.synchronize()
+    lo = O.lm_head_q_logits(W.HEAD_Q6_K, b.hidden, b.weight_q)
+    assert np.array_equal(out["logits"].cpu().numpy().view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(out["ids"].cpu().numpy().view(np.uint32), O.sample_rows(b.with_logits(lo))["ids"])
+
+
+def test_gguf_head_argument_errors(sampler):
+    import torch
+    from shared_amd import SasError
+    hid = torch.zeros((1, 256), dtype=torch.float32, device="cuda")
+    w = torch.zeros((10, 210), dtype=torch.uint8, device="cuda")
+    short = torch.zeros((10, 200), dtype=torch.uint8, device="cuda")  # rows of 200 < 210 bytes
+    with pytest.raises(SasError, match="weight_stride"):
+        sampler.lm_head_sample(hid, short, fmt=W.HEAD_Q6_K, params=Params())
+    with pytest.raises(SasError, match="format"):
+        sampler.lm_head_sample(hid, w, fmt=7, params=Params())
+    with pytest.raises(SasError, match="aligned"):
+        sampler.lm_head_sample(hid, w.view(-1)[2:2 + 9 * 210].view(9, 210), fmt=W.HEAD_Q6_K, params=Params())
+
+
+@pytest.mark.parametrize("fmt", [W.HEAD_BF16, W.HEAD_Q6_K])
+def test_fused_head_decode_steps(sampler, fmt):
+    """sas_lm_head_sample_step: k steps of the in-graph decode loop with the
+    head fused (the reference's per-iteration lm -> topk -> sampler with
+    tokens[0] fed back, model.js:711-717): every step's token, candidates and
+    probabilities, and the state (stop flags, iterations, sampled, next
+    tokens, rings) equal the oracle's head logits stepped with the sampling
+    oracle; a planted stop freezes one row mid-loop."""
+    import torch
+    from gpu_helpers import oracle_steps, ring_of
+    from shared_amd import DecodeState
+    from shared_amd._capi import MAX_TOP_K
+    rows, steps, vocab, dim, ring_len = 3, 5, 20_000, 512, 64
+    rng = np.random.default_rng(50 + fmt)
+    if fmt == W.HEAD_BF16:
+        b = W.lmh(rows=rows, vocab=vocab, dim=dim, seed=51, hist=0, softcap=30.0, mask=True)
+        wt = to_dev(b.weight_bits.view(np.int16))
+        logits_of = lambda h: O.lm_head_logits(h, b.weight_bits)  # noqa: E731
+    else:
+        b = W.lmhq(fmt, rows=rows, vocab=vocab, dim=dim, seed=52, hist=0, mask=True)
+        wt = to_dev(b.weight_q)
+        logits_of = lambda h: O.lm_head_q_logits(fmt, h, b.weight_q)  # noqa: E731
+    hs = rng.standard_normal((steps, rows, dim)).astype(np.float32)
+    xs = np.stack([logits_of(hs[t]) for t in range(steps)])
+    # row 1's step-2 token is its stop id
+    prm = [Params(temperature=0.9, top_k=40, top_p=0.9, repetition_penalty=1.2, presence_penalty=0.4,
+                  softcap=b.params.softcap)] * rows
+    seeds = rng.integers(0, 2**32, rows, dtype=np.uint64).astype(np.uint32)
+    history = [[int(i) for i in rng.integers(0, vocab, 20)] for _ in range(rows)]
+    free, _, _, _ = oracle_steps(xs, prm, mask=b.mask, seeds=seeds, history=history, ring_len=ring_len)
+    stop_ids = [[], [int(free[2]["ids"][1])], []]
+    want, stopped, it, window = oracle_steps(xs, prm, mask=b.mask, seeds=seeds, history=history, ring_len=ring_len,
+                                             stop_ids=stop_ids)
+    assert stopped[1], "the planted stop must freeze row 1"
+    print(f"[gpu] fused head decode steps {W.HEAD_NAMES[fmt]}: {steps} x {rows} rows, vocab {vocab}", flush=True)
+    st = DecodeState(rows, max_steps=steps, ring_len=ring_len, stop_ids=stop_ids, seeds=seeds, history=history)
+    rp = to_dev(pack_params(prm).view(np.uint8))
+    mask = to_dev(b.mask, torch.int32)
+    ids = torch.empty(rows, dtype=torch.int32, device="cuda")
+    probs = torch.empty((rows, MAX_TOP_K), dtype=torch.float64, device="cuda")
+    cand = torch.empty((rows, MAX_TOP_K), dtype=torch.int32, device="cuda")
+    for t in range(steps):
+        sampler.lm_head_step_into(to_dev(hs[t]), wt, ids, st, fmt=fmt, mask=mask, row_params=rp,
+                                  row_hints=row_hints(prm), out_probs=probs, out_cand_ids=cand)
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy().view(np.uint32), want[t]["ids"]), f"step {t}: ids"
+        assert np.array_equal(cand.cpu().numpy().view(np.uint32), want[t]["cand_ids"]), f"step {t}: candidates"
+        assert np.array_equal(probs.cpu().numpy().view(np.uint64), want[t]["probs"].view(np.uint64)), f"step {t}: probs"
+    sv = st.state.cpu().numpy()
+    assert sv[:, 0].tolist() == [int(x) for x in stopped] and sv[:, 1].tolist() == it
+    sampled = st.sampled.cpu().numpy().view(np.uint32)
+    ring = st.ring.cpu().numpy().view(np.uint32)
+    for r in range(rows):
+        assert sampled[r].tolist() == [int(w["ids"][r]) for w in want], f"sampled row {r}"
+        assert np.array_equal(ring[r], ring_of(window[r], ring_len)), f"ring row {r}"
+    assert np.array_equal(st.next_tokens.cpu().numpy().view(np.uint32), want[-1]["ids"])

@@ -250,6 +250,11 @@ def test_node_lm_head_sample(tmp_path):
     np.ascontiguousarray(b.hidden, np.float32).tofile(os.path.join(d, "hidden.f32"))
     np.ascontiguousarray(b.weight_bits, np.uint16).tofile(os.path.join(d, "weight.u16"))
     want = O.sample_rows(bl)
+    # the same rows over a GGUF Q6_K head
+    wq = W.gguf_head(np.random.default_rng(45), W.HEAD_Q6_K, b.vocab, b.dim)
+    wq.tofile(os.path.join(d, "q6k.u8"))
+    lq = O.lm_head_q_logits(W.HEAD_Q6_K, b.hidden, wq)
+    want_q = O.sample_rows(b.with_logits(lq))
 
     print("[gpu] node lmhead_gpu.js", d, flush=True)
     proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "lmhead_gpu.js"), d], stdout=subprocess.PIPE,
@@ -265,3 +270,7 @@ def test_node_lm_head_sample(tmp_path):
     assert np.array_equal(_u32(d, "lmh_sync_cand.u32").reshape(b.rows, -1), want["cand_ids"])
     for name in ("lmh_async_ids.u32", "lmh_unfused_ids.u32"):
         assert np.array_equal(_u32(d, name), want["ids"]), name
+    gq = np.fromfile(os.path.join(d, "lmh_q6k_logits.f32"), np.float32).reshape(b.rows, b.vocab)
+    assert np.array_equal(gq.view(np.uint32), lq.view(np.uint32))
+    assert np.array_equal(_u32(d, "lmh_q6k_ids.u32"), want_q["ids"])
+    assert np.array_equal(np.fromfile(os.path.join(d, "lmh_q6k_probs.f64")).reshape(b.rows, -1), want_q["probs"])

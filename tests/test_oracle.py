@@ -580,3 +580,108 @@ def test_lm_head_within_the_chain_bound_of_the_exact_dot():
     bound = 512 * 2.0 ** -24 * (np.abs(h.astype(np.float64)) @ np.abs(wf).T)
     assert np.all(np.abs(got - exact) <= bound)
     assert np.any(got != exact)  # the f32 chain does round
+
+
+# ------------------------------------------------------ quantized LM head --
+
+def test_f16_round_is_numpys_float16():
+    """orc_f16_round (the Q8_1 operand's f16 fields) rounds to nearest, ties
+    to even, with subnormals and overflow, as numpy's float16 does."""
+    rng = np.random.default_rng(31)
+    xs = np.concatenate([rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+                         np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e6, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26,
+                                   1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, np.inf, -np.inf], np.float32)])
+    want = xs.astype(np.float16).astype(np.float32)
+    got = np.array([O.f16_round(float(x)) for x in xs], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q81_quantize_hand_blocks():
+    """q8.js:27-42 on blocks worked out by hand: amax 127 gives d = 1 and
+    q = round-half-even(x); amax 63.5 gives d = 0.5 and q = rint(2 x); an
+    all-zero block has d = 0 and q = 0; d8 and s8 are the f16 d and d * sum."""
+    x = np.zeros(96, np.float32)
+    x[0:8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, 3.49, -126.5]
+    x[32:36] = [63.5, 0.25, -0.75, 10.0]
+    q, d8, s8 = O.q81_quantize(x)
+    assert q[0:8].tolist() == [127, 0, 2, 2, 0, -2, 3, -126]
+    assert (q[8:32] == 0).all()
+    assert q[32:36].tolist() == [127, 0, -2, 20] and (q[36:64] == 0).all()
+    assert (q[64:] == 0).all()
+    assert d8.tolist() == [1.0, 0.5, 0.0]
+    assert s8.tolist() == [float(np.float16(127 + 2 + 2 - 2 + 3 - 126)), float(np.float16(0.5 * 145)), 0.0]
+
+
+def _ref_weight(fmt, row: np.ndarray, k: int) -> float:
+    """The reference's per-element dequantization (ggml/kernels.js:64-80,
+    loadWeight) of value k of one GGUF row, exactly (float64)."""
+    def f16(off):
+        return float(row[off:off + 2].copy().view(np.float16)[0])
+    if fmt == O.HEAD_Q8_0:
+        base = (k >> 5) * 34
+        return f16(base) * float(np.int8(row[base + 2 + (k & 31)]))
+    if fmt == O.HEAD_Q4_0:
+        base, i = (k >> 5) * 18, k & 31
+        qb = int(row[base + 2 + (i & 15)])
+        return f16(base) * ((qb >> 4 if i >= 16 else qb & 15) - 8.0)
+    base, i = (k >> 8) * 210, k & 255
+    half, p = i >> 7, i & 127
+    quarter, l = p >> 5, p & 31
+    packed = int(row[base + half * 64 + (32 if quarter & 1 else 0) + l])
+    nib = packed >> 4 if quarter >= 2 else packed & 15
+    high = (int(row[base + 128 + half * 32 + l]) >> (quarter * 2)) & 3
+    sc = float(np.int8(row[base + 192 + half * 8 + (l >> 4) + quarter * 2]))
+    return f16(base + 208) * sc * ((nib | (high << 4)) - 32.0)
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3])
+def test_gguf_head_one_hot_reads_the_reference_weight(fmt):
+    """hidden = 127 e_k (its Q8_1 block has d = 1, q = 127 at k, every other
+    block d = 0) makes each logit the term of the one block holding k, which
+    equals 127 times the reference's dequantized weight rounded once to f32
+    (the exact products have at most 32 significant bits): pins every byte,
+    nibble, two-bit field and scale index of the three layouts."""
+    from shared_amd import workloads as W
+    rng = np.random.default_rng(40 + fmt)
+    dim, vocab = 512, 40
+    w = W.gguf_head(rng, fmt, vocab, dim)
+    ks = list(range(0, dim, 7)) + [1, 15, 16, 17, 31, 32, 63, 64, 127, 128, 129, 255, 256, 300, 511]
+    hid = np.zeros((len(ks), dim), np.float32)
+    for r, k in enumerate(ks):
+        hid[r, k] = 127.0
+    got = O.lm_head_q_logits(fmt, hid, w)
+    for r, k in enumerate(ks):
+        want = np.array([127.0 * _ref_weight(fmt, w[i], k) for i in range(vocab)]).astype(np.float32)
+        # values equal (a zero weight under a negative scale is -0 in the
+        # formula, +0 once added to the partial sums)
+        assert np.array_equal(got[r], want), (fmt, k)
+
+
+def test_gguf_head_partials_add_in_the_fixed_tree():
+    """Q8_0 rows whose block terms are planted (hidden 127 at the first value
+    of every block: each block's term is 127 q d rounded once): the logit is
+    the eight lane chains (blocks g, g + 8) added in the pairwise tree, and a
+    left-to-right sum of the same terms differs for the planted rows."""
+    from shared_amd import workloads as W
+    dim = 512
+    hid = np.zeros((1, dim), np.float32)
+    hid[0, ::32] = 127.0
+    found = 0
+    for seed in range(200):
+        rng = np.random.default_rng(seed)
+        w = W.gguf_head(rng, O.HEAD_Q8_0, 8, dim)
+        got = O.lm_head_q_logits(O.HEAD_Q8_0, hid, w)[0]
+        for i in range(8):
+            t = [np.float32(np.float32(127.0 * float(np.int8(w[i, 34 * b + 2]))) *
+                            np.float32(w[i, 34 * b:34 * b + 2].copy().view(np.float16)[0])) for b in range(16)]
+            p = [np.float32(np.float32(np.float32(0.0) + t[g]) + t[g + 8]) for g in range(8)]
+            tree = np.float32(np.float32(np.float32(p[0] + p[1]) + np.float32(p[2] + p[3])) +
+                              np.float32(np.float32(p[4] + p[5]) + np.float32(p[6] + p[7])))
+            seq = np.float32(0.0)
+            for x in t:
+                seq = np.float32(seq + x)
+            assert got[i] == tree
+            found += int(tree != seq)
+        if found >= 3:
+            break
+    assert found >= 3
