@@ -452,7 +452,7 @@ __device__ __forceinline__ void q_terms(const QItem<kFmt> &x, int it, const int3
       }
       // scale byte h*8 + lh + 2 qt: word qt >> 1 of the pair, byte lh + 2 (qt & 1)
       const uint32_t sw = (qt >> 1) ? s1 : s0;
-      const float sc = (float)__builtin_amdgcn_sbfe((int)sw, 8u * (uint32_t)(lh + 2 * (qt & 1)), 8u);
+      const float sc = (float)(int)(int8_t)(uint8_t)(sw >> (8u * (uint32_t)(lh + 2 * (qt & 1))));
       const float ds = x.d * sc;
       const int qb = sb * 8 + h * 4 + qt;  // the Q8_1 block of these 16 values
 #pragma unroll
