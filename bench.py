@@ -49,6 +49,10 @@ WORKLOAD_DOC = {
             "a 262144 x 2560 bf16 head (Gemma-4 E4B shape), softcap 30, then C3P's mask, penalties and "
             "top-k 50 / top-p 0.9",
     "LMH3": "as LMH1 with the three rows of a speculative verify round over the same head",
+    "LMQ1": "the LM head with the sampling step fused over Qwen3.5-4B's tied Q6_K head (GGUF blocks, vocabulary "
+            "248320, hidden 2560, the hidden state quantized to Q8_1 on chip, exact integer block dots), one decode "
+            "row, then C3P's mask, penalties and top-k 50 / top-p 0.9",
+    "LMQ3": "as LMQ1 with the three rows of a speculative verify round over the same head",
 }
 CPU_THREADS = 16  # the GPU box's CPU share for one GPU (its nproc may show more)
 
@@ -448,7 +452,8 @@ def bench_lm_head(args) -> int:
     from shared_amd import workloads as W
 
     rows = int(args.workload[3:])
-    b = W.lmh(rows=rows)
+    quant = args.workload.startswith("LMQ")
+    b = W.lmhq(W.HEAD_Q6_K, rows=rows) if quant else W.lmh(rows=rows)
     set_bytes = b.algorithmic_bytes()
     base = None
     if not args.no_cpu_baseline and args.cpu_seconds > 0:
@@ -457,7 +462,8 @@ def bench_lm_head(args) -> int:
         import oracle as O
 
         def cpu_step():
-            O.sample_rows(b.with_logits(O.lm_head_logits(b.hidden, b.weight_bits)), threads=1)
+            lo = O.lm_head_q_logits(b.fmt, b.hidden, b.weight_q) if quant else O.lm_head_logits(b.hidden, b.weight_bits)
+            O.sample_rows(b.with_logits(lo), threads=1)
         t0 = time.perf_counter()
         cpu_step()
         one = time.perf_counter() - t0
@@ -470,8 +476,10 @@ def bench_lm_head(args) -> int:
         med = sorted(times)[len(times) // 2]
         base = {"value": rows / med, "unit": "rows/s", "cores": 1, "kind": "port",
                 "sample": f"the whole step ({rows} row(s), vocab {b.vocab}, dim {b.dim}), {reps} passes (median): "
-                          "the C restatement of the head's dot products (orc_lm_head_logits, eight FMA chains "
-                          "per id) then of the sampling step (oracle/sampler_oracle.c), single thread"}
+                          "the C restatement of the head's dot products ("
+                          + ("orc_lm_head_q_logits: Q8_1 operand, integer block dots" if quant else
+                             "orc_lm_head_logits, eight FMA chains per id")
+                          + ") then of the sampling step (oracle/sampler_oracle.c), single thread"}
     if not torch.cuda.is_available():
         print("bench.py: no HIP device is visible", file=sys.stderr)
         return 1
@@ -483,22 +491,26 @@ def bench_lm_head(args) -> int:
         t = torch.from_numpy(np.ascontiguousarray(a))
         return (t.view(view) if view is not None else t).cuda()
 
-    hidden, weight = dev(b.hidden), dev(b.weight_bits.view(np.int16))
+    hidden = dev(b.hidden)
+    weight = dev(b.weight_q) if quant else dev(b.weight_bits.view(np.int16))
+    fmt = b.fmt
     kw = dict(mask=dev(b.mask, torch.int32), hist_ids=dev(b.hist_ids, torch.int32),
               hist_offsets=dev(b.hist_offsets), uniforms=dev(b.uniforms), params=b.params)
     out_ids = torch.empty(rows, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream()
     with Sampler(0) as s:
         for _ in range(args.warmup):
-            s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, **kw)
+            s.lm_head_sample_into(hidden, weight, out_ids, stream=stream, fmt=fmt, **kw)
         torch.cuda.synchronize()
-        t = timed_steps(args, stream, lambda i, st: s.lm_head_sample_into(hidden, weight, out_ids, stream=st, **kw))
+        t = timed_steps(args, stream,
+                        lambda i, st: s.lm_head_sample_into(hidden, weight, out_ids, stream=st, fmt=fmt, **kw))
     ms_step = t["mean_ms"]
     achieved = set_bytes / (ms_step * 1e-3) / 1e9
     line = {
         "metric": METRIC, "value": rows / (ms_step / 1e3), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32 (bf16 head widened to f32)", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "Q6_K x Q8_1 int8 dots, f32 scales" if quant else "f32 (bf16 head widened to f32)", "data": "synthetic",
         "config": {"workload": f"{args.workload}: {WORKLOAD_DOC[args.workload]}", "rows": rows,
                    "vocab": b.vocab, "dim": b.dim, "top_k": b.params.top_k, "top_p": b.params.top_p,
                    "temperature": b.params.temperature, "softcap": b.params.softcap, "launch": launch_doc(args)},
@@ -506,6 +518,7 @@ def bench_lm_head(args) -> int:
         "gbps": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic_from_profiles(args.workload, "lm_head"),
+                     "head_format": W.HEAD_NAMES[fmt], "head_bytes": int(b.weight.nbytes),
                      "kernel": "sas::lmh_parts_kernel + lmh_group_kernel + sample_merge_kernel (one step)",
                      "algorithmic_bytes_per_launch": set_bytes},
         "cpu_baseline": base,
@@ -529,7 +542,7 @@ def main() -> int:
         return mask_probe(args)
     if args.workload == "C5":
         return bench_verify(args)
-    if args.workload.startswith("LMH"):
+    if args.workload.startswith("LMH") or args.workload.startswith("LMQ"):
         return bench_lm_head(args)
 
     import numpy as np

@@ -296,47 +296,48 @@ __device__ __forceinline__ void lmh_select_rows(const LmhArgs &L, LmhLds<R> &S, 
 
 // ---- GGUF heads: the Q8_1 operand on chip, exact integer block dots ----
 
-// Dwords 0..N-1 of the bytes at p (p even): aligned loads of the dwords that
-// cover them, shifted by two bytes when p is not a multiple of four.  Reads
-// nothing outside [p, p + 4 N) when p is aligned, else at most the two bytes
-// on each side (inside the neighbouring fields of the same head).
+// GGUF rows are staged through LDS: 8 items of a row at a time (a stage:
+// 8 blocks of Q8_0 / Q4_0, 8 units = 2 super-blocks of Q6_K), loaded as the
+// 16-byte aligned chunks that cover them, so the 8 lanes of a row read 128
+// contiguous bytes per load and every load is a whole aligned chunk.  A
+// chunk that holds one byte of the head lies in the head's pages, so the
+// few bytes it holds past either end of the stage are safe to read.
+template <int kFmt>
+struct QStage {
+  static constexpr int bytes = kFmt == SAS_HEAD_Q6_K ? 420 : kFmt == SAS_HEAD_Q8_0 ? 272 : 144;
+  static constexpr int chunks = (bytes + 14 + 15) / 16;  // the stage starts 0 .. 14 bytes into its first chunk
+  static constexpr int loads = (chunks + 7) / 8;         // per lane
+  static constexpr int pitch = 4 * (chunks + 1);         // LDS dwords per row (one chunk of bank skew)
+  static constexpr int depth = 4;                        // stages in flight per wave
+};
+
+__device__ __forceinline__ float f16_value(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// N words of the staged row `rb` starting at byte x (x even): N + 1 dword
+// reads shifted by x % 4.
 template <int N>
-__device__ __forceinline__ void load_span(const uint8_t *p, uint32_t (&out)[N]) {
-  static_assert(N % 4 == 0, "whole 16-byte loads");
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
-  const bool mis = (a & 2u) != 0u;
-  typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));  // 16 bytes, 4-byte aligned
+__device__ __forceinline__ void lds_words(const uint32_t *rb, uint32_t x, uint32_t (&out)[N]) {
+  const uint32_t *q = rb + (x >> 2);
   uint32_t u[N + 1];
 #pragma unroll
-  for (int i = 0; i < N; i += 4) {
-    const u32x4a4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4a4 *>(q + i));
-    u[i] = v.x;
-    u[i + 1] = v.y;
-    u[i + 2] = v.z;
-    u[i + 3] = v.w;
-  }
-  u[N] = 0u;
-  if (mis) u[N] = __builtin_nontemporal_load(q + N);
+  for (int i = 0; i <= N; ++i) u[i] = q[i];
 #pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = mis ? __builtin_amdgcn_alignbyte(u[i + 1], u[i], 2u) : u[i];
+  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(u[i + 1], u[i], x & 3u);
 }
-
-__device__ __forceinline__ float f16_at(const uint8_t *p) {
-  return (float)__builtin_bit_cast(_Float16, __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p)));
-}
-
-// Four six-bit values q (bytes of `raw`, 0..63) as the bytes of q - 32.
-__device__ __forceinline__ uint32_t center32(uint32_t raw) {
-  return ((raw | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+// the f16 at byte x of `rb` (x even)
+__device__ __forceinline__ float lds_f16(const uint32_t *rb, uint32_t x) {
+  return f16_value(rb[x >> 2] >> (8u * (x & 2u)));
 }
 
 // The Q8_1 operand of R hidden rows, in LDS: q8[r][dim / 4] (four int8 per
-// word), d8[r][dim / 32], s8[r][dim / 32].  One 32-value block per thread per
-// round (q8.js:27-42): amax, d = amax / 127, q = round-half-even(x * (1 / d)),
-// the f16 d and d * sum(q).
+// word), d8[r][dim / 32], s8[r][dim / 32], and qs[r][dim / 16] the sum of each
+// 16 values' q.  One 32-value block per thread per round (q8.js:27-42):
+// amax, d = amax / 127, q = round-half-even(x * (1 / d)), the f16 d and
+// d * sum(q).
 template <int R>
-__device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *d8, float *s8) {
+__device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *d8, float *s8, int32_t *qs) {
   const int dim = L.dim, nq = dim / 32;
   for (int t = threadIdx.x; t < R * nq; t += kThreads) {
     const int r = t / nq, b = t - r * nq;
@@ -349,7 +350,7 @@ __device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
     const float d = amax / 127.0f;
     const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-    int sum = 0;
+    int sum = 0, half = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       uint32_t w = 0u;
@@ -362,62 +363,30 @@ __device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *
         w |= ((uint32_t)qi & 0xFFu) << (8 * i);
       }
       q8[r * (dim / 4) + 8 * b + j] = (int32_t)w;
+      if (j == 3) half = sum;
     }
+    qs[r * (dim / 16) + 2 * b] = half;
+    qs[r * (dim / 16) + 2 * b + 1] = sum - half;
     d8[r * nq + b] = (float)(_Float16)d;
     s8[r * nq + b] = (float)(_Float16)(d * (float)sum);
   }
 }
 
-template <int kFmt>
-struct QItem;  // the raw words of one work item of a lane
-
-// Q8_0 / Q4_0: one 32-value block
-template <>
-struct QItem<SAS_HEAD_Q8_0> {
-  uint32_t w[8];
-  float d;
-};
-template <>
-struct QItem<SAS_HEAD_Q4_0> {
-  uint32_t w[4];
-  float d;
-};
-// Q6_K: one 64-value unit of a super-block: its two ql spans, its qh span,
-// the super-block's scales and d
-template <>
-struct QItem<SAS_HEAD_Q6_K> {
-  uint32_t la[4], lb[4], qh[4], sc[4];
-  float d;
-};
-
-template <int kFmt>
-__device__ __forceinline__ void q_load(const uint8_t *row, int it, QItem<kFmt> &x) {
-  if constexpr (kFmt == SAS_HEAD_Q8_0) {
-    const uint8_t *blk = row + 34 * it;
-    load_span<8>(blk + 2, x.w);
-    x.d = f16_at(blk);
-  } else if constexpr (kFmt == SAS_HEAD_Q4_0) {
-    const uint8_t *blk = row + 18 * it;
-    load_span<4>(blk + 2, x.w);
-    x.d = f16_at(blk);
-  } else {
-    const int sb = it >> 2, un = it & 3, h = un >> 1, lh = un & 1;
-    const uint8_t *blk = row + 210 * sb;
-    load_span<4>(blk + h * 64 + lh * 16, x.la);
-    load_span<4>(blk + h * 64 + 32 + lh * 16, x.lb);
-    load_span<4>(blk + 128 + h * 32 + lh * 16, x.qh);
-    load_span<4>(blk + 192, x.sc);
-    x.d = f16_at(blk + 208);
-  }
-}
-
-// Adds item `it`'s terms to acc[r] for every row (the order of the header).
+// Adds item `it` (lane g of its row's group: item g of the stage) to
+// acc[r] for every row, in the order of the header, from the stage in `rb`
+// that starts at byte `off`.
 template <int R, int kFmt>
-__device__ __forceinline__ void q_terms(const QItem<kFmt> &x, int it, const int32_t *q8, const float *d8,
-                                        const float *s8, int dim, float (&acc)[R]) {
+__device__ __forceinline__ void q_terms(const uint32_t *rb, uint32_t off, int g, int it, const int32_t *q8,
+                                        const float *d8, const float *s8, const int32_t *qs, int dim,
+                                        float (&acc)[R]) {
   typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
   const int nq = dim / 32;
   if constexpr (kFmt == SAS_HEAD_Q8_0 || kFmt == SAS_HEAD_Q4_0) {
+    constexpr int NW = kFmt == SAS_HEAD_Q8_0 ? 8 : 4;
+    const uint32_t b = off + (uint32_t)((kFmt == SAS_HEAD_Q8_0 ? 34 : 18) * g);
+    uint32_t wv[NW];
+    lds_words<NW>(rb, b + 2u, wv);
+    const float dw = lds_f16(rb, b);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const i32x4 *qa = reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * it);
@@ -426,42 +395,53 @@ __device__ __forceinline__ void q_terms(const QItem<kFmt> &x, int it, const int3
       int dot = 0;
       if constexpr (kFmt == SAS_HEAD_Q8_0) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)x.w[j], qv[j], dot, false);
-        acc[r] = acc[r] + ((float)dot * x.d) * d8[r * nq + it];
+        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)wv[j], qv[j], dot, false);
+        acc[r] = acc[r] + ((float)dot * dw) * d8[r * nq + it];
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          dot = __builtin_amdgcn_sdot4((int)(x.w[j] & 0x0F0F0F0Fu), qv[j], dot, false);
-          dot = __builtin_amdgcn_sdot4((int)((x.w[j] >> 4) & 0x0F0F0F0Fu), qv[4 + j], dot, false);
+          dot = __builtin_amdgcn_sdot4((int)(wv[j] & 0x0F0F0F0Fu), qv[j], dot, false);
+          dot = __builtin_amdgcn_sdot4((int)((wv[j] >> 4) & 0x0F0F0F0Fu), qv[4 + j], dot, false);
         }
-        acc[r] = acc[r] + (((float)dot * x.d) * d8[r * nq + it] - (8.0f * x.d) * s8[r * nq + it]);
+        acc[r] = acc[r] + (((float)dot * dw) * d8[r * nq + it] - (8.0f * dw) * s8[r * nq + it]);
       }
     }
   } else {
-    const int sb = it >> 2, un = it & 3, h = un >> 1, lh = un & 1;
-    const uint32_t s0 = h ? x.sc[2] : x.sc[0], s1 = h ? x.sc[3] : x.sc[1];  // scales h*8 .. h*8 + 7
+    // unit un = g % 4 of the stage's super-block g / 4: half h, quarter
+    // pair lh; super-block it / 4 of the row
+    const int sb = it >> 2, un = g & 3, h = un >> 1, lh = un & 1;
+    const uint32_t b = off + 210u * (uint32_t)(g >> 2);
+    uint32_t la[4], lb[4], qh[4], sc[2];
+    lds_words<4>(rb, b + (uint32_t)(h * 64 + lh * 16), la);
+    lds_words<4>(rb, b + (uint32_t)(h * 64 + 32 + lh * 16), lb);
+    lds_words<4>(rb, b + (uint32_t)(128 + h * 32 + lh * 16), qh);
+    lds_words<2>(rb, b + (uint32_t)(192 + h * 8), sc);  // scales h*8 .. h*8 + 7
+    const float dq = lds_f16(rb, b + 208u);
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
-      const uint32_t *src = (qt & 1) ? x.lb : x.la;
-      uint32_t cen[4];
+      // the 16 six-bit values q of quarter qt, one per byte (0 .. 63): the
+      // low or high nibbles of its ql span, bits 2 qt, 2 qt + 1 of qh moved
+      // to bits 4, 5.  sum (q - 32) q8 = sum q q8 - 32 sum q8, exactly.
+      const uint32_t *src = (qt & 1) ? lb : la;
+      uint32_t raw[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t nib = (qt >= 2 ? src[j] >> 4 : src[j]) & 0x0F0F0F0Fu;
-        const uint32_t hi = ((x.qh[j] >> (2 * qt)) & 0x03030303u) << 4;
-        cen[j] = center32(nib | hi);
+        const uint32_t nib = qt >= 2 ? src[j] >> 4 : src[j];
+        const uint32_t hi = qt == 3 ? qh[j] >> 2 : qh[j] << (4 - 2 * qt);
+        raw[j] = (nib & 0x0F0F0F0Fu) | (hi & 0x30303030u);
       }
-      // scale byte h*8 + lh + 2 qt: word qt >> 1 of the pair, byte lh + 2 (qt & 1)
-      const uint32_t sw = (qt >> 1) ? s1 : s0;
-      const float sc = (float)(int)(int8_t)(uint8_t)(sw >> (8u * (uint32_t)(lh + 2 * (qt & 1))));
-      const float ds = x.d * sc;
+      // scale byte h*8 + lh + 2 qt: word qt >> 1, byte lh + 2 (qt & 1)
+      const uint32_t sw = sc[qt >> 1];
+      const float scv = (float)(int)(int8_t)(uint8_t)(sw >> (8u * (uint32_t)(lh + 2 * (qt & 1))));
+      const float ds = dq * scv;
       const int qb = sb * 8 + h * 4 + qt;  // the Q8_1 block of these 16 values
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const i32x4 qa = *reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * qb + 4 * lh);
-        int dot = __builtin_amdgcn_sdot4((int)cen[0], qa.x, 0, false);
-        dot = __builtin_amdgcn_sdot4((int)cen[1], qa.y, dot, false);
-        dot = __builtin_amdgcn_sdot4((int)cen[2], qa.z, dot, false);
-        dot = __builtin_amdgcn_sdot4((int)cen[3], qa.w, dot, false);
+        int dot = __builtin_amdgcn_sdot4((int)raw[0], qa.x, -32 * qs[r * (dim / 16) + 2 * qb + lh], false);
+        dot = __builtin_amdgcn_sdot4((int)raw[1], qa.y, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)raw[2], qa.z, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)raw[3], qa.w, dot, false);
         acc[r] = acc[r] + (ds * d8[r * nq + qb]) * (float)dot;
       }
     }
@@ -474,6 +454,8 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
   extern __shared__ __attribute__((aligned(16))) float xs[];
   __shared__ LmhLds<R> S;
   __shared__ float s_logit[R][kLmhSpan];  // the part's logits, row by row
+  // GGUF: each wave's staged rows (8 rows of one stage)
+  __shared__ __attribute__((aligned(16))) uint32_t stg[kFmt == SAS_HEAD_BF16 ? 4 : kWaves * 8 * QStage<kFmt>::pitch];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int part = blockIdx.x;
   const int base = part * kLmhSpan;
@@ -563,51 +545,95 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
       }
     }
   } else {
+    using St = QStage<kFmt>;
+    constexpr int J = St::loads, D = St::depth;
     const uint8_t *W = static_cast<const uint8_t *>(L.weight);
     // items per id: blocks (Q8_0, Q4_0) or 64-value units (Q6_K); lane g
-    // takes g, g + 8, ... (a lane past the last item loads the last one and
-    // adds nothing)
+    // takes g, g + 8, ...: item g of each stage of its row
     const int items = kFmt == SAS_HEAD_Q6_K ? dim / 64 : dim / 32;
-    const int per = (items + 7) / 8;
-    const int total = (kLmhSpan / 32) * per;
-    auto row_of = [&](int m) __attribute__((always_inline)) {
-      const int id = min(base + grp + 32 * m, vocab - 1);  // loads stay inside the head
-      return W + (int64_t)id * L.weight_stride;
+    const int rowbytes = kFmt == SAS_HEAD_Q6_K ? 210 * (dim / 256) : (kFmt == SAS_HEAD_Q8_0 ? 34 : 18) * (dim / 32);
+    const int per = (items + 7) / 8;          // stages per id
+    const int total = (kLmhSpan / 32) * per;  // stages per wave: 16 per (a multiple of D)
+    static_assert((kLmhSpan / 32) % D == 0, "the ring divides the stages");
+    uint32_t *rb = stg + (wave * 8 + (lane >> 3)) * St::pitch;  // the lane's row of its wave's buffer
+    // stage t of the wave: ids base + 8 wave + 32 m + 0 .. 7 (this lane:
+    // its group's id), items 8 c .. 8 c + 7, t = m per + c
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    struct Ring {
+      u32x4 v[J];
+      uint32_t off;  // the stage's first byte in its first chunk; chunks in use << 8
     };
-    auto load_at = [&](int t, QItem<kFmt> &dst) __attribute__((always_inline)) {
-      const int m2 = t / per;
-      q_load<kFmt>(row_of(m2), min(g + 8 * (t - m2 * per), items - 1), dst);
+    Ring ring[D];
+    auto stage_load = [&](int m2, int c2, Ring &s) __attribute__((always_inline)) {
+      const int id = min(base + grp + 32 * m2, vocab - 1);  // loads stay inside the head
+      const uint8_t *p = W + (int64_t)id * L.weight_stride + St::bytes * c2;
+      const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(p) & 15u;
+      const uint32_t nch = (off + (uint32_t)min(St::bytes, rowbytes - St::bytes * c2) + 15u) >> 4;
+      const u32x4 *a = reinterpret_cast<const u32x4 *>(p - off);  // keeps the pointer's address space
+      // chunks g, g + 8, ... (past the last: the last again, so that every
+      // lane loads and no branch splits the loads in flight)
+#pragma unroll
+      for (int j = 0; j < J; ++j) s.v[j] = __builtin_nontemporal_load(a + min((uint32_t)(g + 8 * j), nch - 1u));
+      s.off = off | (nch << 8);
     };
-    QItem<kFmt> nxt, nx2;
-    load_at(0, nxt);
-    if (total > 1) load_at(1, nx2);
+    int ml = 0, cl = 0;  // the next stage to load
+    auto advance = [&](int &m2, int &c2) __attribute__((always_inline)) {
+      if (++c2 == per) {
+        c2 = 0;
+        ++m2;
+      }
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      stage_load(min(ml, kLmhSpan / 32 - 1), cl, ring[d]);
+      advance(ml, cl);
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
     int32_t *q8 = reinterpret_cast<int32_t *>(xs);
     float *d8 = reinterpret_cast<float *>(q8 + R * (dim / 4));
     float *s8 = d8 + R * (dim / 32);
-    q81_stage<R>(L, q8, d8, s8);
+    int32_t *qs = reinterpret_cast<int32_t *>(s8 + R * (dim / 32));
+    q81_stage<R>(L, q8, d8, s8, qs);
 #pragma unroll
     for (int r = 0; r < R; ++r) lmh_prefetch_ids(pre[r]);
     __syncthreads();  // the Q8_1 operand is in LDS
-    for (int m = 0; m < kLmhSpan / 32; ++m) {
-      float acc[R];
+    float acc[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-      for (int c = 0; c < per; ++c) {
-        const QItem<kFmt> cur = nxt;
-        nxt = nx2;
-        const int t2 = m * per + c + 2;
-        if (t2 < total) load_at(t2, nx2);
-        if (g + 8 * c < items) q_terms<R, kFmt>(cur, g + 8 * c, q8, d8, s8, dim, acc);
-      }
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    int m = 0, c = 0;  // the stage computed
+    for (int t0 = 0; t0 < total; t0 += D) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float v = acc[r];
-        v = v + __shfl_xor(v, 1, 64);
-        v = v + __shfl_xor(v, 2, 64);
-        v = v + __shfl_xor(v, 4, 64);
-        if (g == 0) s_logit[r][grp + 32 * m] = v;
+      for (int d = 0; d < D; ++d) {
+        // stage t0 + d: its chunks into the row's LDS copy (the wave's LDS
+        // operations run in order, so the reads below see them and the
+        // previous stage's reads came first), then the slot loads stage
+        // t0 + d + D (past the last stage: the last stage again)
+        const uint32_t off = ring[d].off & 0xFFu, nch = ring[d].off >> 8;
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          *reinterpret_cast<u32x4 *>(rb + 4 * min((uint32_t)(g + 8 * j), nch - 1u)) = ring[d].v[j];
+        __asm__ volatile("" ::: "memory");
+        const bool more = ml < kLmhSpan / 32;
+        stage_load(more ? ml : kLmhSpan / 32 - 1, more ? cl : per - 1, ring[d]);
+        advance(ml, cl);
+        const int it = 8 * c + g;
+        if (it < items) q_terms<R, kFmt>(rb, off, g, it, q8, d8, s8, qs, dim, acc);
+        if (c == per - 1) {
+          // the id's eight partial sums, in one fixed tree: lane 0 of the
+          // group holds ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float v = acc[r];
+            v = v + __shfl_xor(v, 1, 64);
+            v = v + __shfl_xor(v, 2, 64);
+            v = v + __shfl_xor(v, 4, 64);
+            if (g == 0) s_logit[r][grp + 32 * m] = v;
+            acc[r] = 0.0f;
+          }
+        }
+        advance(m, c);
       }
     }
   }
@@ -903,9 +929,10 @@ void lmh_layout(LmhArgs *a, void *scratch) {
 
 template <int R, int kFmt>
 static hipError_t launch_parts(const LmhArgs &a, hipStream_t stream) {
-  // bf16: the f32 hidden rows; GGUF: q8 (dim bytes) + d8 + s8 per row
+  // bf16: the f32 hidden rows; GGUF: q8 (dim bytes), d8, s8 and the 16-value sums per row
   const size_t lds = kFmt == SAS_HEAD_BF16 ? (size_t)R * a.dim * sizeof(float)
-                                           : (size_t)R * ((size_t)a.dim + 2 * sizeof(float) * (a.dim / 32));
+                                           : (size_t)R * ((size_t)a.dim + 2 * sizeof(float) * (a.dim / 32) +
+                                                          sizeof(int32_t) * (a.dim / 16));
   hipLaunchKernelGGL((lmh_parts_kernel<R, kFmt>), dim3((unsigned)a.s.parts), dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
