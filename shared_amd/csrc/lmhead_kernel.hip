@@ -315,20 +315,17 @@ __device__ __forceinline__ float f16_value(uint32_t bits) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 
-// N words of the staged row `rb` starting at byte x (x even): N + 1 dword
-// reads shifted by x % 4.
+// N words that start `sh` bytes (0 or 2) into u[0]: the N + 1 dwords
+// read from LDS, shifted.
 template <int N>
-__device__ __forceinline__ void lds_words(const uint32_t *rb, uint32_t x, uint32_t (&out)[N]) {
-  const uint32_t *q = rb + (x >> 2);
-  uint32_t u[N + 1];
+__device__ __forceinline__ void words_of(const uint32_t (&u)[N + 1], uint32_t sh, uint32_t (&out)[N]) {
 #pragma unroll
-  for (int i = 0; i <= N; ++i) u[i] = q[i];
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(u[i + 1], u[i], x & 3u);
+  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(u[i + 1], u[i], sh);
 }
-// the f16 at byte x of `rb` (x even)
-__device__ __forceinline__ float lds_f16(const uint32_t *rb, uint32_t x) {
-  return f16_value(rb[x >> 2] >> (8u * (x & 2u)));
+template <int N>
+__device__ __forceinline__ void lds_dwords(const uint32_t *p, uint32_t (&u)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = p[i];
 }
 
 // The Q8_1 operand of R hidden rows, in LDS: q8[r][dim / 4] (four int8 per
@@ -372,51 +369,147 @@ __device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *
   }
 }
 
-// Adds item `it` (lane g of its row's group: item g of the stage) to
-// acc[r] for every row, in the order of the header, from the stage in `rb`
-// that starts at byte `off`.
+// Where a lane's item lies in its row's staged copy: `c0` its byte offset
+// from the stage's first byte, and the LDS dword index of each field for a
+// stage that starts at dword 0 (the stage adds its own base).
+template <int kFmt>
+struct QLane {
+  uint32_t c0, row;  // Q8_0 / Q4_0: the block (its f16 d, then its values)
+};
+template <>
+struct QLane<SAS_HEAD_Q6_K> {
+  uint32_t c0, la, lb, qh, sc, d;  // Q6_K: the unit's ql spans, qh span, scales, the super-block's d
+  uint32_t lh8;                    // 8 lh: the bit offset of the unit's scales in a scale word
+};
+
+// Item g of a stage of the lane's row, whose copy starts at LDS dword `row`.
+template <int kFmt>
+__device__ __forceinline__ QLane<kFmt> q_lane(int g, uint32_t row) {
+  QLane<kFmt> ln;
+  if constexpr (kFmt == SAS_HEAD_Q6_K) {
+    // unit g % 4 (half h, quarter pair lh) of the stage's super-block g / 4
+    const uint32_t h = (uint32_t)(g & 3) >> 1, lh = (uint32_t)g & 1u;
+    ln.c0 = 210u * (uint32_t)(g >> 2);
+    ln.la = row + h * 16u + lh * 4u;        // byte h*64 + lh*16
+    ln.lb = ln.la + 8u;                     // byte h*64 + 32 + lh*16
+    ln.qh = row + 32u + h * 8u + lh * 4u;   // byte 128 + h*32 + lh*16
+    ln.sc = row + 48u + h * 2u;             // byte 192 + h*8: scales h*8 .. h*8 + 7
+    ln.d = row + 52u;                       // byte 208
+    ln.lh8 = 8u * lh;
+  } else {
+    ln.c0 = (uint32_t)((kFmt == SAS_HEAD_Q8_0 ? 34 : 18) * g);
+    ln.row = row;
+  }
+  return ln;
+}
+
+// A lane's Q8_1 operand for its item `it`, read from LDS where it is used.
+struct QOp {
+  const int32_t *q8;
+  const float *d8, *s8;
+  const int32_t *qs;
+  int dim, it;
+  // Q8_0 / Q4_0: block it's 32 values, d and the f16 of d * sum
+  __device__ __forceinline__ void block(int r, int32_t (&q)[8], float &d, float &sd) const {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const i32x4 *qa = reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * it);
+    const i32x4 a0 = qa[0], a1 = qa[1];
+    q[0] = a0.x;
+    q[1] = a0.y;
+    q[2] = a0.z;
+    q[3] = a0.w;
+    q[4] = a1.x;
+    q[5] = a1.y;
+    q[6] = a1.z;
+    q[7] = a1.w;
+    d = d8[r * (dim / 32) + it];
+    sd = s8[r * (dim / 32) + it];
+  }
+  // Q6_K: quarter qt of unit it, -32 x its sum, its Q8_1 block's d
+  __device__ __forceinline__ void quarter(int r, int qt, int32_t (&q4)[4], int32_t &zq, float &dq) const {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int lh = it & 1;
+    const int qb = (it >> 2) * 8 + ((it & 3) >> 1) * 4 + qt;  // the Q8_1 block of quarter qt
+    const i32x4 a = *reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * qb + 4 * lh);
+    q4[0] = a.x;
+    q4[1] = a.y;
+    q4[2] = a.z;
+    q4[3] = a.w;
+    zq = -32 * qs[r * (dim / 16) + 2 * qb + lh];
+    dq = d8[r * (dim / 32) + qb];
+  }
+};
+
+// The dwords of a lane's item of a stage, read from its row's copy in LDS
+// one stage ahead of their use (so that the LDS round trip overlaps the
+// previous stage's arithmetic).
+template <int kFmt>
+struct QRaw {
+  uint32_t w[kFmt == SAS_HEAD_Q8_0 ? 9 : 5];  // Q8_0 / Q4_0: the values' dwords
+  uint32_t d;                                // the dword of the f16 d
+  uint32_t x0;                               // the item's first byte in the copy
+};
+template <>
+struct QRaw<SAS_HEAD_Q6_K> {
+  uint32_t la[5], lb[5], qh[5], sc[3], d;
+  uint32_t x0;
+};
+
+template <int kFmt>
+__device__ __forceinline__ void q_fetch(const uint32_t *stg, const QLane<kFmt> &ln, uint32_t off, QRaw<kFmt> &x) {
+  const uint32_t x0 = off + ln.c0;  // the item's first byte (even)
+  x.x0 = x0;
+  if constexpr (kFmt == SAS_HEAD_Q8_0 || kFmt == SAS_HEAD_Q4_0) {
+    lds_dwords(stg + ln.row + ((x0 + 2u) >> 2), x.w);
+    x.d = stg[ln.row + (x0 >> 2)];
+  } else {
+    // every field of the unit starts a multiple of 4 bytes after x0: one
+    // dword base and one shift for all
+    const uint32_t bdw = x0 >> 2;
+    lds_dwords(stg + ln.la + bdw, x.la);
+    lds_dwords(stg + ln.lb + bdw, x.lb);
+    lds_dwords(stg + ln.qh + bdw, x.qh);
+    lds_dwords(stg + ln.sc + bdw, x.sc);
+    x.d = stg[ln.d + bdw];
+  }
+}
+
+// Adds the lane's item (fetched by q_fetch) to acc[r] for every row, in the
+// order of the header.
 template <int R, int kFmt>
-__device__ __forceinline__ void q_terms(const uint32_t *rb, uint32_t off, int g, int it, const int32_t *q8,
-                                        const float *d8, const float *s8, const int32_t *qs, int dim,
-                                        float (&acc)[R]) {
-  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-  const int nq = dim / 32;
+__device__ __forceinline__ void q_terms(const QRaw<kFmt> &x, const QLane<kFmt> &ln, const QOp &op, float (&acc)[R]) {
   if constexpr (kFmt == SAS_HEAD_Q8_0 || kFmt == SAS_HEAD_Q4_0) {
     constexpr int NW = kFmt == SAS_HEAD_Q8_0 ? 8 : 4;
-    const uint32_t b = off + (uint32_t)((kFmt == SAS_HEAD_Q8_0 ? 34 : 18) * g);
     uint32_t wv[NW];
-    lds_words<NW>(rb, b + 2u, wv);
-    const float dw = lds_f16(rb, b);
+    words_of<NW>(x.w, (x.x0 + 2u) & 3u, wv);
+    const float dw = f16_value(x.d >> (8u * (x.x0 & 2u)));
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const i32x4 *qa = reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * it);
-      const i32x4 a0 = qa[0], a1 = qa[1];
-      const int32_t qv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      int32_t q[8];
+      float d8b, s8b;
+      op.block(r, q, d8b, s8b);
       int dot = 0;
       if constexpr (kFmt == SAS_HEAD_Q8_0) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)wv[j], qv[j], dot, false);
-        acc[r] = acc[r] + ((float)dot * dw) * d8[r * nq + it];
+        for (int j = 0; j < 8; ++j) dot = __builtin_amdgcn_sdot4((int)wv[j], q[j], dot, false);
+        acc[r] = acc[r] + ((float)dot * dw) * d8b;
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          dot = __builtin_amdgcn_sdot4((int)(wv[j] & 0x0F0F0F0Fu), qv[j], dot, false);
-          dot = __builtin_amdgcn_sdot4((int)((wv[j] >> 4) & 0x0F0F0F0Fu), qv[4 + j], dot, false);
+          dot = __builtin_amdgcn_sdot4((int)(wv[j] & 0x0F0F0F0Fu), q[j], dot, false);
+          dot = __builtin_amdgcn_sdot4((int)((wv[j] >> 4) & 0x0F0F0F0Fu), q[4 + j], dot, false);
         }
-        acc[r] = acc[r] + (((float)dot * dw) * d8[r * nq + it] - (8.0f * dw) * s8[r * nq + it]);
+        acc[r] = acc[r] + (((float)dot * dw) * d8b - (8.0f * dw) * s8b);
       }
     }
   } else {
-    // unit un = g % 4 of the stage's super-block g / 4: half h, quarter
-    // pair lh; super-block it / 4 of the row
-    const int sb = it >> 2, un = g & 3, h = un >> 1, lh = un & 1;
-    const uint32_t b = off + 210u * (uint32_t)(g >> 2);
+    const uint32_t sh = x.x0 & 3u;
     uint32_t la[4], lb[4], qh[4], sc[2];
-    lds_words<4>(rb, b + (uint32_t)(h * 64 + lh * 16), la);
-    lds_words<4>(rb, b + (uint32_t)(h * 64 + 32 + lh * 16), lb);
-    lds_words<4>(rb, b + (uint32_t)(128 + h * 32 + lh * 16), qh);
-    lds_words<2>(rb, b + (uint32_t)(192 + h * 8), sc);  // scales h*8 .. h*8 + 7
-    const float dq = lds_f16(rb, b + 208u);
+    words_of<4>(x.la, sh, la);
+    words_of<4>(x.lb, sh, lb);
+    words_of<4>(x.qh, sh, qh);
+    words_of<2>(x.sc, sh, sc);  // scales h*8 .. h*8 + 7
+    const float dq = f16_value(x.d >> (8u * sh));
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
       // the 16 six-bit values q of quarter qt, one per byte (0 .. 63): the
@@ -432,17 +525,18 @@ __device__ __forceinline__ void q_terms(const uint32_t *rb, uint32_t off, int g,
       }
       // scale byte h*8 + lh + 2 qt: word qt >> 1, byte lh + 2 (qt & 1)
       const uint32_t sw = sc[qt >> 1];
-      const float scv = (float)(int)(int8_t)(uint8_t)(sw >> (8u * (uint32_t)(lh + 2 * (qt & 1))));
+      const float scv = (float)(int)(int8_t)(uint8_t)(sw >> (ln.lh8 + 16u * (uint32_t)(qt & 1)));
       const float ds = dq * scv;
-      const int qb = sb * 8 + h * 4 + qt;  // the Q8_1 block of these 16 values
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const i32x4 qa = *reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * qb + 4 * lh);
-        int dot = __builtin_amdgcn_sdot4((int)raw[0], qa.x, -32 * qs[r * (dim / 16) + 2 * qb + lh], false);
-        dot = __builtin_amdgcn_sdot4((int)raw[1], qa.y, dot, false);
-        dot = __builtin_amdgcn_sdot4((int)raw[2], qa.z, dot, false);
-        dot = __builtin_amdgcn_sdot4((int)raw[3], qa.w, dot, false);
-        acc[r] = acc[r] + (ds * d8[r * nq + qb]) * (float)dot;
+        int32_t q4[4], zq;
+        float d8q;
+        op.quarter(r, qt, q4, zq, d8q);
+        int dot = __builtin_amdgcn_sdot4((int)raw[0], q4[0], zq, false);
+        dot = __builtin_amdgcn_sdot4((int)raw[1], q4[1], dot, false);
+        dot = __builtin_amdgcn_sdot4((int)raw[2], q4[2], dot, false);
+        dot = __builtin_amdgcn_sdot4((int)raw[3], q4[3], dot, false);
+        acc[r] = acc[r] + (ds * d8q) * (float)dot;
       }
     }
   }
@@ -546,25 +640,27 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
     }
   } else {
     using St = QStage<kFmt>;
-    constexpr int J = St::loads, D = St::depth;
+    constexpr int J = St::loads, D = St::depth, NM = kLmhSpan / 32;
+    static_assert(NM % D == 0, "the ring divides a pass over the wave's batches");
     const uint8_t *W = static_cast<const uint8_t *>(L.weight);
     // items per id: blocks (Q8_0, Q4_0) or 64-value units (Q6_K); lane g
     // takes g, g + 8, ...: item g of each stage of its row
     const int items = kFmt == SAS_HEAD_Q6_K ? dim / 64 : dim / 32;
     const int rowbytes = kFmt == SAS_HEAD_Q6_K ? 210 * (dim / 256) : (kFmt == SAS_HEAD_Q8_0 ? 34 : 18) * (dim / 32);
-    const int per = (items + 7) / 8;          // stages per id
-    const int total = (kLmhSpan / 32) * per;  // stages per wave: 16 per (a multiple of D)
-    static_assert((kLmhSpan / 32) % D == 0, "the ring divides the stages");
-    uint32_t *rb = stg + (wave * 8 + (lane >> 3)) * St::pitch;  // the lane's row of its wave's buffer
-    // stage t of the wave: ids base + 8 wave + 32 m + 0 .. 7 (this lane:
-    // its group's id), items 8 c .. 8 c + 7, t = m per + c
+    const int per = (items + 7) / 8;  // stages per id
+    // Stage (m, c) of the wave: items 8 c .. 8 c + 7 of ids base + 8 wave +
+    // 32 m + 0 .. 7 (this lane: its group's id), m outer, c inner: a row's
+    // stages follow one another, so the line two stages share comes from
+    // L2 the second time.  The loads are plain (cached) loads for that.
+    const uint32_t rbi = (uint32_t)((wave * 8 + (lane >> 3)) * St::pitch);  // the lane's row copy in stg
+    const QLane<kFmt> ln = q_lane<kFmt>(g, rbi);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     struct Ring {
       u32x4 v[J];
       uint32_t off;  // the stage's first byte in its first chunk; chunks in use << 8
     };
     Ring ring[D];
-    auto stage_load = [&](int m2, int c2, Ring &s) __attribute__((always_inline)) {
+    auto stage_load = [&](int c2, int m2, Ring &s) __attribute__((always_inline)) {
       const int id = min(base + grp + 32 * m2, vocab - 1);  // loads stay inside the head
       const uint8_t *p = W + (int64_t)id * L.weight_stride + St::bytes * c2;
       const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(p) & 15u;
@@ -573,20 +669,37 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
       // chunks g, g + 8, ... (past the last: the last again, so that every
       // lane loads and no branch splits the loads in flight)
 #pragma unroll
-      for (int j = 0; j < J; ++j) s.v[j] = __builtin_nontemporal_load(a + min((uint32_t)(g + 8 * j), nch - 1u));
+      for (int j = 0; j < J; ++j) s.v[j] = a[min((uint32_t)(g + 8 * j), nch - 1u)];
       s.off = off | (nch << 8);
     };
-    int ml = 0, cl = 0;  // the next stage to load
-    auto advance = [&](int &m2, int &c2) __attribute__((always_inline)) {
-      if (++c2 == per) {
-        c2 = 0;
-        ++m2;
+    int cl = 0, ml = 0;  // the next stage to load
+    auto advance = [&]() __attribute__((always_inline)) {
+      if (++cl == per) {
+        cl = 0;
+        ++ml;
       }
+    };
+    // the chunks of the stage in slot rs into the row's copy (the wave's LDS
+    // operations run in order, so the reads that follow see them and the
+    // previous stage's reads came first), then the slot loads the stage D
+    // ahead (past the last stage: the last stage again); returns the
+    // stage's offset
+    auto stage_take = [&](Ring &rs) __attribute__((always_inline)) {
+      const uint32_t off = rs.off & 0xFFu, nch = rs.off >> 8;
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        *reinterpret_cast<u32x4 *>(stg + rbi + 4u * min((uint32_t)(g + 8 * j), nch - 1u)) = rs.v[j];
+      __asm__ volatile("" ::: "memory");
+      const bool more = ml < NM;
+      stage_load(more ? cl : per - 1, more ? ml : NM - 1, rs);
+      advance();
+      return off;
     };
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      stage_load(min(ml, kLmhSpan / 32 - 1), cl, ring[d]);
-      advance(ml, cl);
+      stage_load(cl, ml, ring[d]);  // D <= NM stages: all exist
+      advance();
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
@@ -598,42 +711,43 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
 #pragma unroll
     for (int r = 0; r < R; ++r) lmh_prefetch_ids(pre[r]);
     __syncthreads();  // the Q8_1 operand is in LDS
+    // an id's eight partial sums, in one fixed tree: lane 0 of the group
+    // holds ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
+    auto id_done = [&](float (&a)[R], int m2) __attribute__((always_inline)) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float v = a[r];
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        if (g == 0) s_logit[r][grp + 32 * m2] = v;
+      }
+    };
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     int m = 0, c = 0;  // the stage computed
-    for (int t0 = 0; t0 < total; t0 += D) {
+    // the fields of stage t + 1 are read while stage t is computed (after
+    // the last stage: the last stage's copy again, unused)
+    QRaw<kFmt> cur;
+    q_fetch<kFmt>(stg, ln, stage_take(ring[0]), cur);
+    for (int t0 = 0; t0 < NM * per; t0 += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        // stage t0 + d: its chunks into the row's LDS copy (the wave's LDS
-        // operations run in order, so the reads below see them and the
-        // previous stage's reads came first), then the slot loads stage
-        // t0 + d + D (past the last stage: the last stage again)
-        const uint32_t off = ring[d].off & 0xFFu, nch = ring[d].off >> 8;
-        __asm__ volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-          *reinterpret_cast<u32x4 *>(rb + 4 * min((uint32_t)(g + 8 * j), nch - 1u)) = ring[d].v[j];
-        __asm__ volatile("" ::: "memory");
-        const bool more = ml < kLmhSpan / 32;
-        stage_load(more ? ml : kLmhSpan / 32 - 1, more ? cl : per - 1, ring[d]);
-        advance(ml, cl);
+        QRaw<kFmt> nxt;
+        q_fetch<kFmt>(stg, ln, stage_take(ring[(d + 1) % D]), nxt);
         const int it = 8 * c + g;
-        if (it < items) q_terms<R, kFmt>(rb, off, g, it, q8, d8, s8, qs, dim, acc);
+        if (it < items) q_terms<R, kFmt>(cur, ln, QOp{q8, d8, s8, qs, dim, it}, acc);
+        cur = nxt;
         if (c == per - 1) {
-          // the id's eight partial sums, in one fixed tree: lane 0 of the
-          // group holds ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7))
+          id_done(acc, m);
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            float v = acc[r];
-            v = v + __shfl_xor(v, 1, 64);
-            v = v + __shfl_xor(v, 2, 64);
-            v = v + __shfl_xor(v, 4, 64);
-            if (g == 0) s_logit[r][grp + 32 * m] = v;
-            acc[r] = 0.0f;
-          }
+          for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+          c = 0;
+          ++m;
+        } else {
+          ++c;
         }
-        advance(m, c);
       }
     }
   }

@@ -207,9 +207,14 @@ def test_gemma_shape_q8_0_q4_0(sampler, fmt):
 
 @pytest.mark.parametrize("fmt,vocab,dim,rows", [(W.HEAD_Q6_K, 300, 256, 2), (W.HEAD_Q6_K, 4097, 768, 4),
                                                 (W.HEAD_Q6_K, 20000, 1280, 3), (W.HEAD_Q8_0, 777, 256, 4),
-                                                (W.HEAD_Q4_0, 5000, 512, 2), (W.HEAD_Q8_0, 1, 256, 1)])
+                                                (W.HEAD_Q4_0, 5000, 512, 2), (W.HEAD_Q8_0, 1, 256, 1),
+                                                (W.HEAD_Q6_K, 6000, 2304, 1), (W.HEAD_Q6_K, 5000, 2304, 2),
+                                                (W.HEAD_Q8_0, 2000, 1280, 3), (W.HEAD_Q4_0, 3000, 768, 3),
+                                                (W.HEAD_Q4_0, 999, 256, 4), (W.HEAD_Q8_0, 333, 2560, 2)])
 def test_gguf_shapes(sampler, fmt, vocab, dim, rows):
-    # dims of 256 and 768 leave lanes with fewer Q6_K units than others
+    # dims of 256, 768 and 2304 leave lanes with fewer Q6_K units than
+    # others; at 2304 a row is 9 super-blocks (1,890 bytes), so consecutive
+    # rows alternate between 4-byte and 2-byte alignment
     check(sampler, W.lmhq(fmt, rows=rows, vocab=vocab, dim=dim, seed=vocab + dim + fmt, hist=min(300, vocab)),
           f"{W.HEAD_NAMES[fmt]} {rows}x{vocab}x{dim}")
 
