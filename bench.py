@@ -81,6 +81,9 @@ def parse_args():
                     help="time sasp_masked_read (libsas_probe.so): C3's logits read whole or only where the "
                          "grammar mask allows an id")
     ap.add_argument("--mask-probe-mode", type=int, default=-1, help="with --mask-probe: one mode only")
+    ap.add_argument("--memset-order-probe", action="store_true",
+                    help="sasp_memset_order (libsas_probe.so): whether a kernel on a non-blocking stream "
+                         "launched right after hipMemset sees the fill")
     ap.add_argument("--calibrate-copy-mb", type=float, default=0.0,
                     help="instead of the benchmark, run device-to-device copies of this many MB (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -118,7 +121,31 @@ def _probe_lib():
     lib.sasp_read.argtypes = [c_void_p, c_size_t, c_int32, c_void_p, c_void_p]
     lib.sasp_masked_read.restype = c_int
     lib.sasp_masked_read.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]
+    lib.sasp_memset_order.restype = c_int
+    lib.sasp_memset_order.argtypes = [c_size_t, c_int32, c_void_p]
     return lib
+
+
+def memset_order_probe(args) -> int:
+    """Whether hipMemset (the null stream) is ordered before a kernel that a
+    non-blocking stream runs right after it: sasp_memset_order over a 256 MB
+    buffer, 20 runs.  Prints one JSON line."""
+    import ctypes
+
+    class Res(ctypes.Structure):
+        _fields_ = [("reps", ctypes.c_int32), ("stale_runs", ctypes.c_int32), ("host_us", ctypes.c_double),
+                    ("fill_us", ctypes.c_double)]
+
+    lib = _probe_lib()
+    r = Res()
+    rc = lib.sasp_memset_order(256 << 20, 20, ctypes.byref(r))
+    if rc != 0:
+        raise RuntimeError(f"sasp_memset_order failed ({rc})")
+    print(json.dumps({"probe": "hipMemset then a kernel on a non-blocking stream (sasp_memset_order)",
+                      "bytes": 256 << 20, "runs": r.reps, "runs_reading_unfilled_words": r.stale_runs,
+                      "hipMemset_host_us": round(r.host_us, 2), "fill_us_on_a_stream": round(r.fill_us, 2)}),
+          flush=True)
+    return 0
 
 
 def _probe_time(args, stream, launch) -> float:
@@ -538,6 +565,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy_mb, min(args.steps, 50))
     if args.stream_probe:
         return stream_probe(args)
+    if args.memset_order_probe:
+        return memset_order_probe(args)
     if args.mask_probe:
         return mask_probe(args)
     if args.workload == "C5":

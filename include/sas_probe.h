@@ -36,6 +36,19 @@ int sasp_read(const void *src, size_t bytes, int32_t blocks, float *sink, void *
 int sasp_masked_read(const float *logits, const uint32_t *mask, int32_t rows, int32_t vocab, int32_t mode,
                      float *sink, void *stream);
 
+/* Whether hipMemset, which runs on the null stream, is ordered before a
+ * kernel launched right after it on a non-blocking stream: `reps` times, a
+ * buffer of `bytes` filled with 0xFF (finished), then hipMemset to 0 and at
+ * once a kernel on a non-blocking stream that reads 128 of its words.
+ * Allocates its own buffers and stream. */
+typedef struct sasp_memset_result {
+  int32_t reps;
+  int32_t stale_runs; /* runs whose kernel read a word the fill had not reached */
+  double host_us;     /* average host time of the hipMemset call */
+  double fill_us;     /* the same fill, timed on a stream with events */
+} sasp_memset_result;
+int sasp_memset_order(size_t bytes, int32_t reps, sasp_memset_result *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,9 +1,14 @@
 // probe_kernel.hip - measurement probes (libsas_probe.so), never loaded by
 // the sampling library.  They time the HBM stream the sampling kernels
 // read: the plain read, and reads that skip the logits a grammar mask
-// disallows at 16-, 32-, 64- and 128-byte granularity.
+// disallows at 16-, 32-, 64- and 128-byte granularity.  One more checks a
+// property of the HIP runtime that a kernel design relied on: whether
+// hipMemset (the null stream) is ordered before work on a non-blocking
+// stream.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <chrono>
 
 #include "sas_probe.h"
 
@@ -70,6 +75,13 @@ __global__ __launch_bounds__(kThreads) void masked_kernel(const float *logits, c
   if (__float_as_uint(m) == 0x7FBADBADu) sink[blockIdx.x & 255] = m;
 }
 
+// Reads 128 words of b (n words): the last 64 and 64 spread over it.
+__global__ void peek_kernel(const uint32_t *b, size_t n, uint32_t *out) {
+  const int t = threadIdx.x;
+  if (t < 64) out[t] = b[n - 1 - t];
+  else if (t < 128) out[t] = b[(size_t)(t - 64) * (n / 64)];
+}
+
 template <int kMode>
 void launch_masked(const float *logits, const uint32_t *mask, int rows, int vocab, float *sink, hipStream_t st) {
   hipLaunchKernelGGL(masked_kernel<kMode>, dim3((unsigned)(rows * (vocab / kSpan))), dim3(kThreads), 0, st, logits,
@@ -103,6 +115,60 @@ int sasp_masked_read(const float *logits, const uint32_t *mask, int32_t rows, in
     default: return -1;
   }
   return (int)hipGetLastError();
+}
+
+int sasp_memset_order(size_t bytes, int32_t reps, sasp_memset_result *out) {
+  if (!out || reps < 1 || bytes < 4096 || bytes % 4) return -1;
+  const size_t n = bytes / 4;
+  uint32_t *b = nullptr, *peek = nullptr;
+  hipStream_t s = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e = hipMalloc(&b, bytes);
+  if (e == hipSuccess) e = hipMalloc(&peek, 128 * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  out->reps = reps;
+  out->stale_runs = 0;
+  out->host_us = 0.0;
+  // the first hipMemset of a process also initializes the runtime's fill
+  // path: one untimed call first
+  if (e == hipSuccess) e = hipMemset(b, 0, bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  for (int r = 0; e == hipSuccess && r < reps; ++r) {
+    // every word 0xFFFFFFFF, finished; then hipMemset to 0 and, at once, a
+    // kernel on the non-blocking stream that reads 128 of the words
+    e = hipMemsetAsync(b, 0xFF, bytes, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) break;
+    const auto t0 = std::chrono::steady_clock::now();
+    e = hipMemset(b, 0, bytes);
+    const auto t1 = std::chrono::steady_clock::now();
+    if (e != hipSuccess) break;
+    hipLaunchKernelGGL(peek_kernel, dim3(1), dim3(128), 0, s, b, n, peek);
+    if ((e = hipGetLastError()) != hipSuccess) break;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) break;
+    uint32_t h[128];
+    if ((e = hipMemcpy(h, peek, sizeof h, hipMemcpyDeviceToHost)) != hipSuccess) break;
+    int stale = 0;
+    for (int i = 0; i < 128; ++i) stale += h[i] != 0u;
+    out->stale_runs += stale > 0;
+    out->host_us += std::chrono::duration<double, std::micro>(t1 - t0).count() / reps;
+  }
+  // the same fill timed on a stream
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventRecord(e0, s);
+  if (e == hipSuccess) e = hipMemsetAsync(b, 0, bytes, s);
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  out->fill_us = 1000.0 * ms;
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (s) (void)hipStreamDestroy(s);
+  if (peek) (void)hipFree(peek);
+  if (b) (void)hipFree(b);
+  return (int)e;
 }
 
 }  // extern "C"
