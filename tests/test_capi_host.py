@@ -32,7 +32,7 @@ def test_probe_library_exports_its_header():
         pytest.skip("libsas_probe.so is not built")
     text = open(os.path.join(root, "include", "sas_probe.h")).read()
     names = sorted(set(re.findall(r"^int\s+(sasp_[a-z_0-9]+)\s*\(", text, flags=re.M)))
-    assert names == ["sasp_masked_read", "sasp_read"]
+    assert names == ["sasp_masked_read", "sasp_memset_order", "sasp_read"]
     lib = ctypes.CDLL(path)
     for name in names:
         assert hasattr(lib, name), name
