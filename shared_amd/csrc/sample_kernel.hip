@@ -76,7 +76,11 @@ __device__ __forceinline__ bool before(double va, uint32_t ia, double vb, uint32
 // each wave's lane maxima, ranks the records at or above the bound exactly
 // by (value desc, id asc) and runs the reference's sample() tail.
 
-constexpr int kMR = 16;           // plain record slots per thread loaded before the counts are known
+// The merge kernel loads kMR plain record slots per thread before the
+// counts are known (G threads per part: the part's first kMR * G slots); a
+// part's records past them are loaded where they are used.  launch_merge
+// picks kMR from the expected count per part (about 2 k plus a few).
+constexpr int kMRMax = 16;
 constexpr int kSurvCap = 512;     // survivors the merge ranks
 constexpr uint32_t kInexact = 0x80000000u;  // composite bit: the exact value lies above the key
 
@@ -348,8 +352,10 @@ __device__ __forceinline__ uint4 load_rec4(const uint4 *p) {
 }
 
 // Merge of row `row`: one block.
+template <int kMR>
 __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int row, const sas_params &p,
                                           uint32_t *s_hist, uint32_t *s_sel) {
+  static_assert(kMR >= 1 && kMR <= kMRMax, "record slots per thread");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int P = a.parts;
   const bool greedy = !(p.temperature > 0.0);
@@ -696,6 +702,7 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
 // visible).  Block b takes the row whose parts ran on its XCD (the parts
 // kernel gives each XCD a contiguous run of rows), so the records come from
 // that XCD's L2.
+template <int kMR>
 __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs a) {
   __shared__ MergeLds ml;
   __shared__ uint32_t s_hist[256];
@@ -726,7 +733,7 @@ __global__ __launch_bounds__(kThreads) void sample_merge_kernel(const SampleArgs
   }
   sas_params p = a.params;
   if (a.row_params) p = load_row_params(a.row_params + (a.group > 1 ? row / a.group : row));
-  merge_row(a, ml, row, p, s_hist, s_sel);
+  merge_row<kMR>(a, ml, row, p, s_hist, s_sel);
 }
 
 // The exact-match cascade (kernels.js:328-339): a = 1, next = pick[0];
@@ -1479,8 +1486,27 @@ hipError_t launch_sample(const SampleArgs &a, bool softcap, hipStream_t stream) 
   return launch_merge(a, stream);
 }
 
+// Record slots per thread for the merge: a part emits about k to 2 k
+// records (its bound certifies k of its own values; ties and the bound's
+// slack add more), so the first 2 k + 8 slots hold nearly every part's
+// records.  Per-row parameters are unknown here: the most slots.
+int merge_slots(const SampleArgs &a) {
+  if (a.row_params) return kMRMax;
+  const bool greedy = !(a.params.temperature > 0.0);
+  const int k = greedy ? 1 : std::min(std::max(a.params.top_k, 1), SAS_MAX_TOP_K);
+  const int G = kThreads / std::max(a.parts, 1);
+  const int want = (2 * k + 8 + G - 1) / G;
+  return want <= 4 ? 4 : want <= 8 ? 8 : kMRMax;
+}
+
 hipError_t launch_merge(const SampleArgs &a, hipStream_t stream) {
-  hipLaunchKernelGGL(sample_merge_kernel, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+  switch (merge_slots(a)) {
+    case 4: hipLaunchKernelGGL(sample_merge_kernel<4>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(sample_merge_kernel<8>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a); break;
+    default:
+      hipLaunchKernelGGL(sample_merge_kernel<kMRMax>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a);
+      break;
+  }
   return hipGetLastError();
 }
 
