@@ -295,6 +295,10 @@ int lm_head_on(sas_sampler *s, const sas_lm_head *h, const sas_rows *r, const sa
       return fail(s, SAS_ERR_INVALID,
                   w + ": weight_stride must be >= the row's " + std::to_string(rb) +
                       " bytes and a multiple of 4 (Q8_0, Q4_0) or 2 (Q6_K)");
+    // the kernels address a GGUF head by 32-bit byte offsets (whole 16-byte
+    // chunks: up to 15 bytes past the last row)
+    if ((int64_t)(r->vocab - 1) * h->weight_stride + rb + 16 > (int64_t)UINT32_MAX)
+      return fail(s, SAS_ERR_INVALID, w + ": a GGUF head must span less than 4 GiB");
   }
   if (reinterpret_cast<uintptr_t>(h->weight) % 16 != 0)
     return fail(s, SAS_ERR_INVALID, w + ": weight must be 16-byte aligned");

@@ -328,14 +328,28 @@ __device__ __forceinline__ void lds_dwords(const uint32_t *p, uint32_t (&u)[N]) 
   for (int i = 0; i < N; ++i) u[i] = p[i];
 }
 
-// The Q8_1 operand of R hidden rows, in LDS: q8[r][dim / 4] (four int8 per
-// word), d8[r][dim / 32], s8[r][dim / 32], and qs[r][dim / 16] the sum of each
-// 16 values' q.  One 32-value block per thread per round (q8.js:27-42):
-// amax, d = amax / 127, q = round-half-even(x * (1 / d)), the f16 d and
-// d * sum(q).
-template <int R>
-__device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *d8, float *s8, int32_t *qs) {
-  const int dim = L.dim, nq = dim / 32;
+// The Q8_1 operand of R hidden rows, in LDS, packed per item so that a
+// lane reads its item's operand from one base address in whole 16-byte
+// loads: kQOpWords dwords per item, rows one after another.
+//   Q8_0 / Q4_0, per 32-value block: q (8 words, four int8 each), d8, s8
+//     (the f16 d and d * sum(q), as f32), 2 words of padding;
+//   Q6_K, per 64-value unit u (super-block u / 4, half h = (u / 2) % 2,
+//     16-value half lh = u % 2): for its quarters qt = 0 .. 3 (the Q8_1
+//     block 8 (u / 4) + 4 h + qt, its half lh): the 16 q (4 words each,
+//     quarter after quarter), then -32 x each quarter's sum of q, then each
+//     quarter's d8.
+// One 32-value block per thread per round (q8.js:27-42): amax,
+// d = amax / 127, q = round-half-even(x * (1 / d)), the f16 d and d * sum(q).
+template <int kFmt>
+constexpr int kQOpWords = kFmt == SAS_HEAD_Q6_K ? 24 : 12;
+template <int kFmt>
+__host__ __device__ constexpr int q_items(int dim) {
+  return kFmt == SAS_HEAD_Q6_K ? dim / 64 : dim / 32;
+}
+
+template <int R, int kFmt>
+__device__ __forceinline__ void q81_stage(const LmhArgs &L, uint32_t *U) {
+  const int dim = L.dim, nq = dim / 32, rw = q_items<kFmt>(dim) * kQOpWords<kFmt>;
   for (int t = threadIdx.x; t < R * nq; t += kThreads) {
     const int r = t / nq, b = t - r * nq;
     const float *h = L.hidden + (int64_t)r * L.hidden_stride + 32 * b;
@@ -347,25 +361,41 @@ __device__ __forceinline__ void q81_stage(const LmhArgs &L, int32_t *q8, float *
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
     const float d = amax / 127.0f;
     const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w[8];
     int sum = 0, half = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      uint32_t w = 0u;
+      uint32_t x = 0u;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x = v[4 * j + i] * inv;
-        const float rq = x != x ? 0.0f : fminf(fmaxf(rintf(x), -128.0f), 127.0f);
+        const float xs = v[4 * j + i] * inv;
+        const float rq = xs != xs ? 0.0f : fminf(fmaxf(rintf(xs), -128.0f), 127.0f);
         const int qi = (int)rq;
         sum += qi;
-        w |= ((uint32_t)qi & 0xFFu) << (8 * i);
+        x |= ((uint32_t)qi & 0xFFu) << (8 * i);
       }
-      q8[r * (dim / 4) + 8 * b + j] = (int32_t)w;
+      w[j] = x;
       if (j == 3) half = sum;
     }
-    qs[r * (dim / 16) + 2 * b] = half;
-    qs[r * (dim / 16) + 2 * b + 1] = sum - half;
-    d8[r * nq + b] = (float)(_Float16)d;
-    s8[r * nq + b] = (float)(_Float16)(d * (float)sum);
+    const float d16 = (float)(_Float16)d;
+    uint32_t *ur = U + r * rw;
+    if constexpr (kFmt == SAS_HEAD_Q6_K) {
+      const int sb = b >> 3, hh = (b >> 2) & 1, qt = b & 3;
+#pragma unroll
+      for (int lh = 0; lh < 2; ++lh) {
+        uint32_t *o = ur + (sb * 4 + hh * 2 + lh) * 24;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[4 * qt + j] = w[4 * lh + j];
+        o[16 + qt] = (uint32_t)(-32 * (lh ? sum - half : half));
+        o[20 + qt] = __float_as_uint(d16);
+      }
+    } else {
+      uint32_t *o = ur + b * 12;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = w[j];
+      o[8] = __float_as_uint(d16);
+      o[9] = __float_as_uint((float)(_Float16)(d * (float)sum));
+    }
   }
 }
 
@@ -403,40 +433,38 @@ __device__ __forceinline__ QLane<kFmt> q_lane(int g, uint32_t row) {
   return ln;
 }
 
-// A lane's Q8_1 operand for its item `it`, read from LDS where it is used.
+// A lane's Q8_1 operand for its item, read from LDS where it is used: `u`
+// the item's words for row 0, `rw` words between rows.
 struct QOp {
-  const int32_t *q8;
-  const float *d8, *s8;
-  const int32_t *qs;
-  int dim, it;
-  // Q8_0 / Q4_0: block it's 32 values, d and the f16 of d * sum
+  const uint32_t *u;
+  int rw;
+  // Q8_0 / Q4_0: the block's 32 values, d and the f16 of d * sum
   __device__ __forceinline__ void block(int r, int32_t (&q)[8], float &d, float &sd) const {
-    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-    const i32x4 *qa = reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * it);
-    const i32x4 a0 = qa[0], a1 = qa[1];
-    q[0] = a0.x;
-    q[1] = a0.y;
-    q[2] = a0.z;
-    q[3] = a0.w;
-    q[4] = a1.x;
-    q[5] = a1.y;
-    q[6] = a1.z;
-    q[7] = a1.w;
-    d = d8[r * (dim / 32) + it];
-    sd = s8[r * (dim / 32) + it];
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(u + r * rw);
+    const u32x4 a0 = p[0], a1 = p[1], a2 = p[2];
+    q[0] = (int32_t)a0.x;
+    q[1] = (int32_t)a0.y;
+    q[2] = (int32_t)a0.z;
+    q[3] = (int32_t)a0.w;
+    q[4] = (int32_t)a1.x;
+    q[5] = (int32_t)a1.y;
+    q[6] = (int32_t)a1.z;
+    q[7] = (int32_t)a1.w;
+    d = __uint_as_float(a2.x);
+    sd = __uint_as_float(a2.y);
   }
-  // Q6_K: quarter qt of unit it, -32 x its sum, its Q8_1 block's d
+  // Q6_K: quarter qt of the unit, -32 x its sum, its Q8_1 block's d
   __device__ __forceinline__ void quarter(int r, int qt, int32_t (&q4)[4], int32_t &zq, float &dq) const {
-    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-    const int lh = it & 1;
-    const int qb = (it >> 2) * 8 + ((it & 3) >> 1) * 4 + qt;  // the Q8_1 block of quarter qt
-    const i32x4 a = *reinterpret_cast<const i32x4 *>(q8 + r * (dim / 4) + 8 * qb + 4 * lh);
-    q4[0] = a.x;
-    q4[1] = a.y;
-    q4[2] = a.z;
-    q4[3] = a.w;
-    zq = -32 * qs[r * (dim / 16) + 2 * qb + lh];
-    dq = d8[r * (dim / 32) + qb];
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const uint32_t *b = u + r * rw;
+    const u32x4 a = reinterpret_cast<const u32x4 *>(b)[qt];
+    q4[0] = (int32_t)a.x;
+    q4[1] = (int32_t)a.y;
+    q4[2] = (int32_t)a.z;
+    q4[3] = (int32_t)a.w;
+    zq = (int32_t)b[16 + qt];
+    dq = __uint_as_float(b[20 + qt]);
   }
 };
 
@@ -660,16 +688,20 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
       uint32_t off;  // the stage's first byte in its first chunk; chunks in use << 8
     };
     Ring ring[D];
+    // byte offsets into the head are 32-bit (the host checks that it spans
+    // less than 4 GiB); the head is 16-byte aligned
+    const uint32_t wstride = (uint32_t)L.weight_stride;
     auto stage_load = [&](int c2, int m2, Ring &s) __attribute__((always_inline)) {
-      const int id = min(base + grp + 32 * m2, vocab - 1);  // loads stay inside the head
-      const uint8_t *p = W + (int64_t)id * L.weight_stride + St::bytes * c2;
-      const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(p) & 15u;
+      const uint32_t id = (uint32_t)min(base + grp + 32 * m2, vocab - 1);  // loads stay inside the head
+      const uint32_t o = id * wstride + (uint32_t)(St::bytes * c2);        // the stage's first byte
+      const uint32_t off = o & 15u;
       const uint32_t nch = (off + (uint32_t)min(St::bytes, rowbytes - St::bytes * c2) + 15u) >> 4;
-      const u32x4 *a = reinterpret_cast<const u32x4 *>(p - off);  // keeps the pointer's address space
+      const uint32_t o16 = o - off;
       // chunks g, g + 8, ... (past the last: the last again, so that every
       // lane loads and no branch splits the loads in flight)
 #pragma unroll
-      for (int j = 0; j < J; ++j) s.v[j] = a[min((uint32_t)(g + 8 * j), nch - 1u)];
+      for (int j = 0; j < J; ++j)
+        s.v[j] = *reinterpret_cast<const u32x4 *>(W + (o16 + 16u * min((uint32_t)(g + 8 * j), nch - 1u)));
       s.off = off | (nch << 8);
     };
     int cl = 0, ml = 0;  // the next stage to load
@@ -703,11 +735,9 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) lmh_prefetch_range(L.s, r, base + kLmhIds * tid, pre[r]);
-    int32_t *q8 = reinterpret_cast<int32_t *>(xs);
-    float *d8 = reinterpret_cast<float *>(q8 + R * (dim / 4));
-    float *s8 = d8 + R * (dim / 32);
-    int32_t *qs = reinterpret_cast<int32_t *>(s8 + R * (dim / 32));
-    q81_stage<R>(L, q8, d8, s8, qs);
+    uint32_t *U = reinterpret_cast<uint32_t *>(xs);
+    const int rw = items * kQOpWords<kFmt>;
+    q81_stage<R, kFmt>(L, U);
 #pragma unroll
     for (int r = 0; r < R; ++r) lmh_prefetch_ids(pre[r]);
     __syncthreads();  // the Q8_1 operand is in LDS
@@ -737,7 +767,7 @@ __global__ __launch_bounds__(kThreads, 2) void lmh_parts_kernel(const LmhArgs L)
         QRaw<kFmt> nxt;
         q_fetch<kFmt>(stg, ln, stage_take(ring[(d + 1) % D]), nxt);
         const int it = 8 * c + g;
-        if (it < items) q_terms<R, kFmt>(cur, ln, QOp{q8, d8, s8, qs, dim, it}, acc);
+        if (it < items) q_terms<R, kFmt>(cur, ln, QOp{U + it * kQOpWords<kFmt>, rw}, acc);
         cur = nxt;
         if (c == per - 1) {
           id_done(acc, m);
@@ -1043,10 +1073,9 @@ void lmh_layout(LmhArgs *a, void *scratch) {
 
 template <int R, int kFmt>
 static hipError_t launch_parts(const LmhArgs &a, hipStream_t stream) {
-  // bf16: the f32 hidden rows; GGUF: q8 (dim bytes), d8, s8 and the 16-value sums per row
+  // bf16: the f32 hidden rows; GGUF: the packed Q8_1 operand of every row
   const size_t lds = kFmt == SAS_HEAD_BF16 ? (size_t)R * a.dim * sizeof(float)
-                                           : (size_t)R * ((size_t)a.dim + 2 * sizeof(float) * (a.dim / 32) +
-                                                          sizeof(int32_t) * (a.dim / 16));
+                                           : (size_t)R * q_items<kFmt>(a.dim) * kQOpWords<kFmt> * sizeof(uint32_t);
   hipLaunchKernelGGL((lmh_parts_kernel<R, kFmt>), dim3((unsigned)a.s.parts), dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
