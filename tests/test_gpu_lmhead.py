@@ -250,6 +250,21 @@ def test_gguf_head_argument_errors(sampler):
         sampler.lm_head_sample(hid, w, fmt=7, params=Params())
     with pytest.raises(SasError, match="aligned"):
         sampler.lm_head_sample(hid, w.view(-1)[2:2 + 9 * 210].view(9, 210), fmt=W.HEAD_Q6_K, params=Params())
+    # rows 2^31 bytes apart: three rows span more than 4 GiB (rejected
+    # before anything is read)
+    import ctypes
+    from shared_amd import _capi
+    from shared_amd.sampler import rows_descriptor
+    out = torch.empty(1, dtype=torch.int32, device="cuda")
+    h = sampler._head(hid, w, None, None, W.HEAD_Q6_K)
+    h.weight_stride = 1 << 31
+    d = rows_descriptor(hid, out, vocab=3, params=Params())
+    d.logits = None
+    d.logits_stride = 0
+    lib = _capi.load()
+    rc = lib.sas_lm_head_sample(sampler._h, ctypes.byref(h), ctypes.byref(d), None)
+    assert rc == _capi.ERR_INVALID
+    assert b"4 GiB" in lib.sas_last_error(sampler._h)
 
 
 @pytest.mark.parametrize("fmt", [W.HEAD_BF16, W.HEAD_Q6_K])
