@@ -620,6 +620,8 @@ int sas_verify(sas_sampler *s, const sas_verify_rows *v, void *stream) {
   a.part = a.stats + positions * a.chunks * 4;
   a.seqrec = a.part + (size_t)v->seqs * a.chunks * 2;
   a.dtok = reinterpret_cast<float *>(a.seqrec + (size_t)v->seqs * 8);
+  a.pk_n = reinterpret_cast<uint32_t *>(a.dtok + positions * 2);
+  a.pk_v = reinterpret_cast<float *>(a.pk_n + positions * a.chunks * sas::kWaves);
   a.aligned = (reinterpret_cast<uintptr_t>(v->target_logits) & 15u) == 0 &&
               (reinterpret_cast<uintptr_t>(v->draft_logits) & 15u) == 0 && (v->logits_stride & 3) == 0;
   hipError_t e = sas::launch_verify(a, pick_stream(s, stream));

@@ -179,6 +179,8 @@ struct VerifyArgs {
   double *part;    // [seqs][chunks][2]: residual mass, target mass of the decided position
   double *seqrec;  // [seqs][8]: decided position, its target max / sum, draft max / sum
   float *dtok;     // [positions][2]: target and draft logit of the position's draft token (NaN: masked)
+  uint32_t *pk_n;  // [positions][chunks][4 waves]: how the statistics pass packed the wave's allowed values
+  float *pk_v;     // [positions][chunks][4 waves][2][256]: those values, target then draft
   int32_t vocab;
   int32_t seqs;
   int32_t L;

@@ -121,12 +121,28 @@ __device__ __forceinline__ uint32_t allow_strided(const uint32_t *mrow, int64_t 
   return bits;
 }
 
+// The number of set bits of `ok` over the wave.
+__device__ __forceinline__ uint32_t wave_count(uint32_t ok) {
+  const uint32_t n = (uint32_t)__popc(ok);
+  uint32_t tot = 0u;
+#pragma unroll
+  for (int bit = 0; bit < 5; ++bit) tot += (uint32_t)__popcll(__ballot((n >> bit) & 1u)) << bit;
+  return tot;
+}
+
 // A wave's allowed values of one side, packed, when they are few.
 constexpr int kCompact = 256;
+// pk_n words: the wave's values were packed for both rows (the same ids),
+// or for the target row only (a position without a draft); the count in
+// the low bits.  0: not packed (too many allowed, or the rows' NaNs differ).
+constexpr uint32_t kPkJoint = 1u << 30;
+constexpr uint32_t kPkTarget = 1u << 29;
+constexpr uint32_t kPkCount = 0xFFFFu;
 
 struct StatsLds {
   float m[kWaves][2];
   double z[kWaves][2];
+  uint32_t pk[kWaves];  // how each wave packed its values (pk_n)
   float cv[kWaves][2][kCompact];
 };
 
@@ -254,15 +270,33 @@ __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
   const double Mt = (double)bt, Mq = (double)bq;
   double zt = 0.0, zq = 0.0;
   const bool same = has_draft && __ballot(okt != okq) == 0ull;  // uniform over the wave
-  if (!(same && joint_sums(xt, xq, okt, Mt, Mq, a.inv_t, l.cv[wave][0], l.cv[wave][1], zt, zq))) {
+  const bool joint = same && joint_sums(xt, xq, okt, Mt, Mq, a.inv_t, l.cv[wave][0], l.cv[wave][1], zt, zq);
+  if (!joint) {
     zt = side_sum(xt, okt, Mt, a.inv_t, l.cv[wave][0]);
     zq = has_draft ? side_sum(xq, okq, Mq, a.inv_t, l.cv[wave][1]) : 0.0;
   }
+  // how the wave's values were packed: the count of its allowed target ids
+  // (both helpers pack exactly when it is at most kCompact)
+  const uint32_t nt = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_count(okt));
+  const uint32_t pk = nt > (uint32_t)kCompact ? 0u : joint ? (kPkJoint | nt) : !has_draft ? (kPkTarget | nt) : 0u;
   if (lane == 0) {
     l.z[wave][0] = zt;
     l.z[wave][1] = zq;
+    l.pk[wave] = pk;
   }
   __syncthreads();
+  // the wave's packed values (in the order the decide pass packs them from
+  // the rows, so that its sums are the same) and how they were packed
+  {
+    const uint32_t pw = l.pk[wave], n = pw & kPkCount;
+    const int64_t w = ((int64_t)pos * a.chunks + c) * kWaves + wave;
+    float *pv = a.pk_v + w * (2 * kCompact);
+    for (uint32_t e = (uint32_t)lane; pw && e < n; e += 64u) {
+      pv[e] = l.cv[wave][0][e];
+      if (pw & kPkJoint) pv[kCompact + e] = l.cv[wave][1][e];
+    }
+    if (lane == 0) a.pk_n[w] = pw;
+  }
   if (tid == 0) {
     double t = l.z[0][0], q = l.z[0][1];
 #pragma unroll
@@ -383,48 +417,64 @@ __global__ __launch_bounds__(kThreads) void verify_decide_kernel(VerifyArgs a) {
   const int pos = s * P1 + d.a;
   const bool resid = d.a < a.L;
   const int64_t base = (int64_t)c * kVChunk;
-  float xt[kPerThread], xq[kPerThread];
-  load_strided(a.target + (int64_t)pos * a.stride, base, a.vocab, a.aligned, xt);
-  if (resid) load_strided(a.draft + ((int64_t)s * a.L + d.a) * a.stride, base, a.vocab, a.aligned, xq);
-  const uint32_t ok = nan_free(xt, allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr,
-                                                         base, a.vocab));
   const Weights w{d.mt, 1.0 / d.zt, d.mq, resid ? 1.0 / d.zq : 0.0, a.inv_t, resid};
   double pm = 0.0, rs = 0.0;
-  // the allowed ids' values, packed per wave when few (a sparse mask)
-  const uint32_t n = (uint32_t)__popc(ok);
-  uint32_t pre = 0u, tot = 0u;
-#pragma unroll
-  for (int bit = 0; bit < 5; ++bit) {
-    const uint64_t bb = __ballot((n >> bit) & 1u);
-    pre += lanes_below(bb) << bit;
-    tot += (uint32_t)__popcll(bb) << bit;
-  }
-  if (tot <= (uint32_t)kCompact) {
-    uint32_t jj = pre;
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i)
-      if ((ok >> i) & 1u) {
-        l.ct[wave][jj] = xt[i];
-        l.cq[wave][jj] = resid ? xq[i] : 0.0f;
-        ++jj;
-      }
-    wave_lds_sync();
+  // the wave's allowed ids as the statistics pass packed them (both rows,
+  // or the target row where no residual is drawn); else the rows again
+  const int64_t wpk = ((int64_t)pos * a.chunks + c) * kWaves + wave;
+  const uint32_t pk = a.pk_n[wpk];
+  if (resid ? (pk & kPkJoint) != 0u : (pk & (kPkJoint | kPkTarget)) != 0u) {
+    const float *pv = a.pk_v + wpk * (2 * kCompact);
+    const uint32_t tot = pk & kPkCount;
     for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
-      const float vq = l.cq[wave][e];
+      const float vq = resid ? pv[kCompact + e] : 0.0f;
       double wt, r;
-      w.at(l.ct[wave][e], vq, resid && vq == vq, wt, r);
+      w.at(pv[e], vq, resid && vq == vq, wt, r);
       pm += wt;
       rs += r;
     }
   } else {
+    float xt[kPerThread], xq[kPerThread];
+    load_strided(a.target + (int64_t)pos * a.stride, base, a.vocab, a.aligned, xt);
+    if (resid) load_strided(a.draft + ((int64_t)s * a.L + d.a) * a.stride, base, a.vocab, a.aligned, xq);
+    const uint32_t ok = nan_free(xt, allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr,
+                                                           base, a.vocab));
+    // the allowed ids' values, packed per wave when few (a sparse mask)
+    const uint32_t n = (uint32_t)__popc(ok);
+    uint32_t pre = 0u, tot = 0u;
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i)
-      if ((ok >> i) & 1u) {
+    for (int bit = 0; bit < 5; ++bit) {
+      const uint64_t bb = __ballot((n >> bit) & 1u);
+      pre += lanes_below(bb) << bit;
+      tot += (uint32_t)__popcll(bb) << bit;
+    }
+    if (tot <= (uint32_t)kCompact) {
+      uint32_t jj = pre;
+#pragma unroll
+      for (int i = 0; i < kPerThread; ++i)
+        if ((ok >> i) & 1u) {
+          l.ct[wave][jj] = xt[i];
+          l.cq[wave][jj] = resid ? xq[i] : 0.0f;
+          ++jj;
+        }
+      wave_lds_sync();
+      for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
+        const float vq = l.cq[wave][e];
         double wt, r;
-        w.at(xt[i], resid ? xq[i] : 0.0f, resid && xq[i] == xq[i], wt, r);
+        w.at(l.ct[wave][e], vq, resid && vq == vq, wt, r);
         pm += wt;
         rs += r;
       }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPerThread; ++i)
+        if ((ok >> i) & 1u) {
+          double wt, r;
+          w.at(xt[i], resid ? xq[i] : 0.0f, resid && xq[i] == xq[i], wt, r);
+          pm += wt;
+          rs += r;
+        }
+    }
   }
   pm = wave_sum_d(pm);
   rs = wave_sum_d(rs);
@@ -666,7 +716,8 @@ size_t verify_scratch_bytes(int seqs, int L, int vocab) {
   const size_t chunks = ((size_t)vocab + kVChunk - 1) / kVChunk;
   const size_t positions = (size_t)seqs * (L + 1);
   return (positions * chunks * 4 + (size_t)seqs * chunks * 2 + (size_t)seqs * 8) * sizeof(double) +
-         positions * 2 * sizeof(float);
+         positions * 2 * sizeof(float) + positions * chunks * kWaves * sizeof(uint32_t) +
+         positions * chunks * kWaves * 2 * kCompact * sizeof(float);
 }
 
 hipError_t launch_verify(const VerifyArgs &a, hipStream_t stream) {
