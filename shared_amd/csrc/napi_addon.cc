@@ -486,6 +486,22 @@ napi_value LmHeadSample(napi_env env, napi_callback_info info) {
   return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
 }
 
+// The fused head as a step of the in-graph decode loop.
+napi_value LmHeadStep(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!args(env, info, 4, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_rows r;
+  sas_lm_head hd;
+  sas_step st;
+  if (!read_rows(env, argv[1], &r) || !read_head(env, argv[2], &hd) || !read_step(env, argv[3], &st)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad lm head step descriptor");
+    return nullptr;
+  }
+  int rc = sas_lm_head_sample_step(s, &hd, &r, &st, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
 napi_value Verify(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!args(env, info, 2, argv)) return throw_napi(env, "arguments");
@@ -512,6 +528,36 @@ napi_value SpecExact(napi_env env, napi_callback_info info) {
   return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
 }
 
+// A sas_spec_state descriptor: {state, ring?, ringLen?, log?, maxRounds?,
+// nextTokens?} of device addresses (BigInt) and sizes.
+bool read_spec_state(napi_env env, napi_value d, sas_spec_state *st) {
+  std::memset(st, 0, sizeof *st);
+  int64_t ring_len = 0, max_rounds = 0;
+  const bool ok = get_ptr(env, d, "state", (void **)&st->state) && get_ptr(env, d, "ring", (void **)&st->ring) &&
+                  get_i64(env, d, "ringLen", &ring_len) && get_ptr(env, d, "log", (void **)&st->log) &&
+                  get_i64(env, d, "maxRounds", &max_rounds) &&
+                  get_ptr(env, d, "nextTokens", (void **)&st->next_tokens);
+  if (!ok || ring_len < 0 || ring_len > INT32_MAX || max_rounds < 0 || max_rounds > INT32_MAX) return false;
+  st->ring_len = (int32_t)ring_len;
+  st->max_rounds = (int32_t)max_rounds;
+  return true;
+}
+
+// One chained speculative round with the on-device commit.
+napi_value SpecStep(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  HANDLE_OR_THROW(argv[0], s);
+  sas_spec_rows r;
+  sas_spec_state st;
+  if (!read_spec(env, argv[1], &r) || !read_spec_state(env, argv[2], &st)) {
+    napi_throw_type_error(env, nullptr, "sas_napi: bad spec step descriptor");
+    return nullptr;
+  }
+  int rc = sas_spec_step(s, &r, &st, sas_stream(s));
+  return rc == SAS_OK ? undefined(env) : throw_sas(env, s, rc);
+}
+
 // --------------------------------------------------------------- async --
 
 struct AsyncCall {
@@ -523,7 +569,10 @@ struct AsyncCall {
   bool step = false;
   bool spec = false;
   bool head = false;
+  bool head_step = false;
+  bool spec_step = false;
   sas_lm_head hd;
+  sas_spec_state sst;
   sas_spec_rows srows;
   sas_rows rows;
   sas_step srow;
@@ -541,11 +590,13 @@ void async_execute(napi_env, void *data) {
     return;
   }
   sas_sampler *s = c->h->s;
-  c->rc = c->verify ? sas_verify(s, &c->vrows, sas_stream(s))
-          : c->step ? sas_sample_step(s, &c->rows, &c->srow, sas_stream(s))
-          : c->spec ? sas_spec_exact(s, &c->srows, sas_stream(s))
-          : c->head ? sas_lm_head_sample(s, &c->hd, &c->rows, sas_stream(s))
-                    : sas_sample(s, &c->rows, sas_stream(s));
+  c->rc = c->verify      ? sas_verify(s, &c->vrows, sas_stream(s))
+          : c->head_step ? sas_lm_head_sample_step(s, &c->hd, &c->rows, &c->srow, sas_stream(s))
+          : c->spec_step ? sas_spec_step(s, &c->srows, &c->sst, sas_stream(s))
+          : c->step      ? sas_sample_step(s, &c->rows, &c->srow, sas_stream(s))
+          : c->spec      ? sas_spec_exact(s, &c->srows, sas_stream(s))
+          : c->head      ? sas_lm_head_sample(s, &c->hd, &c->rows, sas_stream(s))
+                         : sas_sample(s, &c->rows, sas_stream(s));
   if (c->rc == SAS_OK) c->rc = sas_synchronize(s, sas_stream(s));
   if (c->rc != SAS_OK) c->err = sas_last_error(s);
 }
@@ -665,6 +716,38 @@ napi_value SpecExactAsync(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   return start_async(env, c, argv[0], "sas_spec_exact");
+}
+
+napi_value LmHeadStepAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!args(env, info, 4, argv)) return throw_napi(env, "arguments");
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
+  AsyncCall *c = new AsyncCall();
+  c->h = h;
+  c->head_step = true;
+  if (!read_rows(env, argv[1], &c->rows) || !read_head(env, argv[2], &c->hd) || !read_step(env, argv[3], &c->srow)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad lm head step descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, argv[0], "sas_lm_head_sample_step");
+}
+
+napi_value SpecStepAsync(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!args(env, info, 3, argv)) return throw_napi(env, "arguments");
+  Handle *h = open_wrapper(env, argv[0]);
+  if (!h) return nullptr;
+  AsyncCall *c = new AsyncCall();
+  c->h = h;
+  c->spec_step = true;
+  if (!read_spec(env, argv[1], &c->srows) || !read_spec_state(env, argv[2], &c->sst)) {
+    delete c;
+    napi_throw_type_error(env, nullptr, "sas_napi: bad spec step descriptor");
+    return nullptr;
+  }
+  return start_async(env, c, argv[0], "sas_spec_step");
 }
 
 napi_value VerifyAsync(napi_env env, napi_callback_info info) {
@@ -837,6 +920,10 @@ napi_value Init(napi_env env, napi_value exports) {
       {"sampleStepAsync", nullptr, SampleStepAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"lmHeadSample", nullptr, LmHeadSample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"lmHeadSampleAsync", nullptr, LmHeadSampleAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHeadStep", nullptr, LmHeadStep, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHeadStepAsync", nullptr, LmHeadStepAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"specStep", nullptr, SpecStep, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"specStepAsync", nullptr, SpecStepAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verify", nullptr, Verify, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"verifyAsync", nullptr, VerifyAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"specExact", nullptr, SpecExact, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

@@ -223,6 +223,38 @@ export interface SpecExactOptions {
   maskStride?: number;
 }
 
+/** decodeSteps with the LM head fused into each step (rows <= LMH_MAX_ROWS). */
+export interface DecodeStepsWithHeadOptions extends Omit<DecodeStepsOptions, 'logits' | 'stride'> {
+  /** Step i's final-normed hidden states [rows][hiddenStride], computed from the tokens in nextTokens. */
+  hidden(i: number, nextTokens: DeviceBuffer): DeviceBuffer | Float32Array | Promise<DeviceBuffer | Float32Array>;
+  head: Omit<LmHead, 'hidden' | 'outLogits'>;
+}
+
+/** A chain of speculative rounds with acceptSpec's commit on the device. */
+export interface SpecStepsOptions extends Omit<SpecExactOptions, 'target' | 'draft' | 'draftIds' | 'history'> {
+  rounds: number;
+  /** Round r's verify rows and draft head rows (or drafts), computed from the tokens in nextTokens. */
+  logits(r: number, nextTokens: DeviceBuffer): SpecRoundLogits | Promise<SpecRoundLogits>;
+  /** The tokens fed to round 0, one per sequence. */
+  firstTokens?: Uint32Array | number[];
+  /** The sequences' positions at the chain's start (posBuf[0]); default 0. */
+  positions?: Uint32Array | number[];
+  windowSize?: number;
+}
+
+export interface SpecRoundLogits {
+  target: DeviceBuffer | Float32Array;
+  draft?: DeviceBuffer | Float32Array;
+  draftIds?: Uint32Array | number[];
+}
+
+/** A chain's rounds: the log entry of each sequence in each round, the final positions and stop state. */
+export interface SpecStepsResult {
+  rounds: Array<Array<{ a: number; next: number; drafts: number[]; frozen: boolean }>>;
+  pos: number[];
+  stopped: boolean[];
+}
+
 /** One sequence's round (the reference's SpecRound, model.d.ts, plus the picks). */
 export interface SpecExactResult {
   a: number;
@@ -259,6 +291,8 @@ export declare class Sampler {
   decodeRowsAsync(opts: SampleRowsOptions): Promise<DecodeBatchResult[]>;
   decodeSteps(opts: DecodeStepsOptions): DecodeBatchResult[];
   decodeStepsAsync(opts: DecodeStepsOptions): Promise<DecodeBatchResult[]>;
+  decodeStepsWithHead(opts: DecodeStepsWithHeadOptions): DecodeBatchResult[];
+  decodeStepsWithHeadAsync(opts: DecodeStepsWithHeadOptions): Promise<DecodeBatchResult[]>;
   sample(
     cands: { ids: ArrayLike<number>; vals: ArrayLike<number> },
     opts?: {
@@ -272,6 +306,8 @@ export declare class Sampler {
   ): number;
   specExact(opts: SpecExactOptions): SpecExactResult[];
   specExactAsync(opts: SpecExactOptions): Promise<SpecExactResult[]>;
+  specSteps(opts: SpecStepsOptions): SpecStepsResult;
+  specStepsAsync(opts: SpecStepsOptions): Promise<SpecStepsResult>;
   verify(opts: VerifyOptions): VerifyResult;
   verifyAsync(opts: VerifyOptions): Promise<VerifyResult>;
 }

@@ -964,6 +964,53 @@ class Sampler {
   }
 
   /**
+   * decodeSteps with the LM head fused into each step: the reference's
+   * per-iteration lm -> topk -> sampler with tokens[0] fed back
+   * (model.js:711-717, kernels.js:189-199).  Step i's logits are
+   * opts.head.weight times opts.hidden(i, nextTokens): the final-normed
+   * hidden states [rows][hiddenStride] (a DeviceBuffer or a Float32Array) the
+   * caller's model computed from the tokens in nextTokens.  opts.head:
+   * {weight, dim, format?, weightStride?, hiddenStride?} as for
+   * lmHeadSample; rows <= LMH_MAX_ROWS.  Everything else, and the result, as
+   * decodeSteps.
+   */
+  decodeStepsWithHead(opts) {
+    this._idle('decodeStepsWithHead');
+    const k = Math.floor(opts.k);
+    if (!(k >= 1)) throw new RangeError('k must be >= 1');
+    if (typeof opts.hidden !== 'function') throw new TypeError('hidden must be a function (step, nextTokens)');
+    const r = this._describe(opts, true);
+    const st = this._stepState(opts, r.packed, k);
+    const next = this._scratch.stNext;
+    for (let i = 0; i < k; i++) {
+      const hd = this._describeHead({ rows: opts.rows, head: Object.assign({}, opts.head, { hidden: opts.hidden(i, next) }) });
+      addon.lmHeadStep(this._handle(), r.desc, hd, st);
+    }
+    return this._stepResults(opts, r.packed, k);
+  }
+
+  /** decodeStepsWithHead with each launch and wait on a worker thread; opts.hidden may return a promise. */
+  decodeStepsWithHeadAsync(opts) {
+    const self = this;
+    return this._enqueue(function () {
+      const k = Math.floor(opts.k);
+      if (!(k >= 1)) throw new RangeError('k must be >= 1');
+      if (typeof opts.hidden !== 'function') throw new TypeError('hidden must be a function (step, nextTokens)');
+      const r = self._describe(opts, true);
+      const st = self._stepState(opts, r.packed, k);
+      const next = self._scratch.stNext;
+      let chain = Promise.resolve();
+      for (let i = 0; i < k; i++) {
+        chain = chain.then(function () { return opts.hidden(i, next); }).then(function (h) {
+          const hd = self._describeHead({ rows: opts.rows, head: Object.assign({}, opts.head, { hidden: h }) });
+          return self._worker(addon.lmHeadStepAsync(self._handle(), r.desc, hd, st));
+        });
+      }
+      return chain.then(function () { return self._stepResults(opts, r.packed, k); });
+    });
+  }
+
+  /**
    * The reference's sample(cands, opts) signature (tokenizer.js:151): a
    * candidate list [id, value] interleaved in ids/vals, presence penalty
    * over opts.recentIds.  Runs on the GPU over a row that holds the
@@ -1045,6 +1092,167 @@ class Sampler {
       return self._worker(addon.specExactAsync(self._handle(), r.desc))
         .then(function () { return self._collectSpec(opts, r.packed); });
     });
+  }
+
+  // The device state of a chain of speculative rounds (acceptSpec's ctl,
+  // posBuf and ring, kernels.js:211-367): {frozen, round, pos, accepted} per
+  // sequence (round opts.round, pos opts.positions or 0), the rings seeded
+  // from opts.windows, the round log and the next input tokens
+  // (opts.firstTokens).
+  _specState(opts, rounds) {
+    const seqs = opts.seqs;
+    const L = opts.draftLen;
+    const W = Math.floor(orDefault(opts.windowSize, opts.windows && opts.windows.length ? opts.windows[0].size : 512));
+    if (!(W >= 1 && W <= addon.MAX_HISTORY)) throw new RangeError('windowSize must be in [1, ' + addon.MAX_HISTORY + ']');
+    const state = new Uint32Array(seqs * 4);
+    const pos = opts.positions ? toU32(opts.positions) : null;
+    if (pos && pos.length !== seqs) throw new RangeError('positions must have one entry per sequence');
+    for (let q = 0; q < seqs; q++) {
+      state[q * 4 + 1] = (orDefault(opts.round, 0)) >>> 0;
+      state[q * 4 + 2] = pos ? pos[q] : 0;
+    }
+    const ring = new Uint32Array(seqs * (1 + W));
+    if (opts.windows) {
+      if (opts.windows.length !== seqs) throw new RangeError('windows must have one PenaltyWindow per sequence');
+      for (let q = 0; q < seqs; q++) {
+        const g = opts.windows[q].genIds;
+        const n = g.length;
+        const base = q * (1 + W);
+        ring[base] = n;
+        for (let i = Math.max(0, n - W); i < n; i++) ring[base + 1 + (i % W)] = g[i];
+      }
+    }
+    const next = new Uint32Array(seqs);
+    if (opts.firstTokens) {
+      const f = toU32(opts.firstTokens);
+      if (f.length !== seqs) throw new RangeError('firstTokens must have one id per sequence');
+      next.set(f);
+    }
+    return {
+      state: this._buf('spState', state.byteLength).upload(state).ptr,
+      ring: this._buf('spRing', ring.byteLength).upload(ring).ptr, ringLen: W,
+      log: this._buf('spLog', seqs * rounds * (L + 2) * 4).ptr, maxRounds: rounds,
+      nextTokens: this._buf('spNext', seqs * 4).upload(next).ptr,
+    };
+  }
+
+  // Round r's logits from the caller's producer: {target, draft?, draftIds?}.
+  _specRound(d, lg, opts) {
+    const self = this;
+    const dev = function (name, x) {
+      if (x instanceof DeviceBuffer) return x.ptr;
+      if (x instanceof Float32Array) return self._buf(name, x.byteLength).upload(x).ptr;
+      throw new TypeError('round logits must be DeviceBuffers or Float32Arrays');
+    };
+    if (!lg || !lg.target) throw new TypeError('the logits producer must return {target, draft?, draftIds?}');
+    d.targetLogits = dev('sTarget', lg.target);
+    if (lg.draft) {
+      d.draftLogits = dev('sDraft', lg.draft);
+      d.draftIds = this._buf('sIds', opts.seqs * opts.draftLen * 4).ptr;
+    } else {
+      const ids = toU32(lg.draftIds);
+      if (ids.length !== opts.seqs * opts.draftLen) throw new RangeError('draftIds must hold seqs * draftLen ids');
+      d.draftLogits = null;
+      d.draftIds = this._buf('sIds', ids.byteLength).upload(ids).ptr;
+    }
+  }
+
+  // The chain's outcome: each round's log entry per sequence, the state,
+  // and the windows mirroring the device rings (the committed tokens that
+  // are not stop ids, kernels.js:341-357).
+  _specChainResults(opts, packed, rounds) {
+    const seqs = opts.seqs;
+    const L = opts.draftLen;
+    const log = this._scratch.spLog.download(new Uint32Array(seqs * rounds * (L + 2)));
+    const state = this._scratch.spState.download(new Uint32Array(seqs * 4));
+    const out = [];
+    for (let r = 0; r < rounds; r++) {
+      const row = [];
+      for (let q = 0; q < seqs; q++) {
+        const e = log.subarray((q * rounds + r) * (L + 2), (q * rounds + r + 1) * (L + 2));
+        const a = e[0];
+        const drafts = Array.from(e.subarray(2, 2 + L));
+        row.push({ a: a, next: e[1], drafts: drafts, frozen: a === 0 });
+        if (opts.windows && a > 0) {
+          const pk = packed[packed.length > 1 ? q : 0];
+          const committed = drafts.slice(0, a - 1).concat([e[1]]);
+          for (let i = 0; i < committed.length; i++) if (!pk.stopSet.has(committed[i])) opts.windows[q].note(committed[i]);
+        }
+      }
+      out.push(row);
+    }
+    const pos = [];
+    const stopped = [];
+    for (let q = 0; q < seqs; q++) {
+      stopped.push(state[q * 4] !== 0);
+      pos.push(state[q * 4 + 2]);
+    }
+    return { rounds: out, pos: pos, stopped: stopped };
+  }
+
+  /**
+   * specChain's rounds (model.js:867-1008) with acceptSpec's commit on the
+   * device (kernels.js:340-367), so that no host work runs between rounds.
+   * Round r is specExact's round over opts.logits(r, nextTokens) ->
+   * {target, draft?, draftIds?}: the verify rows [seqs*(draftLen+1)][stride]
+   * and the draft head's rows [seqs*draftLen][stride] (or the drafts), each
+   * a DeviceBuffer or a Float32Array, that the caller's models computed from
+   * the tokens in nextTokens (a DeviceBuffer of seqs uint32: opts.firstTokens,
+   * then each round's next token).  A sequence's history is its device ring
+   * (the last windowSize tokens, seeded from opts.windows); one whose next
+   * token is one of its stop ids freezes and reads no logits from then on.
+   * opts as specExact otherwise, with opts.rounds (>= 1), opts.round the
+   * chain's first round (posBuf[4]; default 0) and opts.positions the
+   * sequences' positions.  Returns {rounds: [[{a, next, drafts, frozen}]
+   * per sequence] per round, pos, stopped}; each window receives the
+   * committed tokens that are not stop ids.
+   */
+  specSteps(opts) {
+    this._idle('specSteps');
+    const R = Math.floor(opts.rounds);
+    if (!(R >= 1)) throw new RangeError('rounds must be >= 1');
+    if (typeof opts.logits !== 'function') throw new TypeError('logits must be a function (round, nextTokens)');
+    const st = this._specState(opts, R);
+    const next = this._scratch.spNext;
+    let r0 = null;
+    for (let i = 0; i < R; i++) {
+      const lg = opts.logits(i, next);
+      if (!r0) r0 = this._describeSpec(this._chainOpts(opts, lg));
+      this._specRound(r0.desc, lg, opts);
+      addon.specStep(this._handle(), r0.desc, st);
+    }
+    return this._specChainResults(opts, r0.packed, R);
+  }
+
+  /** specSteps with each launch and wait on a worker thread; opts.logits may return a promise. */
+  specStepsAsync(opts) {
+    const self = this;
+    return this._enqueue(function () {
+      const R = Math.floor(opts.rounds);
+      if (!(R >= 1)) throw new RangeError('rounds must be >= 1');
+      if (typeof opts.logits !== 'function') throw new TypeError('logits must be a function (round, nextTokens)');
+      const st = self._specState(opts, R);
+      const next = self._scratch.spNext;
+      let r0 = null;
+      let chain = Promise.resolve();
+      for (let i = 0; i < R; i++) {
+        chain = chain.then(function () { return opts.logits(i, next); }).then(function (lg) {
+          if (!r0) r0 = self._describeSpec(self._chainOpts(opts, lg));
+          self._specRound(r0.desc, lg, opts);
+          return self._worker(addon.specStepAsync(self._handle(), r0.desc, st));
+        });
+      }
+      return chain.then(function () { return self._specChainResults(opts, r0.packed, R); });
+    });
+  }
+
+  // specExact's options for a chain's descriptor: the first round's
+  // logits, no host history (the rings are the history).
+  _chainOpts(opts, lg) {
+    const o = Object.assign({}, opts, { target: lg.target, draft: lg.draft, draftIds: lg.draftIds });
+    delete o.windows;
+    delete o.history;
+    return o;
   }
 
   _describeSpec(opts) {

@@ -6,6 +6,7 @@ import numpy as np
 
 import oracle as O
 from shared_amd import Sampler
+from shared_amd import workloads as W
 from shared_amd._capi import FLAG_DRAW_EDGE, FLAG_EMPTY_ROW, FLAG_TOPP_EDGE, MAX_TOP_K, NO_TOKEN, STOP_PAD
 
 ORACLE_FLAGS = FLAG_EMPTY_ROW | FLAG_TOPP_EDGE | FLAG_DRAW_EDGE
@@ -98,3 +99,26 @@ def ring_of(window, ring_len):
         ring[1 + i % ring_len] = window[i]
     ring[0] = len(window)
     return ring
+
+
+def oracle_chain(cases, seeds, stop_ids, rounds, ring0, first_round):
+    """orc_spec_exact then orc_spec_commit, round by round, every sequence's
+    history being its ring as of the round's start."""
+    seqs, L = cases[0]["seqs"], cases[0]["drafts"]
+    ring = ring0.copy()
+    ring_len = ring.shape[1] - 1
+    state = np.zeros((seqs, 4), np.uint32)
+    state[:, 1] = first_round
+    log = np.zeros((seqs, rounds, L + 2), np.uint32)
+    per = []
+    for r in range(rounds):
+        c = dict(cases[r])
+        hist = [ring[s, 1:1 + min(int(ring[s, 0]), ring_len)] for s in range(seqs)]
+        c["hist_ids"], c["hist_offsets"] = W._csr(hist)
+        c["seeds"], c["stop_ids"], c["round"] = seeds, stop_ids, int(state[0, 1])
+        frozen = state[:, 0].copy()
+        o = O.spec_exact(c)
+        nxt, acc = O.spec_commit(o["picks"], o["draft_ids"], o["accepted"], stop_ids, state, ring, log)
+        per.append({"frozen": frozen, "draft_ids": o["draft_ids"], "picks": o["picks"], "accepted": acc,
+                    "next": nxt})
+    return per, state, ring, log

@@ -274,3 +274,136 @@ def test_node_lm_head_sample(tmp_path):
     assert np.array_equal(gq.view(np.uint32), lq.view(np.uint32))
     assert np.array_equal(_u32(d, "lmh_q6k_ids.u32"), want_q["ids"])
     assert np.array_equal(np.fromfile(os.path.join(d, "lmh_q6k_probs.f64")).reshape(b.rows, -1), want_q["probs"])
+
+
+def _step_expectations(want, stops, k):
+    """decodeBatch's per-row result (model.js:727-741) of oracle steps."""
+    rows = len(stops)
+    seqs = [[int(w["ids"][r]) for w in want] for r in range(rows)]
+    expect = []
+    for r in range(rows):
+        ids = seqs[r]
+        at = next((i for i, t in enumerate(ids) if t in stops[r]), -1)
+        hit = at >= 0
+        expect.append({"ids": ids[:at + 1] if hit else ids, "fed": at + 1 if hit else k,
+                       "eos": hit and ids[at] == stops[r][0], "stopped": hit, "stopId": ids[at] if hit else None})
+    return expect
+
+
+def test_node_decode_steps_with_head(tmp_path):
+    """decodeStepsWithHead / decodeStepsWithHeadAsync over Qwen's head format
+    (Q6_K): each step's logits are the oracle's head logits of that step's
+    hidden states, sampled and fed back as the reference's per-iteration
+    lm -> topk -> sampler does (model.js:711-717, kernels.js:174-199); a
+    planted stop freezes one row mid-loop."""
+    if shutil.which("node") is None:
+        pytest.skip("node is not installed")
+    from gpu_helpers import oracle_steps
+    d = str(tmp_path)
+    rows, vocab, dim, k, wsize = 3, 20_000, 512, 5, 16
+    rng = np.random.default_rng(61)
+    head = W.gguf_head(rng, W.HEAD_Q6_K, vocab, dim)
+    hs = rng.standard_normal((k, rows, dim)).astype(np.float32)
+    xs = np.stack([O.lm_head_q_logits(W.HEAD_Q6_K, hs[t], head) for t in range(k)])
+    mask = W.random_mask(rng, rows, vocab, 0.05, 0.3)
+    js = [dict(temperature=0.9, topK=40, topP=0.9, repetitionPenalty=1.2, presencePenalty=0.4, frequencyPenalty=0.0,
+               softcap=0, seed=int(rng.integers(1, 2**31))) for _ in range(rows)]
+    prm = [Params(temperature=p["temperature"], top_k=p["topK"], top_p=p["topP"],
+                  repetition_penalty=p["repetitionPenalty"], presence_penalty=p["presencePenalty"]) for p in js]
+    seeds = np.array([p["seed"] for p in js], np.uint32)
+    hist = [[5, 17, 19_999], [], [1_000, 1_000]]
+    free, _, _, _ = oracle_steps(xs, prm, mask=mask, seeds=seeds, history=hist, ring_len=wsize)
+    stops = [[], [int(free[2]["ids"][1])], []]
+    js[1]["stopIds"] = stops[1]
+    want, stopped, _, window = oracle_steps(xs, prm, mask=mask, seeds=seeds, stop_ids=stops, history=hist,
+                                            ring_len=wsize)
+    assert stopped[1], "the planted stop must freeze row 1"
+    hs.tofile(os.path.join(d, "hs.f32"))
+    head.tofile(os.path.join(d, "head.u8"))
+    mask.tofile(os.path.join(d, "mask.u32"))
+    first = np.arange(rows, dtype=np.uint32) + 7
+    first.tofile(os.path.join(d, "first.u32"))
+    with open(os.path.join(d, "headsteps.json"), "w") as f:
+        json.dump({"rows": rows, "vocab": vocab, "k": k, "dim": dim, "params": js, "windows": hist,
+                   "windowSize": wsize}, f)
+    print("[gpu] node headsteps_gpu.js", d, flush=True)
+    proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "headsteps_gpu.js"), d], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-3000:]
+    expect = _step_expectations(want, stops, k)
+    for name in ("js_headsteps.json", "js_headsteps_async.json"):
+        with open(os.path.join(d, name)) as f:
+            got = json.load(f)
+        assert got["results"] == expect, name
+        assert got["windows"] == window, name
+    with open(os.path.join(d, "js_headsteps.json")) as f:
+        fed = json.load(f)["fed"]
+    assert fed[0] == first.tolist()
+    for i in range(1, k):
+        assert fed[i] == [int(x) for x in want[i - 1]["ids"]], i
+
+
+def test_node_spec_steps(tmp_path):
+    """specSteps / specStepsAsync: four chained rounds with acceptSpec's
+    commit on the device (kernels.js:340-367, model.js:867-1008) against the
+    oracle stepped round by round (orc_spec_exact, then orc_spec_commit):
+    the round log, the positions, the stop state, and the windows mirroring
+    the device rings; one sequence draws its stop id mid-chain."""
+    if shutil.which("node") is None:
+        pytest.skip("node is not installed")
+    from gpu_helpers import oracle_chain
+    from shared_amd.sampler import ring_rows
+    d = str(tmp_path)
+    seqs, L, vocab, rounds, ring_len = 6, 2, 32_000, 4, 48
+    cases = [W.spec_case(seqs=seqs, vocab=vocab, drafts=L, hist=0, seed=400 + r) for r in range(rounds)]
+    for c in cases[1:]:
+        c["seq_params"] = cases[0]["seq_params"]
+    rng = np.random.default_rng(19)
+    seeds = rng.integers(1, 2**31, seqs, dtype=np.int64).astype(np.uint32)
+    hist = [[int(i) for i in rng.integers(0, vocab, 5 + 11 * q)] for q in range(seqs)]
+    ring0 = ring_rows(seqs, ring_len, hist)
+    pad = 0xFFFFFFFF
+    stops = np.full((seqs, 4), pad, np.uint32)
+    stops[:, 0] = 151645
+    per0, _, _, _ = oracle_chain(cases, seeds, stops, rounds, ring0, 0)
+    stops[2, 1] = per0[1]["next"][2]
+    _, want_state, _, want_log = oracle_chain(cases, seeds, stops, rounds, ring0, 0)
+    assert want_state[2, 0] == 1, "the plant must freeze sequence 2 mid-chain"
+    js = []
+    for q, p in enumerate(cases[0]["seq_params"]):
+        js.append(dict(temperature=p.temperature, topK=p.top_k, topP=p.top_p, presencePenalty=p.presence_penalty,
+                       repetitionPenalty=p.repetition_penalty, frequencyPenalty=p.frequency_penalty, softcap=0,
+                       seed=int(seeds[q]), stopIds=[int(x) for x in stops[q] if x != pad]))
+    for r, c in enumerate(cases):
+        c["target"].tofile(os.path.join(d, f"target_{r}.f32"))
+        c["draft"].tofile(os.path.join(d, f"draft_{r}.f32"))
+    with open(os.path.join(d, "specsteps.json"), "w") as f:
+        json.dump({"vocab": vocab, "seqs": seqs, "drafts": L, "rounds": rounds, "params": js, "windows": hist,
+                   "windowSize": ring_len}, f)
+    print("[gpu] node specsteps_gpu.js", d, flush=True)
+    proc = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "specsteps_gpu.js"), d], stdout=subprocess.PIPE,
+                          stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout, flush=True)
+    assert proc.returncode == 0, proc.stdout[-3000:]
+    stop_sets = [set(int(x) for x in stops[q] if x != pad) for q in range(seqs)]
+    want_windows = [list(h) for h in hist]
+    for r in range(rounds):
+        for q in range(seqs):
+            a, nxt = int(want_log[q, r, 0]), int(want_log[q, r, 1])
+            if a > 0:
+                committed = [int(x) for x in want_log[q, r, 2:2 + a - 1]] + [nxt]
+                want_windows[q] += [t for t in committed if t not in stop_sets[q]]
+    for name in ("js_specsteps.json", "js_specsteps_async.json"):
+        with open(os.path.join(d, name)) as f:
+            got = json.load(f)
+        for r in range(rounds):
+            for q in range(seqs):
+                e = got["rounds"][r][q]
+                a = int(want_log[q, r, 0])
+                assert e["a"] == a and e["next"] == int(want_log[q, r, 1]), (name, r, q, e)
+                assert e["drafts"] == [int(x) for x in want_log[q, r, 2:]], (name, r, q)
+                assert e["frozen"] == (a == 0), (name, r, q)
+        assert got["pos"] == [int(x) for x in want_state[:, 2]], name
+        assert got["stopped"] == [bool(x) for x in want_state[:, 0]], name
+        assert got["windows"] == want_windows, name

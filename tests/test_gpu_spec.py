@@ -9,6 +9,7 @@ import oracle as O
 from shared_amd import Params, SasError
 from shared_amd import workloads as W
 from shared_amd.sampler import pack_params, row_hints
+from gpu_helpers import oracle_chain
 
 pytestmark = pytest.mark.gpu
 
@@ -124,29 +125,6 @@ def test_random_sweep(sampler):
         check(run_spec(sampler, c, drafts_given=given), O.spec_exact(c), label)
 
 
-def _oracle_chain(cases, seeds, stop_ids, rounds, ring0, first_round):
-    """orc_spec_exact then orc_spec_commit, round by round, every sequence's
-    history being its ring as of the round's start."""
-    seqs, L = cases[0]["seqs"], cases[0]["drafts"]
-    ring = ring0.copy()
-    ring_len = ring.shape[1] - 1
-    state = np.zeros((seqs, 4), np.uint32)
-    state[:, 1] = first_round
-    log = np.zeros((seqs, rounds, L + 2), np.uint32)
-    per = []
-    for r in range(rounds):
-        c = dict(cases[r])
-        hist = [ring[s, 1:1 + min(int(ring[s, 0]), ring_len)] for s in range(seqs)]
-        c["hist_ids"], c["hist_offsets"] = W._csr(hist)
-        c["seeds"], c["stop_ids"], c["round"] = seeds, stop_ids, int(state[0, 1])
-        frozen = state[:, 0].copy()
-        o = O.spec_exact(c)
-        nxt, acc = O.spec_commit(o["picks"], o["draft_ids"], o["accepted"], stop_ids, state, ring, log)
-        per.append({"frozen": frozen, "draft_ids": o["draft_ids"], "picks": o["picks"], "accepted": acc,
-                    "next": nxt})
-    return per, state, ring, log
-
-
 def test_spec_chain_of_rounds_in_a_graph(sampler):
     """sas_spec_step: four chained rounds recorded into one HIP graph (the
     reference's specChain submits R rounds at once, model.js:867-1008), every
@@ -169,9 +147,9 @@ def test_spec_chain_of_rounds_in_a_graph(sampler):
     stops = np.full((seqs, 4), pad, np.uint32)
     stops[:, 0] = 151645
     # plant: sequence 2's round-1 next token becomes one of its stop ids
-    per0, _, _, _ = _oracle_chain(cases, seeds, stops, rounds, ring0, first)
+    per0, _, _, _ = oracle_chain(cases, seeds, stops, rounds, ring0, first)
     stops[2, 1] = per0[1]["next"][2]
-    per, want_state, want_ring, want_log = _oracle_chain(cases, seeds, stops, rounds, ring0, first)
+    per, want_state, want_ring, want_log = oracle_chain(cases, seeds, stops, rounds, ring0, first)
     assert want_state[2, 0] == 1 and (want_log[2, 2:, 0] == 0).all(), "the plant must freeze seq 2 mid-chain"
     print(f"[gpu] spec chain: {rounds} rounds x {seqs} seqs, L={L}, vocab={vocab}, ring {ring_len}", flush=True)
     sp = dev(pack_params(cases[0]["seq_params"]).view(np.uint8))
