@@ -97,7 +97,7 @@ struct MergeLds {
   double t_pre[SAS_MAX_TOP_K + 8];   // running weight sums
   double t_cum[SAS_MAX_TOP_K + 8];   // running top-p masses
   double t_r[SAS_MAX_TOP_K + 8];     // running draw residuals
-  uint32_t m, clash;
+  uint32_t m;
   double g_v[kWaves];                // greedy rows: each wave's best (value, id), has-any | slow bits
   uint32_t g_id[kWaves];
   uint32_t g_f[kWaves];
@@ -163,14 +163,26 @@ __device__ __forceinline__ int first_true(bool c_lo, bool c_hi, int n) {
   return n;
 }
 
-// Inclusive prefix sum of a double over the wave (a tree of depth 6).
+// A double moved between lanes by DPP (both halves); lanes without a
+// source read +0.0.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ double dpp0_d(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = dpp0<kCtrl, kRowMask>((uint32_t)b), hi = dpp0<kCtrl, kRowMask>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Inclusive prefix sum of a double over the wave (a tree of depth 6):
+// Hillis-Steele within each row of 16 lanes, then the rows' totals carried
+// forward.  Adding the +0.0 of a lane without a source leaves x unchanged
+// (the weights are >= +0.0).
 __device__ __forceinline__ double wave_scan_d(double x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const double y = __shfl_up(x, o, 64);
-    if (lane >= o) x = x + y;
-  }
+  x = x + dpp0_d<kDppRowShr1>(x);
+  x = x + dpp0_d<kDppRowShr2>(x);
+  x = x + dpp0_d<kDppRowShr4>(x);
+  x = x + dpp0_d<kDppRowShr8>(x);
+  x = x + dpp0_d<kDppRowBcast15, 0xA>(x);
+  x = x + dpp0_d<kDppRowBcast31, 0xC>(x);
   return x;
 }
 
@@ -210,17 +222,15 @@ __device__ __forceinline__ uint32_t sample_tail(MergeLds &ml, int kk, int row, d
   } else {
     const double v0 = ml.t_val[0];
     // p_i = exp((v_i - v_0) / T), zero past kk (x / 1 is x)
+    double d_a = lane < kk ? ml.t_val[lane] - v0 : 0.0;
+    double d_b = lane + 64 < kk ? ml.t_val[lane + 64] - v0 : 0.0;
+    if (T != 1.0) {  // uniform: no division at T = 1
+      d_a = d_a / T;
+      if (kk > 64) d_b = d_b / T;
+    }
     double p_a = 0.0, p_b = 0.0;
-    if (lane < kk) {
-      double d = ml.t_val[lane] - v0;
-      if (T != 1.0) d = d / T;
-      p_a = fd_exp(d);
-    }
-    if (lane + 64 < kk) {
-      double d = ml.t_val[lane + 64] - v0;
-      if (T != 1.0) d = d / T;
-      p_b = fd_exp(d);
-    }
+    if (lane < kk) p_a = fd_exp(d_a);
+    if (lane + 64 < kk) p_b = fd_exp(d_b);
     ml.t_p[lane] = p_a;
     ml.t_p[lane + 64] = p_b;
     if (lane < 8) ml.t_p[128 + lane] = 0.0;
@@ -243,11 +253,11 @@ __device__ __forceinline__ uint32_t sample_tail(MergeLds &ml, int kk, int row, d
       const double md = (1e-12 + 1e-13) * sub;
       fast = __ballot((lane <= pk && fabs(ra) <= md) || (lane + 64 <= pk && fabs(rb) <= md)) == 0ull;
     }
-    wave_lds_sync();
     if (fast && !o.probs) {
       cut = c;
       out_id = ml.t_id[pk];
     } else {
+      wave_lds_sync();  // the weights in t_p
       // the weight sum and its prefixes (tokenizer.js:164-167)
       if (lane == 0) chain<false>(ml.t_p, ml.t_pre, kk, 0.0);
       wave_lds_sync();
@@ -388,10 +398,7 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   for (int i = tid; i < kSurvCap + 8; i += kThreads) ml.s_c[i] = 0ull;  // padding: ranks after everything
   ml.s_rank[tid] = 0u;
   ml.s_rank[tid + kThreads] = 0u;
-  if (tid == 0) {
-    ml.m = 0u;
-    ml.clash = 0u;
-  }
+  if (tid == 0) ml.m = 0u;
   const uint32_t np = qok ? (uint32_t)info & 0x7FFFu : 0u;          // plain records of part q
   const uint32_t nm = qok ? ((uint32_t)info >> 16) & 0x7FFFu : 0u;  // member records
   const bool pslow = ((uint32_t)info & kPinfoSlow) != 0u;
@@ -652,14 +659,15 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
     }
     __syncthreads();
     // two inexact values of one key within the first k + 1 ranks: their
-    // order needs the doubles
+    // order needs the doubles (every wave reads the same ranks, so the
+    // waves agree without another barrier)
     const uint32_t nt = min(m, (uint32_t)k + 1u);
-    if ((uint32_t)tid + 1u < nt) {
-      const uint64_t x = ml.t_c[tid], y = ml.t_c[tid + 1];
-      if ((x & kInexact) && (y & kInexact) && (x >> 32) == (y >> 32)) ml.clash = 1u;
+    bool cl = false;
+    for (uint32_t t = (uint32_t)lane; t + 1u < nt; t += 64u) {
+      const uint64_t x = ml.t_c[t], y = ml.t_c[t + 1u];
+      cl = cl || ((x & kInexact) && (y & kInexact) && (x >> 32) == (y >> 32));
     }
-    __syncthreads();
-    if (ml.clash) {
+    if (__ballot(cl) != 0ull) {
       exact = true;
       flags |= SAS_FLAG_SLOW_SELECT;
       for (uint32_t i = (uint32_t)tid; i < kSurvCap; i += kThreads) ml.s_rank[i] = 0u;

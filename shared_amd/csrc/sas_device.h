@@ -242,7 +242,6 @@ __device__ __forceinline__ void wave_best(bool &have, double &v, uint32_t &id) {
   }
 }
 
-// Inclusive prefix sum over the wave.
 // DPP lane moves (GFX9 encodings).  dpp0: lanes whose source lies outside
 // their row (or in a row that row_mask leaves out) read 0; dppx: every
 // source lies inside the row.

@@ -145,6 +145,35 @@ def test_signed_zero_ties(sampler):
     assert (g["ids"] == zeros.min()).all()
 
 
+def test_penalized_members_of_one_key(sampler):
+    # two history members whose penalized doubles differ but round to one
+    # float: their ranks need the doubles (the slow select) exactly when
+    # the lower one is among the first k + 1 ranks
+    a, b_id = 1200, 3400
+    xa, xb = np.float32(10.0), np.float32(10.3)
+    va = float(xa) - 0.3 * 1
+    vb = float(xb) - 0.3 * 2
+    assert va < vb and np.float32(va) == np.float32(vb)
+    vocab, rows = 5000, 5
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((rows, vocab)).astype(np.float32)
+    x[:, a], x[:, b_id] = xa, xb
+    above = rng.choice(np.setdiff1d(np.arange(vocab), [a, b_id]), 20, replace=False)
+    # plain values above the pair: the pair takes ranks (n, n + 1)
+    n_above = [0, 5, 10, 9, 20]
+    for r, n in enumerate(n_above):
+        x[r, above[:n]] = np.float32(20.0) + np.arange(n, dtype=np.float32)
+    hi, ho = W._csr([np.array([a, b_id, b_id])] * rows)
+    b = W.Batch("one_key", x, Params(temperature=1.0, top_k=10, top_p=1.0, frequency_penalty=0.3),
+                hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+    g, _ = check(sampler, b, label="one_key")
+    for r, n in enumerate(n_above):
+        slow = bool(g["flags"][r] & FLAG_SLOW_SELECT)
+        assert slow == (n + 1 <= 10), (r, n, g["flags"][r])
+        if n + 1 < 10:
+            assert g["cand_ids"][r, n] == b_id and g["cand_ids"][r, n + 1] == a
+
+
 @pytest.mark.parametrize("vocab", [1, 2, 3, 4, 5, 6, 7, 4097, 8191])
 def test_small_and_ragged_vocab(sampler, vocab):
     # rows of fewer than 4 logits, and rows whose end cuts a float4
