@@ -98,6 +98,7 @@ struct MergeLds {
   double t_cum[SAS_MAX_TOP_K + 8];   // running top-p masses
   double t_r[SAS_MAX_TOP_K + 8];     // running draw residuals
   uint32_t m;
+  uint32_t p_np[kMaxParts];          // the parts' plain record counts
   double g_v[kWaves];                // greedy rows: each wave's best (value, id), has-any | slow bits
   uint32_t g_id[kWaves];
   uint32_t g_f[kWaves];
@@ -370,8 +371,8 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   const int P = a.parts;
   const bool greedy = !(p.temperature > 0.0);
   const int k = greedy ? 1 : min(max(p.top_k, 1), SAS_MAX_TOP_K);
-  // G threads per part; thread (q, sub) reads plain records sub, sub + G,
-  // ... and member record sub of part q
+  // Thread (q, sub) = (tid / G, tid % G), G threads per part, reads part
+  // q's counts and bound and member record sub of part q.
   const int G = kThreads / P;
   const int q = tid / G, sub = tid - q * G;
   const bool qok = q < P;
@@ -379,16 +380,44 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   const uint64_t *rq = a.rec + pq * kListCap;
   const uint4 *mq = a.mrec + pq * kMemSlots;
 
-  // ---- loads: the part's counts and bound, its first kMR * G plain and
-  // first G member records, all in flight at once ----
+  // ---- loads, all in flight at once, none behind a branch ----
+  // The part's counts first: they go to LDS while the records still arrive.
+  const uint64_t i4 = load_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + min(q, P - 1));
+  const uint4 m4 = load_rec4(mq + min(sub, kMemSlots - 1));
+  // Plain records: the first 16 Lc slots of every part as whole 128-byte
+  // lines.  Lanes 8 g .. 8 g + 7 of a wave read one line, 16 bytes (two
+  // records) each; load i of reader R = tid / 8 is chunk z = R + (kThreads
+  // / 8) i, line z / P of part z % P.  A chunk past the part's Lc lines reads
+  // line 0 again, and it is dropped with the slots past the part's count.
+  // (Lanes reading 16-byte pieces of 64 different lines per load took the
+  // step longer: each load then asks the cache for 64 lines.)
+  constexpr int kReaders = kThreads / 8, kChunks = kMR / 2;
+  static_assert(kMR % 2 == 0, "records in pairs");
+  static_assert(kReaders * kChunks >= kMaxParts, "at least one line of every part");
+  const int R = tid >> 3, l8 = tid & 7;
+  const int Lc = min(kReaders * kChunks / P, kListCap / 16);
+  const int zdiv = kReaders / P, zmod = kReaders - zdiv * P;  // chunk z + kReaders: part + zmod, line + zdiv
+  const uint4 *rb = reinterpret_cast<const uint4 *>(a.rec);
+  const uint32_t rrow = (uint32_t)row * (uint32_t)P;
   uint64_t rec[kMR];
+  {
+    int zq = R % P, zc = R / P;
 #pragma unroll
-  for (int r = 0; r < kMR; ++r) {
-    const int j = sub + G * r;
-    rec[r] = qok && j < kListCap ? load_rec(rq + j) : 0ull;
+    for (int i = 0; i < kChunks; ++i) {
+      const uint32_t at = (rrow + (uint32_t)zq) * (uint32_t)(kListCap / 2) + 8u * (uint32_t)(zc < Lc ? zc : 0) + (uint32_t)l8;
+      const uint4 x = load_rec4(rb + at);
+      rec[2 * i] = ((uint64_t)x.y << 32) | x.x;
+      rec[2 * i + 1] = ((uint64_t)x.w << 32) | x.z;
+      zq += zmod;
+      zc += zdiv;
+      if (zq >= P) {
+        zq -= P;
+        ++zc;
+      }
+    }
   }
-  const uint4 mr = qok ? load_rec4(mq + sub) : make_uint4(0u, 0u, 0u, 0u);
-  const uint64_t info = qok ? load_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + q) : 0ull;
+  const uint4 mr = qok ? m4 : make_uint4(0u, 0u, 0u, 0u);
+  const uint64_t info = qok ? i4 : 0ull;
   const int srow = a.group > 1 ? row / a.group : row;
   const double u_row = greedy        ? 0.0
                        : a.spec_seeds ? pcg_uniform(a.spec_seeds[srow], a.sp_state ? a.sp_state[4 * srow + 1] : a.spec_round,
@@ -399,15 +428,17 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   ml.s_rank[tid] = 0u;
   ml.s_rank[tid + kThreads] = 0u;
   if (tid == 0) ml.m = 0u;
-  const uint32_t np = qok ? (uint32_t)info & 0x7FFFu : 0u;          // plain records of part q
-  const uint32_t nm = qok ? ((uint32_t)info >> 16) & 0x7FFFu : 0u;  // member records
+  // plain and member records of part q (within its slots whatever the word holds)
+  const uint32_t np = min((uint32_t)info & 0x7FFFu, (uint32_t)kListCap);
+  const uint32_t nm = min(((uint32_t)info >> 16) & 0x7FFFu, (uint32_t)kMemSlots);
   const bool pslow = ((uint32_t)info & kPinfoSlow) != 0u;
   const uint32_t bq = (uint32_t)(info >> 32);                       // the part's bound key
-  const int nfast = min((int)np, G * kMR);
-  // records past the first kMR * G plain or G member ones of a part (rarely
-  // any) are read again where they are used: f(key, composite, exact value)
+  if (qok && sub == 0) ml.p_np[q] = np;
+  lds_barrier();  // every part's count (the records stay in flight)
+  // records past a part's first 16 Lc plain or G member ones (rarely any)
+  // are read again where they are used: f(key, composite, exact value)
   auto for_extra = [&](auto f) __attribute__((always_inline)) {
-    for (int j = sub + G * kMR; j < (int)np; j += G) {
+    for (int j = 16 * Lc + sub; j < (int)np; j += G) {
       const uint64_t rc = load_rec(rq + j);
       const float x = __uint_as_float((uint32_t)rc);
       const uint32_t kx = okey(x);
@@ -423,11 +454,31 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   // a plain record's value is fkey(key): keep (key, id) pairs
   uint32_t key[kMR], rid[kMR];
   uint32_t kmax = 0u;
+  {
+    int zq = R % P, zc = R / P;
 #pragma unroll
-  for (int r = 0; r < kMR; ++r) {
-    key[r] = sub + G * r < nfast ? okey(__uint_as_float((uint32_t)rec[r])) : 0u;
-    rid[r] = (uint32_t)(rec[r] >> 32);
-    kmax = max(kmax, key[r]);
+    for (int i = 0; i < kChunks; ++i) {
+      // slots 16 zc + 2 l8 and the next, kept below the part's count
+      const uint32_t j0 = 16u * (uint32_t)zc + 2u * (uint32_t)l8;
+      const uint32_t n = zc < Lc ? ml.p_np[zq] : 0u;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 2 * i + h;
+        // okey of every slot, kept where the slot holds a record (no
+        // branch); the opaque copy lets the raw record's register go
+        const uint32_t kx = okey(__uint_as_float((uint32_t)rec[r]));
+        key[r] = kx & (0u - (uint32_t)(j0 + (uint32_t)h < n));
+        rid[r] = (uint32_t)(rec[r] >> 32);
+        asm volatile("" : "+v"(key[r]));
+        kmax = max(kmax, key[r]);
+      }
+      zq += zmod;
+      zc += zdiv;
+      if (zq >= P) {
+        zq -= P;
+        ++zc;
+      }
+    }
   }
   const uint32_t mkey = (uint32_t)sub < nm ? okey(__uint_as_float(mr.x)) : 0u;
   kmax = max(kmax, mkey);
@@ -1508,6 +1559,7 @@ int merge_slots(const SampleArgs &a) {
 }
 
 hipError_t launch_merge(const SampleArgs &a, hipStream_t stream) {
+  if (a.parts < 1 || a.parts > kMaxParts) return hipErrorInvalidValue;  // the merge's count table
   switch (merge_slots(a)) {
     case 4: hipLaunchKernelGGL(sample_merge_kernel<4>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a); break;
     case 8: hipLaunchKernelGGL(sample_merge_kernel<8>, dim3((unsigned)a.rows), dim3(kThreads), 0, stream, a); break;
