@@ -386,15 +386,17 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
   const uint4 m4 = load_rec4(mq + min(sub, kMemSlots - 1));
   // Plain records: the first 16 Lc slots of every part as whole 128-byte
   // lines.  Lanes 8 g .. 8 g + 7 of a wave read one line, 16 bytes (two
-  // records) each; load i of reader R = tid / 8 is chunk z = R + (kThreads
-  // / 8) i, line z / P of part z % P.  A chunk past the part's Lc lines reads
-  // line 0 again, and it is dropped with the slots past the part's count.
-  // (Lanes reading 16-byte pieces of 64 different lines per load took the
-  // step longer: each load then asks the cache for 64 lines.)
+  // records) each; load i of reader R = 4 g + wave is chunk z = R +
+  // (kThreads / 8) i, line z / P of part z % P.  Readers alternate over the
+  // waves, so that every wave holds a fair share of every part's lines (the
+  // bound below takes the weakest wave).  A chunk past the part's Lc lines
+  // reads line 0 again, and it is dropped with the slots past the part's
+  // count.  (Lanes reading 16-byte pieces of 64 different lines per load
+  // took the step longer: each load then asks the cache for 64 lines.)
   constexpr int kReaders = kThreads / 8, kChunks = kMR / 2;
   static_assert(kMR % 2 == 0, "records in pairs");
   static_assert(kReaders * kChunks >= kMaxParts, "at least one line of every part");
-  const int R = tid >> 3, l8 = tid & 7;
+  const int R = (lane >> 3) * kWaves + wave, l8 = tid & 7;
   const int Lc = min(kReaders * kChunks / P, kListCap / 16);
   const int zdiv = kReaders / P, zmod = kReaders - zdiv * P;  // chunk z + kReaders: part + zmod, line + zdiv
   const uint4 *rb = reinterpret_cast<const uint4 *>(a.rec);
