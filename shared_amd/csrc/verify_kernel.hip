@@ -222,8 +222,10 @@ __device__ __forceinline__ bool joint_sums(const float xt[kPerThread], const flo
   return true;
 }
 
+// Seven waves per SIMD (72 VGPRs): the kernel is bound by its VALU issue
+// and hides its loads behind the other waves.
 template <bool kMask>
-__global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
+__global__ __launch_bounds__(kThreads, 7) void verify_stats_kernel(VerifyArgs a) {
   __shared__ StatsLds l;
   const int c = blockIdx.x, pos = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
       a.dtok[2 * pos + 1] = allowed ? a.draft[((int64_t)s * a.L + j) * a.stride + d] : __builtin_nanf("");
     }
   }
-  const uint32_t okt = nan_free(xt, ok), okq = has_draft ? nan_free(xq, ok) : 0u;
+  uint32_t okt = nan_free(xt, ok), okq = has_draft ? nan_free(xq, ok) : 0u;
   // the chunk's masked maxima of both rows
   float mt = -__builtin_inff(), mq = -__builtin_inff();
 #pragma unroll
@@ -253,6 +255,9 @@ __global__ __launch_bounds__(kThreads) void verify_stats_kernel(VerifyArgs a) {
     if ((okt >> i) & 1u) mt = fmaxf(mt, xt[i]);
     if ((okq >> i) & 1u) mq = fmaxf(mq, xq[i]);
   }
+  // opaque copies: the bit tests below are made again from the words, not
+  // kept from the loop above (32 lane masks would not fit the SGPRs)
+  asm volatile("" : "+v"(okt), "+v"(okq));
   mt = wave_max(mt);
   mq = wave_max(mq);
   if (lane == 0) {
