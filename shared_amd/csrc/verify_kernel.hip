@@ -48,6 +48,7 @@ namespace sas {
 namespace {
 
 constexpr int kPerThread = kVChunk / kThreads;  // 16 ids per thread
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 static_assert(kPerThread == 16, "a thread owns four float4 of a chunk");
 
 __device__ __forceinline__ double dneg_inf() { return -__longlong_as_double(0x7ff0000000000000ll); }
@@ -348,21 +349,54 @@ __device__ Decided decide(const VerifyArgs &a, int s, DecideLds &l) {
     dxq = a.dtok[2 * pos + 1];
     u1 = a.uniforms[(int64_t)pos * 2];
   }
-  for (int j = wave; j < P1; j += kWaves) {
-    const double *st = a.stats + (int64_t)(s * P1 + j) * a.chunks * 4;
-    for (int side = 0; side < (j < L ? 2 : 1); ++side) {
-      double m = dneg_inf();
-      for (int c = lane; c < a.chunks; c += 64) m = fmax(m, st[c * 4 + side * 2]);
-      m = wave_max_d(m);
-      double z = 0.0;
-      for (int c = lane; c < a.chunks; c += 64) {
-        const double zc = st[c * 4 + side * 2 + 1];
-        if (zc > 0.0) z += zc * exp_sum((st[c * 4 + side * 2] - m) * a.inv_t);
+  if (a.chunks <= 64 && P1 <= 2 * kWaves) {
+    // at most two positions per wave and one chunk per lane: both
+    // positions' statistics are loaded at once (clamped into the existing
+    // ones), then combined as below
+    const bool cok = lane < a.chunks;
+    const int c = min(lane, a.chunks - 1);
+    f64x2 st[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = min(wave + kWaves * i, P1 - 1);
+      const f64x2 *p = reinterpret_cast<const f64x2 *>(a.stats + ((int64_t)(s * P1 + j) * a.chunks + c) * 4);
+      st[i][0] = p[0];  // (max, sum) of the target row
+      st[i][1] = p[1];  // and of the draft row
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = wave + kWaves * i;
+      if (j < P1) {
+        for (int side = 0; side < (j < L ? 2 : 1); ++side) {
+          const double mc = st[i][side].x, zc = cok ? st[i][side].y : 0.0;
+          const double m = wave_max_d(fmax(dneg_inf(), cok ? mc : dneg_inf()));
+          double z = 0.0;
+          if (zc > 0.0) z += zc * exp_sum((mc - m) * a.inv_t);
+          z = wave_sum_d(z);
+          if (lane == 0) {
+            l.m[j][side] = m;
+            l.z[j][side] = z;
+          }
+        }
       }
-      z = wave_sum_d(z);
-      if (lane == 0) {
-        l.m[j][side] = m;
-        l.z[j][side] = z;
+    }
+  } else {
+    for (int j = wave; j < P1; j += kWaves) {
+      const double *st = a.stats + (int64_t)(s * P1 + j) * a.chunks * 4;
+      for (int side = 0; side < (j < L ? 2 : 1); ++side) {
+        double m = dneg_inf();
+        for (int c = lane; c < a.chunks; c += 64) m = fmax(m, st[c * 4 + side * 2]);
+        m = wave_max_d(m);
+        double z = 0.0;
+        for (int c = lane; c < a.chunks; c += 64) {
+          const double zc = st[c * 4 + side * 2 + 1];
+          if (zc > 0.0) z += zc * exp_sum((st[c * 4 + side * 2] - m) * a.inv_t);
+        }
+        z = wave_sum_d(z);
+        if (lane == 0) {
+          l.m[j][side] = m;
+          l.z[j][side] = z;
+        }
       }
     }
   }
