@@ -565,9 +565,18 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
   const int s = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int L = a.L, P1 = L + 1;
+  const int C = a.chunks;
+  const double *part = a.part + (int64_t)s * C * 2;
+  // Loads that do not wait for the accepted count come first: wave 0's
+  // chunk masses (one chunk per lane when there are at most 64) and the
+  // second uniform of every position of the sequence (P1 <= 64).
+  f64x2 pc = {0.0, 0.0};
+  if (wave == 0 && C <= 64) pc = *reinterpret_cast<const f64x2 *>(part + 2 * min(lane, C - 1));
+  const double u2c = a.uniforms[((int64_t)s * P1 + min(lane, P1 - 1)) * 2 + 1];
   const double *q = a.seqrec + (int64_t)s * 8;
   const int acc = (int)q[0];
   const int pos = s * P1 + acc;
+  const double u2 = __shfl(u2c, acc, 64);
   if (tid == 0) {
     l.found = SAS_NO_TOKEN;
     l.last = 0;
@@ -577,23 +586,27 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
   if (tid <= L && tid != acc)
     a.out_tokens[(int64_t)s * P1 + tid] = tid < acc ? a.draft_ids[(int64_t)s * L + tid] : SAS_NO_TOKEN;
   if (tid == 0) a.out_accepted[s] = acc;
-  const double u2 = a.uniforms[(int64_t)pos * 2 + 1];
 
   // Which weights draw: the residual unless it is all zero, else the target.
   if (wave == 0) {
-    const int C = a.chunks, R = (C + 63) / 64;
+    const int R = (C + 63) / 64;
     const int c0 = lane * R, c1 = min(C, c0 + R);
-    const double *part = a.part + (int64_t)s * C * 2;
+    // chunk c's residual (col 0) or target (col 1) mass; with one chunk
+    // per lane (c == lane) from the registers
+    auto wpart = [&](int c, int col) __attribute__((always_inline)) -> double {
+      if (C <= 64) return col ? pc.y : pc.x;
+      return part[c * 2 + col];
+    };
     bool resid = acc < L;
     if (resid) {
       double v = 0.0;
-      for (int c = c0; c < c1; ++c) v += part[c * 2];
+      for (int c = c0; c < c1; ++c) v += wpart(c, 0);
       v = wave_incl_scan_d(v);
       resid = __shfl(v, 63, 64) > 0.0;
     }
     const int col = resid ? 0 : 1;
     double v = 0.0;
-    for (int c = c0; c < c1; ++c) v += part[c * 2 + col];
+    for (int c = c0; c < c1; ++c) v += wpart(c, col);
     const double incl = wave_incl_scan_d(v);
     double excl = __shfl_up(incl, 1, 64);
     if (lane == 0) excl = 0.0;
@@ -605,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void verify_draw_kernel(VerifyArgs a) {
     int lastc = -1;
     double last_before = 0.0;
     for (int c = c0; c < c1; ++c) {
-      const double wc = part[c * 2 + col];
+      const double wc = wpart(c, col);
       if (!(wc > 0.0)) continue;
       lastc = c;
       last_before = cum;
