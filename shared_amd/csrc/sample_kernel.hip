@@ -71,15 +71,16 @@ __device__ __forceinline__ bool before(double va, uint32_t ia, double vb, uint32
 
 // ----------------------------------------------------------------- merge --
 //
-// The block that finishes a row's last part merges the row: it loads every
+// One block per row merges the row after the parts kernel: it loads every
 // part's records, bounds the row's k-th largest key by the j-th largest of
 // each wave's lane maxima, ranks the records at or above the bound exactly
 // by (value desc, id asc) and runs the reference's sample() tail.
 
 // The merge kernel loads kMR plain record slots per thread before the
-// counts are known (G threads per part: the part's first kMR * G slots); a
-// part's records past them are loaded where they are used.  launch_merge
-// picks kMR from the expected count per part (about 2 k plus a few).
+// counts are known (between them a part's first kThreads * kMR / parts
+// slots, as whole 128-byte lines); a part's records past them are loaded
+// where they are used.  launch_merge picks kMR from the expected count per
+// part (about 2 k plus a few).
 constexpr int kMRMax = 16;
 constexpr int kSurvCap = 512;     // survivors the merge ranks
 constexpr uint32_t kInexact = 0x80000000u;  // composite bit: the exact value lies above the key
