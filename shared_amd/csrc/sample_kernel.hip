@@ -1344,20 +1344,25 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
 
   // ---- records: each wave's values after those of the waves before it, then
   // the exact plain values, in the part's own kListCap slots; the members in
-  // the part's own member slots
+  // the part's own member slots.  The plain records are staged in LDS (over
+  // the lists, read above) and then stored as whole lines, 16 bytes per
+  // thread: stored where they were made, each store instruction touched
+  // many partly written lines.
   uint32_t off = 0u;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) off += w < wave ? nw[w] : 0u;
   const uint32_t nplain = nw[0] + nw[1] + nw[2] + nw[3];
   uint64_t *rrow = a.rec + ((int64_t)row * P + part) * kListCap;
   uint4 *mrow4 = a.mrec + ((int64_t)row * P + part) * kMemSlots;
+  uint64_t *stg = reinterpret_cast<uint64_t *>(L.q_val);
+  static_assert(sizeof(L.q_val) + sizeof(L.q_base) == kListCap * sizeof(uint64_t), "the lists hold a part's records");
   {
     uint32_t j = off + qpre;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if ((pm >> c) & 1u) {
         const float x = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
-        put_rec(rrow + j, (uint64_t)__float_as_uint(x) | ((uint64_t)(qid + (uint32_t)c) << 32));
+        stg[j] = (uint64_t)__float_as_uint(x) | ((uint64_t)(qid + (uint32_t)c) << 32);
         ++j;
       }
     }
@@ -1370,8 +1375,16 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       put_rec(d + 1, (uint64_t)__double_as_longlong(xv));
     } else {
       const uint32_t j = nplain + atomicAdd(&s_nxw, 1u);
-      put_rec(rrow + j, (uint64_t)__float_as_uint((float)xv) | ((uint64_t)xid << 32));
+      stg[j] = (uint64_t)__float_as_uint((float)xv) | ((uint64_t)xid << 32);
     }
+  }
+  lds_barrier();
+  {
+    // nplain + the exact plain values <= kListCap (else the exact
+    // selection ran); the slot past an odd count is written too (unread)
+    const uint32_t ntot = nplain + nx - nxm;
+    for (uint32_t e = 2u * (uint32_t)tid; e < ntot; e += 2u * (uint32_t)kThreads)
+      *reinterpret_cast<uint4 *>(rrow + e) = *reinterpret_cast<const uint4 *>(stg + e);
   }
   // the part's counts, bound and slow-selection flag
   if (tid == 0)
