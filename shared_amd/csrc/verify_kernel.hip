@@ -97,45 +97,58 @@ __device__ __forceinline__ void load_strided(const float *row, int64_t base, int
     for (int f = 0; f < 4; ++f)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
+        // clamped into the row: every load issued, none behind a branch
         const int64_t id = base + (f * kThreads + tid) * 4 + k;
-        x[f * 4 + k] = id < vocab ? row[id] : 0.0f;
+        const float t = row[min(id, (int64_t)vocab - 1)];
+        x[f * 4 + k] = id < vocab ? t : 0.0f;
       }
   }
 }
 
-// Bit f*4+k set: id base + (f*256+t)*4 + k is below vocab and its mask bit is set.
+// Bit f*4+k set: id base + (f*256+t)*4 + k is below vocab and its mask bit
+// is set.  The four mask words are loaded unconditionally (clamped into the
+// row), so that they are in flight together.
 template <bool kMask>
 __device__ __forceinline__ uint32_t allow_strided(const uint32_t *mrow, int64_t base, int vocab) {
   const int tid = threadIdx.x;
+  const int64_t last_word = ((int64_t)vocab + 31) / 32 - 1;
+  uint32_t mw[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int64_t id0 = base + (f * kThreads + tid) * 4;
+    mw[f] = kMask ? mrow[min(id0 >> 5, last_word)] : ~0u;
+  }
   uint32_t bits = 0;
 #pragma unroll
   for (int f = 0; f < 4; ++f) {
     const int64_t id0 = base + (f * kThreads + tid) * 4;
-    uint32_t nib = 0;
-    if (id0 < vocab) {
-      nib = kMask ? (mrow[id0 >> 5] >> (id0 & 31)) & 0xFu : 0xFu;
-      const int64_t left = vocab - id0;
-      if (left < 4) nib &= (1u << left) - 1u;
-    }
-    bits |= nib << (f * 4);
+    // ids of the four below vocab: 0 .. 4 (no branch, so the loads stay
+    // ahead of every use)
+    const int left = (int)min(max((int64_t)vocab - id0, (int64_t)0), (int64_t)4);
+    bits |= ((mw[f] >> (uint32_t)(id0 & 31)) & ((1u << left) - 1u)) << (f * 4);
   }
   return bits;
 }
 
-// The number of set bits of `ok` over the wave.
-__device__ __forceinline__ uint32_t wave_count(uint32_t ok) {
-  const uint32_t n = (uint32_t)__popc(ok);
-  uint32_t tot = 0u;
+// Places n items per lane in one list for the wave: `pre` the lane's first
+// slot (the items of the lanes below it), `tot` the wave's total.  n < 32.
+__device__ __forceinline__ void wave_place(uint32_t n, uint32_t &pre, uint32_t &tot) {
+  pre = 0u;
+  tot = 0u;
 #pragma unroll
-  for (int bit = 0; bit < 5; ++bit) tot += (uint32_t)__popcll(__ballot((n >> bit) & 1u)) << bit;
-  return tot;
+  for (int bit = 0; bit < 5; ++bit) {
+    const uint64_t bb = __ballot((n >> bit) & 1u);
+    pre += lanes_below(bb) << bit;
+    tot += (uint32_t)__popcll(bb) << bit;
+  }
 }
 
 // A wave's allowed values of one side, packed, when they are few.
 constexpr int kCompact = 256;
-// pk_n words: the wave's values were packed for both rows (the same ids),
-// or for the target row only (a position without a draft); the count in
-// the low bits.  0: not packed (too many allowed, or the rows' NaNs differ).
+// pk_n words: the wave's allowed ids' values were packed for both rows
+// (a draft value may be NaN), or for the target row only (a position
+// without a draft); the count in the low bits.  0: not packed (more than
+// kCompact allowed, or a target value among them is NaN).
 constexpr uint32_t kPkJoint = 1u << 30;
 constexpr uint32_t kPkTarget = 1u << 29;
 constexpr uint32_t kPkCount = 0xFFFFu;
@@ -143,7 +156,6 @@ constexpr uint32_t kPkCount = 0xFFFFu;
 struct StatsLds {
   float m[kWaves][2];
   double z[kWaves][2];
-  uint32_t pk[kWaves];  // how each wave packed its values (pk_n)
   float cv[kWaves][2][kCompact];
 };
 
@@ -161,14 +173,8 @@ __device__ __forceinline__ uint32_t nan_free(const float x[kPerThread], uint32_t
 __device__ __forceinline__ double side_sum(const float x[kPerThread], uint32_t ok, double M, double inv_t,
                                            float *cv) {
   const int lane = threadIdx.x & 63;
-  const uint32_t n = (uint32_t)__popc(ok);
-  uint32_t pre = 0u, tot = 0u;
-#pragma unroll
-  for (int bit = 0; bit < 5; ++bit) {
-    const uint64_t bb = __ballot((n >> bit) & 1u);
-    pre += lanes_below(bb) << bit;
-    tot += (uint32_t)__popcll(bb) << bit;
-  }
+  uint32_t pre, tot;
+  wave_place((uint32_t)__popc(ok), pre, tot);
   double z = 0.0;
   if (tot <= (uint32_t)kCompact) {
     uint32_t j = pre;
@@ -187,44 +193,8 @@ __device__ __forceinline__ double side_sum(const float x[kPerThread], uint32_t o
   return wave_sum_d(z);
 }
 
-// Both sides' sums when they allow the same ids (the usual case: a NaN
-// logit in one row and not the other is rare): one packing of the allowed
-// ids' two values into the wave's LDS slots serves both, when at most
-// kCompact are allowed.  Returns false (nothing summed) otherwise.
-__device__ __forceinline__ bool joint_sums(const float xt[kPerThread], const float xq[kPerThread], uint32_t ok,
-                                           double Mt, double Mq, double inv_t, float *cvt, float *cvq, double &zt,
-                                           double &zq) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t n = (uint32_t)__popc(ok);
-  uint32_t pre = 0u, tot = 0u;
-#pragma unroll
-  for (int bit = 0; bit < 5; ++bit) {
-    const uint64_t bb = __ballot((n >> bit) & 1u);
-    pre += lanes_below(bb) << bit;
-    tot += (uint32_t)__popcll(bb) << bit;
-  }
-  if (tot > (uint32_t)kCompact) return false;
-  uint32_t j = pre;
-#pragma unroll
-  for (int i = 0; i < kPerThread; ++i)
-    if ((ok >> i) & 1u) {
-      cvt[j] = xt[i];
-      cvq[j] = xq[i];
-      ++j;
-    }
-  wave_lds_sync();
-  double st = 0.0, sq = 0.0;
-  for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
-    st += exp_sum(((double)cvt[e] - Mt) * inv_t);
-    sq += exp_sum(((double)cvq[e] - Mq) * inv_t);
-  }
-  zt = wave_sum_d(st);
-  zq = wave_sum_d(sq);
-  return true;
-}
-
-// Seven waves per SIMD (72 VGPRs): the kernel is bound by its VALU issue
-// and hides its loads behind the other waves.
+// Seven waves per SIMD (72 VGPRs): the kernel hides its loads behind the
+// other waves.
 template <bool kMask>
 __global__ __launch_bounds__(kThreads, 7) void verify_stats_kernel(VerifyArgs a) {
   __shared__ StatsLds l;
@@ -248,17 +218,51 @@ __global__ __launch_bounds__(kThreads, 7) void verify_stats_kernel(VerifyArgs a)
       a.dtok[2 * pos + 1] = allowed ? a.draft[((int64_t)s * a.L + j) * a.stride + d] : __builtin_nanf("");
     }
   }
-  uint32_t okt = nan_free(xt, ok), okq = has_draft ? nan_free(xq, ok) : 0u;
-  // the chunk's masked maxima of both rows
+  // The wave's allowed ids, when at most kCompact of its 1,024 (a sparse
+  // mask): both rows' values packed into the wave's LDS slots in id order,
+  // NaNs included, so that the NaN tests, the maxima and the exponentials
+  // run over those values only.  Otherwise every value is tested in the
+  // registers.
+  uint32_t pre, tot;
+  wave_place((uint32_t)__popc(ok), pre, tot);
+  const bool packed = tot <= (uint32_t)kCompact;  // uniform over the wave
+  float *cvt = l.cv[wave][0], *cvq = l.cv[wave][1];
   float mt = -__builtin_inff(), mq = -__builtin_inff();
+  uint32_t okt = 0u, okq = 0u;
+  bool tnan = false;  // a packed target value is NaN
+  if (packed) {
+    uint32_t jj = pre;
 #pragma unroll
-  for (int i = 0; i < kPerThread; ++i) {
-    if ((okt >> i) & 1u) mt = fmaxf(mt, xt[i]);
-    if ((okq >> i) & 1u) mq = fmaxf(mq, xq[i]);
+    for (int i = 0; i < kPerThread; ++i)
+      if ((ok >> i) & 1u) {
+        cvt[jj] = xt[i];
+        if (has_draft) cvq[jj] = xq[i];
+        ++jj;
+      }
+    wave_lds_sync();
+    // a NaN compares false: it never becomes a maximum
+    for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
+      const float t = cvt[e];
+      tnan |= t != t;
+      mt = t > mt ? t : mt;
+      if (has_draft) {
+        const float q = cvq[e];
+        mq = q > mq ? q : mq;
+      }
+    }
+  } else {
+    okt = nan_free(xt, ok);
+    okq = has_draft ? nan_free(xq, ok) : 0u;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      if ((okt >> i) & 1u) mt = fmaxf(mt, xt[i]);
+      if ((okq >> i) & 1u) mq = fmaxf(mq, xq[i]);
+    }
+    // opaque copies: the bit tests below are made again from the words, not
+    // kept from the loop above (32 lane masks would not fit the SGPRs)
+    asm volatile("" : "+v"(okt), "+v"(okq));
   }
-  // opaque copies: the bit tests below are made again from the words, not
-  // kept from the loop above (32 lane masks would not fit the SGPRs)
-  asm volatile("" : "+v"(okt), "+v"(okq));
+  // the chunk's maxima of both rows (allowed, not NaN)
   mt = wave_max(mt);
   mq = wave_max(mq);
   if (lane == 0) {
@@ -274,35 +278,43 @@ __global__ __launch_bounds__(kThreads, 7) void verify_stats_kernel(VerifyArgs a)
   }
   // sums of exp((x - max) / T)
   const double Mt = (double)bt, Mq = (double)bq;
-  double zt = 0.0, zq = 0.0;
-  const bool same = has_draft && __ballot(okt != okq) == 0ull;  // uniform over the wave
-  const bool joint = same && joint_sums(xt, xq, okt, Mt, Mq, a.inv_t, l.cv[wave][0], l.cv[wave][1], zt, zq);
-  if (!joint) {
-    zt = side_sum(xt, okt, Mt, a.inv_t, l.cv[wave][0]);
-    zq = has_draft ? side_sum(xq, okq, Mq, a.inv_t, l.cv[wave][1]) : 0.0;
+  double zt, zq;
+  uint32_t pk = 0u;  // how the wave's values were packed for the decide pass
+  if (packed) {
+    double st = 0.0, sq = 0.0;
+    for (uint32_t e = (uint32_t)lane; e < tot; e += 64u) {
+      const float t = cvt[e];
+      if (t == t) st += exp_sum(((double)t - Mt) * a.inv_t);
+      if (has_draft) {
+        const float q = cvq[e];
+        if (q == q) sq += exp_sum(((double)q - Mq) * a.inv_t);
+      }
+    }
+    zt = wave_sum_d(st);
+    zq = has_draft ? wave_sum_d(sq) : 0.0;
+    // the decide pass takes packed target values that are not NaN (a NaN
+    // draft value it tests itself)
+    if (__ballot(tnan) == 0ull) pk = (has_draft ? kPkJoint : kPkTarget) | tot;
+  } else {
+    zt = side_sum(xt, okt, Mt, a.inv_t, cvt);
+    zq = has_draft ? side_sum(xq, okq, Mq, a.inv_t, cvq) : 0.0;
   }
-  // how the wave's values were packed: the count of its allowed target ids
-  // (both helpers pack exactly when it is at most kCompact)
-  const uint32_t nt = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_count(okt));
-  const uint32_t pk = nt > (uint32_t)kCompact ? 0u : joint ? (kPkJoint | nt) : !has_draft ? (kPkTarget | nt) : 0u;
   if (lane == 0) {
     l.z[wave][0] = zt;
     l.z[wave][1] = zq;
-    l.pk[wave] = pk;
   }
-  __syncthreads();
   // the wave's packed values (in the order the decide pass packs them from
   // the rows, so that its sums are the same) and how they were packed
   {
-    const uint32_t pw = l.pk[wave], n = pw & kPkCount;
     const int64_t w = ((int64_t)pos * a.chunks + c) * kWaves + wave;
     float *pv = a.pk_v + w * (2 * kCompact);
-    for (uint32_t e = (uint32_t)lane; pw && e < n; e += 64u) {
-      pv[e] = l.cv[wave][0][e];
-      if (pw & kPkJoint) pv[kCompact + e] = l.cv[wave][1][e];
+    for (uint32_t e = (uint32_t)lane; pk && e < tot; e += 64u) {
+      pv[e] = cvt[e];
+      if (pk & kPkJoint) pv[kCompact + e] = cvq[e];
     }
-    if (lane == 0) a.pk_n[w] = pw;
+    if (lane == 0) a.pk_n[w] = pk;
   }
+  __syncthreads();
   if (tid == 0) {
     double t = l.z[0][0], q = l.z[0][1];
 #pragma unroll
@@ -479,14 +491,8 @@ __global__ __launch_bounds__(kThreads) void verify_decide_kernel(VerifyArgs a) {
     const uint32_t ok = nan_free(xt, allow_strided<kMask>(kMask ? a.mask + (int64_t)pos * a.mask_stride : nullptr,
                                                            base, a.vocab));
     // the allowed ids' values, packed per wave when few (a sparse mask)
-    const uint32_t n = (uint32_t)__popc(ok);
-    uint32_t pre = 0u, tot = 0u;
-#pragma unroll
-    for (int bit = 0; bit < 5; ++bit) {
-      const uint64_t bb = __ballot((n >> bit) & 1u);
-      pre += lanes_below(bb) << bit;
-      tot += (uint32_t)__popcll(bb) << bit;
-    }
+    uint32_t pre, tot;
+    wave_place((uint32_t)__popc(ok), pre, tot);
     if (tot <= (uint32_t)kCompact) {
       uint32_t jj = pre;
 #pragma unroll
