@@ -354,8 +354,8 @@ __device__ __forceinline__ void step_feedback(const SampleArgs &a, int row, uint
 
 // Loads of the records the row's parts published.  A record line is written
 // only by its part (whole lines per part and per row of part counts) and read
-// only by the row's merging block, after the part counted itself: the reading
-// CU and its L2 hold no earlier copy of the line.
+// once, by the row's merge block in the next launch: nontemporal, since no
+// other block reads it again.
 __device__ __forceinline__ uint64_t load_rec(const uint64_t *p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ uint4 load_rec4(const uint4 *p) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -1072,7 +1072,6 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     return c;
   };
   // ---- passes: values, the bound, the lists ---------------------------------
-  const int jw = (k + kWaves - 1) / kWaves;  // per-wave rank of the bound
   // Long (bucketed) histories, whose members are many, with penalties that
   // only lower values (repetition >= 1, frequency >= 0, presence >= 0;
   // rounding keeps this): a member whose raw value is below the bound stays
@@ -1159,12 +1158,24 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
         m = fmaxf(m, fmaxf(fmaxf(v[f].x, v[f].y), fmaxf(v[f].z, v[f].w)));
       }
     }
-    // the bound: at least jw lane maxima of every wave reach its own
-    // result, so at least 4 jw >= k values of the part reach the smallest
-    const uint32_t tw = wave_jth_largest_key16(okey(m), jw);
+    // the bound: at least j lane maxima of each of the first nw waves reach
+    // its own result, so at least nw j >= k values of the part reach the
+    // smallest.  A pass of 1,024 ids or more puts ids in every lane (four
+    // waves at rank ceil(k / 4)); a shorter one (the row's last part) leaves
+    // the last waves' lanes without ids, and those waves take no part (their
+    // results are left out of the minimum, which spills no register).
+    const int rem = lo + nids - base;
+    const BoundRank br = rem >= 4 * 64 * kWaves ? BoundRank{kWaves, (k + kWaves - 1) / kWaves} : bound_rank(rem, 4, k);
+    const uint32_t tw = wave_rank_key(okey(m), br.j);
     if (lane == 0) s_thr[wave] = tw;
     lds_barrier();
-    tkey = max(tkey, min(min(s_thr[0], s_thr[1]), min(s_thr[2], s_thr[3])));
+    {
+      uint32_t t = s_thr[0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w)
+        if (w < br.nw) t = min(t, s_thr[w]);
+      tkey = max(tkey, t);
+    }
     // keys at or below okey(-inf) (0 or truncated) admit every valid value
     const float tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
     // whole float4s with a value at or above the bound go to the list (one

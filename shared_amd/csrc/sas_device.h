@@ -18,6 +18,25 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kCapBlock = 256;          // candidates one exact chunk selection may emit
 constexpr uint32_t kPenFlag = 0x80000000u;
 
+// The waves that bound a part, and the rank each takes: lane l of wave w
+// holds the part's ids from per * (64 w + l) on, `nids` ids in all.  Each
+// of the first nw waves has j lane maxima at or above its j-th largest, so
+// nw j >= k values of the part reach the smallest of those results.  A wave
+// with fewer than j lanes that hold an id cannot bound (its result would be
+// "no value"), so nw is the most waves whose last one has j = ceil(k / nw)
+// such lanes; the other waves take no part.
+struct BoundRank {
+  int nw, j;
+};
+__device__ __forceinline__ BoundRank bound_rank(int nids, int per, int k) {
+  // unrolled: every divisor a constant (no integer division instruction)
+#pragma unroll
+  for (int nw = kWaves; nw > 1; --nw) {
+    const int j = (k + nw - 1) / nw;
+    if ((nids - per * 64 * (nw - 1) + per - 1) / per >= j) return {nw, j};
+  }
+  return {1, k};
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 // A float4 that needs 4-byte alignment only (global loads take it as one 16-byte access).
@@ -283,6 +302,13 @@ __device__ __forceinline__ uint32_t wave_reduce(uint32_t x, Op op) {
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
   return wave_reduce(x, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+// A wave's bound at rank j: a key that at least j lane keys reach.  Rank 1
+// (greedy rows) takes the wave's largest key exactly; other ranks the 16-bit
+// lower bound of wave_jth_largest_key16, at half the ballot steps of the
+// exact search.
+__device__ __forceinline__ uint32_t wave_rank_key(uint32_t u, int j) {
+  return j == 1 ? wave_max_u32(u) : wave_jth_largest_key16(u, j);
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
   return wave_reduce(x, [](uint32_t a, uint32_t b) { return a < b ? a : b; });

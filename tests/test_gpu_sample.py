@@ -57,6 +57,22 @@ def test_random_params(sampler, seed, vocab):
     check(sampler, b)
 
 
+@pytest.mark.parametrize("tail", [1, 5, 255, 257, 384, 511, 513, 767, 769, 1023])
+def test_short_last_part(sampler, tail):
+    # 12 rows of 37 * 4,096 + tail ids: on 256 CUs the library splits each row
+    # into 38 parts of 4,096 ids, so the last part holds `tail` ids and the
+    # lanes of its last waves hold none.  Its bound comes from the waves that
+    # hold ids (rank 1, the exact wave maximum, for greedy rows and small k);
+    # some rows have their best values in that part.
+    vocab = 37 * 4096 + tail
+    for p in (Params(temperature=0.0, repetition_penalty=1.1), Params(temperature=1.0, top_k=3, top_p=1.0),
+              Params(temperature=0.8, top_k=50, top_p=0.9), Params(temperature=1.0, top_k=128, top_p=1.0)):
+        b = _small_batch(7 + tail, rows=12, vocab=vocab, params=p, hist=64)
+        b.logits[::3, vocab - tail:] += np.float32(4.0)
+        print(f"[gpu] short last part tail={tail} {p}", flush=True)
+        check(sampler, b)
+
+
 def test_row_params_mixed(sampler):
     rng = np.random.default_rng(7)
     rows = 24
