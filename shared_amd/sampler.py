@@ -99,13 +99,25 @@ def row_hints(rows: Sequence[Params]) -> int:
     return _capi.HINT_NO_SOFTCAP if all(not (p.softcap > 0) for p in rows) else 0
 
 
-def _ptr(t) -> Optional[int]:
+# Element types the C ABI reads: 4-byte integers (ids, offsets, mask words,
+# seeds, counts, flags; int32 or uint32), float64 (uniforms, probabilities)
+# and float32 (logits).  A tensor of another width would be read as the
+# wrong values, so it is refused here.
+_KINDS = {"i32": (4, False), "f64": (8, True), "f32": (4, True)}
+
+
+def _ptr(t, kind: Optional[str] = None, name: str = "tensor") -> Optional[int]:
     if t is None:
         return None
     if not t.is_cuda:
         raise ValueError("device tensors are required")
     if not t.is_contiguous() and t.dim() == 1:
         raise ValueError("1-D inputs must be contiguous")
+    if kind is not None:
+        size, fp = _KINDS[kind]
+        if t.element_size() != size or t.dtype.is_floating_point != fp:
+            want = f"float{8 * size}" if fp else f"{8 * size}-bit integer"
+            raise ValueError(f"{name} must hold {want} elements (got {t.dtype})")
     return t.data_ptr()
 
 
@@ -130,20 +142,20 @@ def rows_descriptor(logits, out_ids, *, vocab: Optional[int] = None, mask=None, 
     d.vocab = vocab
     d.rows = rows
     if mask is not None:
-        d.mask = _ptr(mask)
+        d.mask = _ptr(mask, "i32", "mask")
         d.mask_stride = mask.stride(0)
-    d.hist_ids = _ptr(hist_ids)
-    d.hist_offsets = _ptr(hist_offsets)
+    d.hist_ids = _ptr(hist_ids, "i32", "hist_ids")
+    d.hist_offsets = _ptr(hist_offsets, "i32", "hist_offsets")
     d.hist_count = hist_ids.numel() if hist_ids is not None else 0
     d.row_hints = int(row_hints)
-    d.uniforms = _ptr(uniforms)
+    d.uniforms = _ptr(uniforms, "f64", "uniforms")
     d.params = (params or Params()).to_c()
     d.row_params = _ptr(row_params)
-    d.out_ids = _ptr(out_ids)
-    d.out_probs = _ptr(out_probs)
-    d.out_cand_ids = _ptr(out_cand_ids)
-    d.out_counts = _ptr(out_counts)
-    d.out_flags = _ptr(out_flags)
+    d.out_ids = _ptr(out_ids, "i32", "out_ids")
+    d.out_probs = _ptr(out_probs, "f64", "out_probs")
+    d.out_cand_ids = _ptr(out_cand_ids, "i32", "out_cand_ids")
+    d.out_counts = _ptr(out_counts, "i32", "out_counts")
+    d.out_flags = _ptr(out_flags, "i32", "out_flags")
     return d
 
 
@@ -322,7 +334,7 @@ class Sampler:
         h.weight = weight.data_ptr()
         h.weight_stride = weight.stride(0)
         h.dim = int(dim if dim is not None else hidden.shape[1])
-        h.out_logits = _ptr(out_logits)
+        h.out_logits = _ptr(out_logits, "f32", "out_logits")
         h.format = int(fmt)
         return h
 
@@ -406,22 +418,22 @@ class Sampler:
         d.vocab = int(vocab if vocab is not None else target.shape[1])
         d.seqs = seqs
         d.draft_len = L
-        d.draft_ids = _ptr(draft_ids)
+        d.draft_ids = _ptr(draft_ids, "i32", "draft_ids")
         if mask is not None:
-            d.mask = _ptr(mask)
+            d.mask = _ptr(mask, "i32", "mask")
             d.mask_stride = mask.stride(0)
-        d.hist_ids = _ptr(hist_ids)
-        d.hist_offsets = _ptr(hist_offsets)
+        d.hist_ids = _ptr(hist_ids, "i32", "hist_ids")
+        d.hist_offsets = _ptr(hist_offsets, "i32", "hist_offsets")
         d.hist_count = hist_ids.numel() if hist_ids is not None else 0
         d.params = (params or Params()).to_c()
         d.seq_params = _ptr(seq_params)
-        d.seeds = _ptr(seeds)
+        d.seeds = _ptr(seeds, "i32", "seeds")
         d.round = int(round) & 0xFFFFFFFF
         d.row_hints = int(row_hints)
-        d.stop_ids = _ptr(stop_ids)
-        d.out_picks = _ptr(out_picks)
-        d.out_accepted = _ptr(out_accepted)
-        d.out_next = _ptr(out_next)
+        d.stop_ids = _ptr(stop_ids, "i32", "stop_ids")
+        d.out_picks = _ptr(out_picks, "i32", "out_picks")
+        d.out_accepted = _ptr(out_accepted, "i32", "out_accepted")
+        d.out_next = _ptr(out_next, "i32", "out_next")
         return d
 
     def spec_exact_into(self, target, draft_ids, seeds, out_picks, out_accepted, *, stream=None, **kw) -> None:
@@ -456,14 +468,14 @@ class Sampler:
         d.vocab = int(vocab if vocab is not None else target.shape[1])
         d.seqs = seqs
         d.draft_len = L
-        d.draft_ids = _ptr(draft_ids)
+        d.draft_ids = _ptr(draft_ids, "i32", "draft_ids")
         if mask is not None:
-            d.mask = _ptr(mask)
+            d.mask = _ptr(mask, "i32", "mask")
             d.mask_stride = mask.stride(0)
-        d.uniforms = _ptr(uniforms)
+        d.uniforms = _ptr(uniforms, "f64", "uniforms")
         d.temperature = float(temperature)
-        d.out_tokens = _ptr(out_tokens)
-        d.out_accepted = _ptr(out_accepted)
+        d.out_tokens = _ptr(out_tokens, "i32", "out_tokens")
+        d.out_accepted = _ptr(out_accepted, "i32", "out_accepted")
         check(self._lib.sas_verify(self._h, ctypes.byref(d), _stream(stream)), self._h)
 
     def verify(self, target, draft, draft_ids, uniforms, **kw):

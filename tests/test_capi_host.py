@@ -192,3 +192,35 @@ def test_rows_struct_matches_the_header():
     body = re.search(r"typedef struct sas_rows \{(.*?)\} sas_rows;", text, re.S).group(1)
     names = re.findall(r"\b([a-z_]+);", re.sub(r"/\*.*?\*/", "", body, flags=re.S))
     assert names == [f for f, _ in _capi.SasRows._fields_]
+
+
+def test_device_pointers_refuse_other_element_types():
+    # the Python mirror checks each tensor's element type against the one the
+    # C ABI reads (a tensor stand-in: no device is needed for the check)
+    import torch
+    from shared_amd import sampler as S
+
+    class DeviceTensor:
+        is_cuda = True
+
+        def __init__(self, dtype):
+            self.dtype = dtype
+
+        def is_contiguous(self):
+            return True
+
+        def dim(self):
+            return 1
+
+        def element_size(self):
+            return self.dtype.itemsize
+
+        def data_ptr(self):
+            return 4096
+
+    for dtype, kind in ((torch.int32, "i32"), (torch.uint32, "i32"), (torch.float64, "f64"), (torch.float32, "f32")):
+        assert S._ptr(DeviceTensor(dtype), kind, "x") == 4096
+    for dtype, kind in ((torch.int64, "i32"), (torch.float32, "i32"), (torch.int16, "i32"), (torch.float32, "f64"),
+                        (torch.int64, "f64"), (torch.float16, "f32")):
+        with pytest.raises(ValueError, match="x must hold"):
+            S._ptr(DeviceTensor(dtype), kind, "x")

@@ -384,6 +384,14 @@ def test_argument_errors_are_reported(sampler):
     with pytest.raises(SasError, match="mask_stride"):
         sampler.sample_into(x, ids, mask=torch.zeros((2, 2), dtype=torch.int32, device="cuda"), params=Params())
     sampler.sample_into(x[:0], ids, params=Params())          # zero rows is a no-op
+    # element types the C ABI would misread are refused before the call
+    hid = torch.zeros(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="hist_offsets"):
+        sampler.sample_into(x, ids, hist_ids=hid, hist_offsets=torch.zeros(3, dtype=torch.int64, device="cuda"),
+                            params=Params())
+    with pytest.raises(ValueError, match="uniforms"):
+        sampler.sample_into(x, ids, uniforms=torch.zeros(2, dtype=torch.float32, device="cuda"),
+                            params=Params(temperature=1.0))
 
 
 def test_one_mask_for_every_row(sampler):
