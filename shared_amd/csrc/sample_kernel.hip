@@ -1082,6 +1082,15 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   const uint32_t sh = 4u * (uint32_t)(tid & 7);
   uint32_t tkey = 0u;  // the part's bound (okey image; 0 = none)
   uint32_t n_q = 0u;   // float4 entries of this wave's list (may pass kQuadCap: overflow)
+  // Softcap rows of one pass, members in the exact list: the values stay raw
+  // until the cut.  The cap is non-decreasing, so the raw bound certifies k
+  // capped values at or above its cap, and a capped value can reach that only
+  // within a margin below the raw bound (the margin spans the cap's f32
+  // plateaus there): the lists take the values down to the margin, and only
+  // they are capped.  Where the cap flattens (a bound beyond 5 cap) the part
+  // caps every value and bounds the capped values instead.
+  const bool raw_cap = kSoftcap && !kList && softcap > 0.0f && npass == 1;
+  bool capped = !raw_cap;  // the registers and lists hold capped values (or the row has no cap)
   auto run_pass = [&](int base) __attribute__((always_inline)) {
     // the history members of this thread's word
     const uint32_t hb = has_hist ? L.hbits[tid] : 0u;
@@ -1109,7 +1118,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
           v[f].z = tw;
         }
       }
-      if (kSoftcap && softcap > 0.0f) {
+      if (kSoftcap && softcap > 0.0f && !raw_cap) {
         v[f].x = softcap_f32(v[f].x, softcap);
         v[f].y = softcap_f32(v[f].y, softcap);
         v[f].z = softcap_f32(v[f].z, softcap);
@@ -1177,7 +1186,38 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
       tkey = max(tkey, t);
     }
     // keys at or below okey(-inf) (0 or truncated) admit every valid value
-    const float tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
+    float tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
+    if (kSoftcap && !capped) {
+      if (tf > -__builtin_inff() && !(fabsf(tf) <= 5.0f * softcap)) {
+        // the cap flattens at the bound: cap every value, bound the capped ones
+        float m2 = qnan();
+#pragma unroll
+        for (int f = 0; f < kSlots; ++f) {
+          v[f].x = softcap_f32(v[f].x, softcap);
+          v[f].y = softcap_f32(v[f].y, softcap);
+          v[f].z = softcap_f32(v[f].z, softcap);
+          v[f].w = softcap_f32(v[f].w, softcap);
+          m2 = fmaxf(m2, fmaxf(fmaxf(v[f].x, v[f].y), fmaxf(v[f].z, v[f].w)));
+        }
+        const uint32_t tw2 = wave_rank_key(okey(m2), br.j);
+        lds_barrier();  // every wave has read the raw results
+        if (lane == 0) s_thr[wave] = tw2;
+        lds_barrier();
+        uint32_t t = s_thr[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w)
+          if (w < br.nw) t = min(t, s_thr[w]);
+        tkey = t;
+        tf = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
+        capped = true;
+      } else if (tf > -__builtin_inff()) {
+        // values whose cap can equal the bound's: the cap rises by 3 ulp of
+        // tanh (near 1) over cap 2^-24 / sech^2(b / cap), plus the rounding
+        // of x / cap; the margin is five times that
+        const float ch = coshf(tf / softcap);
+        tf -= softcap * 0x1p-20f * ch * ch + 1e-5f * (1.0f + fabsf(tf));
+      }
+    }
     // whole float4s with a value at or above the bound go to the list (one
     // ballot per float4); their values are cut to the final bound at the end
 #pragma unroll
@@ -1213,10 +1253,15 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   }
   // this wave's list, one float4 per lane, cut to the final bound: each
   // lane's values at or above it, and their places among the wave's records
-  const float tff = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
+  // (raw values: the listed ones capped here, the bound's cap the final bound)
+  const float tfr = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
+  const float tff = kSoftcap && !capped ? softcap_f32(tfr, softcap) : tfr;
   const uint32_t qat = (uint32_t)wave * kQuadCap + (uint32_t)lane;
   const bool qin = (uint32_t)lane < n_q && n_q <= (uint32_t)kQuadCap;
-  const float4 q = qin ? L.q_val[qat] : make_float4(qnan(), qnan(), qnan(), qnan());
+  float4 q = qin ? L.q_val[qat] : make_float4(qnan(), qnan(), qnan(), qnan());
+  if (kSoftcap && !capped)
+    q = make_float4(softcap_f32(q.x, softcap), softcap_f32(q.y, softcap), softcap_f32(q.z, softcap),
+                    softcap_f32(q.w, softcap));
   const uint32_t qid = L.q_base[qat];
   uint32_t pm = (q.x >= tff ? 1u : 0u) | (q.y >= tff ? 2u : 0u) | (q.z >= tff ? 4u : 0u) | (q.w >= tff ? 8u : 0u);
   if (kList && has_hist && lower) {
@@ -1270,7 +1315,9 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   double xv = 0.0;
   if (has_hist && (uint32_t)tid < min(s_nx, (uint32_t)kXCap)) {
     xid = L.x_id[tid];
-    xv = penalize(L.x_val[tid], hcount(xid), p);
+    // members recorded raw are capped first
+    const double xr = L.x_val[tid];
+    xv = penalize(kSoftcap && raw_cap ? (double)softcap_f32((float)xr, softcap) : xr, hcount(xid), p);
     xw = xv >= (double)tff;
     if (xw) atomicAdd(&s_nxk, 1u);
   }
@@ -1400,7 +1447,8 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   // the part's counts, bound and slow-selection flag
   if (tid == 0)
     put_rec(a.pinfo + (int64_t)row * pinfo_stride(P) + part,
-            (uint64_t)((nplain + nx - nxm) | (nxm << 16) | (s_flags ? kPinfoSlow : 0u)) | ((uint64_t)tkey << 32));
+            (uint64_t)((nplain + nx - nxm) | (nxm << 16) | (s_flags ? kPinfoSlow : 0u)) |
+                ((uint64_t)(kSoftcap && !capped ? (tkey > 0x007FFFFFu ? okey(tff) : 0u) : tkey) << 32));
 }
 
 // Parts per row and ids per part: one pass per part (8192 ids), more

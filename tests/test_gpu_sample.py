@@ -351,6 +351,25 @@ def test_gemma_softcap_rows(sampler, params):
     check(sampler, b, label="softcap")
 
 
+@pytest.mark.parametrize("sigma,shift", [(0.3, 0.0), (12.0, 0.0), (80.0, 0.0), (20.0, 320.0), (20.0, -320.0)])
+def test_softcap_bounds_from_raw_values(sampler, sigma, shift):
+    # The parts bound softcap rows on their raw values and cap only the
+    # values near the bound.  Spreads where the cap is nearly linear (0.3),
+    # curved (12), and flat at the bound (80: bounds beyond 5 cap, where every
+    # value is capped first); rows shifted into the flat ends, where many
+    # values cap to +-30 exactly and ties go by id.
+    rng = np.random.default_rng(int(sigma * 10) + abs(int(shift)))
+    rows, vocab = 8, W.GEMMA_VOCAB
+    x = (rng.standard_normal((rows, vocab)) * sigma + shift).astype(np.float32)
+    hi, ho = W._csr([rng.integers(0, vocab, 64) for _ in range(rows)])
+    for p in (Params(temperature=1.0, top_k=50, top_p=0.9, softcap=30.0),
+              Params(temperature=0.0, repetition_penalty=1.2, softcap=30.0),
+              Params(temperature=0.7, top_k=8, top_p=1.0, presence_penalty=0.5, softcap=30.0)):
+        b = W.Batch("softcap_raw", x, p, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+        print(f"[gpu] softcap raw bound sigma={sigma} shift={shift} {p}", flush=True)
+        check(sampler, b, label="softcap_raw")
+
+
 def test_back_to_back_launches_with_different_inputs(sampler):
     # the record area and its counters are reused by every launch: a stale
     # record would change ids or probabilities of the next batch
