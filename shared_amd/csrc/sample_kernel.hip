@@ -48,8 +48,8 @@ constexpr int kSlots = kSpanPass / (4 * kThreads);  // float4 per thread per pas
 static_assert(kSlots == 8, "a thread holds 32 values of a pass");
 constexpr int kHashSlots = 512;
 constexpr int kHistPre = 2;                          // history ids per thread loaded before the logits
-constexpr int kQuadCap = 64;                         // float4 entries of one wave's candidate list
-static_assert(kQuadCap == 64, "a wave's list is one entry per lane at the end");
+constexpr int kQuadCap = 128;                        // float4 entries of one wave's candidate list: two per lane
+static_assert(kQuadCap == 128, "a wave's list is at most two entries per lane at the end");
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 
 
@@ -914,7 +914,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   __shared__ uint32_t s_nxm;          // members among an exact selection's entries
   __shared__ uint32_t s_flags;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: a scalar
   const int P = a.parts;
   int lb = blockIdx.x;
   // XCD-aware order: consecutive dispatches rotate over the 8 XCDs, so give
@@ -1251,55 +1251,69 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
     lds_barrier();
     run_pass(base);
   }
-  // this wave's list, one float4 per lane, cut to the final bound: each
-  // lane's values at or above it, and their places among the wave's records
+  // this wave's list, cut to the final bound: entries lane and lane + 64 of
+  // each lane (the second only in a wave whose list passed 64 entries,
+  // which takes top-k above 64), each lane's values at or above the bound,
+  // and their places among the wave's records
   // (raw values: the listed ones capped here, the bound's cap the final bound)
   const float tfr = tkey > 0x007FFFFFu ? fkey(tkey) : -__builtin_inff();
   const float tff = kSoftcap && !capped ? softcap_f32(tfr, softcap) : tfr;
   const uint32_t qat = (uint32_t)wave * kQuadCap + (uint32_t)lane;
-  const bool qin = (uint32_t)lane < n_q && n_q <= (uint32_t)kQuadCap;
-  float4 q = qin ? L.q_val[qat] : make_float4(qnan(), qnan(), qnan(), qnan());
-  if (kSoftcap && !capped)
-    q = make_float4(softcap_f32(q.x, softcap), softcap_f32(q.y, softcap), softcap_f32(q.z, softcap),
-                    softcap_f32(q.w, softcap));
-  const uint32_t qid = L.q_base[qat];
-  uint32_t pm = (q.x >= tff ? 1u : 0u) | (q.y >= tff ? 2u : 0u) | (q.z >= tff ? 4u : 0u) | (q.w >= tff ? 8u : 0u);
-  if (kList && has_hist && lower) {
-    // members that reached the bound with their raw values: penalized here,
-    // and written as member records when they still reach it
-    uint4 *mrow4 = a.mrec + ((int64_t)row * P + part) * kMemSlots;
+  auto cut = [&](uint32_t e, float4 &q, uint32_t &qid) __attribute__((always_inline)) -> uint32_t {
+    const bool qin = (uint32_t)lane + e < n_q && n_q <= (uint32_t)kQuadCap;
+    q = qin ? L.q_val[qat + e] : make_float4(qnan(), qnan(), qnan(), qnan());
+    if (kSoftcap && !capped)
+      q = make_float4(softcap_f32(q.x, softcap), softcap_f32(q.y, softcap), softcap_f32(q.z, softcap),
+                      softcap_f32(q.w, softcap));
+    qid = L.q_base[qat + e];
+    uint32_t pm = (q.x >= tff ? 1u : 0u) | (q.y >= tff ? 2u : 0u) | (q.z >= tff ? 4u : 0u) | (q.w >= tff ? 8u : 0u);
+    if (kList && has_hist && lower) {
+      // members that reached the bound with their raw values: penalized here,
+      // and written as member records when they still reach it
+      uint4 *mrow4 = a.mrec + ((int64_t)row * P + part) * kMemSlots;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if ((pm >> c) & 1u) {
-        const uint32_t id = qid + (uint32_t)c;
-        // one pass: the part's history bitmap is still in LDS
-        const uint32_t off = id - (uint32_t)lo;
-        const bool member = npass == 1 ? ((L.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u : hcount(id) != 0u;
-        if (member) {
-          pm &= ~(1u << c);
-          const double pen = penalize((double)(c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w), hcount(id), p);
-          if (pen >= (double)tff) {
-            atomicAdd(&s_nxk, 1u);
-            const uint32_t d = atomicAdd(&s_nmw, 1u);
-            if (d < (uint32_t)kMemSlots) {
-              uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
-              put_rec(w, (uint64_t)__float_as_uint(rd_f32(pen)) | ((uint64_t)id << 32));
-              put_rec(w + 1, (uint64_t)__double_as_longlong(pen));
-            } else {
-              s_qover = 1u;  // more than the part's member slots: the exact selection
+      for (int c = 0; c < 4; ++c) {
+        if ((pm >> c) & 1u) {
+          const uint32_t id = qid + (uint32_t)c;
+          // one pass: the part's history bitmap is still in LDS
+          const uint32_t off = id - (uint32_t)lo;
+          const bool member = npass == 1 ? ((L.hbits[off >> 5] >> (off & 31u)) & 1u) != 0u : hcount(id) != 0u;
+          if (member) {
+            pm &= ~(1u << c);
+            const double pen = penalize((double)(c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w), hcount(id), p);
+            if (pen >= (double)tff) {
+              atomicAdd(&s_nxk, 1u);
+              const uint32_t d = atomicAdd(&s_nmw, 1u);
+              if (d < (uint32_t)kMemSlots) {
+                uint64_t *w = reinterpret_cast<uint64_t *>(mrow4 + d);
+                put_rec(w, (uint64_t)__float_as_uint(rd_f32(pen)) | ((uint64_t)id << 32));
+                put_rec(w + 1, (uint64_t)__double_as_longlong(pen));
+              } else {
+                s_qover = 1u;  // more than the part's member slots: the exact selection
+              }
             }
           }
         }
       }
     }
-  }
-  const uint32_t qcnt = (uint32_t)__popc(pm);
+    return pm;
+  };
+  float4 q, q1 = make_float4(qnan(), qnan(), qnan(), qnan());
+  uint32_t qid, qid1 = 0u;
+  uint32_t pm = cut(0u, q, qid);
+  if (n_q > 64u) pm |= cut(64u, q1, qid1) << 4;  // uniform over the wave
+  const uint32_t qcnt = (uint32_t)__popc(pm);  // at most 4, or 8 with a second entry
   uint32_t qpre = 0u, qtot = 0u;
 #pragma unroll
   for (int bit = 0; bit < 3; ++bit) {
     const uint64_t bb = __ballot((qcnt >> bit) & 1u);
     qpre += lanes_below(bb) << bit;
     qtot += (uint32_t)__popcll(bb) << bit;
+  }
+  if (n_q > 64u) {
+    const uint64_t bb = __ballot((qcnt >> 3) & 1u);
+    qpre += lanes_below(bb) << 3;
+    qtot += (uint32_t)__popcll(bb) << 3;
   }
   if (lane == 0) {
     s_nw[wave] = qtot;
@@ -1413,7 +1427,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   uint64_t *rrow = a.rec + ((int64_t)row * P + part) * kListCap;
   uint4 *mrow4 = a.mrec + ((int64_t)row * P + part) * kMemSlots;
   uint64_t *stg = reinterpret_cast<uint64_t *>(L.q_val);
-  static_assert(sizeof(L.q_val) + sizeof(L.q_base) == kListCap * sizeof(uint64_t), "the lists hold a part's records");
+  static_assert(sizeof(L.q_val) + sizeof(L.q_base) >= kListCap * sizeof(uint64_t), "the lists hold a part's records");
   {
     uint32_t j = off + qpre;
 #pragma unroll
@@ -1422,6 +1436,16 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
         const float x = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
         stg[j] = (uint64_t)__float_as_uint(x) | ((uint64_t)(qid + (uint32_t)c) << 32);
         ++j;
+      }
+    }
+    if (n_q > 64u) {  // the second entries, uniform over the wave
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if ((pm >> (c + 4)) & 1u) {
+          const float x = c == 0 ? q1.x : c == 1 ? q1.y : c == 2 ? q1.z : q1.w;
+          stg[j] = (uint64_t)__float_as_uint(x) | ((uint64_t)(qid1 + (uint32_t)c) << 32);
+          ++j;
+        }
       }
     }
   }
