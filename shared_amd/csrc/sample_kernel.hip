@@ -914,7 +914,7 @@ __global__ __launch_bounds__(kThreads, kSoftcap ? 4 : (kMask && !kHist) ? 5 : 6)
   __shared__ uint32_t s_nxm;          // members among an exact selection's entries
   __shared__ uint32_t s_flags;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: a scalar
+  const int tid = threadIdx.x, lane = tid & 63, wave = kList ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;  // a scalar where registers are short
   const int P = a.parts;
   int lb = blockIdx.x;
   // XCD-aware order: consecutive dispatches rotate over the 8 XCDs, so give
