@@ -321,6 +321,29 @@ def test_long_history_members_in_the_lists(sampler):
             assert g["flags"][0] & FLAG_SLOW_SELECT
 
 
+@pytest.mark.parametrize("top_k", [65, 100, 128])
+@pytest.mark.parametrize("hist_len", [64, 1500])
+def test_top_k_above_64_stays_on_the_lists(sampler, top_k, hist_len):
+    # top-k above 64: a wave's list passes 64 float4s and each lane cuts a
+    # second entry; whole 8192-id parts still emit their records from the
+    # lists (no SAS_FLAG_SLOW_SELECT), with short histories (hash) and long
+    # ones (bucketed, members riding in the lists)
+    rng = np.random.default_rng(top_k + hist_len)
+    vocab, rows = 151936, 8
+    x = (rng.standard_normal((rows, vocab)) * 3.0).astype(np.float32)
+    x[2, 70000:70200] = np.float32(11.0)  # ties across the cut
+    hist = [rng.integers(0, vocab, hist_len) for _ in range(rows)]
+    hist[3] = np.concatenate([np.arange(70000, 70100), hist[3]])
+    hi, ho = W._csr(hist)
+    for p in (Params(temperature=1.0, top_k=top_k, top_p=0.95),
+              Params(temperature=0.7, top_k=top_k, top_p=0.99, repetition_penalty=1.1, frequency_penalty=0.2,
+                     presence_penalty=0.1)):
+        b = W.Batch("top_k_lists", x, p, hist_ids=hi, hist_offsets=ho, uniforms=rng.random(rows))
+        print(f"[gpu] top-k {top_k} hist {hist_len} {p}", flush=True)
+        g, _ = check(sampler, b, label="top_k_lists")
+        assert not np.any(g["flags"] & FLAG_SLOW_SELECT), g["flags"]
+
+
 def test_repeated_launches_reset_state(sampler):
     b = W.c3p(rows=32, vocab=50000)
     first = run_gpu(sampler, b)
