@@ -82,7 +82,7 @@ __device__ __forceinline__ bool before(double va, uint32_t ia, double vb, uint32
 // where they are used.  launch_merge picks kMR from the expected count per
 // part (about 2 k plus a few).
 constexpr int kMRMax = 16;
-constexpr int kSurvCap = 512;     // survivors the merge ranks
+constexpr int kSurvCap = 1024;    // survivors the merge ranks
 constexpr uint32_t kInexact = 0x80000000u;  // composite bit: the exact value lies above the key
 
 struct MergeLds {
@@ -427,7 +427,8 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
                                                     (uint32_t)(row - srow * a.group))
                        : a.seeds      ? pcg_uniform(a.seeds[row], a.st_state[2 * row + 1], 0u)
                                       : a.uniforms[row];
-  for (int i = tid; i < kSurvCap + 8; i += kThreads) ml.s_c[i] = 0ull;  // padding: ranks after everything
+  // padding: ranks after everything (past more survivors, cleared once their count is known)
+  for (int i = tid; i < kSurvCap / 2 + 8; i += kThreads) ml.s_c[i] = 0ull;
   ml.s_rank[tid] = 0u;
   ml.s_rank[tid + kThreads] = 0u;
   if (tid == 0) ml.m = 0u;
@@ -675,6 +676,10 @@ __device__ __forceinline__ void merge_row(const SampleArgs &a, MergeLds &ml, int
     });
     __syncthreads();
     m = min(ml.m, (uint32_t)kSurvCap);
+  }
+  if (m > (uint32_t)(kSurvCap / 2)) {  // m is uniform over the block
+    if ((uint32_t)tid < 8u && m + (uint32_t)tid < (uint32_t)kSurvCap + 8u) ml.s_c[m + (uint32_t)tid] = 0ull;
+    __syncthreads();
   }
   const uint32_t m8 = (m + 7u) & ~7u;
   const uint32_t m64 = (m + 63u) & ~63u;
